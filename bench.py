@@ -1,0 +1,250 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged-KV decode hot path on one MI355X.
+
+Workload (Qwen3-8B-shaped decode, one layer): 32 query heads, 8 KV heads, head_dim 128, bf16,
+page size 16; batch 256 with context lengths ~ U[512, 8192] (including the new token); block
+tables are consecutive slices of one seeded permutation of a 160,000-page pool; K, V, q and the
+new K/V rows ~ N(0,1). One step = slot scatter of the 256 new K/V rows + paged GQA decode
+attention over every sequence. Inputs are resident in HBM before timing starts.
+
+Prints ONE JSON line with the whole-job throughput (algorithmic GB/s of a step), tokens/s,
+the roofline of the dominant kernel (attention: algorithmic bytes / average duration measured
+with HIP events on the launch stream) and the CPU baseline (the oracle's restatement of the
+reference torch path on this host's cores, on a bounded sample of the same inputs).
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-sample-seqs S] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "plastic-infer_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBPS = 8000.0
+B, HQ, HKV, D, P, NUM_PAGES = 256, 32, 8, 128, 16, 160_000
+LEN_LO, LEN_HI, SEED = 512, 8192, 2
+MAX_PAGES = LEN_HI // P
+WORKLOAD = "qwen3-8b paged decode: kv scatter + gqa paged attention, 1 layer"
+PMC_FILE = ROOT / "profiles" / "paged_decode_qwen3_8b_b256_pmc.json"
+
+
+def build_inputs(torch, dev):
+    g = torch.Generator().manual_seed(SEED)
+    lens = torch.randint(LEN_LO, LEN_HI + 1, (B,), generator=g)
+    perm = torch.randperm(NUM_PAGES, generator=g)
+    n_pages = (lens + P - 1) // P
+    bt = torch.zeros(B, MAX_PAGES, dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        n = int(n_pages[b])
+        bt[b, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    last = lens - 1
+    slots = bt[torch.arange(B), last // P].to(torch.int64) * P + last % P
+    gd = torch.Generator(device=dev).manual_seed(SEED)
+    kp = torch.empty(NUM_PAGES, HKV, D, P, dtype=torch.bfloat16, device=dev)
+    vp = torch.empty_like(kp)
+    step = 20_000
+    for pool in (kp, vp):
+        for s in range(0, NUM_PAGES, step):
+            pool[s:s + step] = torch.randn(pool[s:s + step].shape, generator=gd,
+                                           device=dev).to(torch.bfloat16)
+    k_new = torch.randn(B, HKV, D, generator=gd, device=dev).to(torch.bfloat16)
+    v_new = torch.randn(B, HKV, D, generator=gd, device=dev).to(torch.bfloat16)
+    q = torch.randn(B, HQ, D, generator=gd, device=dev).to(torch.bfloat16)
+    return dict(lens=lens, n_pages=n_pages, bt=bt, slots=slots, kp=kp, vp=vp, k_new=k_new,
+                v_new=v_new, q=q, bt_d=bt.to(dev), lens_d=lens.to(torch.int32).to(dev),
+                slots_d=slots.to(dev))
+
+
+def algorithmic_bytes(lens, n_pages, seqs=None):
+    """Bytes a step must move at minimum: K+V of every context token, q in, out, the block
+    table entries and lengths read, and the scatter (new rows read + written, slots)."""
+    idx = range(len(lens)) if seqs is None else seqs
+    tok = sum(int(lens[b]) for b in idx)
+    pages = sum(int(n_pages[b]) for b in idx)
+    nb = len(list(idx))
+    kv_row = 2 * HKV * D * 2                       # K + V bytes of one token, one layer
+    attn = tok * kv_row + nb * HQ * D * 2 * 2 + pages * 4 + nb * 4
+    scatter = nb * kv_row * 2 + nb * 8
+    return attn, scatter
+
+
+def cpu_info():
+    model, phys = "unknown", set()
+    try:
+        cur = {}
+        for line in open("/proc/cpuinfo"):
+            if ":" not in line:
+                if "physical id" in cur and "core id" in cur:
+                    phys.add((cur["physical id"], cur["core id"]))
+                cur = {}
+                continue
+            k, v = (s.strip() for s in line.split(":", 1))
+            cur[k] = v
+            if k == "model name":
+                model = v
+    except OSError:
+        pass
+    return model, len(phys) or None
+
+
+def cpu_baseline(torch, inp, n_seqs):
+    """The oracle (CPU restatement of the reference torch path: per-token index store, then per
+    sequence index_select gather + repeat_interleave + SDPA) on the first n_seqs sequences of
+    the same inputs, copied from the device. 1 warm-up, median of 3."""
+    import oracle.paged_kv as OP
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    seqs = list(range(min(n_seqs, B)))
+    # compact host pool holding only the sample's pages, renumbered 0..n-1
+    tables, ids = [], []
+    for b in seqs:
+        n = int(inp["n_pages"][b])
+        tables.append(list(range(len(ids), len(ids) + n)))
+        ids.extend(inp["bt"][b, :n].tolist())
+    dev_ids = torch.tensor(ids, device=inp["kp"].device)
+    kp = inp["kp"].index_select(0, dev_ids).cpu()
+    vp = inp["vp"].index_select(0, dev_ids).cpu()
+    bt = torch.zeros(len(seqs), MAX_PAGES, dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    lens = inp["lens"][seqs].to(torch.int32)
+    last = lens.long() - 1
+    slots = bt[torch.arange(len(seqs)), last // P].long() * P + last % P
+    k_new, v_new = inp["k_new"][seqs].cpu(), inp["v_new"][seqs].cpu()
+    q = inp["q"][seqs].cpu()
+
+    def step():
+        OP.scatter_slots(k_new, v_new, kp, vp, slots.tolist())
+        OP.decode_batch(q, kp, vp, bt, lens, P)
+
+    step()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    attn, sc = algorithmic_bytes(inp["lens"], inp["n_pages"], seqs)
+    model, phys = cpu_info()
+    return {
+        "value": round((attn + sc) / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+        "kind": "port",
+        "sample": f"first {len(seqs)} of {B} sequences of the same step (same input bits), "
+                  f"1 warm-up + median of 3, {t * 1e3:.1f} ms per sample step",
+        "tokens_per_s": round(len(seqs) / t, 2), "cpu_model": model, "physical_cores": phys,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-sample-seqs", type=int, default=128)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the paged decode path on ONE GPU (per-GPU shard of a "
+              "sequence-sharded deployment); multi-GPU runs are not part of this build.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from plastic_infer.kernel import decode_workspace_bytes, kv_scatter, paged_decode_attention
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    print(f"bench: generating inputs (B={B}, pool={NUM_PAGES} pages)", file=sys.stderr, flush=True)
+    inp = build_inputs(torch, dev)
+    out = torch.empty(B, HQ, D, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(decode_workspace_bytes(B, HQ, D, P, MAX_PAGES), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step(ev_a=None, ev_b=None):
+        kv_scatter(inp["k_new"], inp["v_new"], inp["kp"], inp["vp"], inp["slots_d"])
+        if ev_a is not None:
+            ev_a.record(stream)
+        paged_decode_attention(inp["q"], inp["kp"], inp["vp"], inp["bt_d"], inp["lens_d"],
+                               out=out, workspace=ws)
+        if ev_b is not None:
+            ev_b.record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize(dev)
+    print(f"bench: warmup done, timing {args.steps} steps", file=sys.stderr, flush=True)
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    for i in range(args.steps):
+        step(*ev[i])
+    t_end.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - wall0
+    ms_step = t_start.elapsed_time(t_end) / args.steps
+    attn_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+
+    attn_bytes, scatter_bytes = algorithmic_bytes(inp["lens"], inp["n_pages"])
+    step_bytes = attn_bytes + scatter_bytes
+    gbps = step_bytes / (ms_step / 1e3) / 1e9
+    attn_gbps = attn_bytes / (attn_ms / 1e3) / 1e9
+    traffic = None
+    if PMC_FILE.exists():
+        try:
+            traffic = json.loads(PMC_FILE.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    result = {
+        "metric": "KV scatter + paged decode-attn GB/s (% of HBM peak); decode tokens/s",
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V/q, seeded lengths and block tables)",
+        "config": {"workload": WORKLOAD, "batch": B, "q_heads": HQ, "kv_heads": HKV,
+                   "head_dim": D, "page_size": P, "context_len": f"U[{LEN_LO},{LEN_HI}]",
+                   "pool_pages": NUM_PAGES, "tokens_in_context": int(inp["lens"].sum())},
+        "tokens_per_s": round(B / (ms_step / 1e3), 1),
+        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "bytes_per_step": step_bytes,
+        "wall_s_timed": round(wall, 4),
+        "roofline": {
+            "kernel": "paged_decode_bf16_d128p16 + paged_decode_reduce (one attention call)",
+            "bound": "hbm", "achieved": round(attn_gbps, 2), "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
+            "algorithmic_bytes_per_launch": attn_bytes, "avg_launch_ms": round(attn_ms, 4),
+        },
+    }
+    if not args.no_cpu_baseline:
+        print(f"bench: cpu baseline on {args.cpu_sample_seqs} sequences", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(torch, inp, args.cpu_sample_seqs)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

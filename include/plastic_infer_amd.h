@@ -1,0 +1,249 @@
+/*
+ * plastic_infer_amd.h — C-ABI of the MI355X (gfx950) paged-KV and expert-cache data path.
+ *
+ * One shared library, libplastic_infer_amd.so, built with hipcc for gfx950. Every entry point
+ * takes plain device/host pointers, sizes and a HIP stream handle (hipStream_t passed as void*;
+ * NULL = the legacy default stream), enqueues its kernels asynchronously on that stream and
+ * returns an int status:
+ *     0                 success
+ *     PIA_EINVAL (-1)   invalid argument (shape, dtype, alignment, size limit); nothing enqueued
+ *     PIA_EUNSUPPORTED  (-2) a valid combination this build does not implement; nothing enqueued
+ *     > 0               a hipError_t returned by the HIP runtime
+ * pia_last_error() returns a NUL-terminated, thread-local description of the last failure.
+ *
+ * Ownership: the caller owns every buffer. The library never allocates or frees device memory;
+ * scratch space is passed in as a caller-owned workspace whose size a *_workspace_bytes query
+ * reports. Index/slot arguments that point outside the pool are skipped by the kernels (never
+ * dereferenced), mirroring a bounds-checked store rather than faulting.
+ *
+ * Layouts (row-major, innermost last):
+ *   KV pool   k_pages / v_pages : [num_pages, num_kv_heads, head_dim, page_size]   (token innermost)
+ *   new rows  k / v             : [num_tokens, num_kv_heads, head_dim] with a token stride
+ *   queries   q / out           : [rows, num_heads, head_dim]
+ *   block tables                : int32 [num_seqs, bt_stride]  (logical page -> physical page)
+ *
+ * This is the boundary that replaces the reference's torch data path and its nvcc-JIT ctypes
+ * shims (reference: src/plastic_infer/kernel/jit.py:87-124, kernel/fast_index_copy.py:78-243).
+ */
+#ifndef PLASTIC_INFER_AMD_H
+#define PLASTIC_INFER_AMD_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PIA_EINVAL (-1)
+#define PIA_EUNSUPPORTED (-2)
+
+/* Element type codes (dtype arguments). */
+#define PIA_DTYPE_F32 0
+#define PIA_DTYPE_F16 1
+#define PIA_DTYPE_BF16 2
+
+/* ---------------------------------------------------------------------------------------------
+ * Library
+ * ------------------------------------------------------------------------------------------- */
+
+/* Thread-local message of the last non-zero status returned on this thread. */
+const char* pia_last_error(void);
+
+/* ABI version of this build (bumped on any signature change). */
+int pia_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * (a3/a4) Slot-mapped KV scatter.
+ * Replaces the per-token advanced-index store of _write_kv_layer
+ * (reference: src/plastic_infer/exec/runner_paged.py:112-129) and of KVRequestCache.append_token
+ * (src/plastic_infer/kv/kv_store.py:124-143):  for i < num_tokens with slot = slot_mapping[i],
+ *     k_pages[slot / page_size, h, d, slot % page_size] = k[i, h, d]   (same for v)
+ * Slots < 0 (padding) or >= num_pages*page_size are skipped. Bit-exact byte copy;
+ * elem_bytes is 2 or 4. k_token_stride / v_token_stride are in elements.
+ * ------------------------------------------------------------------------------------------- */
+int pia_kv_scatter(const void* k, const void* v, void* k_pages, void* v_pages,
+                   const int64_t* slot_mapping, int64_t num_tokens,
+                   int64_t k_token_stride, int64_t v_token_stride,
+                   int num_kv_heads, int head_dim, int page_size, int64_t num_pages,
+                   int elem_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * (a5) Block-table gather into contiguous rows, batched over sequences.
+ * Replaces gather_paged_kv (reference: src/plastic_infer/exec/attention.py:103-148):
+ *     k_out[cu_seqlens[b] + t, h, d] = k_pages[block_tables[b, t / P], h, d, t % P]
+ * for t < cu_seqlens[b+1] - cu_seqlens[b]. max_seq_len bounds the grid (tokens beyond a row's
+ * table capacity bt_stride*P are not read). Bit-exact.
+ * ------------------------------------------------------------------------------------------- */
+int pia_kv_gather(void* k_out, void* v_out, const void* k_pages, const void* v_pages,
+                  const int32_t* block_tables, int64_t bt_stride, const int64_t* cu_seqlens,
+                  int num_seqs, int64_t max_seq_len,
+                  int num_kv_heads, int head_dim, int page_size, int64_t num_pages,
+                  int elem_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Page <-> chunk copies for KV chunk sinking / prefix loading
+ * (reference: src/plastic_infer/kv/kv_store.py:230-276 sink, :282-334 load_prefix).
+ * A chunk buffer is [num_layers, num_kv_heads, head_dim, pages_per_chunk * page_size];
+ * page_ids is int64 [num_layers * pages_per_chunk] (layer-major), -1 = absent page (skipped).
+ *   to_chunk != 0 : chunk[l, h, d, p*P + t] = pages[page_ids[l*ppc + p], h, d, t]
+ *   to_chunk == 0 : pages[page_ids[l*ppc + p], h, d, t] = chunk[l, h, d, p*P + t]
+ * ------------------------------------------------------------------------------------------- */
+int pia_kv_pages_chunk_copy(void* chunk, void* pages, const int64_t* page_ids,
+                            int num_layers, int pages_per_chunk,
+                            int num_kv_heads, int head_dim, int page_size, int64_t num_pages,
+                            int elem_bytes, int to_chunk, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * (a6) Paged GQA decode attention, batched: one query row per sequence.
+ * Per-row semantics of paged_attention_v1(q[b][None,None], ..., kv_num_tokens=L_b, causal=False)
+ * (reference: src/plastic_infer/exec/attention.py:151-190, decode call
+ * src/plastic_infer/exec/runner_paged.py:253-255): head hq reads kv head hq / (H / Hkv),
+ *     out[b, hq, :] = softmax(scale * q[b, hq, :] . K_b^T) V_b   over the L_b = context_lens[b]
+ * tokens of block_tables[b, :ceil(L_b / P)]. fp32 accumulation and online softmax.
+ * q row stride between sequences is q_seq_stride elements; heads are contiguous [H, D].
+ * out is contiguous [num_seqs, num_heads, head_dim]; L_b == 0 writes zeros.
+ * workspace: caller-owned device scratch of at least
+ *     pia_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim, page_size, bt_stride)
+ * bytes (may be NULL when that query returns 0).
+ * bf16 with head_dim 128 and page_size 16 takes the split-context fast kernel; every other
+ * supported combination (f32/f16/bf16, head_dim <= 512, any page_size) takes the general kernel.
+ * ------------------------------------------------------------------------------------------- */
+int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim,
+                                         int page_size, int64_t bt_stride);
+
+int pia_paged_decode_attention(void* out, const void* q, int64_t q_seq_stride,
+                               const void* k_pages, const void* v_pages,
+                               const int32_t* block_tables, int64_t bt_stride,
+                               const int32_t* context_lens, int num_seqs,
+                               int num_heads, int num_kv_heads, int head_dim, int page_size,
+                               int64_t num_pages, float scale, int dtype,
+                               void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * (a6/a7) General paged attention over several query rows per sequence (prefill / chunked
+ * prefill / the drop-in paged_attention_v1 and _attn_paged paths).
+ * Rows of sequence b are q[cu_q[b] .. cu_q[b+1]) (cu_q NULL: one row per sequence). Row s of b
+ * attends keys j < kv_lens[b]; when q_pos_offsets != NULL additionally j <= q_pos_offsets[b] + s
+ * (offset 0 = torch SDPA is_causal=True top-left alignment, reference
+ * src/plastic_infer/exec/attention.py:189; offset q_start_pos = the explicit mask of
+ * src/plastic_infer/exec/runner_paged.py:61-95). A row with no admissible key writes zeros.
+ * ------------------------------------------------------------------------------------------- */
+int pia_paged_attention(void* out, const void* q, const void* k_pages, const void* v_pages,
+                        const int32_t* block_tables, int64_t bt_stride,
+                        const int32_t* kv_lens, const int32_t* cu_q, const int32_t* q_pos_offsets,
+                        int num_seqs, int64_t total_q_rows,
+                        int num_heads, int num_kv_heads, int head_dim, int page_size,
+                        int64_t num_pages, float scale, int dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * (a8) Router: top-k expert selection per token.
+ * mode 0 = _torch_fused_topk (reference: src/plastic_infer/moe/fused.py:11-30):
+ *     p = softmax(float(logits)); (w, ids) = topk(p, k); w /= sum(w) if renormalize.
+ * mode 1 = topk_route (reference: src/plastic_infer/exec/moe.py:19-38):
+ *     (x, ids) = topk(logits, k); w = softmax(float(x)).
+ * Selection order: descending logit, lowest expert index first on exact ties. Weights are
+ * written as fp32 [T, k], ids as int32 [T, k]. logits_dtype: PIA_DTYPE_*; num_experts <= 1024.
+ * Rows t >= num_token_non_padded (when >= 0) get ids = -1, as the reference's padding rule.
+ * ------------------------------------------------------------------------------------------- */
+int pia_moe_topk(float* topk_weights, int32_t* topk_ids, const void* logits, int logits_dtype,
+                 int64_t num_tokens, int num_experts, int topk, int renormalize, int mode,
+                 int64_t num_token_non_padded, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * (a9) Permute plan (moe_align_block_size, reference: src/plastic_infer/moe/fused.py:48-94,
+ * semantics src/plastic_infer/kernel/triton/moe_align.py:9-20,216-239).
+ * effective_E = num_experts + 1 (ids in [0, num_experts] are routed, others dropped).
+ *   count[e], padded cumsum in multiples of block_size, num_tokens_post_pad = cumsum[E+1],
+ *   expert_ids[blk] = owning expert for blk < npp/block (-1 beyond),
+ *   sorted_token_ids[cumsum[e] + r] = r-th route (flattened index t*k+s) of expert e in
+ *   ASCENDING route order (the deterministic order moe_forward_sparse's nonzero() yields,
+ *   reference src/plastic_infer/exec/moe.py:149); every other entry = numel (sentinel).
+ *   route_pos (optional, may be NULL): route_pos[i] = row of route i in sorted order, -1 if dropped.
+ * Sizes: sorted_token_ids [max_num_tokens_padded], expert_ids [ceil(max_num_tokens_padded/block)]
+ * with max_num_tokens_padded as the reference computes it. workspace >= pia_moe_align_workspace_bytes.
+ * ------------------------------------------------------------------------------------------- */
+int64_t pia_moe_align_workspace_bytes(int num_experts);
+
+int pia_moe_align_block_size(int32_t* sorted_token_ids, int32_t* expert_ids,
+                             int32_t* num_tokens_post_pad, int32_t* route_pos,
+                             const int32_t* topk_ids, int64_t numel, int num_experts,
+                             int block_size, int64_t max_num_tokens_padded,
+                             void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Permute: x_perm[r, :] = hidden[sorted_token_ids[r] / topk, :] for r < *num_tokens_post_pad
+ * and sorted_token_ids[r] < numel; padding rows (sentinel) are zero-filled; rows at or beyond
+ * *num_tokens_post_pad are left untouched. Bit-exact row copy (row_bytes multiple of 4).
+ * (reference: the per-expert hidden[rows] gather of src/plastic_infer/exec/moe.py:150-153,
+ * and the sorted_token_ids / topk A-row read of src/plastic_infer/kernel/triton/fused_moe.py:156-302)
+ * ------------------------------------------------------------------------------------------- */
+int pia_moe_permute(void* x_perm, const void* hidden, const int32_t* sorted_token_ids,
+                    const int32_t* num_tokens_post_pad, int64_t max_rows, int64_t numel,
+                    int topk, int64_t row_bytes, int64_t hidden_row_stride_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Unpermute / combine: out[t, :] = cast( sum_{s<k} w[t,s] * y[route_pos[t*k+s], :] )
+ * accumulated in fp32 in slot order s = 0..k-1 (each step a separately rounded multiply and add),
+ * routes with route_pos < 0 or >= y_rows contribute nothing; topk_weights NULL means weight 1
+ * (moe_sum_reduce, reference src/plastic_infer/kernel/triton/fused_moe.py:111-153 with the
+ * weight of fused_moe.py:292-294; combine of src/plastic_infer/exec/moe.py:155-158).
+ * y rows: [*, hidden_dim] of dtype; out [num_tokens, hidden_dim] of dtype.
+ * ------------------------------------------------------------------------------------------- */
+int pia_moe_unpermute(void* out, const void* y, int64_t y_rows, const int32_t* route_pos,
+                      const float* topk_weights, int64_t num_tokens, int topk, int hidden_dim,
+                      int dtype, void* stream);
+
+/* Plain sum over the top-k axis: out[t, :] = cast(sum_s in[t, s, :]) with fp32 accumulation
+ * (moe_sum_reduce_triton, reference src/plastic_infer/kernel/moe_impl.py:169-197). */
+int pia_moe_sum_reduce(void* out, const void* in, int64_t num_tokens, int topk, int hidden_dim,
+                       int dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * (a14) Row index copy kernel (fast_index_copy, reference
+ * src/plastic_infer/kernel/fast_index_copy.py:124-186, kernel .cuh:190-286):
+ *     for i < n:  dst + dst_idx[i]*row_bytes  <-  src + src_idx[i]*row_bytes
+ * n = min(*num_indices, length) when num_indices != NULL (device int64), else length.
+ * index_is_int32 selects the index width. src/dst may be device memory or pinned host memory
+ * mapped into the device address space. Rows whose index is negative or not below the table's
+ * row count (dst_num_rows / src_num_rows) are skipped. row_bytes % 16 == 0 and 16-byte aligned
+ * bases take the 16-byte vector path; any other row size is copied bytewise.
+ * ------------------------------------------------------------------------------------------- */
+int pia_index_copy_rows(void* dst, const void* dst_indices, int64_t dst_num_rows,
+                        const void* src, const void* src_indices, int64_t src_num_rows,
+                        int64_t length, const int64_t* num_indices, int64_t row_bytes,
+                        int index_is_int32, void* stream);
+
+/* Device address for kernel access to `ptr`: device memory is returned as is, pinned host
+ * memory through its device mapping (the reference's cudaHostGetDevicePointer step,
+ * src/plastic_infer/kernel/pinned.py:67-137). Memory HIP does not know (pageable host memory)
+ * is rejected with PIA_EINVAL, so a kernel is never handed an address it cannot reach.
+ * pia_index_copy_rows applies this to its src/dst itself. */
+int pia_device_pointer(const void* ptr, void** device_ptr);
+
+/* Multi-bank variant (fast_index_copy_multi, reference src/plastic_infer/kernel/fast_index_copy.py:
+ * 190-243, .cuh:436-505): the same (dst_idx, src_idx) rows for every bank b < num_banks, with
+ * per-bank base pointers and row bytes given as DEVICE int64 arrays. Row bytes % 16 == 0. */
+int pia_index_copy_rows_multi(const int64_t* dst_ptrs, const int64_t* src_ptrs,
+                              const int64_t* row_bytes, int num_banks,
+                              const void* dst_indices, const void* src_indices, int64_t length,
+                              const int64_t* num_indices, int index_is_int32, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * (4) Host-planned row copies with the DMA engines: for i < n,
+ *     hipMemcpyAsync(dst + dst_rows[i]*row_bytes, src + src_rows[i]*row_bytes, row_bytes)
+ * on `stream`, merging runs where both row indices advance by one into single copies.
+ * dst_rows/src_rows are HOST int64 arrays (the plan is host-known, as ExpertSlotPool's LRU is,
+ * reference src/plastic_infer/store/experts.py:178-223). dst/src: any of device memory or
+ * pinned host memory (the runtime picks the direction). Returns the number of copies issued
+ * through *copies_issued when non-NULL.
+ * ------------------------------------------------------------------------------------------- */
+int pia_copy_rows_async(void* dst, const int64_t* dst_rows, const void* src,
+                        const int64_t* src_rows, int64_t n, int64_t row_bytes,
+                        int64_t* copies_issued, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PLASTIC_INFER_AMD_H */

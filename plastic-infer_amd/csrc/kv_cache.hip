@@ -1,0 +1,248 @@
+// KV pool data movement for the page layout [num_pages, Hkv, D, P] (token innermost):
+//   - slot-mapped scatter of new K/V rows (decode and ragged prefill),
+//   - block-table gather back into contiguous [tokens, Hkv, D] rows,
+//   - page <-> chunk copies used by chunk sinking and prefix loading.
+// All three are byte-exact copies; elements are moved as 16- or 32-bit words.
+#include "pia_internal.h"
+
+namespace pia {
+namespace {
+
+// ---------------------------------------------------------------------------------------------
+// Scatter
+// ---------------------------------------------------------------------------------------------
+// Full-page fast path: a block owns one destination page-run of up to P tokens. When the P
+// tokens i0..i0+P-1 land on one page at offsets 0..P-1 (the prefill case: a sequence's tokens
+// fill whole pages in order), the block stages their [Hkv*D] rows in LDS and writes every
+// (h, d) row of the page tile as one contiguous P-element run, i.e. whole 32-byte sectors for
+// bf16 / P = 16, instead of P scattered 2-byte stores.
+//
+// General path (any slot pattern): one element store per (token, h, d).
+//
+// Grid: one block per group of P consecutive input tokens. Each block first checks whether its
+// group is a full aligned page run; if yes it takes the tile path, otherwise the per-token path.
+
+template <typename W>
+__global__ __launch_bounds__(256) void kv_scatter_kernel(
+    const W* __restrict__ k, const W* __restrict__ v, W* __restrict__ kp, W* __restrict__ vp,
+    const int64_t* __restrict__ slots, int64_t n, int64_t k_stride, int64_t v_stride, int HD,
+    int P, int64_t total_slots, int use_tile) {
+  extern __shared__ unsigned char smem_raw[];
+  W* tile = reinterpret_cast<W*>(smem_raw);  // [HD][P+1] staged K then V rows (tile path only)
+  __shared__ int s_full;
+
+  const int64_t i0 = int64_t(blockIdx.x) * P;
+  const int ntok = int(min<int64_t>(P, n - i0));
+  if (threadIdx.x == 0) {
+    int full = use_tile && (ntok == P);
+    if (full) {
+      const int64_t s0 = slots[i0];
+      full = (s0 >= 0) && (s0 + P <= total_slots) && (s0 % P == 0);
+      for (int t = 1; full && t < P; ++t) full = (slots[i0 + t] == s0 + t);
+    }
+    s_full = full;
+  }
+  __syncthreads();
+
+  if (s_full) {
+    const int64_t page = slots[i0] / P;
+    for (int pass = 0; pass < 2; ++pass) {
+      const W* src = pass == 0 ? k : v;
+      const int64_t stride = pass == 0 ? k_stride : v_stride;
+      W* dst = (pass == 0 ? kp : vp) + page * int64_t(HD) * P;
+      for (int e = threadIdx.x; e < P * HD; e += blockDim.x) {
+        const int t = e / HD, r = e - t * HD;
+        tile[r * (P + 1) + t] = src[(i0 + t) * stride + r];
+      }
+      __syncthreads();
+      // dst row r = (h, d) holds P consecutive tokens: write them contiguously.
+      for (int e = threadIdx.x; e < P * HD; e += blockDim.x) {
+        const int r = e / P, t = e - r * P;
+        dst[int64_t(r) * P + t] = tile[r * (P + 1) + t];
+      }
+      __syncthreads();
+    }
+    return;
+  }
+
+  for (int t = 0; t < ntok; ++t) {
+    const int64_t slot = slots[i0 + t];
+    if (slot < 0 || slot >= total_slots) continue;
+    const int64_t page = slot / P;
+    const int off = int(slot - page * P);
+    const W* ks = k + (i0 + t) * k_stride;
+    const W* vs = v + (i0 + t) * v_stride;
+    W* kd = kp + page * int64_t(HD) * P + off;
+    W* vd = vp + page * int64_t(HD) * P + off;
+    for (int r = threadIdx.x; r < HD; r += blockDim.x) {
+      kd[int64_t(r) * P] = ks[r];
+      vd[int64_t(r) * P] = vs[r];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Gather: one block per (logical page, sequence); stage each head's [D][P] tile in LDS and write
+// rows [t][h][d] contiguously.
+// ---------------------------------------------------------------------------------------------
+template <typename W>
+__global__ __launch_bounds__(256) void kv_gather_kernel(
+    W* __restrict__ ko, W* __restrict__ vo, const W* __restrict__ kp, const W* __restrict__ vp,
+    const int32_t* __restrict__ bt, int64_t bt_stride, const int64_t* __restrict__ cu, int H,
+    int D, int P, int64_t num_pages) {
+  extern __shared__ unsigned char smem_raw[];
+  W* tile = reinterpret_cast<W*>(smem_raw);  // [D][P+1]
+  const int lp = blockIdx.x, b = blockIdx.y;
+  const int64_t row0 = cu[b];
+  const int64_t len = cu[b + 1] - row0;
+  if (int64_t(lp) * P >= len || lp >= bt_stride) return;
+  const int ntok = int(min<int64_t>(P, len - int64_t(lp) * P));
+  const int64_t phys = bt[b * bt_stride + lp];
+  const bool ok = phys >= 0 && phys < num_pages;
+  const int HD = H * D;
+  for (int pass = 0; pass < 2; ++pass) {
+    const W* src = pass == 0 ? kp : vp;
+    W* dst = pass == 0 ? ko : vo;
+    for (int h = 0; h < H; ++h) {
+      if (ok) {
+        const W* tsrc = src + (phys * H + h) * int64_t(D) * P;
+        for (int e = threadIdx.x; e < D * P; e += blockDim.x) {
+          const int d = e / P, t = e - d * P;
+          tile[d * (P + 1) + t] = tsrc[e];
+        }
+      }
+      __syncthreads();
+      for (int e = threadIdx.x; e < ntok * D; e += blockDim.x) {
+        const int t = e / D, d = e - t * D;
+        const int64_t row = row0 + int64_t(lp) * P + t;
+        dst[row * HD + int64_t(h) * D + d] = ok ? tile[d * (P + 1) + t] : W(0);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Page <-> chunk copy: element-parallel, both sides contiguous along the token axis.
+// ---------------------------------------------------------------------------------------------
+template <typename W>
+__global__ __launch_bounds__(256) void kv_chunk_copy_kernel(
+    W* __restrict__ chunk, W* __restrict__ pages, const int64_t* __restrict__ ids, int L,
+    int ppc, int H, int D, int P, int64_t num_pages, int to_chunk, int64_t total) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    int64_t r = i;
+    const int t = int(r % P); r /= P;
+    const int d = int(r % D); r /= D;
+    const int h = int(r % H); r /= H;
+    const int p = int(r % ppc);
+    const int l = int(r / ppc);
+    const int64_t phys = ids[int64_t(l) * ppc + p];
+    if (phys < 0 || phys >= num_pages) continue;
+    const int64_t ci = ((int64_t(l) * H + h) * D + d) * (int64_t(ppc) * P) + int64_t(p) * P + t;
+    const int64_t pi = ((phys * H + h) * D + d) * P + t;
+    if (to_chunk)
+      chunk[ci] = pages[pi];
+    else
+      pages[pi] = chunk[ci];
+  }
+}
+
+int check_common(int H, int D, int P, int64_t num_pages, int eb) {
+  if (H <= 0 || D <= 0 || P <= 0 || num_pages <= 0)
+    return fail(PIA_EINVAL, "kv: num_kv_heads, head_dim, page_size and num_pages must be > 0");
+  if (eb != 2 && eb != 4) return fail(PIA_EINVAL, "kv: elem_bytes must be 2 or 4");
+  return 0;
+}
+
+}  // namespace
+}  // namespace pia
+
+using namespace pia;
+
+extern "C" int pia_kv_scatter(const void* k, const void* v, void* k_pages, void* v_pages,
+                              const int64_t* slot_mapping, int64_t num_tokens,
+                              int64_t k_token_stride, int64_t v_token_stride, int num_kv_heads,
+                              int head_dim, int page_size, int64_t num_pages, int elem_bytes,
+                              void* stream) {
+  if (int rc = check_common(num_kv_heads, head_dim, page_size, num_pages, elem_bytes)) return rc;
+  if (num_tokens < 0) return fail(PIA_EINVAL, "kv_scatter: num_tokens < 0");
+  if (num_tokens == 0) return 0;
+  if (!k || !v || !k_pages || !v_pages || !slot_mapping)
+    return fail(PIA_EINVAL, "kv_scatter: null pointer");
+  const int HD = num_kv_heads * head_dim;
+  if (k_token_stride < HD || v_token_stride < HD)
+    return fail(PIA_EINVAL, "kv_scatter: token stride smaller than num_kv_heads*head_dim");
+  // Tile path only when the staged [HD][P+1] tile fits in 64 KiB of LDS.
+  size_t smem = size_t(page_size + 1) * HD * elem_bytes;
+  const int use_tile = smem <= 65536 ? 1 : 0;
+  if (!use_tile) smem = 0;
+  const int64_t blocks = ceil_div(num_tokens, page_size);
+  if (blocks > 0x7fffffff) return fail(PIA_EINVAL, "kv_scatter: too many tokens");
+  const int64_t total_slots = num_pages * page_size;
+  hipStream_t s = as_stream(stream);
+  if (elem_bytes == 2)
+    hipLaunchKernelGGL(kv_scatter_kernel<uint16_t>, dim3(blocks), dim3(256), smem, s,
+                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)k_pages,
+                       (uint16_t*)v_pages, slot_mapping, num_tokens, k_token_stride,
+                       v_token_stride, HD, page_size, total_slots, use_tile);
+  else
+    hipLaunchKernelGGL(kv_scatter_kernel<uint32_t>, dim3(blocks), dim3(256), smem, s,
+                       (const uint32_t*)k, (const uint32_t*)v, (uint32_t*)k_pages,
+                       (uint32_t*)v_pages, slot_mapping, num_tokens, k_token_stride,
+                       v_token_stride, HD, page_size, total_slots, use_tile);
+  return check_launch("kv_scatter");
+}
+
+extern "C" int pia_kv_gather(void* k_out, void* v_out, const void* k_pages, const void* v_pages,
+                             const int32_t* block_tables, int64_t bt_stride,
+                             const int64_t* cu_seqlens, int num_seqs, int64_t max_seq_len,
+                             int num_kv_heads, int head_dim, int page_size, int64_t num_pages,
+                             int elem_bytes, void* stream) {
+  if (int rc = check_common(num_kv_heads, head_dim, page_size, num_pages, elem_bytes)) return rc;
+  if (num_seqs < 0 || max_seq_len < 0 || bt_stride < 0)
+    return fail(PIA_EINVAL, "kv_gather: negative size");
+  if (num_seqs == 0 || max_seq_len == 0 || bt_stride == 0) return 0;
+  if (!k_out || !v_out || !k_pages || !v_pages || !block_tables || !cu_seqlens)
+    return fail(PIA_EINVAL, "kv_gather: null pointer");
+  if (num_seqs > 65535) return fail(PIA_EINVAL, "kv_gather: num_seqs > 65535");
+  const size_t smem = size_t(page_size + 1) * head_dim * elem_bytes;
+  if (smem > 65536) return fail(PIA_EUNSUPPORTED, "kv_gather: page tile exceeds 64 KiB of LDS");
+  const int64_t pages = std::min<int64_t>(ceil_div(max_seq_len, page_size), bt_stride);
+  if (pages > 0x7fffffff) return fail(PIA_EINVAL, "kv_gather: too many pages");
+  hipStream_t s = as_stream(stream);
+  dim3 grid = dim3(unsigned(pages), unsigned(num_seqs));
+  if (elem_bytes == 2)
+    hipLaunchKernelGGL(kv_gather_kernel<uint16_t>, grid, dim3(256), smem, s, (uint16_t*)k_out,
+                       (uint16_t*)v_out, (const uint16_t*)k_pages, (const uint16_t*)v_pages,
+                       block_tables, bt_stride, cu_seqlens, num_kv_heads, head_dim, page_size,
+                       num_pages);
+  else
+    hipLaunchKernelGGL(kv_gather_kernel<uint32_t>, grid, dim3(256), smem, s, (uint32_t*)k_out,
+                       (uint32_t*)v_out, (const uint32_t*)k_pages, (const uint32_t*)v_pages,
+                       block_tables, bt_stride, cu_seqlens, num_kv_heads, head_dim, page_size,
+                       num_pages);
+  return check_launch("kv_gather");
+}
+
+extern "C" int pia_kv_pages_chunk_copy(void* chunk, void* pages, const int64_t* page_ids,
+                                       int num_layers, int pages_per_chunk, int num_kv_heads,
+                                       int head_dim, int page_size, int64_t num_pages,
+                                       int elem_bytes, int to_chunk, void* stream) {
+  if (int rc = check_common(num_kv_heads, head_dim, page_size, num_pages, elem_bytes)) return rc;
+  if (num_layers < 0 || pages_per_chunk < 0) return fail(PIA_EINVAL, "kv_chunk_copy: negative size");
+  const int64_t total = int64_t(num_layers) * pages_per_chunk * num_kv_heads * head_dim * page_size;
+  if (total == 0) return 0;
+  if (!chunk || !pages || !page_ids) return fail(PIA_EINVAL, "kv_chunk_copy: null pointer");
+  const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 65536);
+  hipStream_t s = as_stream(stream);
+  if (elem_bytes == 2)
+    hipLaunchKernelGGL(kv_chunk_copy_kernel<uint16_t>, dim3(blocks), dim3(256), 0, s,
+                       (uint16_t*)chunk, (uint16_t*)pages, page_ids, num_layers, pages_per_chunk,
+                       num_kv_heads, head_dim, page_size, num_pages, to_chunk, total);
+  else
+    hipLaunchKernelGGL(kv_chunk_copy_kernel<uint32_t>, dim3(blocks), dim3(256), 0, s,
+                       (uint32_t*)chunk, (uint32_t*)pages, page_ids, num_layers, pages_per_chunk,
+                       num_kv_heads, head_dim, page_size, num_pages, to_chunk, total);
+  return check_launch("kv_chunk_copy");
+}

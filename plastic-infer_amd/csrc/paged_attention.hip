@@ -1,0 +1,606 @@
+// Paged GQA attention over the KV pool layout [num_pages, Hkv, D, P] (token innermost).
+//
+// 1. paged_decode_bf16_d128p16<G>: the decode hot path (bf16, D = 128, P = 16, G = Hq/Hkv in
+//    {1,2,4,8}). Split-context: one 256-thread workgroup per (512-token partition, kv head,
+//    sequence); each of its 4 waves owns 8 pages (128 tokens) of the partition.
+//      K tile loads: lane l reads page l/8, rows d = 4i + (l&3), token half (l>>2)&1, so load i
+//        of the wave covers one whole 128-byte line of each of the 8 pages (32 loads / 8 pages).
+//      QK^T: pairs of rows (d, d+4) are packed per token with v_perm, then v_dot2_f32_bf16
+//        against (q[d], q[d+4]); partial sums over the 4 row subsets are folded by two DPP
+//        quad exchanges, after which lane l owns the scores of tokens 2l and 2l+1.
+//      Softmax: fp32, base-2 with the scale folded in; wave max by DPP/shuffles.
+//      PV: lane l reads V rows d = 32j + l/2, token half l&1 (1 KiB contiguous per load); the
+//        probabilities of its 8 tokens come from LDS as bf16 pairs, v_dot2 accumulates in fp32.
+//      The 4 waves merge through LDS; a sequence with one partition writes its output directly,
+//      longer ones write (max, sum, unnormalised acc) partials merged by paged_decode_reduce.
+// 2. paged_attention_generic<DT, DPL>: any dtype / head_dim <= 512 / page size, several query
+//    rows per sequence with optional causal offsets. One wave per (query row, head); keys are
+//    processed 64 at a time (lane = key for QK, lane = head-dim element for PV).
+#include "pia_internal.h"
+
+namespace pia {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegBig = -1.0e30f;  // finite "no key yet" running max (avoids inf - inf)
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (KV tiles are read once per launch: non-temporal hint).
+__device__ __forceinline__ uint4 load16_nt(const uint16_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return uint4{v.x, v.y, v.z, v.w};
+}
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// DPP lane exchanges within a quad (row_mask/bank_mask all lanes, every source lane valid).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppRowRor4 = 0x124;  // row_ror:4
+constexpr int kDppRowRor8 = 0x128;  // row_ror:8
+
+// Max over all 64 lanes: quad xor by DPP, rows of 16 by DPP rotations, then across rows.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_f32<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp_f32<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_f32<kDppRowRor4>(v));
+  v = fmaxf(v, dpp_f32<kDppRowRor8>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f32<kDppQuadXor1>(v);
+  v += dpp_f32<kDppQuadXor2>(v);
+  v += dpp_f32<kDppRowRor4>(v);
+  v += dpp_f32<kDppRowRor8>(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+// (lo16(a), lo16(c)) and (hi16(a), hi16(c)) — v_perm_b32 byte selects over {S0 = c, S1 = a}.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t c) {
+  return __builtin_amdgcn_perm(c, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t c) {
+  return __builtin_amdgcn_perm(c, a, 0x07060302u);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+}
+
+// Zero the bf16 tokens of a dword pair (t, t+1) that lie at or beyond nvalid.
+__device__ __forceinline__ uint32_t mask_pair(uint32_t x, int t, int nvalid) {
+  const uint32_t lo = (t < nvalid) ? 0x0000ffffu : 0u;
+  const uint32_t hi = (t + 1 < nvalid) ? 0xffff0000u : 0u;
+  return x & (lo | hi);
+}
+
+constexpr int FD_D = 128;
+constexpr int FD_P = 16;
+constexpr int FD_WAVES = 4;
+constexpr int FD_PAGES_PER_WAVE = 8;
+constexpr int FD_PART_PAGES = FD_WAVES * FD_PAGES_PER_WAVE;  // 32 pages = 512 tokens
+
+__device__ __forceinline__ int clamp_len(int L, int64_t bt_stride, int P) {
+  const int64_t cap = bt_stride * P;
+  if (L < 0) return 0;
+  return int64_t(L) > cap ? int(cap) : L;
+}
+
+template <int G>
+__global__ __launch_bounds__(256, 2) void paged_decode_bf16_d128p16(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
+    const uint16_t* __restrict__ kpool, const uint16_t* __restrict__ vpool,
+    const int32_t* __restrict__ block_tables, int64_t bt_stride,
+    const int32_t* __restrict__ context_lens, float* __restrict__ ws_acc,
+    float* __restrict__ ws_ml, int Hkv, int64_t num_pages, int max_parts, float scale_log2) {
+  constexpr int D = FD_D, P = FD_P, TILE = D * P;
+  const int part = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int Hq = Hkv * G;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int L = clamp_len(context_lens[b], bt_stride, P);
+  const int n_pages = (L + P - 1) / P;
+  const int n_parts = (n_pages + FD_PART_PAGES - 1) / FD_PART_PAGES;
+  const int64_t row0 = int64_t(b) * Hq + int64_t(h) * G;  // first output row of this kv head
+
+  if (n_parts == 0) {
+    if (part == 0)
+      for (int i = tid; i < G * D; i += 256) out[row0 * D + i] = 0;
+    return;
+  }
+  if (part >= n_parts) return;
+
+  __shared__ uint32_t q_lds[4][16][G];          // [d&3 of row d=8p+(d&3)][p][g]: (q[d], q[d+4])
+  __shared__ uint32_t p_lds[FD_WAVES][64][G];   // probabilities of tokens (2l, 2l+1) as bf16x2
+  __shared__ float m_lds[FD_WAVES][G];
+  __shared__ float l_lds[FD_WAVES][G];
+  __shared__ float acc_lds[FD_WAVES][G][D];
+
+  const uint16_t* qb = q + int64_t(b) * q_seq_stride + int64_t(h) * G * D;
+  for (int i = tid; i < 4 * 16 * G; i += 256) {
+    const int g = i % G, pp = (i / G) % 16, dsub = i / (G * 16);
+    const int d0 = 8 * pp + dsub;
+    q_lds[dsub][pp][g] = uint32_t(qb[g * D + d0]) | (uint32_t(qb[g * D + d0 + 4]) << 16);
+  }
+  __syncthreads();
+
+  float m[G], lsum[G], acc[4][G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = kNegBig;
+    lsum[g] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j][g] = 0.f;
+  }
+
+  const int page0 = part * FD_PART_PAGES + wave * FD_PAGES_PER_WAVE;
+  if (page0 < n_pages) {
+    const int32_t* bt = block_tables + int64_t(b) * bt_stride;
+    int lp = page0 + (lane & 7);
+    if (lp > n_pages - 1) lp = n_pages - 1;  // pages past the end re-read the last page (masked)
+    int phys = bt[lp];
+    if (phys < 0 || int64_t(phys) >= num_pages) phys = 0;
+
+    // ---- K: 32 loads of 16 B; load i = one full 128-byte line of each of the 8 pages ----
+    const int kphys = __shfl(phys, lane >> 3, 64);
+    const uint16_t* kb = kpool + (int64_t(kphys) * Hkv + h) * TILE + (lane & 3) * P +
+                         ((lane >> 2) & 1) * 8;
+    uint4 kr[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) kr[i] = load16_nt(kb + 64 * i);
+
+    float s[8][G];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int g = 0; g < G; ++g) s[t][g] = 0.f;
+
+    const uint32_t* qrow = &q_lds[lane & 3][0][0];
+#pragma unroll
+    for (int pp = 0; pp < 16; ++pp) {
+      // one row pair at a time: hoisting every pair's q reads would cost 16*G VGPRs
+      __builtin_amdgcn_sched_barrier(0);
+      const uint4 a = kr[2 * pp], c = kr[2 * pp + 1];  // rows d = 8pp + (l&3) and d + 4
+      uint32_t kk[8];
+      kk[0] = pack_lo(a.x, c.x); kk[1] = pack_hi(a.x, c.x);
+      kk[2] = pack_lo(a.y, c.y); kk[3] = pack_hi(a.y, c.y);
+      kk[4] = pack_lo(a.z, c.z); kk[5] = pack_hi(a.z, c.z);
+      kk[6] = pack_lo(a.w, c.w); kk[7] = pack_hi(a.w, c.w);
+      uint32_t qq[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) qq[g] = qrow[pp * G + g];
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int g = 0; g < G; ++g) s[t][g] = dot2_bf16(kk[t], qq[g], s[t][g]);
+    }
+
+    // ---- fold the 4 row subsets of each quad; lane l keeps tokens 2l, 2l+1 ----
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        s[t][g] += dpp_f32<kDppQuadXor1>(s[t][g]);
+        s[t][g] += dpp_f32<kDppQuadXor2>(s[t][g]);
+      }
+    const int qp = lane & 3;
+    float sc[2][G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      sc[0][g] = qp == 0 ? s[0][g] : qp == 1 ? s[2][g] : qp == 2 ? s[4][g] : s[6][g];
+      sc[1][g] = qp == 0 ? s[1][g] : qp == 1 ? s[3][g] : qp == 2 ? s[5][g] : s[7][g];
+    }
+
+    // Keep the V loads below the QK^T math: hoisting them would hold K and V tiles (256 VGPRs)
+    // live together.
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- V loads for all 8 pages (issued before the softmax so they overlap it) ----
+    uint4 vr[8][4];
+#pragma unroll
+    for (int pg = 0; pg < 8; ++pg) {
+      const int vphys = __builtin_amdgcn_readlane(phys, pg);
+      const uint16_t* vb = vpool + (int64_t(vphys) * Hkv + h) * TILE + lane * 8;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        vr[pg][j] = load16_nt(vb + 512 * j);
+    }
+
+    const int tok0 = page0 * P + 2 * lane;
+    uint32_t pw[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float s0 = sc[0][g], s1 = sc[1][g];
+      const float x0 = tok0 < L ? s0 * scale_log2 : -INFINITY;
+      const float x1 = tok0 + 1 < L ? s1 * scale_log2 : -INFINITY;
+      const float mnew = fmaxf(m[g], wave_max_dpp(fmaxf(x0, x1)));
+      const float alpha = exp2f(m[g] - mnew);
+      const float p0 = exp2f(x0 - mnew), p1 = exp2f(x1 - mnew);
+      lsum[g] = lsum[g] * alpha + (p0 + p1);
+      m[g] = mnew;
+      pw[g] = pack_bf16x2(p0, p1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j][g] *= alpha;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) p_lds[wave][lane][g] = pw[g];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+
+    // ---- PV ----
+    const int vhalf = lane & 1;
+    // PV over the 8 pages as straight-line code. Tokens at or past L (the sequence's partial
+    // last page and the clamped re-reads after it) carry P = 0, but their stale V words may be
+    // non-finite, so a wave whose pages reach past L zeroes them first (branch-free selects).
+    // Waves of full pages (the common case) take the variant without any masking.
+    auto pv_pages = [&](auto masked) {
+#pragma unroll
+      for (int pg = 0; pg < 8; ++pg) {
+        // one page at a time: hoisting later pages' probability reads costs 4*G VGPRs each
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (decltype(masked)::value) {
+          const int nvalid = L - ((page0 + pg) * P + vhalf * 8);  // valid tokens of this half
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            vr[pg][j].x = mask_pair(vr[pg][j].x, 0, nvalid);
+            vr[pg][j].y = mask_pair(vr[pg][j].y, 2, nvalid);
+            vr[pg][j].z = mask_pair(vr[pg][j].z, 4, nvalid);
+            vr[pg][j].w = mask_pair(vr[pg][j].w, 6, nvalid);
+          }
+        }
+        const uint32_t* prow = &p_lds[wave][pg * 8 + vhalf * 4][0];
+        uint32_t pr[4][G];
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm)
+#pragma unroll
+          for (int g = 0; g < G; ++g) pr[mm][g] = prow[mm * G + g];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            float a = acc[j][g];
+            a = dot2_bf16(vr[pg][j].x, pr[0][g], a);
+            a = dot2_bf16(vr[pg][j].y, pr[1][g], a);
+            a = dot2_bf16(vr[pg][j].z, pr[2][g], a);
+            a = dot2_bf16(vr[pg][j].w, pr[3][g], a);
+            acc[j][g] = a;
+          }
+      }
+    };
+    if ((page0 + FD_PAGES_PER_WAVE) * P <= L)
+      pv_pages(std::false_type{});
+    else
+      pv_pages(std::true_type{});
+
+    // lanes l and l^1 hold the two token halves of the same rows d
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc[j][g] += dpp_f32<kDppQuadXor1>(acc[j][g]);
+#pragma unroll
+    for (int g = 0; g < G; ++g) lsum[g] = wave_sum_dpp(lsum[g]);
+  }
+
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m_lds[wave][g] = m[g];
+      l_lds[wave][g] = lsum[g];
+    }
+  }
+  if ((lane & 1) == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc_lds[wave][g][32 * j + (lane >> 1)] = acc[j][g];
+  }
+  __syncthreads();
+
+  for (int i = tid; i < G * D; i += 256) {
+    const int g = i / D, d = i - g * D;
+    float M = m_lds[0][g];
+#pragma unroll
+    for (int w = 1; w < FD_WAVES; ++w) M = fmaxf(M, m_lds[w][g]);
+    float o = 0.f, lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < FD_WAVES; ++w) {
+      const float f = exp2f(m_lds[w][g] - M);
+      o += f * acc_lds[w][g][d];
+      lt += f * l_lds[w][g];
+    }
+    const int64_t row = row0 + g;
+    if (n_parts == 1) {
+      out[row * D + d] = f32_to_bf16(o / lt);
+    } else {
+      const int64_t slot = row * max_parts + part;
+      ws_acc[slot * D + d] = o;
+      if (d == 0) {
+        ws_ml[slot * 2 + 0] = M;
+        ws_ml[slot * 2 + 1] = lt;
+      }
+    }
+  }
+}
+
+// Merge the partition partials of sequences with more than one partition.
+__global__ __launch_bounds__(FD_D) void paged_decode_reduce(
+    uint16_t* __restrict__ out, const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
+    const int32_t* __restrict__ context_lens, int64_t bt_stride, int Hq, int max_parts) {
+  constexpr int D = FD_D, P = FD_P;
+  const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int L = clamp_len(context_lens[b], bt_stride, P);
+  const int n_parts = ((L + P - 1) / P + FD_PART_PAGES - 1) / FD_PART_PAGES;
+  if (n_parts <= 1) return;
+  const int64_t row = int64_t(b) * Hq + hq;
+  const float* ml = ws_ml + row * max_parts * 2;
+  float M = kNegBig;
+  for (int p = 0; p < n_parts; ++p) M = fmaxf(M, ml[2 * p]);
+  float o = 0.f, lt = 0.f;
+  for (int p = 0; p < n_parts; ++p) {
+    const float f = exp2f(ml[2 * p] - M);
+    lt += f * ml[2 * p + 1];
+    o += f * ws_acc[(row * max_parts + p) * D + d];
+  }
+  out[row * D + d] = f32_to_bf16(o / lt);
+}
+
+// ---------------------------------------------------------------------------------------------
+// General kernel
+// ---------------------------------------------------------------------------------------------
+template <int DT, int DPL>
+__global__ __launch_bounds__(64) void paged_attention_generic(
+    void* __restrict__ out_, const void* __restrict__ q_, int64_t q_row_stride,
+    const void* __restrict__ kp_, const void* __restrict__ vp_,
+    const int32_t* __restrict__ bt, int64_t bt_stride, const int32_t* __restrict__ kv_lens,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ offsets, int num_seqs, int Hq,
+    int Hkv, int D, int P, int64_t num_pages, float scale_log2) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  T* out = reinterpret_cast<T*>(out_);
+  const T* q = reinterpret_cast<const T*>(q_);
+  const T* kp = reinterpret_cast<const T*>(kp_);
+  const T* vp = reinterpret_cast<const T*>(vp_);
+  __shared__ float q_s[64 * DPL];
+  __shared__ float p_s[64];
+  __shared__ int64_t base_s[64];
+
+  const int64_t row = blockIdx.x;
+  const int hq = blockIdx.y, lane = threadIdx.x;
+  int b = int(row), s = 0;
+  if (cu_q) {
+    int lo = 0, hi = num_seqs - 1;  // largest b with cu_q[b] <= row
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (int64_t(cu_q[mid]) <= row) lo = mid; else hi = mid - 1;
+    }
+    b = lo;
+    s = int(row - cu_q[b]);
+  }
+  const int kv_len = clamp_len(kv_lens[b], bt_stride, P);
+  int limit = kv_len;
+  if (offsets) limit = min(limit, offsets[b] + s + 1);
+  if (limit < 0) limit = 0;
+  const int G = Hq / Hkv;
+  const int hk = hq / G;
+  const int64_t qoff = row * q_row_stride + int64_t(hq) * D;
+  for (int d = lane; d < 64 * DPL; d += 64) q_s[d] = d < D ? E::load(q, qoff + d) : 0.f;
+  __syncthreads();
+
+  float m = kNegBig, l = 0.f, acc[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+  const int32_t* btb = bt + int64_t(b) * bt_stride;
+  const int64_t DP = int64_t(D) * P;
+
+  for (int j0 = 0; j0 < limit; j0 += 64) {
+    const int j = j0 + lane;
+    const bool valid = j < limit;
+    int64_t base = 0;
+    float sc = 0.f;
+    if (valid) {
+      const int lp = j / P, off = j - lp * P;
+      int64_t phys = btb[lp];
+      if (phys < 0 || phys >= num_pages) phys = 0;
+      base = (phys * Hkv + hk) * DP + off;
+      for (int d = 0; d < D; ++d) sc = fmaf(q_s[d], E::load(kp, base + int64_t(d) * P), sc);
+    }
+    const float x = valid ? sc * scale_log2 : -INFINITY;
+    const float mnew = fmaxf(m, wave_max(x));
+    const float alpha = exp2f(m - mnew);
+    const float p = exp2f(x - mnew);
+    l = l * alpha + wave_sum(p);
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) acc[i] *= alpha;
+    p_s[lane] = p;
+    base_s[lane] = base;
+    __syncthreads();
+    const int cnt = min(64, limit - j0);
+    for (int jj = 0; jj < cnt; ++jj) {
+      const float pj = p_s[jj];
+      const int64_t bj = base_s[jj];
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) {
+        const int d = lane + 64 * i;
+        if (d < D) acc[i] = fmaf(pj, E::load(vp, bj + int64_t(d) * P), acc[i]);
+      }
+    }
+    __syncthreads();
+    m = mnew;
+  }
+  const int64_t ooff = (row * Hq + hq) * D;
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) {
+    const int d = lane + 64 * i;
+    if (d < D) E::store(out, ooff + d, l > 0.f ? acc[i] / l : 0.f);
+  }
+}
+
+template <int DT>
+int launch_generic(void* out, const void* q, int64_t q_row_stride, const void* kp, const void* vp,
+                   const int32_t* bt, int64_t bt_stride, const int32_t* kv_lens,
+                   const int32_t* cu_q, const int32_t* offsets, int num_seqs, int64_t rows, int Hq,
+                   int Hkv, int D, int P, int64_t num_pages, float scale_log2, hipStream_t s) {
+  dim3 grid = dim3(unsigned(rows), unsigned(Hq));
+#define PIA_GEN(DPL)                                                                        \
+  hipLaunchKernelGGL((paged_attention_generic<DT, DPL>), grid, dim3(64), 0, s, out, q,      \
+                     q_row_stride, kp, vp, bt, bt_stride, kv_lens, cu_q, offsets, num_seqs, \
+                     Hq, Hkv, D, P, num_pages, scale_log2)
+  if (D <= 64) PIA_GEN(1);
+  else if (D <= 128) PIA_GEN(2);
+  else if (D <= 256) PIA_GEN(4);
+  else PIA_GEN(8);
+#undef PIA_GEN
+  return check_launch("paged_attention_generic");
+}
+
+int launch_generic_any(int dtype, void* out, const void* q, int64_t q_row_stride, const void* kp,
+                       const void* vp, const int32_t* bt, int64_t bt_stride,
+                       const int32_t* kv_lens, const int32_t* cu_q, const int32_t* offsets,
+                       int num_seqs, int64_t rows, int Hq, int Hkv, int D, int P,
+                       int64_t num_pages, float scale_log2, hipStream_t s) {
+  switch (dtype) {
+    case PIA_DTYPE_F32:
+      return launch_generic<PIA_DTYPE_F32>(out, q, q_row_stride, kp, vp, bt, bt_stride, kv_lens,
+                                           cu_q, offsets, num_seqs, rows, Hq, Hkv, D, P,
+                                           num_pages, scale_log2, s);
+    case PIA_DTYPE_F16:
+      return launch_generic<PIA_DTYPE_F16>(out, q, q_row_stride, kp, vp, bt, bt_stride, kv_lens,
+                                           cu_q, offsets, num_seqs, rows, Hq, Hkv, D, P,
+                                           num_pages, scale_log2, s);
+    case PIA_DTYPE_BF16:
+      return launch_generic<PIA_DTYPE_BF16>(out, q, q_row_stride, kp, vp, bt, bt_stride,
+                                            kv_lens, cu_q, offsets, num_seqs, rows, Hq, Hkv, D,
+                                            P, num_pages, scale_log2, s);
+  }
+  return fail(PIA_EINVAL, "paged attention: unknown dtype");
+}
+
+int check_heads(int Hq, int Hkv, int D, int P, int64_t num_pages, int dtype) {
+  if (Hq <= 0 || Hkv <= 0 || D <= 0 || P <= 0 || num_pages <= 0)
+    return fail(PIA_EINVAL, "paged attention: heads, head_dim, page_size, num_pages must be > 0");
+  if (Hq % Hkv) return fail(PIA_EINVAL, "paged attention: num_heads % num_kv_heads != 0");
+  if (D > 512) return fail(PIA_EUNSUPPORTED, "paged attention: head_dim > 512");
+  if (Hq > 65535) return fail(PIA_EINVAL, "paged attention: num_heads > 65535");
+  if (dtype != PIA_DTYPE_F32 && dtype != PIA_DTYPE_F16 && dtype != PIA_DTYPE_BF16)
+    return fail(PIA_EINVAL, "paged attention: unknown dtype");
+  return 0;
+}
+
+bool fast_path(int dtype, int Hq, int Hkv, int D, int P) {
+  const int G = Hq / Hkv;
+  return dtype == PIA_DTYPE_BF16 && D == FD_D && P == FD_P &&
+         (G == 1 || G == 2 || G == 4 || G == 8);
+}
+
+int64_t fast_max_parts(int64_t bt_stride) { return ceil_div(bt_stride, FD_PART_PAGES); }
+
+}  // namespace
+}  // namespace pia
+
+using namespace pia;
+
+extern "C" int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim,
+                                                    int page_size, int64_t bt_stride) {
+  if (head_dim != FD_D || page_size != FD_P || num_seqs <= 0 || num_heads <= 0 || bt_stride <= 0)
+    return 0;
+  return int64_t(num_seqs) * num_heads * fast_max_parts(bt_stride) * (FD_D + 2) *
+         int64_t(sizeof(float));
+}
+
+extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_seq_stride,
+                                          const void* k_pages, const void* v_pages,
+                                          const int32_t* block_tables, int64_t bt_stride,
+                                          const int32_t* context_lens, int num_seqs,
+                                          int num_heads, int num_kv_heads, int head_dim,
+                                          int page_size, int64_t num_pages, float scale,
+                                          int dtype, void* workspace, int64_t workspace_bytes,
+                                          void* stream) {
+  if (int rc = check_heads(num_heads, num_kv_heads, head_dim, page_size, num_pages, dtype))
+    return rc;
+  if (num_seqs < 0 || bt_stride < 0) return fail(PIA_EINVAL, "paged_decode: negative size");
+  if (num_seqs == 0) return 0;
+  if (!out || !q || !k_pages || !v_pages || !block_tables || !context_lens)
+    return fail(PIA_EINVAL, "paged_decode: null pointer");
+  if (bt_stride == 0) return fail(PIA_EINVAL, "paged_decode: bt_stride == 0");
+  if (num_seqs > 65535) return fail(PIA_EINVAL, "paged_decode: num_seqs > 65535");
+  if (q_seq_stride < int64_t(num_heads) * head_dim)
+    return fail(PIA_EINVAL, "paged_decode: q_seq_stride < num_heads*head_dim");
+  const float scale_log2 = scale * kLog2e;
+  hipStream_t s = as_stream(stream);
+  if (fast_path(dtype, num_heads, num_kv_heads, head_dim, page_size)) {
+    const int64_t need = pia_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim,
+                                                          page_size, bt_stride);
+    if (!workspace || workspace_bytes < need) {
+      set_error("paged_decode: workspace of %lld bytes needed, %lld given", (long long)need,
+                (long long)workspace_bytes);
+      return PIA_EINVAL;
+    }
+    if (!aligned(q, 4) || !aligned(k_pages, 16) || !aligned(v_pages, 16) || (q_seq_stride & 1))
+      return fail(PIA_EINVAL, "paged_decode: q must be 4-byte and pools 16-byte aligned");
+    const int max_parts = int(fast_max_parts(bt_stride));
+    float* ws_acc = reinterpret_cast<float*>(workspace);
+    float* ws_ml = ws_acc + int64_t(num_seqs) * num_heads * max_parts * FD_D;
+    const int G = num_heads / num_kv_heads;
+    dim3 grid = dim3(unsigned(max_parts), unsigned(num_kv_heads), unsigned(num_seqs));
+#define PIA_FD(GG)                                                                              \
+  hipLaunchKernelGGL((paged_decode_bf16_d128p16<GG>), grid, dim3(256), 0, s, (uint16_t*)out,   \
+                     (const uint16_t*)q, q_seq_stride, (const uint16_t*)k_pages,               \
+                     (const uint16_t*)v_pages, block_tables, bt_stride, context_lens, ws_acc,  \
+                     ws_ml, num_kv_heads, num_pages, max_parts, scale_log2)
+    switch (G) {
+      case 1: PIA_FD(1); break;
+      case 2: PIA_FD(2); break;
+      case 4: PIA_FD(4); break;
+      default: PIA_FD(8); break;
+    }
+#undef PIA_FD
+    if (int rc = check_launch("paged_decode_bf16_d128p16")) return rc;
+    if (max_parts > 1) {
+      hipLaunchKernelGGL(paged_decode_reduce, dim3(unsigned(num_heads), unsigned(num_seqs)),
+                         dim3(FD_D), 0, s, (uint16_t*)out, ws_acc, ws_ml, context_lens,
+                         bt_stride, num_heads, max_parts);
+      if (int rc = check_launch("paged_decode_reduce")) return rc;
+    }
+    return 0;
+  }
+  return launch_generic_any(dtype, out, q, q_seq_stride, k_pages, v_pages, block_tables,
+                            bt_stride, context_lens, nullptr, nullptr, num_seqs, num_seqs,
+                            num_heads, num_kv_heads, head_dim, page_size, num_pages, scale_log2,
+                            s);
+}
+
+extern "C" int pia_paged_attention(void* out, const void* q, const void* k_pages,
+                                   const void* v_pages, const int32_t* block_tables,
+                                   int64_t bt_stride, const int32_t* kv_lens, const int32_t* cu_q,
+                                   const int32_t* q_pos_offsets, int num_seqs,
+                                   int64_t total_q_rows, int num_heads, int num_kv_heads,
+                                   int head_dim, int page_size, int64_t num_pages, float scale,
+                                   int dtype, void* stream) {
+  if (int rc = check_heads(num_heads, num_kv_heads, head_dim, page_size, num_pages, dtype))
+    return rc;
+  if (num_seqs < 0 || total_q_rows < 0 || bt_stride < 0)
+    return fail(PIA_EINVAL, "paged_attention: negative size");
+  if (num_seqs == 0 || total_q_rows == 0) return 0;
+  if (!out || !q || !k_pages || !v_pages || !block_tables || !kv_lens)
+    return fail(PIA_EINVAL, "paged_attention: null pointer");
+  if (bt_stride == 0) return fail(PIA_EINVAL, "paged_attention: bt_stride == 0");
+  if (!cu_q && total_q_rows != num_seqs)
+    return fail(PIA_EINVAL, "paged_attention: without cu_q, total_q_rows must equal num_seqs");
+  if (total_q_rows > 0x7fffffff) return fail(PIA_EINVAL, "paged_attention: too many rows");
+  return launch_generic_any(dtype, out, q, int64_t(num_heads) * head_dim, k_pages, v_pages,
+                            block_tables, bt_stride, kv_lens, cu_q, q_pos_offsets, num_seqs,
+                            total_q_rows, num_heads, num_kv_heads, head_dim, page_size,
+                            num_pages, scale * kLog2e, as_stream(stream));
+}

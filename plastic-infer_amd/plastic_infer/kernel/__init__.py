@@ -1,0 +1,27 @@
+"""HIP kernel layer: batched entry points over libplastic_infer_amd.so (gfx950)."""
+
+from .index_copy import copy_rows_async, fast_index_copy, fast_index_copy_multi
+from .moe_ops import (
+    max_num_tokens_padded,
+    moe_align_block_size,
+    moe_permute,
+    moe_sum_reduce,
+    moe_topk,
+    moe_unpermute,
+)
+from .paged_kv import (
+    decode_workspace_bytes,
+    kv_gather,
+    kv_scatter,
+    paged_attention,
+    paged_decode_attention,
+    pages_chunk_copy,
+)
+
+__all__ = [
+    "copy_rows_async", "fast_index_copy", "fast_index_copy_multi",
+    "max_num_tokens_padded", "moe_align_block_size", "moe_permute", "moe_sum_reduce",
+    "moe_topk", "moe_unpermute",
+    "decode_workspace_bytes", "kv_gather", "kv_scatter", "paged_attention",
+    "paged_decode_attention", "pages_chunk_copy",
+]

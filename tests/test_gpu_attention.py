@@ -1,0 +1,255 @@
+"""GPU parity of paged attention against the oracle.
+
+Tolerances: bf16 inputs with fp32 accumulation -> max |err| <= 2e-2 against the oracle (the
+reference's torch path on the same bf16 inputs); fp32 inputs -> 1e-4 (the reference tests'
+tolerance) and 1e-5 against the fp64 brute force.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle.paged_kv as OP
+import oracle.workloads as W
+from plastic_infer.exec.attention import (
+    gather_paged_kv,
+    host_stream_attention_v1,
+    paged_attention_v1,
+)
+from plastic_infer.kernel import kv_scatter, paged_attention, paged_decode_attention
+from test_oracle_paged import brute_attention
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+
+
+def _run_decode_step(wl: W.DecodeWorkload, dev):
+    gk, gv = wl.k_pages.to(dev), wl.v_pages.to(dev)
+    kv_scatter(wl.k_new.to(dev), wl.v_new.to(dev), gk, gv, wl.slot_mapping.to(dev))
+    out = paged_decode_attention(wl.q.to(dev), gk, gv, wl.block_tables.to(dev),
+                                 wl.context_lens.to(dev))
+    return out.cpu()
+
+
+def _oracle_decode_step(wl: W.DecodeWorkload, seqs=None):
+    kp, vp = wl.k_pages.clone(), wl.v_pages.clone()
+    OP.scatter_slots(wl.k_new, wl.v_new, kp, vp, wl.slot_mapping.tolist())
+    idx = list(range(wl.q.shape[0])) if seqs is None else seqs
+    return OP.decode_batch(wl.q[idx], kp, vp, wl.block_tables[idx], wl.context_lens[idx],
+                           wl.page_size)
+
+
+def test_decode_config1_fast_path(dev):
+    wl = W.config1()
+    got = _run_decode_step(wl, dev)
+    ref = _oracle_decode_step(wl)
+    err = (got.float() - ref.float()).abs().max().item()
+    assert err <= BF16_TOL, err
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_decode_group_sizes_and_lengths(dev, G):
+    Hkv = 8 if G < 8 else 4
+    wl = W.decode_workload(20 + G, 900, 12, 1, 1100, Hkv * G, Hkv, max_len=1200)
+    lens = torch.tensor([1, 15, 16, 17, 127, 128, 129, 511, 512, 513, 1024, 1100], dtype=torch.int32)
+    wl.context_lens = lens          # edge lengths around page and partition boundaries
+    n_pages = (lens + 15) // 16
+    perm = torch.randperm(900, generator=torch.Generator().manual_seed(G))
+    off = 0
+    bt = torch.zeros_like(wl.block_tables)
+    for b in range(12):
+        bt[b, :n_pages[b]] = perm[off:off + n_pages[b]].to(torch.int32)
+        off += int(n_pages[b])
+    wl.block_tables = bt
+    last = lens.long() - 1
+    wl.slot_mapping = bt[torch.arange(12), last // 16].long() * 16 + last % 16
+    got = _run_decode_step(wl, dev)
+    ref = _oracle_decode_step(wl)
+    err = (got.float() - ref.float()).abs().max().item()
+    assert err <= BF16_TOL, err
+
+
+def test_decode_config2_full_shape(dev):
+    """Qwen3-8B decode at full size (B = 256, L ~ U[512, 8192], 160k-page pool) generated on
+    the device; five sequences (the longest, shortest and three seeded picks) are checked
+    against the oracle from their own pages."""
+    B, Hq, Hkv, D, P, N_ = 256, 32, 8, 128, 16, 160_000
+    g = torch.Generator().manual_seed(2)
+    lens = torch.randint(512, 8193, (B,), generator=g)
+    perm = torch.randperm(N_, generator=g)
+    n_pages = (lens + P - 1) // P
+    bt = torch.zeros(B, 512, dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        bt[b, :n_pages[b]] = perm[off:off + n_pages[b]].to(torch.int32)
+        off += int(n_pages[b])
+    gd = torch.Generator(device=dev).manual_seed(2)
+    kp = torch.empty(N_, Hkv, D, P, dtype=torch.bfloat16, device=dev)
+    vp = torch.empty_like(kp)
+    for pool in (kp, vp):
+        for s in range(0, N_, 20_000):
+            pool[s:s + 20_000] = torch.randn(pool[s:s + 20_000].shape, generator=gd,
+                                             device=dev).to(torch.bfloat16)
+    q = torch.randn(B, Hq, D, generator=gd, device=dev).to(torch.bfloat16)
+    out = paged_decode_attention(q, kp, vp, bt.to(dev), lens.to(torch.int32).to(dev))
+    picks = [int(lens.argmax()), int(lens.argmin()), 3, 100, 255]
+    for b in picks:
+        table = bt[b, :n_pages[b]].tolist()
+        ids = torch.tensor(table, device=dev)
+        kl = kp.index_select(0, ids).cpu()
+        vl = vp.index_select(0, ids).cpu()
+        ref = OP.paged_attention(q[b].cpu()[None, None], kl, vl, list(range(len(table))), P,
+                                 kv_num_tokens=int(lens[b]), causal=False)[0, 0]
+        err = (out[b].cpu().float() - ref.float()).abs().max().item()
+        assert err <= BF16_TOL, (b, err)
+
+
+def test_decode_empty_and_clamped_lengths(dev):
+    g = torch.Generator().manual_seed(31)
+    kp = torch.randn(8, 2, 128, 16, generator=g).to(torch.bfloat16)
+    vp = torch.randn(8, 2, 128, 16, generator=g).to(torch.bfloat16)
+    q = torch.randn(3, 4, 128, generator=g).to(torch.bfloat16)
+    bt = torch.tensor([[1, 2], [3, 4], [5, 6]], dtype=torch.int32)
+    lens = torch.tensor([0, 40, 32], dtype=torch.int32)    # 40 > table capacity 32: clamped
+    out = paged_decode_attention(q.to(dev), kp.to(dev), vp.to(dev), bt.to(dev), lens.to(dev)).cpu()
+    assert not out[0].any()
+    for b in (1, 2):
+        ref = OP.paged_attention(q[b][None, None], kp, vp, bt[b].tolist(), 16, 32, causal=False)
+        assert (out[b].float() - ref[0, 0].float()).abs().max() <= BF16_TOL
+
+
+def test_decode_nonfinite_stale_tokens_are_ignored(dev):
+    """Tokens past L in the last page may hold NaN/Inf (stale memory): output stays finite."""
+    g = torch.Generator().manual_seed(32)
+    kp = torch.randn(4, 1, 128, 16, generator=g).to(torch.bfloat16)
+    vp = torch.randn(4, 1, 128, 16, generator=g).to(torch.bfloat16)
+    kp[2, :, :, 5:] = float("nan")
+    vp[2, :, :, 5:] = float("inf")
+    q = torch.randn(1, 2, 128, generator=g).to(torch.bfloat16)
+    bt = torch.tensor([[0, 2]], dtype=torch.int32)
+    out = paged_decode_attention(q.to(dev), kp.to(dev), vp.to(dev), bt.to(dev),
+                                 torch.tensor([21], dtype=torch.int32, device=dev)).cpu()
+    ref = OP.paged_attention(q[0][None, None], kp, vp, [0, 2], 16, 21, causal=False)
+    assert torch.isfinite(out).all()
+    assert (out[0].float() - ref[0, 0].float()).abs().max() <= BF16_TOL
+
+
+# ---- general kernel ---------------------------------------------------------------------------
+
+GEN_CASES = [  # (seed, n_pages, Hkv, G, D, P, table, kv_len, Sq, mode)
+    (0, 6, 2, 2, 8, 4, [5, 0, 3], 11, 1, "none"),
+    (1, 7, 1, 4, 16, 3, [2, 6, 1, 4], 12, 3, "top_left"),
+    (2, 9, 2, 1, 64, 16, [8, 3], 20, 4, "offset"),
+    (3, 5, 2, 4, 256, 16, [1], 1, 1, "none"),
+    (4, 8, 4, 2, 96, 2, [7, 0, 6, 1, 5], 9, 2, "offset"),
+    (5, 40, 2, 3, 128, 8, list(range(39, 0, -1)), 300, 5, "offset"),
+]
+
+
+@pytest.mark.parametrize("case", GEN_CASES)
+def test_general_kernel_fp32_vs_brute_force(dev, case):
+    seed, n, Hkv, G, D, P, table, kv_len, Sq, mode = case
+    g = torch.Generator().manual_seed(seed)
+    kp = torch.randn(n, Hkv, D, P, generator=g)
+    vp = torch.randn(n, Hkv, D, P, generator=g)
+    q = torch.randn(Sq, Hkv * G, D, generator=g)
+    q_start = kv_len - Sq if mode == "offset" else 0
+    offs = None if mode == "none" else torch.tensor([q_start], dtype=torch.int32, device=dev)
+    out = paged_attention(q.to(dev), kp.to(dev), vp.to(dev),
+                          torch.tensor([table], dtype=torch.int32, device=dev),
+                          torch.tensor([kv_len], dtype=torch.int32, device=dev),
+                          cu_q=torch.tensor([0, Sq], dtype=torch.int32, device=dev),
+                          q_pos_offsets=offs).cpu()
+    ref = brute_attention(q.double().numpy(), kp.double().numpy(), vp.double().numpy(), table, P,
+                          kv_len, None if mode == "none" else q_start)
+    np.testing.assert_allclose(out.double().numpy(), ref, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_general_kernel_half_types_batched(dev, dtype):
+    g = torch.Generator().manual_seed(7)
+    kp = torch.randn(30, 2, 64, 8, generator=g).to(dtype)
+    vp = torch.randn(30, 2, 64, 8, generator=g).to(dtype)
+    tables = [[3, 9, 27, 1], [0], [12, 13, 14, 15, 16, 17]]
+    kv = [29, 8, 41]
+    qlen = [3, 1, 4]
+    bt = torch.zeros(3, 6, dtype=torch.int32)
+    for b, t in enumerate(tables):
+        bt[b, :len(t)] = torch.tensor(t)
+    q = torch.randn(sum(qlen), 4, 64, generator=g).to(dtype)
+    cu = torch.tensor([0, 3, 4, 8], dtype=torch.int32)
+    offs = torch.tensor([kv[b] - qlen[b] for b in range(3)], dtype=torch.int32)
+    out = paged_attention(q.to(dev), kp.to(dev), vp.to(dev), bt.to(dev),
+                          torch.tensor(kv, dtype=torch.int32, device=dev), cu_q=cu.to(dev),
+                          q_pos_offsets=offs.to(dev)).cpu()
+    for b in range(3):
+        rows = q[cu[b]:cu[b + 1]]
+        ref = OP.paged_attention(rows[None], kp, vp, tables[b], 8, kv[b], causal=True,
+                                 q_start_pos=int(offs[b]))
+        assert (out[cu[b]:cu[b + 1]].float() - ref[0].float()).abs().max() <= BF16_TOL
+
+
+# ---- drop-in API (the reference's tests/test_ops.py scenarios on the device) -----------------
+
+def test_dropin_gather_paged_kv(dev):
+    torch.manual_seed(1)
+    kp = torch.randn(5, 2, 4, 8)
+    vp = torch.randn(5, 2, 4, 8)
+    k, v = gather_paged_kv(kp.to(dev), vp.to(dev), [0, 2, 4], 8)
+    rk, rv = OP.gather_paged_kv(kp, vp, [0, 2, 4], 8)
+    assert torch.equal(k.cpu(), rk) and torch.equal(v.cpu(), rv)
+    k, _ = gather_paged_kv(kp.to(dev), vp.to(dev), [0, 1], 8, num_tokens=11)
+    assert k.shape == (1, 11, 2, 4)
+    k, v = gather_paged_kv(kp.to(dev), vp.to(dev), [], 8)
+    assert k.shape == (1, 0, 2, 4) and v.shape == (1, 0, 2, 4)
+
+
+def test_dropin_paged_attention_v1(dev):
+    torch.manual_seed(7)
+    q = torch.randn(1, 8, 4, 16) * 0.1
+    kc = torch.randn(1, 12, 2, 16) * 0.1
+    vc = torch.randn(1, 12, 2, 16) * 0.1
+    kp = kc[0].view(3, 4, 2, 16).permute(0, 2, 3, 1).contiguous()
+    vp = vc[0].view(3, 4, 2, 16).permute(0, 2, 3, 1).contiguous()
+    out = paged_attention_v1(q.to(dev), kp.to(dev), vp.to(dev), [0, 1, 2], 4, 12, causal=True)
+    ref = F.scaled_dot_product_attention(
+        q.transpose(1, 2), kc.transpose(1, 2).repeat_interleave(2, 1),
+        vc.transpose(1, 2).repeat_interleave(2, 1), is_causal=True).transpose(1, 2)
+    assert torch.allclose(out.cpu(), ref, atol=1e-4)
+    one = paged_attention_v1(q[:, :1].to(dev), kp.to(dev), vp.to(dev), [0, 1, 2], 4, 12,
+                             causal=True)
+    assert one.shape == (1, 1, 4, 16) and torch.isfinite(one).all()
+    dec = paged_attention_v1(q[:, :1].to(dev), kp.to(dev), vp.to(dev), [2, 0], 4, 7,
+                             causal=False)
+    refd = OP.paged_attention(q[:, :1], kp, vp, [2, 0], 4, 7, causal=False)
+    assert torch.allclose(dec.cpu(), refd, atol=1e-5)
+
+
+@pytest.mark.parametrize("seed,total,host_len,chunk,q_len,q_start", [
+    (1, 10, 6, 3, 2, 10), (2, 8, 5, 4, 1, 8), (3, 8, 4, 2, 2, 5), (4, 6, 6, 3, 6, 0)])
+def test_dropin_host_stream_attention(dev, seed, total, host_len, chunk, q_len, q_start):
+    torch.manual_seed(seed)
+    kf = torch.randn(1, total, 2, 16) * 0.1
+    vf = torch.randn(1, total, 2, 16) * 0.1
+    chunks = []
+    for s in range(0, host_len, chunk):
+        e = min(s + chunk, host_len)
+        chunks.append((kf[0, s:e].permute(1, 2, 0).contiguous(), vf[0, s:e].permute(1, 2, 0).contiguous()))
+    rk, rv = kf[:, host_len:], vf[:, host_len:]
+    if host_len == total:
+        chunks, rk, rv = [], kf, vf
+    q = torch.randn(1, q_len, 4, 16) * 0.1
+    out = host_stream_attention_v1(q.to(dev), chunks, rk.to(dev), rv.to(dev), q_start_pos=q_start)
+    ref = OP.host_stream_attention(q, chunks, rk, rv, q_start_pos=q_start)
+    assert torch.allclose(out.cpu(), ref, atol=1e-4)
+
+
+def test_rejects_host_tensors():
+    with pytest.raises(ValueError):
+        paged_decode_attention(torch.zeros(1, 2, 128), torch.zeros(2, 1, 128, 16),
+                               torch.zeros(2, 1, 128, 16), torch.zeros(1, 1, dtype=torch.int32),
+                               torch.ones(1, dtype=torch.int32))

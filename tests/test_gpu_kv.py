@@ -1,0 +1,194 @@
+"""GPU parity: slot scatter, block-table gather, page<->chunk copies and the HBM KV store
+against the oracle — bit-exact (pure copies)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle.paged_kv as OP
+import oracle.workloads as W
+from plastic_infer.kernel import kv_gather, kv_scatter, pages_chunk_copy
+from plastic_infer.kv.kv_store import KVConfig, KVStore
+
+pytestmark = pytest.mark.gpu
+
+
+def test_decode_scatter_config1(dev):
+    wl = W.config1()
+    kp, vp = wl.k_pages.clone(), wl.v_pages.clone()
+    OP.scatter_slots(wl.k_new, wl.v_new, kp, vp, wl.slot_mapping.tolist())
+    gk, gv = wl.k_pages.to(dev), wl.v_pages.to(dev)
+    kv_scatter(wl.k_new.to(dev), wl.v_new.to(dev), gk, gv, wl.slot_mapping.to(dev))
+    assert torch.equal(gk.cpu(), kp) and torch.equal(gv.cpu(), vp)
+
+
+def test_prefill_scatter_and_gather_round_trip_config3(dev):
+    wl = W.prefill_write_workload()
+    H, D, P = wl.k.shape[1], wl.k.shape[2], wl.page_size
+    kp = torch.zeros(wl.num_pages, H, D, P, dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    OP.scatter_slots(wl.k, wl.v, kp, vp, wl.slot_mapping.tolist())
+    gk, gv = torch.zeros_like(kp, device=dev), torch.zeros_like(vp, device=dev)
+    kv_scatter(wl.k.to(dev), wl.v.to(dev), gk, gv, wl.slot_mapping.to(dev))
+    assert torch.equal(gk.cpu(), kp) and torch.equal(gv.cpu(), vp)
+    k_back, v_back = kv_gather(gk, gv, wl.block_tables.to(dev), wl.cu_seqlens.to(dev), wl.max_len)
+    assert torch.equal(k_back.cpu(), wl.k) and torch.equal(v_back.cpu(), wl.v)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_scatter_edge_slots(dev, dtype):
+    g = torch.Generator().manual_seed(11)
+    N_, H, D, P = 6, 2, 8, 4
+    kp = torch.randn(N_, H, D, P, generator=g).to(dtype)
+    vp = torch.randn(N_, H, D, P, generator=g).to(dtype)
+    k = torch.randn(9, H, D, generator=g).to(dtype)
+    v = torch.randn(9, H, D, generator=g).to(dtype)
+    slots = [3, -1, 23, 0, 24, 1000, 7, 7, 12]   # padding, last slot, out of range, repeats
+    ref_k, ref_v = kp.clone(), vp.clone()
+    OP.scatter_slots(k, v, ref_k, ref_v, [s if s < N_ * P else -1 for s in slots])
+    gk, gv = kp.to(dev), vp.to(dev)
+    kv_scatter(k.to(dev), v.to(dev), gk, gv, torch.tensor(slots, device=dev))
+    assert torch.equal(gk.cpu(), ref_k) and torch.equal(gv.cpu(), ref_v)
+    kv_scatter(k[:0].to(dev), v[:0].to(dev), gk, gv, torch.empty(0, dtype=torch.int64, device=dev))
+
+
+def test_scatter_strided_rows_and_tile_path(dev):
+    g = torch.Generator().manual_seed(12)
+    H, D, P = 2, 16, 4
+    src = torch.randn(13, 3, H, D, generator=g).to(torch.bfloat16)
+    k, v = src[:, 0], src[:, 2]                    # token stride 3*H*D, rows [H, D] contiguous
+    slots = list(range(8, 16)) + [40, 41, 42, 3, 2]   # two full aligned pages then scattered
+    kp = torch.zeros(12, H, D, P, dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    ref_k, ref_v = kp.clone(), vp.clone()
+    OP.scatter_slots(k, v, ref_k, ref_v, slots)
+    gk, gv = kp.to(dev), vp.to(dev)
+    gsrc = src.to(dev)
+    kv_scatter(gsrc[:, 0], gsrc[:, 2], gk, gv, torch.tensor(slots, device=dev))
+    assert torch.equal(gk.cpu(), ref_k) and torch.equal(gv.cpu(), ref_v)
+
+
+def test_gather_matches_oracle_and_empty(dev):
+    g = torch.Generator().manual_seed(13)
+    kp = torch.randn(9, 3, 8, 5, generator=g)
+    vp = torch.randn(9, 3, 8, 5, generator=g)
+    tables = [[4, 0, 7], [2], [8, 1, 3]]
+    lens = [13, 0, 15]
+    bt = torch.zeros(3, 3, dtype=torch.int32)
+    for b, t in enumerate(tables):
+        bt[b, :len(t)] = torch.tensor(t)
+    cu = torch.tensor([0, 13, 13, 28])
+    k, v = kv_gather(kp.to(dev), vp.to(dev), bt.to(dev), cu.to(dev), 15)
+    for b, t in enumerate(tables):
+        rk, rv = OP.gather_paged_kv(kp, vp, t, 5, lens[b])
+        assert torch.equal(k[cu[b]:cu[b + 1]].cpu(), rk[0])
+        assert torch.equal(v[cu[b]:cu[b + 1]].cpu(), rv[0])
+
+
+def test_pages_chunk_copy_both_ways(dev):
+    g = torch.Generator().manual_seed(14)
+    pages = torch.randn(20, 2, 4, 4, generator=g)
+    ids = [3, 9, -1, 0, 17, 5]                  # 2 layers x 3 pages per chunk, one absent
+    ref = OP.pages_to_chunk(pages, ids, 2, 3)
+    chunk = torch.zeros(2, 2, 4, 12, device=dev)
+    pages_chunk_copy(chunk, pages.to(dev), torch.tensor(ids, device=dev), to_chunk=True)
+    assert torch.equal(chunk.cpu(), ref)
+    back = torch.zeros(20, 2, 4, 4, device=dev)
+    pages_chunk_copy(chunk, back, torch.tensor(ids, device=dev), to_chunk=False)
+    for l in range(2):
+        for p in range(3):
+            pid = ids[l * 3 + p]
+            if pid >= 0:
+                assert torch.equal(back[pid].cpu(), pages[pid])
+
+
+# ---- KV store (the reference's tests/test_kv_store.py scenarios, pools in HBM) ----------------
+
+@pytest.fixture
+def store(dev) -> KVStore:
+    return KVStore(KVConfig(n_layers=2, n_kv_heads=2, head_dim=4, page_size=4, pages_per_chunk=2,
+                            max_pages=64, max_host_chunks=8, dtype=torch.float32, device=dev))
+
+
+def _kv(store, seed):
+    g = torch.Generator().manual_seed(seed)
+    c = store.config
+    k = torch.randn(c.n_layers, c.n_kv_heads, c.head_dim, generator=g)
+    v = torch.randn(c.n_layers, c.n_kv_heads, c.head_dim, generator=g)
+    return k.to(store.gpu.device), v.to(store.gpu.device)
+
+
+def test_store_rejects_host_device():
+    with pytest.raises(ValueError):
+        KVStore(KVConfig(n_layers=1, n_kv_heads=1, head_dim=4, device=torch.device("cpu")))
+
+
+def test_store_append_and_placement(store):
+    cache = store.new_request()
+    for i in range(5):
+        cache.append_token(*_kv(store, i))
+    assert cache.length == 5 and cache.block_table.num_logical_pages(0) == 2
+    assert store.gpu.allocator.used_pages == 4
+    k, v = _kv(store, 4)
+    phys = cache.block_table.get_page(1, 1)
+    assert torch.equal(store.gpu.k_pages[phys, :, :, 0], k[1])
+    assert torch.equal(store.gpu.v_pages[phys, :, :, 0], v[1])
+    store.free_request(cache)
+    assert store.gpu.allocator.free_pages == 64
+
+
+def test_store_sink_round_trip_and_host_lru(store):
+    cfg = store.config
+    cache = store.new_request()
+    n = cfg.tokens_per_chunk * (cfg.max_host_chunks + 3)
+    for i in range(n):
+        cache.append_token(*_kv(store, i * 7))
+    cache.set_token_ids(list(range(n)))
+    assert store.sink_completed_chunks(cache) == cfg.max_host_chunks + 3
+    assert store.host_cache_size == cfg.max_host_chunks
+    key = cache.chunk_keys[-1].full_key
+    hk, hv = store._host_cache[key]
+    c = len(cache.chunk_keys) - 1
+    for layer in range(cfg.n_layers):
+        for t in range(cfg.tokens_per_chunk):
+            g = c * cfg.tokens_per_chunk + t
+            phys = cache.block_table.get_page(layer, g // cfg.page_size)
+            assert torch.equal(hk[layer, :, :, t], store.gpu.k_pages[phys, :, :, g % cfg.page_size].cpu())
+            assert torch.equal(hv[layer, :, :, t], store.gpu.v_pages[phys, :, :, g % cfg.page_size].cpu())
+
+
+def test_store_prefix_load(store):
+    cfg = store.config
+    C = cfg.tokens_per_chunk
+    c1 = store.new_request()
+    toks = list(range(2 * C))
+    for i in range(len(toks)):
+        c1.append_token(*_kv(store, i))
+    c1.set_token_ids(toks)
+    store.sink_completed_chunks(c1)
+    ref = {}
+    for layer in range(cfg.n_layers):
+        for t in range(2 * C):
+            phys = c1.block_table.get_page(layer, t // cfg.page_size)
+            ref[(layer, t)] = store.gpu.k_pages[phys, :, :, t % cfg.page_size].clone()
+    store.free_request(c1)
+    c2 = store.new_request()
+    matched, keys = store.load_prefix(c2, toks + [999])
+    assert matched == 2 * C and len(keys) == 2 and c2.length == 2 * C
+    for (layer, t), val in ref.items():
+        phys = c2.block_table.get_page(layer, t // cfg.page_size)
+        assert torch.equal(store.gpu.k_pages[phys, :, :, t % cfg.page_size], val)
+    c3 = store.new_request()
+    assert store.load_prefix(c3, [999, 998, 997]) == (0, [])
+
+
+def test_store_evict_chunks(store):
+    C = store.config.tokens_per_chunk
+    cache = store.new_request()
+    for i in range(4 * C):
+        cache.append_token(*_kv(store, i))
+    cache.set_token_ids(list(range(4 * C)))
+    used = store.gpu.allocator.used_pages
+    freed = store.evict_chunks(need_pages=1, protected_request=cache)
+    assert freed >= 1 and store.gpu.allocator.used_pages == used - freed

@@ -1,0 +1,127 @@
+"""GPU parity of routing / permute plan / permute / combine against the oracle.
+
+Indices, the permute plan, the permuted rows and the combine (fp32, fixed order, separately
+rounded multiply and add) are bit-exact; router weights are compared at 1e-6 relative (exp and
+the order of the renormalising sum differ from torch's CPU kernels).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle.moe_route as OM
+import oracle.workloads as W
+from plastic_infer.exec.moe import moe_forward_sparse, swiglu_mlp, topk_route
+from plastic_infer.kernel import moe_align_block_size, moe_permute, moe_sum_reduce, moe_unpermute
+from plastic_infer.moe.fused import fused_topk
+from plastic_infer.store.experts import ExpertWeights
+
+pytestmark = pytest.mark.gpu
+
+
+def test_router_config4_indices_bit_exact(dev):
+    wl = W.moe_workload()
+    w, ids = fused_topk(wl.hidden.to(dev), wl.logits.to(dev), wl.topk, True)
+    rw, rids = OM.fused_topk(wl.logits, wl.topk, True)
+    assert torch.equal(ids.cpu(), rids)
+    assert torch.allclose(w.cpu(), rw, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_router_dtypes_and_padding(dev, dtype):
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(37, 200, generator=g).to(dtype)
+    w, ids = fused_topk(torch.zeros(37, 1), logits.to(dev), 6, False, num_token_non_padded=30)
+    p = torch.softmax(logits.float(), -1)
+    ref_ids = torch.from_numpy(np.argsort(-logits.float().numpy(), 1, kind="stable")[:, :6].copy())
+    assert torch.equal(ids.cpu()[:30].long(), ref_ids[:30])
+    assert (ids.cpu()[30:] == -1).all()
+    assert torch.allclose(w.cpu(), torch.gather(p, 1, ref_ids), rtol=1e-5, atol=1e-7)
+
+
+def test_topk_route_kats(dev):
+    ids, w = topk_route(torch.tensor([[1.0, 5.0, 3.0, 0.5, 2.0]], device=dev), k=2)
+    assert set(ids[0].tolist()) == {1, 2} and torch.allclose(w.sum(-1).cpu(), torch.ones(1))
+    ids, w = topk_route(torch.tensor([[1.0, 2.0, 3.0, 4.0]], device=dev), k=2)
+    assert ids[0].tolist() == [3, 2] and ids.dtype == torch.int64
+    assert torch.allclose(w.cpu(), F.softmax(torch.tensor([[4.0, 3.0]]), -1), atol=1e-6)
+
+
+def _check_align(dev, ids_np, bs, E):
+    s, e, npp, pos = moe_align_block_size(torch.from_numpy(ids_np).to(dev), bs, E,
+                                          return_route_pos=True)
+    rs, re_, rnpp, rpos = OM.moe_align_block_size(ids_np, bs, E)
+    assert int(npp.item()) == rnpp
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(e.cpu().numpy()[:rnpp // bs], re_[:rnpp // bs])
+    assert np.array_equal(pos.cpu().numpy(), rpos)
+
+
+def test_align_reference_docstring_example(dev):
+    _check_align(dev, np.array([[2, 3, 4], [1, 2, 4], [1, 3, 4], [1, 2, 3]], np.int32), 4, 4)
+
+
+@pytest.mark.parametrize("seed,T,k,E,bs", [(0, 4096, 8, 128, 64), (1, 1, 8, 128, 16),
+                                           (2, 300, 8, 128, 1), (3, 77, 3, 5, 7),
+                                           (4, 2000, 2, 1023, 16)])
+def test_align_random_bit_exact(dev, seed, T, k, E, bs):
+    rng = np.random.default_rng(seed)
+    _check_align(dev, rng.integers(-1, E + 2, size=(T, k)).astype(np.int32), bs, E)
+
+
+def test_align_empty(dev):
+    s, e, npp = moe_align_block_size(torch.empty(0, 8, dtype=torch.int32, device=dev), 16, 128)
+    assert int(npp.item()) == 0 and s.numel() == 0
+
+
+def test_permute_combine_config4(dev):
+    wl = W.moe_workload()
+    w, ids = OM.fused_topk(wl.logits, wl.topk, True)
+    T, k = ids.shape
+    s, e, npp, pos = moe_align_block_size(ids.to(dev), 64, 128, return_route_pos=True)
+    hidden = wl.hidden.to(dev)
+    xp = moe_permute(hidden, s, npp, k)
+    rs, _, rnpp, rpos = OM.moe_align_block_size(ids.numpy(), 64, 128)
+    ref_xp = OM.permute(wl.hidden, rs, rnpp, k)
+    assert torch.equal(xp[:rnpp].cpu(), ref_xp)
+    out = moe_unpermute(xp, pos, w.to(dev), T, k)              # identity expert stand-in
+    ref = OM.unpermute(ref_xp, rpos, w.numpy(), T, k, torch.bfloat16)
+    assert torch.equal(out.cpu(), ref)
+    closed = (wl.hidden.double() * w.double().sum(1, keepdim=True)).to(torch.bfloat16)
+    assert (out.cpu().float() - closed.float()).abs().max() <= 2e-2
+
+
+@pytest.mark.parametrize("dtype,H", [(torch.bfloat16, 2048), (torch.float32, 100), (torch.float16, 12)])
+def test_sum_reduce(dev, dtype, H):
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(33, 8, H, generator=g).to(dtype)
+    out = torch.empty(33, H, dtype=dtype, device=dev)
+    moe_sum_reduce(x.to(dev), out)
+    assert torch.equal(out.cpu(), OM.sum_reduce(x, dtype))
+
+
+def _experts(E, H, I, seed=7):
+    g = torch.Generator().manual_seed(seed)
+    return {e: ExpertWeights(torch.randn(I, H, generator=g) * 0.1, torch.randn(H, I, generator=g) * 0.1,
+                             torch.randn(I, H, generator=g) * 0.1) for e in range(E)}
+
+
+def test_moe_forward_sparse_vs_loop(dev):
+    torch.manual_seed(11)
+    T, H, I, E, k = 8, 16, 32, 4, 2
+    hidden = torch.randn(T, H) * 0.5
+    experts = _experts(E, H, I)
+    eids, weights = topk_route(torch.randn(T, E).to(dev), k=k)
+    routed = {int(x) for x in eids.flatten().tolist()}
+    dev_experts = {e: ExpertWeights(*(t.to(dev) for t in (w.w1, w.w2, w.w3)))
+                   for e, w in experts.items() if e in routed}
+    out = moe_forward_sparse(hidden.to(dev), dev_experts, eids, weights).cpu()
+    ref = torch.zeros(T, H)
+    for t in range(T):
+        for s_ in range(k):
+            w = experts[int(eids[t, s_])]
+            ref[t] += swiglu_mlp(hidden[t], w.w1, w.w2, w.w3) * weights[t, s_].cpu()
+    assert torch.allclose(out, ref, atol=1e-5)

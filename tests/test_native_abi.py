@@ -1,0 +1,58 @@
+"""The C-ABI library loads and exports exactly what include/plastic_infer_amd.h declares
+(CPU: no compute call is made; argument validation returns before any device work)."""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+from plastic_infer import _native as N
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "plastic_infer_amd.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(pia_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exists_and_loads():
+    assert N.LIB_PATH.exists(), "build the library first (plastic-infer_amd/csrc/build.py)"
+    lib = N.load()
+    assert lib.pia_abi_version() == N.EXPECTED_ABI
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    names = declared_functions()
+    assert len(names) >= 15
+    lib = ctypes.CDLL(str(N.LIB_PATH))
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared but not exported"
+    assert set(names) == set(N._SIGNATURES), "ctypes bindings drift from the header"
+
+
+def test_exports_are_c_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(N.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert set(declared_functions()) <= exported
+
+
+def test_invalid_arguments_are_rejected_without_device_work():
+    lib = N.load()
+    rc = lib.pia_kv_scatter(None, None, None, None, None, 4, 8, 8, 2, 4, 16, 10, 3, None)
+    assert rc == -1 and b"elem_bytes" in lib.pia_last_error()
+    rc = lib.pia_paged_attention(None, None, None, None, None, 1, None, None, None, 1, 1,
+                                 3, 2, 16, 16, 10, 1.0, 2, None)
+    assert rc == -1 and b"num_heads % num_kv_heads" in lib.pia_last_error()
+    rc = lib.pia_moe_topk(None, None, None, 0, 4, 8, 9, 1, 0, -1, None)
+    assert rc == -1
+    assert N.query("pia_paged_decode_workspace_bytes", 256, 32, 128, 16, 512) == \
+        256 * 32 * 16 * 130 * 4
+    assert N.query("pia_paged_decode_workspace_bytes", 4, 4, 64, 16, 8) == 0
+    with pytest.raises(N.NativeError):
+        N.call("pia_moe_sum_reduce", None, None, 1, 0, 4, 2, None)
