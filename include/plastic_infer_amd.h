@@ -60,7 +60,8 @@ int pia_abi_version(void);
  * (src/plastic_infer/kv/kv_store.py:124-143):  for i < num_tokens with slot = slot_mapping[i],
  *     k_pages[slot / page_size, h, d, slot % page_size] = k[i, h, d]   (same for v)
  * Slots < 0 (padding) or >= num_pages*page_size are skipped. Bit-exact byte copy;
- * elem_bytes is 2 or 4. k_token_stride / v_token_stride are in elements.
+ * elem_bytes is 2 or 4; page_size <= 1024. k_token_stride / v_token_stride are in elements.
+ * Tokens sharing a slot land in unspecified order (the reference writes them in token order).
  * ------------------------------------------------------------------------------------------- */
 int pia_kv_scatter(const void* k, const void* v, void* k_pages, void* v_pages,
                    const int64_t* slot_mapping, int64_t num_tokens,

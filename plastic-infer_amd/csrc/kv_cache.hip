@@ -19,8 +19,10 @@ namespace {
 //
 // General path (any slot pattern): one element store per (token, h, d).
 //
-// Grid: one block per group of P consecutive input tokens. Each block first checks whether its
-// group is a full aligned page run; if yes it takes the tile path, otherwise the per-token path.
+// Grid: (groups of P consecutive input tokens) x P. Every block of a group first checks whether
+// the group is a full aligned page run; if so block y == 0 writes the page tile and the others
+// exit, otherwise block y writes token y of the group (decode: one block per token).
+// Two tokens with the same slot land in unspecified order.
 
 template <typename W>
 __global__ __launch_bounds__(256) void kv_scatter_kernel(
@@ -33,6 +35,7 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(
 
   const int64_t i0 = int64_t(blockIdx.x) * P;
   const int ntok = int(min<int64_t>(P, n - i0));
+  const int y = blockIdx.y;
   if (threadIdx.x == 0) {
     int full = use_tile && (ntok == P);
     if (full) {
@@ -45,6 +48,7 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(
   __syncthreads();
 
   if (s_full) {
+    if (y != 0) return;
     const int64_t page = slots[i0] / P;
     for (int pass = 0; pass < 2; ++pass) {
       const W* src = pass == 0 ? k : v;
@@ -65,19 +69,18 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(
     return;
   }
 
-  for (int t = 0; t < ntok; ++t) {
-    const int64_t slot = slots[i0 + t];
-    if (slot < 0 || slot >= total_slots) continue;
-    const int64_t page = slot / P;
-    const int off = int(slot - page * P);
-    const W* ks = k + (i0 + t) * k_stride;
-    const W* vs = v + (i0 + t) * v_stride;
-    W* kd = kp + page * int64_t(HD) * P + off;
-    W* vd = vp + page * int64_t(HD) * P + off;
-    for (int r = threadIdx.x; r < HD; r += blockDim.x) {
-      kd[int64_t(r) * P] = ks[r];
-      vd[int64_t(r) * P] = vs[r];
-    }
+  if (y >= ntok) return;
+  const int64_t slot = slots[i0 + y];
+  if (slot < 0 || slot >= total_slots) return;
+  const int64_t page = slot / P;
+  const int off = int(slot - page * P);
+  const W* ks = k + (i0 + y) * k_stride;
+  const W* vs = v + (i0 + y) * v_stride;
+  W* kd = kp + page * int64_t(HD) * P + off;
+  W* vd = vp + page * int64_t(HD) * P + off;
+  for (int r = threadIdx.x; r < HD; r += blockDim.x) {
+    kd[int64_t(r) * P] = ks[r];
+    vd[int64_t(r) * P] = vs[r];
   }
 }
 
@@ -149,8 +152,9 @@ __global__ __launch_bounds__(256) void kv_chunk_copy_kernel(
 }
 
 int check_common(int H, int D, int P, int64_t num_pages, int eb) {
-  if (H <= 0 || D <= 0 || P <= 0 || num_pages <= 0)
-    return fail(PIA_EINVAL, "kv: num_kv_heads, head_dim, page_size and num_pages must be > 0");
+  if (H <= 0 || D <= 0 || P <= 0 || P > 1024 || num_pages <= 0)
+    return fail(PIA_EINVAL, "kv: num_kv_heads, head_dim, num_pages must be > 0 and page_size "
+                            "in [1, 1024]");
   if (eb != 2 && eb != 4) return fail(PIA_EINVAL, "kv: elem_bytes must be 2 or 4");
   return 0;
 }
@@ -182,12 +186,14 @@ extern "C" int pia_kv_scatter(const void* k, const void* v, void* k_pages, void*
   const int64_t total_slots = num_pages * page_size;
   hipStream_t s = as_stream(stream);
   if (elem_bytes == 2)
-    hipLaunchKernelGGL(kv_scatter_kernel<uint16_t>, dim3(blocks), dim3(256), smem, s,
+    hipLaunchKernelGGL(kv_scatter_kernel<uint16_t>, dim3(unsigned(blocks), unsigned(page_size)),
+                       dim3(256), smem, s,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)k_pages,
                        (uint16_t*)v_pages, slot_mapping, num_tokens, k_token_stride,
                        v_token_stride, HD, page_size, total_slots, use_tile);
   else
-    hipLaunchKernelGGL(kv_scatter_kernel<uint32_t>, dim3(blocks), dim3(256), smem, s,
+    hipLaunchKernelGGL(kv_scatter_kernel<uint32_t>, dim3(unsigned(blocks), unsigned(page_size)),
+                       dim3(256), smem, s,
                        (const uint32_t*)k, (const uint32_t*)v, (uint32_t*)k_pages,
                        (uint32_t*)v_pages, slot_mapping, num_tokens, k_token_stride,
                        v_token_stride, HD, page_size, total_slots, use_tile);

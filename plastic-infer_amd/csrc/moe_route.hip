@@ -343,8 +343,8 @@ extern "C" int pia_moe_align_block_size(int32_t* sorted_token_ids, int32_t* expe
     return fail(PIA_EINVAL, "moe_align: sizes must fit int32");
   const int E_eff = num_experts + 1;
   if (E_eff > 16384) return fail(PIA_EUNSUPPORTED, "moe_align: more than 16383 experts");
-  if (!sorted_token_ids || !expert_ids || !num_tokens_post_pad || !workspace ||
-      (numel > 0 && !topk_ids))
+  if (!num_tokens_post_pad || !workspace || (numel > 0 && !topk_ids) ||
+      (max_num_tokens_padded > 0 && (!sorted_token_ids || !expert_ids)))
     return fail(PIA_EINVAL, "moe_align: null pointer");
   if (workspace_bytes < pia_moe_align_workspace_bytes(num_experts))
     return fail(PIA_EINVAL, "moe_align: workspace too small");

