@@ -171,7 +171,7 @@ def main() -> int:
     print(f"bench: generating inputs (B={B}, pool={NUM_PAGES} pages)", file=sys.stderr, flush=True)
     inp = build_inputs(torch, dev)
     out = torch.empty(B, HQ, D, dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(decode_workspace_bytes(B, HQ, D, P, MAX_PAGES), dtype=torch.uint8, device=dev)
+    ws = torch.empty(decode_workspace_bytes(B, HQ, HKV, D, P, MAX_PAGES), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
 
     def step(ev_a=None, ev_b=None):
@@ -233,7 +233,7 @@ def main() -> int:
         "bytes_per_step": step_bytes,
         "wall_s_timed": round(wall, 4),
         "roofline": {
-            "kernel": "paged_decode_bf16_d128p16 + paged_decode_reduce (one attention call)",
+            "kernel": "paged_decode_stream<4> + paged_decode_stream_reduce (one attention call)",
             "bound": "hbm", "achieved": round(attn_gbps, 2), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
             "algorithmic_bytes_per_launch": attn_bytes, "avg_launch_ms": round(attn_ms, 4),

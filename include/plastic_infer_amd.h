@@ -105,13 +105,17 @@ int pia_kv_pages_chunk_copy(void* chunk, void* pages, const int64_t* page_ids,
  * q row stride between sequences is q_seq_stride elements; heads are contiguous [H, D].
  * out is contiguous [num_seqs, num_heads, head_dim]; L_b == 0 writes zeros.
  * workspace: caller-owned device scratch of at least
- *     pia_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim, page_size, bt_stride)
- * bytes (may be NULL when that query returns 0).
- * bf16 with head_dim 128 and page_size 16 takes the split-context fast kernel; every other
- * supported combination (f32/f16/bf16, head_dim <= 512, any page_size) takes the general kernel.
+ *     pia_paged_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim, page_size,
+ *                                      bt_stride)
+ * bytes, 4-byte aligned (may be NULL when that query returns 0). Calls that share a workspace
+ * must be ordered (same stream): the kernels keep partials in it between their two launches.
+ * bf16 with head_dim 128 and page_size 16 and Hq/Hkv in {1, 2, 4, 8} takes the fast kernels
+ * (an even split of the batch's KV steps over persistent waves for Hq/Hkv <= 4, split-context
+ * partitions for 8); every other supported combination (f32/f16/bf16, head_dim <= 512, any
+ * page_size) takes the general kernel.
  * ------------------------------------------------------------------------------------------- */
-int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim,
-                                         int page_size, int64_t bt_stride);
+int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_heads,
+                                         int head_dim, int page_size, int64_t bt_stride);
 
 int pia_paged_decode_attention(void* out, const void* q, int64_t q_seq_stride,
                                const void* k_pages, const void* v_pages,

@@ -1,8 +1,10 @@
 // Paged GQA attention over the KV pool layout [num_pages, Hkv, D, P] (token innermost).
 //
-// 1. paged_decode_bf16_d128p16<G>: the decode hot path (bf16, D = 128, P = 16, G = Hq/Hkv in
-//    {1,2,4,8}). Split-context: one 256-thread workgroup per (512-token partition, kv head,
-//    sequence); each of its 4 waves owns 8 pages (128 tokens) of the partition.
+// 1. paged_decode_stream<G> (G = Hq/Hkv in {1,2,4}) and paged_decode_bf16_d128p16<8>: the
+//    decode hot path for bf16, D = 128, P = 16. The stream kernel (described where it is
+//    defined) spreads the batch's 128-token steps evenly over persistent single waves; the
+//    G = 8 kernel is split-context: one 256-thread workgroup per (512-token partition, kv head,
+//    sequence); each of its 4 waves owns 8 pages (128 tokens) of the partition. Both use:
 //      K tile loads: lane l reads page l/8, rows d = 4i + (l&3), token half (l>>2)&1, so load i
 //        of the wave covers one whole 128-byte line of each of the 8 pages (32 loads / 8 pages).
 //      QK^T: pairs of rows (d, d+4) are packed per token with v_perm, then v_dot2_f32_bf16
@@ -16,6 +18,9 @@
 // 2. paged_attention_generic<DT, DPL>: any dtype / head_dim <= 512 / page size, several query
 //    rows per sequence with optional causal offsets. One wave per (query row, head); keys are
 //    processed 64 at a time (lane = key for QK, lane = head-dim element for PV).
+#include <algorithm>
+#include <atomic>
+
 #include "pia_internal.h"
 
 namespace pia {
@@ -361,63 +366,163 @@ __global__ __launch_bounds__(256, 2) void paged_decode_bf16_d128p16(
 }
 
 // ---------------------------------------------------------------------------------------------
-// Software-pipelined single-wave decode kernel (G <= 4).
+// Stream decode kernel (G <= 4): persistent single waves over an even split of the batch.
 //
-// One 64-thread workgroup per (512-token partition, kv head, sequence); the wave walks its
-// partition in steps of 8 pages with the same lane mappings as the kernel above, but splits the
-// step's tiles into four 16 KiB load groups — K rows 0..63 (ka), K rows 64..127 (kb), V of pages
-// 0..3 (va), V of pages 4..7 (vb) — and always issues the next group before consuming the
-// current one:
+// The work of a launch is the ordered list of 128-token steps of every (sequence, kv head)
+// segment, sequence-major then head then step: T = Hkv * sum_b ceil(L_b / 128) steps. Wave w of
+// the NW launched (every CU full at two single-wave workgroups per SIMD) walks the contiguous
+// steps [w*C, min((w+1)*C, T)), C = ceil(T / NW), so every wave streams the same number of KV
+// bytes whatever the mix of context lengths, and only the first step of a wave waits on a
+// prologue: the next step's block-table row (and its q, when it opens a segment) is fetched one
+// step ahead and its K tiles are prefetched during the current step's PV, across segment
+// boundaries. Per step the tile work uses the lane mappings above in four 16 KiB load groups,
+// K rows 0..63 (ka), K rows 64..127 (kb), V of pages 0..3 (va), V of pages 4..7 (vb):
 //     QK(ka) | issue va | QK(kb) | softmax | issue vb | PV(va) | issue ka' | PV(vb) | issue kb'
-// so ~32 KiB stay in flight per wave through compute, with 128 VGPRs of tile data. There is no
-// workgroup barrier; the partial (max, sum, acc) of the partition goes to the same workspace as
-// above (or the final output for a one-partition sequence).
+// so about 32 KiB stay in flight per wave through the compute, with 128 VGPRs of tile data.
+// A segment that lies inside one wave's range is finished there (output written directly); a
+// segment cut by a range boundary leaves (max, sum, unnormalised acc) partials, at most two per
+// wave: slot 0 for the segment that began before the wave's range, slot 1 for the one that
+// began inside it and continues after. paged_decode_stream_reduce merges them.
 // ---------------------------------------------------------------------------------------------
+constexpr int SD_MAX_SEQS = 1024;   // sequences per launch (step-prefix table in LDS)
+constexpr int SD_MAX_WAVES = 4096;  // partial slots are sized for this many waves
+constexpr int SD_WAVES_PER_CU = 8;  // two single-wave workgroups per SIMD
+constexpr int SD_STEP_TOKENS = FD_PAGES_PER_WAVE * FD_P;  // 128 tokens per step
+constexpr int SD_META_INTS = SD_MAX_SEQS + 4;              // step prefix [B + 1], range size C
+
+struct StreamCursor {
+  int b, h, ls, ns, L;  // sequence, kv head, step in the segment, steps in it, its tokens
+};
+
+__device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
 template <int G>
-__global__ __launch_bounds__(64, 2) void paged_decode_pipelined(
+__global__ __launch_bounds__(64, 2) void paged_decode_stream(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
     const uint16_t* __restrict__ kpool, const uint16_t* __restrict__ vpool,
     const int32_t* __restrict__ block_tables, int64_t bt_stride,
-    const int32_t* __restrict__ context_lens, float* __restrict__ ws_acc,
-    float* __restrict__ ws_ml, int Hkv, int64_t num_pages, int max_parts, float scale_log2) {
-  constexpr int D = FD_D, P = FD_P, TILE = D * P;
-  constexpr int STEP = FD_PAGES_PER_WAVE;        // 8 pages per step
-  const int part = blockIdx.x, h = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
+    const int32_t* __restrict__ context_lens, int B, int Hkv, int64_t num_pages,
+    float* __restrict__ ws_part, int32_t* __restrict__ ws_meta, float scale_log2) {
+  constexpr int D = FD_D, P = FD_P, TILE = D * P, STEP = FD_PAGES_PER_WAVE;
+  constexpr int NCH = SD_MAX_SEQS / 64;
+  const int lane = threadIdx.x, w = blockIdx.x, NW = gridDim.x;
   const int Hq = Hkv * G;
-  const int L = clamp_len(context_lens[b], bt_stride, P);
-  const int n_pages = (L + P - 1) / P;
-  const int n_parts = (n_pages + FD_PART_PAGES - 1) / FD_PART_PAGES;
-  const int64_t row0 = int64_t(b) * Hq + int64_t(h) * G;
-  if (n_parts == 0) {
-    if (part == 0)
-      for (int i = lane; i < G * D; i += 64) out[row0 * D + i] = 0;
-    return;
-  }
-  if (part >= n_parts) return;
-
+  extern __shared__ int sd_lds[];
+  int* seq_q = sd_lds;            // [B + 1]: steps of the sequences before b
+  int* seq_len = sd_lds + B + 1;  // [B]: clamped context length
   __shared__ uint32_t q_lds[4][16][G];
   __shared__ uint32_t p_lds[64][G];
-  const uint16_t* qb = q + int64_t(b) * q_seq_stride + int64_t(h) * G * D;
-  for (int i = lane; i < 4 * 16 * G; i += 64) {
-    const int g = i % G, pp = (i / G) % 16, dsub = i / (G * 16);
-    const int d0 = 8 * pp + dsub;
-    q_lds[dsub][pp][g] = uint32_t(qb[g * D + d0]) | (uint32_t(qb[g * D + d0 + 4]) << 16);
+
+  // Step prefix over the batch: every wave builds its own copy in LDS, wave 0 also publishes
+  // it (and C) for the merge kernel.
+  int lv[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int i = c * 64 + lane;
+    lv[c] = (c * 64 < B && i < B) ? clamp_len(context_lens[i], bt_stride, P) : 0;
+  }
+  int carry = 0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (c * 64 >= B) break;
+    const int incl = wave_inclusive_scan((lv[c] + SD_STEP_TOKENS - 1) / SD_STEP_TOKENS, lane);
+    const int i = c * 64 + lane;
+    if (i < B) {
+      seq_q[i + 1] = carry + incl;
+      seq_len[i] = lv[c];
+      if (w == 0) ws_meta[i + 1] = carry + incl;
+    }
+    carry = uniform(carry + __shfl(incl, 63, 64));
+  }
+  const int T = Hkv * carry;
+  const int C = (T + NW - 1) / NW;
+  if (lane == 0) {
+    seq_q[0] = 0;
+    if (w == 0) {
+      ws_meta[0] = 0;
+      ws_meta[B + 1] = C;
+    }
   }
   __syncthreads();
+  const int start = w * C;
+  if (start >= T) return;
+  const int end = min(start + C, T);
 
-  const int pbase = part * FD_PART_PAGES;
-  const int npg = min(FD_PART_PAGES, n_pages - pbase);
-  const int nsteps = (npg + STEP - 1) / STEP;
-  // lane i (< 32) holds the physical id of partition page min(i, npg - 1)
-  int myp = lane & 31;
-  if (myp > npg - 1) myp = npg - 1;
-  int phys = block_tables[int64_t(b) * bt_stride + pbase + myp];
-  if (phys < 0 || int64_t(phys) >= num_pages) phys = 0;
+  // cursor of global step gs: the last sequence b with Hkv * seq_q[b] <= gs (it has steps)
+  auto seg_of = [&](int gs) {
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (Hkv * uniform(seq_q[mid]) <= gs) lo = mid; else hi = mid - 1;
+    }
+    StreamCursor c;
+    c.b = lo;
+    const int q0 = uniform(seq_q[lo]);
+    c.ns = uniform(seq_q[lo + 1]) - q0;
+    const int r = gs - Hkv * q0;
+    c.h = r / c.ns;
+    c.ls = r - c.h * c.ns;
+    c.L = uniform(seq_len[lo]);
+    return c;
+  };
+  // the step after c (only asked for when one exists inside the range)
+  auto next_of = [&](StreamCursor c) {
+    if (++c.ls == c.ns) {
+      c.ls = 0;
+      if (++c.h == Hkv) {
+        c.h = 0;
+        do { ++c.b; } while (c.b < B - 1 && uniform(seq_q[c.b + 1]) == uniform(seq_q[c.b]));
+        c.ns = uniform(seq_q[c.b + 1]) - uniform(seq_q[c.b]);
+        c.L = uniform(seq_len[c.b]);
+      }
+    }
+    return c;
+  };
+  // lane l: block-table entry of page l/8 of the step (entries past the sequence repeat its
+  // last page; ids are range-checked where they are used)
+  auto load_bt = [&](const StreamCursor& c) -> int {
+    const int npg = (c.L + P - 1) / P;
+    const int i = min(c.ls * STEP + (lane >> 3), npg - 1);
+    return block_tables[int64_t(c.b) * bt_stride + i];
+  };
+  auto page_ok = [&](int p) -> int64_t {
+    return (p < 0 || int64_t(p) >= num_pages) ? 0 : int64_t(p);
+  };
+  // q rows of a segment: lane l < 16G holds q[g][8pp .. 8pp+7], g = l/16, pp = l%16 (four dword
+  // loads: q is only 4-byte aligned); staged as the (d, d+4) pairs of row-pair pp.
+  auto load_q = [&](const StreamCursor& c) -> uint4 {
+    uint4 r = make_uint4(0u, 0u, 0u, 0u);
+    if (lane < 16 * G) {
+      const uint32_t* qw = reinterpret_cast<const uint32_t*>(
+          q + int64_t(c.b) * q_seq_stride + int64_t(c.h) * G * D + (lane >> 4) * D +
+          8 * (lane & 15));
+      r = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+    }
+    return r;
+  };
+  auto stage_q = [&](const uint4 wq) {
+    if (lane < 16 * G) {
+      const int g = lane >> 4, pp = lane & 15;
+      q_lds[0][pp][g] = pack_lo(wq.x, wq.z);
+      q_lds[1][pp][g] = pack_hi(wq.x, wq.z);
+      q_lds[2][pp][g] = pack_lo(wq.y, wq.w);
+      q_lds[3][pp][g] = pack_hi(wq.y, wq.w);
+    }
+  };
 
   const int dsub = lane & 3, vhalf = lane & 1;
-  const uint16_t* head_k = kpool + int64_t(h) * TILE + dsub * P + ((lane >> 2) & 1) * 8;
-  const uint16_t* head_v = vpool + int64_t(h) * TILE + lane * 8;
   const int64_t page_stride = int64_t(Hkv) * TILE;
+  const uint16_t* kbase = kpool + dsub * P + ((lane >> 2) & 1) * 8;
+  const uint16_t* vbase = vpool + lane * 8;
 
   float m[G], lsum[G], acc[4][G];
 #pragma unroll
@@ -428,16 +533,23 @@ __global__ __launch_bounds__(64, 2) void paged_decode_pipelined(
     for (int j = 0; j < 4; ++j) acc[j][g] = 0.f;
   }
 
+  int gs = start;
+  StreamCursor cur = seg_of(gs);
+  int bt_cur;
   // Two 16 KiB register buffers whose role rotates through a step:
   //   A: K rows 0..63 -> V pages 0..3 -> next step's K rows 0..63
   //   B: K rows 64..127 -> V pages 4..7 -> next step's K rows 64..127
   uint4 bufA[16], bufB[16];
   {
-    const uint16_t* kp = head_k + int64_t(__shfl(phys, lane >> 3, 64)) * page_stride;
+    const uint4 q0 = load_q(cur);
+    bt_cur = load_bt(cur);
+    const uint16_t* kp = kbase + int64_t(cur.h) * TILE + page_ok(bt_cur) * page_stride;
 #pragma unroll
     for (int i = 0; i < 16; ++i) bufA[i] = load16_nt(kp + 64 * i);
 #pragma unroll
     for (int i = 0; i < 16; ++i) bufB[i] = load16_nt(kp + 64 * (16 + i));
+    stage_q(q0);
+    __syncthreads();
   }
 
   auto qk_rows = [&](const uint4 (&kr)[16], int pp0, float (&sacc)[8][G]) {
@@ -459,30 +571,30 @@ __global__ __launch_bounds__(64, 2) void paged_decode_pipelined(
     }
   };
 
-  // V of pages pg0..pg0+3 of step s; vr[4*pg + j] holds rows d = 32j + lane/2 of page pg.
-  auto load_v = [&](uint4 (&vr)[16], int s, int pg0) {
+  // V of pages pg0..pg0+3 of the step; vr[4*pg + j] holds rows d = 32j + lane/2 of page pg.
+  auto load_v = [&](uint4 (&vr)[16], const uint16_t* head_v, int bt, int pg0) {
 #pragma unroll
     for (int pg = 0; pg < 4; ++pg) {
-      const int vphys = __builtin_amdgcn_readlane(phys, s * STEP + pg0 + pg);
-      const uint16_t* vp = head_v + int64_t(vphys) * page_stride;
+      const int64_t vphys = page_ok(__builtin_amdgcn_readlane(bt, 8 * (pg0 + pg)));
+      const uint16_t* vp = head_v + vphys * page_stride;
 #pragma unroll
       for (int j = 0; j < 4; ++j) vr[4 * pg + j] = load16_nt(vp + 512 * j);
     }
   };
 
-  // Tokens at or past L (the partial last page, clamped re-reads after it) carry P = 0, but
-  // their stale V words may be non-finite: zero them before the PV products.
-  auto mask_tail = [&](uint4 (&vr)[16], int page0, int pg0) {
+  // Tokens at or past the step's valid count (partial last page, re-read pages after it) carry
+  // P = 0, but their stale V words may be non-finite: zero them before the PV products.
+  auto mask_tail = [&](uint4 (&vr)[16], int pg0, int valid) {
 #pragma unroll
     for (int pgi = 0; pgi < 4; ++pgi) {
-      const int nvalid = L - ((page0 + pg0 + pgi) * P + vhalf * 8);
+      const int nvalid = valid - ((pg0 + pgi) * P + vhalf * 8);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        uint4& w = vr[4 * pgi + j];
-        w.x = mask_pair(w.x, 0, nvalid);
-        w.y = mask_pair(w.y, 2, nvalid);
-        w.z = mask_pair(w.z, 4, nvalid);
-        w.w = mask_pair(w.w, 6, nvalid);
+        uint4& wv = vr[4 * pgi + j];
+        wv.x = mask_pair(wv.x, 0, nvalid);
+        wv.y = mask_pair(wv.y, 2, nvalid);
+        wv.z = mask_pair(wv.z, 4, nvalid);
+        wv.w = mask_pair(wv.w, 6, nvalid);
       }
     }
   };
@@ -502,25 +614,30 @@ __global__ __launch_bounds__(64, 2) void paged_decode_pipelined(
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const uint4 w = vr[4 * pgi + j];
+          const uint4 wv = vr[4 * pgi + j];
           float a = acc[j][g];
-          a = dot2_bf16(w.x, pr[0][g], a);
-          a = dot2_bf16(w.y, pr[1][g], a);
-          a = dot2_bf16(w.z, pr[2][g], a);
-          a = dot2_bf16(w.w, pr[3][g], a);
+          a = dot2_bf16(wv.x, pr[0][g], a);
+          a = dot2_bf16(wv.y, pr[1][g], a);
+          a = dot2_bf16(wv.z, pr[2][g], a);
+          a = dot2_bf16(wv.w, pr[3][g], a);
           acc[j][g] = a;
         }
     }
   };
 
-  // Steps 0..nsteps-2 are full pages below L and prefetch the next step's K; the last step
-  // prefetches nothing and masks the tokens at or past L. Both are straight-line code
-  // (compile-time variants): a runtime branch around the prefetch or the mask makes the
-  // register allocator keep extra copies of the tile buffers.
-  auto run_step = [&](int s, auto last) {
-    constexpr bool more = !decltype(last)::value;
-    constexpr bool tail = decltype(last)::value;
-    const int page0 = pbase + s * STEP;
+  for (;;) {
+    const bool has_next = gs + 1 < end;
+    // The next step's block-table row and (when it opens a segment) q go out first, ahead of
+    // this step's V loads, so they have landed by the time they are consumed. At the end of
+    // the range the "next" step repeats the current one (its K prefetch is never used).
+    const StreamCursor nxt = has_next ? next_of(cur) : cur;
+    const bool nxt_opens = has_next && nxt.ls == 0;
+    const int bt_nxt = load_bt(nxt);
+    uint4 q_nxt = make_uint4(0u, 0u, 0u, 0u);
+    if (nxt_opens) q_nxt = load_q(nxt);
+    const int valid = min(SD_STEP_TOKENS, cur.L - cur.ls * SD_STEP_TOKENS);
+    const uint16_t* head_v = vbase + int64_t(cur.h) * TILE;
+
     float sacc[8][G];
 #pragma unroll
     for (int t = 0; t < 8; ++t)
@@ -530,19 +647,18 @@ __global__ __launch_bounds__(64, 2) void paged_decode_pipelined(
     // most two groups (128 VGPRs) of tile data are live at any point.
     qk_rows(bufA, 0, sacc);
     __builtin_amdgcn_sched_barrier(0);
-    load_v(bufA, s, 0);
+    load_v(bufA, head_v, bt_cur, 0);
     __builtin_amdgcn_sched_barrier(0);
     qk_rows(bufB, 8, sacc);
     // quad reduce-scatter: lane l ends with the scores of tokens 2l, 2l+1 of the step
     float sc[2][G];
     quad_reduce_scatter<G>(sacc, sc, lane);
-    const int tok0 = page0 * P + 2 * lane;
+    const int tok0 = 2 * lane;
     uint32_t pw[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float s0 = sc[0][g], s1 = sc[1][g];
-      const float x0 = tok0 < L ? s0 * scale_log2 : -INFINITY;
-      const float x1 = tok0 + 1 < L ? s1 * scale_log2 : -INFINITY;
+      const float x0 = tok0 < valid ? sc[0][g] * scale_log2 : -INFINITY;
+      const float x1 = tok0 + 1 < valid ? sc[1][g] * scale_log2 : -INFINITY;
       const float mnew = fmaxf(m[g], wave_max_dpp(fmaxf(x0, x1)));
       const float alpha = fast_exp2(m[g] - mnew);
       const float p0 = fast_exp2(x0 - mnew), p1 = fast_exp2(x1 - mnew);
@@ -557,72 +673,125 @@ __global__ __launch_bounds__(64, 2) void paged_decode_pipelined(
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    load_v(bufB, s, 4);
+    load_v(bufB, head_v, bt_cur, 4);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (tail) mask_tail(bufA, page0, 0);
-    pv_pages(bufA, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    const uint16_t* kp = head_k;
-    if constexpr (more) {
-      kp += int64_t(__shfl(phys, (s + 1) * STEP + (lane >> 3), 64)) * page_stride;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) bufA[i] = load16_nt(kp + 64 * i);
+    if (valid < SD_STEP_TOKENS) {
+      mask_tail(bufA, 0, valid);
+      pv_pages(bufA, 0);
+    } else {
+      pv_pages(bufA, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (tail) mask_tail(bufB, page0, 4);
-    pv_pages(bufB, 4);
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (more) {
+    const uint16_t* kp = kbase + int64_t(nxt.h) * TILE + page_ok(bt_nxt) * page_stride;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) bufB[i] = load16_nt(kp + 64 * (16 + i));
+    for (int i = 0; i < 16; ++i) bufA[i] = load16_nt(kp + 64 * i);
+    __builtin_amdgcn_sched_barrier(0);
+    if (valid < SD_STEP_TOKENS) {
+      mask_tail(bufB, 4, valid);
+      pv_pages(bufB, 4);
+    } else {
+      pv_pages(bufB, 4);
     }
-    // the next step overwrites p_lds: keep this step's reads ahead of those writes
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) bufB[i] = load16_nt(kp + 64 * (16 + i));
+    // the next step overwrites p_lds (and maybe q_lds): keep this step's reads ahead of them
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
-  };
 
-  for (int s = 0; s + 1 < nsteps; ++s) run_step(s, std::false_type{});
-  run_step(nsteps - 1, std::true_type{});
-
+    const bool seg_last = cur.ls == cur.ns - 1;
+    if (seg_last || !has_next) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int g = 0; g < G; ++g) acc[j][g] += dpp_f32<kDppQuadXor1>(acc[j][g]);
+        for (int g = 0; g < G; ++g) acc[j][g] += dpp_f32<kDppQuadXor1>(acc[j][g]);
 #pragma unroll
-  for (int g = 0; g < G; ++g) lsum[g] = wave_sum_dpp(lsum[g]);
-
-  if ((lane & 1) == 0) {
+      for (int g = 0; g < G; ++g) lsum[g] = wave_sum_dpp(lsum[g]);
+      const int seg_first = gs - cur.ls;  // global index of the segment's first step
+      const int64_t row0 = int64_t(cur.b) * Hq + int64_t(cur.h) * G;
+      if (seg_last && seg_first >= start) {
+        if ((lane & 1) == 0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int64_t row = row0 + g;
+          for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d = 32 * j + (lane >> 1);
-        if (n_parts == 1)
-          out[row * D + d] = f32_to_bf16(acc[j][g] / lsum[g]);
-        else
-          ws_acc[(row * max_parts + part) * D + d] = acc[j][g];
+            for (int j = 0; j < 4; ++j)
+              out[(row0 + g) * D + 32 * j + (lane >> 1)] = f32_to_bf16(acc[j][g] / lsum[g]);
+        }
+      } else {
+        float* part = ws_part + (int64_t(w) * 2 + (seg_first < start ? 0 : 1)) * G * (D + 2);
+        if ((lane & 1) == 0) {
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) part[g * (D + 2) + 32 * j + (lane >> 1)] = acc[j][g];
+        }
+        if (lane == 0) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            part[g * (D + 2) + D] = m[g];
+            part[g * (D + 2) + D + 1] = lsum[g];
+          }
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        m[g] = kNegBig;
+        lsum[g] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j][g] = 0.f;
       }
     }
+    if (!has_next) break;
+    if (nxt_opens) stage_q(q_nxt);
+    cur = nxt;
+    bt_cur = bt_nxt;
+    ++gs;
   }
-  if (n_parts > 1 && lane == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int64_t slot = (row0 + g) * max_parts + part;
-      ws_ml[slot * 2 + 0] = m[g];
-      ws_ml[slot * 2 + 1] = lsum[g];
-    }
+}
+
+// Merge the partials of segments that cross a wave-range boundary (and zero the output of
+// empty sequences). One 128-thread block per (q head, sequence).
+__global__ __launch_bounds__(FD_D) void paged_decode_stream_reduce(
+    uint16_t* __restrict__ out, const float* __restrict__ ws_part,
+    const int32_t* __restrict__ ws_meta, const int32_t* __restrict__ context_lens,
+    int64_t bt_stride, int B, int Hkv, int G) {
+  constexpr int D = FD_D;
+  const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int64_t row = int64_t(b) * Hkv * G + hq;
+  if (clamp_len(context_lens[b], bt_stride, FD_P) == 0) {
+    out[row * D + d] = 0;
+    return;
   }
+  const int C = ws_meta[B + 1];
+  const int q0 = ws_meta[b], ns = ws_meta[b + 1] - q0;
+  const int h = hq / G, g = hq - h * G;
+  const int s0 = Hkv * q0 + h * ns;
+  const int c0 = s0 / C, c1 = (s0 + ns - 1) / C;
+  if (c0 == c1) return;  // finished inside one wave's range
+  auto part = [&](int c) {
+    return ws_part + (int64_t(c) * 2 + (c == c0 ? 1 : 0)) * G * (D + 2) + g * (D + 2);
+  };
+  float M = kNegBig;
+  for (int c = c0; c <= c1; ++c) M = fmaxf(M, part(c)[D]);
+  float o = 0.f, lt = 0.f;
+  for (int c = c0; c <= c1; ++c) {
+    const float* pp = part(c);
+    const float f = fast_exp2(pp[D] - M);
+    lt += f * pp[D + 1];
+    o += f * pp[d];
+  }
+  out[row * D + d] = f32_to_bf16(o / lt);
 }
 
 // Merge the partition partials of sequences with more than one partition.
 __global__ __launch_bounds__(FD_D) void paged_decode_reduce(
     uint16_t* __restrict__ out, const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
-    const int32_t* __restrict__ context_lens, int64_t bt_stride, int Hq, int max_parts) {
+    const int32_t* __restrict__ context_lens, int64_t bt_stride, int Hq, int max_parts,
+    int part_pages) {
   constexpr int D = FD_D, P = FD_P;
   const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int L = clamp_len(context_lens[b], bt_stride, P);
-  const int n_parts = ((L + P - 1) / P + FD_PART_PAGES - 1) / FD_PART_PAGES;
+  const int n_parts = ((L + P - 1) / P + part_pages - 1) / part_pages;
   if (n_parts <= 1) return;
   const int64_t row = int64_t(b) * Hq + hq;
   const float* ml = ws_ml + row * max_parts * 2;
@@ -785,19 +954,41 @@ bool fast_path(int dtype, int Hq, int Hkv, int D, int P) {
          (G == 1 || G == 2 || G == 4 || G == 8);
 }
 
-int64_t fast_max_parts(int64_t bt_stride) { return ceil_div(bt_stride, FD_PART_PAGES); }
+// Waves of a stream launch: every CU at two single-wave workgroups per SIMD (CU count cached
+// per device), capped by the partial slots the workspace holds.
+int stream_waves() {
+  static std::atomic<int> cus_of[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int cus = cus_of[dev].load(std::memory_order_relaxed);
+  if (cus <= 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cus_of[dev].store(cus, std::memory_order_relaxed);
+  }
+  return std::min(cus * SD_WAVES_PER_CU, SD_MAX_WAVES);
+}
 
 }  // namespace
 }  // namespace pia
 
 using namespace pia;
 
-extern "C" int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim,
-                                                    int page_size, int64_t bt_stride) {
-  if (head_dim != FD_D || page_size != FD_P || num_seqs <= 0 || num_heads <= 0 || bt_stride <= 0)
+extern "C" int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_heads,
+                                                    int head_dim, int page_size,
+                                                    int64_t bt_stride) {
+  if (head_dim != FD_D || page_size != FD_P || num_seqs <= 0 || num_heads <= 0 ||
+      num_kv_heads <= 0 || num_heads % num_kv_heads || bt_stride <= 0)
     return 0;
-  return int64_t(num_seqs) * num_heads * fast_max_parts(bt_stride) * (FD_D + 2) *
-         int64_t(sizeof(float));
+  const int G = num_heads / num_kv_heads;
+  if (G == 8)  // partition partials: (acc[128], max, sum) per (sequence, q head, partition)
+    return int64_t(num_seqs) * num_heads * ceil_div(bt_stride, FD_PART_PAGES) * (FD_D + 2) *
+           int64_t(sizeof(float));
+  if (G == 1 || G == 2 || G == 4)  // two partial slots per wave + the step-prefix table
+    return int64_t(SD_MAX_WAVES) * 2 * G * (FD_D + 2) * int64_t(sizeof(float)) +
+           int64_t(SD_META_INTS) * int64_t(sizeof(int32_t));
+  return 0;
 }
 
 extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_seq_stride,
@@ -821,38 +1012,67 @@ extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_se
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = as_stream(stream);
   if (fast_path(dtype, num_heads, num_kv_heads, head_dim, page_size)) {
-    const int64_t need = pia_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim,
-                                                          page_size, bt_stride);
+    const int64_t need = pia_paged_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads,
+                                                          head_dim, page_size, bt_stride);
     if (!workspace || workspace_bytes < need) {
       set_error("paged_decode: workspace of %lld bytes needed, %lld given", (long long)need,
                 (long long)workspace_bytes);
       return PIA_EINVAL;
     }
-    if (!aligned(q, 4) || !aligned(k_pages, 16) || !aligned(v_pages, 16) || (q_seq_stride & 1))
-      return fail(PIA_EINVAL, "paged_decode: q must be 4-byte and pools 16-byte aligned");
-    const int max_parts = int(fast_max_parts(bt_stride));
-    float* ws_acc = reinterpret_cast<float*>(workspace);
-    float* ws_ml = ws_acc + int64_t(num_seqs) * num_heads * max_parts * FD_D;
+    if (!aligned(q, 4) || !aligned(k_pages, 16) || !aligned(v_pages, 16) ||
+        !aligned(workspace, 4) || (q_seq_stride & 1))
+      return fail(PIA_EINVAL, "paged_decode: q and workspace must be 4-byte and pools "
+                              "16-byte aligned");
     const int G = num_heads / num_kv_heads;
-    dim3 grid = dim3(unsigned(max_parts), unsigned(num_kv_heads), unsigned(num_seqs));
-#define PIA_FD(KERNEL, GG, THREADS)                                                            \
-  hipLaunchKernelGGL((KERNEL<GG>), grid, dim3(THREADS), 0, s, (uint16_t*)out,                  \
-                     (const uint16_t*)q, q_seq_stride, (const uint16_t*)k_pages,               \
-                     (const uint16_t*)v_pages, block_tables, bt_stride, context_lens, ws_acc,  \
-                     ws_ml, num_kv_heads, num_pages, max_parts, scale_log2)
-    switch (G) {
-      case 1: PIA_FD(paged_decode_pipelined, 1, 64); break;
-      case 2: PIA_FD(paged_decode_pipelined, 2, 64); break;
-      case 4: PIA_FD(paged_decode_pipelined, 4, 64); break;
-      default: PIA_FD(paged_decode_bf16_d128p16, 8, 256); break;
+    if (G == 8) {
+      const int max_parts = int(ceil_div(bt_stride, FD_PART_PAGES));
+      float* ws_acc = reinterpret_cast<float*>(workspace);
+      float* ws_ml = ws_acc + int64_t(num_seqs) * num_heads * max_parts * FD_D;
+      dim3 grid = dim3(unsigned(max_parts), unsigned(num_kv_heads), unsigned(num_seqs));
+      hipLaunchKernelGGL((paged_decode_bf16_d128p16<8>), grid, dim3(256), 0, s, (uint16_t*)out,
+                         (const uint16_t*)q, q_seq_stride, (const uint16_t*)k_pages,
+                         (const uint16_t*)v_pages, block_tables, bt_stride, context_lens, ws_acc,
+                         ws_ml, num_kv_heads, num_pages, max_parts, scale_log2);
+      if (int rc = check_launch("paged_decode")) return rc;
+      if (max_parts > 1) {
+        hipLaunchKernelGGL(paged_decode_reduce, dim3(unsigned(num_heads), unsigned(num_seqs)),
+                           dim3(FD_D), 0, s, (uint16_t*)out, ws_acc, ws_ml, context_lens,
+                           bt_stride, num_heads, max_parts, int(FD_PART_PAGES));
+        if (int rc = check_launch("paged_decode_reduce")) return rc;
+      }
+      return 0;
     }
-#undef PIA_FD
-    if (int rc = check_launch("paged_decode_bf16_d128p16")) return rc;
-    if (max_parts > 1) {
-      hipLaunchKernelGGL(paged_decode_reduce, dim3(unsigned(num_heads), unsigned(num_seqs)),
-                         dim3(FD_D), 0, s, (uint16_t*)out, ws_acc, ws_ml, context_lens,
-                         bt_stride, num_heads, max_parts);
-      if (int rc = check_launch("paged_decode_reduce")) return rc;
+    // Stream kernel, in launches of up to SD_MAX_SEQS sequences. Its step arithmetic is int32:
+    // Hkv * (sequences) * (steps per sequence) plus a wave count must stay below 2^31.
+    const int NW = stream_waves();
+    if (int64_t(num_kv_heads) * std::min(num_seqs, SD_MAX_SEQS) * ceil_div(bt_stride, 8) +
+            2 * int64_t(NW) >= (int64_t(1) << 31))
+      return fail(PIA_EUNSUPPORTED, "paged_decode: batch too large for int32 step indices");
+    float* ws_part = reinterpret_cast<float*>(workspace);
+    int32_t* ws_meta =
+        reinterpret_cast<int32_t*>(ws_part + int64_t(SD_MAX_WAVES) * 2 * G * (FD_D + 2));
+    for (int b0 = 0; b0 < num_seqs; b0 += SD_MAX_SEQS) {
+      const int Bs = std::min(SD_MAX_SEQS, num_seqs - b0);
+      uint16_t* o = reinterpret_cast<uint16_t*>(out) + int64_t(b0) * num_heads * FD_D;
+      const uint16_t* qq = reinterpret_cast<const uint16_t*>(q) + int64_t(b0) * q_seq_stride;
+      const int32_t* bt = block_tables + int64_t(b0) * bt_stride;
+      const int32_t* cl = context_lens + b0;
+      const size_t lds = size_t(2 * Bs + 1) * sizeof(int32_t);
+#define PIA_SD(GG)                                                                             \
+  hipLaunchKernelGGL((paged_decode_stream<GG>), dim3(unsigned(NW)), dim3(64), lds, s, o, qq,   \
+                     q_seq_stride, (const uint16_t*)k_pages, (const uint16_t*)v_pages, bt,     \
+                     bt_stride, cl, Bs, num_kv_heads, num_pages, ws_part, ws_meta, scale_log2)
+      switch (G) {
+        case 1: PIA_SD(1); break;
+        case 2: PIA_SD(2); break;
+        default: PIA_SD(4); break;
+      }
+#undef PIA_SD
+      if (int rc = check_launch("paged_decode_stream")) return rc;
+      hipLaunchKernelGGL(paged_decode_stream_reduce, dim3(unsigned(num_heads), unsigned(Bs)),
+                         dim3(FD_D), 0, s, o, ws_part, ws_meta, cl, bt_stride, Bs, num_kv_heads,
+                         G);
+      if (int rc = check_launch("paged_decode_stream_reduce")) return rc;
     }
     return 0;
   }

@@ -30,7 +30,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_kv_scatter": (_I, [_P, _P, _P, _P, _P, _L, _L, _L, _I, _I, _I, _L, _I, _P]),
     "pia_kv_gather": (_I, [_P, _P, _P, _P, _P, _L, _P, _I, _L, _I, _I, _I, _L, _I, _P]),
     "pia_kv_pages_chunk_copy": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _L, _I, _I, _P]),
-    "pia_paged_decode_workspace_bytes": (_L, [_I, _I, _I, _I, _L]),
+    "pia_paged_decode_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _L]),
     "pia_paged_decode_attention": (
         _I, [_P, _P, _L, _P, _P, _P, _L, _P, _I, _I, _I, _I, _I, _L, _F, _I, _P, _L, _P]),
     "pia_paged_attention": (
@@ -47,7 +47,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_copy_rows_async": (_I, [_P, _P, _P, _P, _L, _L, _P, _P]),
 }
 
-EXPECTED_ABI = 1
+EXPECTED_ABI = 2
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

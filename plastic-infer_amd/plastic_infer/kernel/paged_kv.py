@@ -102,11 +102,11 @@ def kv_gather(k_pages: torch.Tensor, v_pages: torch.Tensor, block_tables: torch.
     return k_out, v_out
 
 
-def decode_workspace_bytes(num_seqs: int, num_heads: int, head_dim: int, page_size: int,
-                           max_pages_per_seq: int) -> int:
+def decode_workspace_bytes(num_seqs: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                           page_size: int, max_pages_per_seq: int) -> int:
     """Scratch bytes paged_decode_attention needs for these shapes (0 if none)."""
-    return N.query("pia_paged_decode_workspace_bytes", num_seqs, num_heads, head_dim, page_size,
-                   max_pages_per_seq)
+    return N.query("pia_paged_decode_workspace_bytes", num_seqs, num_heads, num_kv_heads,
+                   head_dim, page_size, max_pages_per_seq)
 
 
 def paged_decode_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
@@ -139,7 +139,7 @@ def paged_decode_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torc
         raise ValueError("out must be a contiguous [B, Hq, D] tensor of q's dtype")
     if B == 0:
         return out
-    need = decode_workspace_bytes(B, Hq, D, P, block_tables.shape[1])
+    need = decode_workspace_bytes(B, Hq, Hkv, D, P, block_tables.shape[1])
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     scale = (1.0 / math.sqrt(D)) if scale is None else float(scale)

@@ -19,7 +19,12 @@ from plastic_infer.exec.attention import (
     host_stream_attention_v1,
     paged_attention_v1,
 )
-from plastic_infer.kernel import kv_scatter, paged_attention, paged_decode_attention
+from plastic_infer.kernel import (
+    decode_workspace_bytes,
+    kv_scatter,
+    paged_attention,
+    paged_decode_attention,
+)
 from test_oracle_paged import brute_attention
 
 pytestmark = pytest.mark.gpu
@@ -70,6 +75,62 @@ def test_decode_group_sizes_and_lengths(dev, G):
     got = _run_decode_step(wl, dev)
     ref = _oracle_decode_step(wl)
     err = (got.float() - ref.float()).abs().max().item()
+    assert err <= BF16_TOL, err
+
+
+def _decode_case(seed: int, lens: list[int], Hq: int, Hkv: int, num_pages: int):
+    """Random pools and tables for the given context lengths (pages drawn without reuse)."""
+    g = torch.Generator().manual_seed(seed)
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    n_pages = (lens_t + 15) // 16
+    max_pages = max(1, int(n_pages.max()))
+    perm = torch.randperm(num_pages, generator=g)
+    bt = torch.full((len(lens), max_pages), -1, dtype=torch.int32)  # unused entries invalid
+    off = 0
+    for b, n in enumerate(n_pages.tolist()):
+        bt[b, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    kp = torch.randn(num_pages, Hkv, 128, 16, generator=g).to(torch.bfloat16)
+    vp = torch.randn(num_pages, Hkv, 128, 16, generator=g).to(torch.bfloat16)
+    q = torch.randn(len(lens), Hq, 128, generator=g).to(torch.bfloat16)
+    return q, kp, vp, bt, lens_t
+
+
+@pytest.mark.parametrize("G,lens", [
+    (4, [8192]),                 # one segment per kv head, cut into one-step wave ranges
+    (1, [8191, 3]),
+    (2, [0, 4097, 0, 129, 0]),   # empty sequences between and around long ones
+])
+def test_decode_stream_few_long_sequences(dev, G, lens):
+    """Few long sequences: every segment is split across many waves and merged from partials."""
+    Hkv = 8
+    q, kp, vp, bt, lens_t = _decode_case(40 + G, lens, Hkv * G, Hkv, 1100)
+    out = paged_decode_attention(q.to(dev), kp.to(dev), vp.to(dev), bt.to(dev),
+                                 lens_t.to(dev)).cpu()
+    live = lens_t > 0
+    assert not out[~live].any()
+    ref = OP.decode_batch(q[live], kp, vp, bt[live].clamp(min=0), lens_t[live], 16)
+    err = (out[live].float() - ref.float()).abs().max().item()
+    assert err <= BF16_TOL, err
+
+
+def test_decode_stream_batch_over_one_launch(dev):
+    """1100 sequences (more than one launch's 1024), a third of them empty, short lengths."""
+    g = torch.Generator().manual_seed(44)
+    lens = torch.randint(1, 300, (1100,), generator=g)
+    lens[torch.randperm(1100, generator=g)[:370]] = 0
+    q, kp, vp, bt, lens_t = _decode_case(45, lens.tolist(), 8, 2, 14000)
+    ws_dev = torch.empty(decode_workspace_bytes(1100, 8, 2, 128, 16, bt.shape[1]),
+                         dtype=torch.uint8, device=dev)
+    outs = []
+    for _ in range(2):   # the same workspace twice in a row
+        outs.append(paged_decode_attention(q.to(dev), kp.to(dev), vp.to(dev), bt.to(dev),
+                                           lens_t.to(dev), workspace=ws_dev).cpu())
+    assert torch.equal(outs[0], outs[1])
+    live = lens_t > 0
+    assert not outs[0][~live].any()
+    ref = OP.decode_batch(q[live], kp, vp, bt[live].clamp(min=0), lens_t[live], 16)
+    err = (outs[0][live].float() - ref.float()).abs().max().item()
     assert err <= BF16_TOL, err
 
 

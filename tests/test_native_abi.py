@@ -51,8 +51,17 @@ def test_invalid_arguments_are_rejected_without_device_work():
     assert rc == -1 and b"num_heads % num_kv_heads" in lib.pia_last_error()
     rc = lib.pia_moe_topk(None, None, None, 0, 4, 8, 9, 1, 0, -1, None)
     assert rc == -1
-    assert N.query("pia_paged_decode_workspace_bytes", 256, 32, 128, 16, 512) == \
-        256 * 32 * 16 * 130 * 4
-    assert N.query("pia_paged_decode_workspace_bytes", 4, 4, 64, 16, 8) == 0
+    # G = 4: two partial slots (128 accumulators + max + sum, fp32) per wave for up to 4096
+    # waves, plus the step-prefix table (1024 sequences + 4 ints); independent of the batch
+    assert N.query("pia_paged_decode_workspace_bytes", 256, 32, 8, 128, 16, 512) == \
+        4096 * 2 * 4 * 130 * 4 + 1028 * 4
+    assert N.query("pia_paged_decode_workspace_bytes", 1, 32, 8, 128, 16, 4) == \
+        4096 * 2 * 4 * 130 * 4 + 1028 * 4
+    # G = 8: one partial per (sequence, q head, 32-page partition)
+    assert N.query("pia_paged_decode_workspace_bytes", 256, 64, 8, 128, 16, 512) == \
+        256 * 64 * 16 * 130 * 4
+    # general kernel (head_dim 64, or G = 3): no workspace
+    assert N.query("pia_paged_decode_workspace_bytes", 4, 4, 4, 64, 16, 8) == 0
+    assert N.query("pia_paged_decode_workspace_bytes", 4, 24, 8, 128, 16, 8) == 0
     with pytest.raises(N.NativeError):
         N.call("pia_moe_sum_reduce", None, None, 1, 0, 4, 2, None)
