@@ -13,6 +13,8 @@ with HIP events on the launch stream) and the CPU baseline (the oracle's restate
 reference torch path on this host's cores, on a bounded sample of the same inputs).
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-sample-seqs S] [--no-cpu-baseline]
+  python bench.py --calibrate-copy     # 1 GiB read + 1 GiB write elementwise copy, three times:
+                                       # the known-size reference for HBM byte counters
 """
 
 from __future__ import annotations
@@ -148,6 +150,20 @@ def cpu_baseline(torch, inp, n_seqs):
     }
 
 
+def calibrate_copy(torch, dev) -> int:
+    """A plain elementwise copy of known size (2^30 bytes read, 2^30 written per launch) for
+    scaling FETCH_SIZE / WRITE_SIZE readings of the attention kernel to bytes."""
+    n = (1 << 30) // 2
+    src = torch.ones(n, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize(dev)
+    print(json.dumps({"calibration": "elementwise copy", "bytes_read": 1 << 30,
+                      "bytes_written": 1 << 30, "launches": 3}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -155,6 +171,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-sample-seqs", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the paged decode path on ONE GPU (per-GPU shard of a "
@@ -168,6 +185,8 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        return calibrate_copy(torch, dev)
     print(f"bench: generating inputs (B={B}, pool={NUM_PAGES} pages)", file=sys.stderr, flush=True)
     inp = build_inputs(torch, dev)
     out = torch.empty(B, HQ, D, dtype=torch.bfloat16, device=dev)
