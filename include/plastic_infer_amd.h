@@ -247,6 +247,54 @@ int pia_copy_rows_async(void* dst, const int64_t* dst_rows, const void* src,
                         const int64_t* src_rows, int64_t n, int64_t row_bytes,
                         int64_t* copies_issued, void* stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * (a15) Device-side LRU admission of a slot cache (lru_ensure, reference
+ * src/plastic_infer/kernel/lru_ensure.py:371-438, victim rule of its sequential kernel
+ * :200-265; MoE use src/plastic_infer/moe/offload_kernels.py:19-40). Device arrays:
+ *   slot_of_id [num_total] i32 (id -> slot or -1), id_of_slot [num_cached] i32 (-1 = empty),
+ *   lru_usage [num_cached] i64, lru_step [] i64 (+1 per call).
+ * query [num_queries] i32 ids (+ id_base = global id); duplicates collapse to one slot. Hits
+ * get usage = step. The distinct missing ids, ascending, take the evictable slots (usage !=
+ * step) in ascending (usage, slot) order; the previous owner of each victim is unmapped.
+ * out_indices[i] = slot of query i (may alias query); src_indices[j] = id - id_base and
+ * dst_indices[j] = slot for j < *num_copy (the copy plan); stats (NULL or i64[3]) +=
+ * (distinct ids, admitted misses, 1). Ids outside [0, num_total) are inert (out = -1). Misses
+ * beyond the evictable slots are not admitted (out = -1); the reference leaves that case
+ * undefined. Limits: num_queries <= 2048, 1 <= num_cached <= 16384.
+ * ------------------------------------------------------------------------------------------- */
+int pia_lru_ensure(const int32_t* query, int64_t num_queries, int32_t* slot_of_id,
+                   int64_t num_total, int32_t* id_of_slot, int64_t* lru_usage,
+                   int64_t num_cached, int64_t* lru_step, int32_t* out_indices,
+                   int32_t* src_indices, int32_t* dst_indices, int64_t* num_copy,
+                   int64_t* stats, int64_t id_base, void* stream);
+
+/* (a13) Slot-cache bookkeeping of OffloadMoeCache (reference
+ * src/plastic_infer/moe/offload_kernels.py:208-285, offload_cache.py:597-605):
+ *   reset       every id non-resident, every slot empty with usage 0, step = 0, active_mask
+ *               (NULL or i32[num_experts]) = 0, *num_indices = 0 (when non-NULL);
+ *   materialize partition layer_id's E ids into slots [0, E) in id order (owners of those
+ *               slots from other partitions unmapped, this partition's copies elsewhere
+ *               emptied), usage = ++step, plan = (src e -> slot e) for e < E, *num_indices = E;
+ *   invalidate  slots [slot_begin, slot_end) emptied: owners unmapped, usage 0. */
+int pia_slot_cache_reset(int32_t* slot_of_id, int64_t num_total, int32_t* id_of_slot,
+                         int64_t* usage, int64_t num_cached, int64_t* step, int32_t* active_mask,
+                         int num_experts, int64_t* num_indices, void* stream);
+int pia_slot_cache_materialize(int32_t* slot_of_id, int64_t num_total, int32_t* id_of_slot,
+                               int64_t* usage, int64_t num_cached, int64_t* step,
+                               int32_t* evict_slots, int32_t* src_indices, int64_t* num_indices,
+                               int layer_id, int num_experts, void* stream);
+int pia_slot_cache_invalidate(int32_t* slot_of_id, int64_t num_total, int32_t* id_of_slot,
+                              int64_t* usage, int64_t num_cached, int64_t slot_begin,
+                              int64_t slot_end, void* stream);
+
+/* (a16) Prefill hit compaction (prefill_hit_compact, reference
+ * src/plastic_infer/moe/offload_kernels.py:63-82,413-431): experts e < num_experts whose slot
+ * slot_row[e] >= threshold, in expert order: dst[j] = buffer_base + e, src[j] = slot_row[e];
+ * *num = count. */
+int pia_prefill_hit_compact(const int32_t* slot_row, int32_t* dst, int32_t* src, int64_t* num,
+                            int64_t buffer_base, int64_t threshold, int num_experts,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,397 @@
+// Device-side slot cache over an out-of-core table (the MoE expert cache): LRU admission and
+// the bookkeeping kernels around it. Only the maps and the copy plan are touched here; the
+// rows themselves move with the index-copy kernels of expert_copy.hip.
+//
+// Maps (all device memory, owned by the caller):
+//   slot_of_id [num_total]  int32  id -> slot, -1 when not resident
+//   id_of_slot [num_cached] int32  slot -> id, -1 when empty
+//   usage      [num_cached] int64  step at which each slot was last touched
+//   step       []           int64  monotonic clock, +1 per admission call
+// Ids are flat: a caller whose table is split (one partition per MoE layer) passes
+// partition-local ids with id_base = partition * partition_size.
+//
+// lru_ensure_kernel is one 1024-thread workgroup: admission is a small sequential decision
+// (a few hundred ids against a few thousand slots), so the whole state of a call lives in LDS
+// and every phase is a barrier-separated parallel pass:
+//   1. dedup the query, split hits and misses, rank the distinct misses by id, bump hits;
+//   2. victims: the evictable slots (not touched by this call) sorted by (usage, slot) with a
+//      bitonic sort of packed 64-bit keys in LDS;
+//   3. the i-th smallest missing id takes the i-th victim: maps, usage and the copy plan.
+#include <algorithm>
+
+#include "pia_internal.h"
+
+namespace pia {
+namespace {
+
+constexpr int LRU_THREADS = 1024;
+constexpr int LRU_MAX_QUERY = 2048;
+constexpr int LRU_MAX_CACHED = 16384;
+constexpr unsigned long long kKeyNone = ~0ull;  // sorts after every evictable slot
+
+__device__ __forceinline__ int block_sum(int v, int* red) {
+  // wave sums, then one wave over the 16 partials
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  int t = (threadIdx.x < LRU_THREADS / 64) ? red[threadIdx.x] : 0;
+  if (wave == 0) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+    if (lane == 0) red[LRU_THREADS / 64] = t;
+  }
+  __syncthreads();
+  return red[LRU_THREADS / 64];
+}
+
+__global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
+    const int32_t* __restrict__ query, int K, int32_t* __restrict__ slot_of_id,
+    int64_t num_total, int32_t* __restrict__ id_of_slot, int64_t* __restrict__ usage,
+    int C, int c_pad, int slot_bits, int64_t* __restrict__ step_ptr,
+    int32_t* __restrict__ out, int32_t* __restrict__ src_plan, int32_t* __restrict__ dst_plan,
+    int64_t* __restrict__ num_copy, int64_t* __restrict__ stats, int64_t id_base) {
+  __shared__ unsigned long long keys[LRU_MAX_CACHED];
+  __shared__ int32_t q_lds[LRU_MAX_QUERY];
+  __shared__ int32_t miss_ids[LRU_MAX_QUERY];
+  __shared__ uint8_t first_miss[LRU_MAX_QUERY];
+  __shared__ int red[LRU_THREADS / 64 + 1];
+  __shared__ int64_t step_lds;
+  const int tid = threadIdx.x;
+  constexpr int QPT = LRU_MAX_QUERY / LRU_THREADS;  // queries per thread
+
+  if (tid == 0) {
+    const int64_t s = *step_ptr + 1;
+    *step_ptr = s;
+    step_lds = s;
+  }
+  // Phase 1a: load the query (global ids; out-of-range ids are inert: never resident,
+  // never admitted, out = -1).
+  int32_t qi[QPT], si[QPT];
+#pragma unroll
+  for (int r = 0; r < QPT; ++r) {
+    const int i = tid + r * LRU_THREADS;
+    qi[r] = -1;
+    si[r] = -1;
+    if (i < K) {
+      const int64_t g = int64_t(query[i]) + id_base;
+      if (g >= 0 && g < num_total) {
+        qi[r] = int32_t(g);
+        si[r] = slot_of_id[g];
+        if (si[r] >= C) si[r] = -1;  // a map entry past the cache is not a hit
+      }
+      q_lds[i] = qi[r];
+    }
+  }
+  __syncthreads();
+  const int64_t step = step_lds;
+
+  // Phase 1b: first occurrences and the first misses among them; bump every hit slot.
+  int nfirst = 0, nfm = 0;
+#pragma unroll
+  for (int r = 0; r < QPT; ++r) {
+    const int i = tid + r * LRU_THREADS;
+    if (i >= K) continue;
+    bool first = qi[r] >= 0;
+    for (int j = 0; j < i && first; ++j) first = q_lds[j] != qi[r];
+    const bool fm = first && si[r] < 0;
+    first_miss[i] = fm ? 1 : 0;
+    nfirst += first ? 1 : 0;
+    nfm += fm ? 1 : 0;
+    if (si[r] >= 0) usage[si[r]] = step;  // duplicated hits store the same value
+  }
+  const int distinct = block_sum(nfirst, red);
+  const int M = block_sum(nfm, red);  // barriers inside also publish first_miss[]
+
+  // Phase 1c: rank of every missing position = number of distinct missing ids below it
+  // (a duplicate shares its first occurrence's rank); the distinct ones list their id.
+  int rank[QPT];
+#pragma unroll
+  for (int r = 0; r < QPT; ++r) {
+    const int i = tid + r * LRU_THREADS;
+    rank[r] = -1;
+    if (i >= K || qi[r] < 0 || si[r] >= 0) continue;
+    int rk = 0;
+    for (int j = 0; j < K; ++j) rk += (first_miss[j] && q_lds[j] < qi[r]) ? 1 : 0;
+    rank[r] = rk;
+    if (first_miss[i]) miss_ids[rk] = qi[r];
+  }
+  __syncthreads();  // also orders the hit bumps before the usage reload below
+
+  int admitted = 0;
+  if (M > 0) {
+    // Phase 2: packed (usage, slot) keys of evictable slots, ascending.
+    for (int c = tid; c < c_pad; c += LRU_THREADS) {
+      unsigned long long k = kKeyNone;
+      if (c < C) {
+        const int64_t u = usage[c];
+        if (u != step) k = (static_cast<unsigned long long>(u) << slot_bits) | unsigned(c);
+      }
+      keys[c] = k;
+    }
+    __syncthreads();
+    for (int size = 2; size <= c_pad; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int t = tid; t < c_pad / 2; t += LRU_THREADS) {
+          const int lo = 2 * t - (t & (stride - 1));
+          const int hi = lo + stride;
+          const bool up = (lo & size) == 0;
+          const unsigned long long a = keys[lo], b = keys[hi];
+          if ((a > b) == up) {
+            keys[lo] = b;
+            keys[hi] = a;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    // Misses beyond the evictable slots (a caller breaking |distinct(query)| <= cache size)
+    // are left unadmitted: out = -1 and no plan entry.
+    int nev = 0;
+    for (int c = tid; c < C; c += LRU_THREADS) nev += keys[c] != kKeyNone ? 1 : 0;
+    const int evictable = block_sum(nev, red);
+    admitted = min(M, evictable);
+
+    // Phase 3: install. Victims are distinct slots and the evicted ids (resident) never
+    // equal the admitted ones (not resident), so the map writes of different i never meet.
+    const unsigned long long slot_mask = (1ull << slot_bits) - 1;
+    for (int i = tid; i < admitted; i += LRU_THREADS) {
+      const int victim = int(keys[i] & slot_mask);
+      const int32_t e = miss_ids[i];
+      const int32_t old = id_of_slot[victim];
+      if (old >= 0 && old < num_total) slot_of_id[old] = -1;
+      id_of_slot[victim] = e;
+      slot_of_id[e] = victim;
+      usage[victim] = step;
+      dst_plan[i] = victim;
+      src_plan[i] = int32_t(int64_t(e) - id_base);
+    }
+  }
+  // out may alias query: every query read happened before the barriers above.
+  const unsigned long long slot_mask = (1ull << slot_bits) - 1;
+#pragma unroll
+  for (int r = 0; r < QPT; ++r) {
+    const int i = tid + r * LRU_THREADS;
+    if (i >= K) continue;
+    int32_t o = si[r];
+    if (rank[r] >= 0) o = rank[r] < admitted ? int32_t(keys[rank[r]] & slot_mask) : -1;
+    out[i] = o;
+  }
+  if (tid == 0) {
+    *num_copy = admitted;
+    if (stats) {
+      stats[0] += distinct;
+      stats[1] += admitted;
+      stats[2] += 1;
+    }
+  }
+}
+
+__global__ void slot_cache_reset_kernel(int32_t* __restrict__ slot_of_id, int64_t num_total,
+                                        int32_t* __restrict__ id_of_slot,
+                                        int64_t* __restrict__ usage, int64_t num_cached,
+                                        int64_t* __restrict__ step,
+                                        int32_t* __restrict__ active_mask, int num_experts,
+                                        int64_t* __restrict__ num_indices) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < std::max(num_total, num_cached); i += stride) {
+    if (i < num_total) slot_of_id[i] = -1;
+    if (i < num_cached) {
+      id_of_slot[i] = -1;
+      usage[i] = 0;
+    }
+    if (active_mask && i < num_experts) active_mask[i] = 0;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    *step = 0;
+    if (num_indices) *num_indices = 0;
+  }
+}
+
+// Place partition `layer` whole into slots [0, E): evict the other partitions' owners of
+// those slots, drop this partition's copies elsewhere, and plan the full-layer copy.
+__global__ __launch_bounds__(LRU_THREADS) void slot_cache_materialize_kernel(
+    int32_t* __restrict__ slot_of_id, int64_t num_total, int32_t* __restrict__ id_of_slot,
+    int64_t* __restrict__ usage, int64_t num_cached, int64_t* __restrict__ step_ptr,
+    int32_t* __restrict__ evict_slots, int32_t* __restrict__ src_indices,
+    int64_t* __restrict__ num_indices, int64_t base, int E) {
+  __shared__ int64_t step_lds;
+  if (threadIdx.x == 0) {
+    const int64_t s = *step_ptr + 1;
+    *step_ptr = s;
+    step_lds = s;
+  }
+  // every owner is read before any map entry changes
+  for (int64_t s = threadIdx.x; s < num_cached; s += blockDim.x) {
+    const int32_t old = id_of_slot[s];
+    const bool same = old >= base && old < base + E;
+    if (same) {
+      id_of_slot[s] = -1;
+      usage[s] = 0;
+    } else if (s < E && old >= 0 && old < num_total) {
+      slot_of_id[old] = -1;
+    }
+  }
+  __syncthreads();
+  const int64_t step = step_lds;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    id_of_slot[e] = int32_t(base + e);
+    slot_of_id[base + e] = e;
+    usage[e] = step;
+    evict_slots[e] = e;
+    src_indices[e] = e;
+  }
+  if (threadIdx.x == 0) *num_indices = E;
+}
+
+// Empty slots [begin, end): their owners become non-resident and the slots the oldest.
+__global__ void slot_cache_invalidate_kernel(int32_t* __restrict__ slot_of_id, int64_t num_total,
+                                             int32_t* __restrict__ id_of_slot,
+                                             int64_t* __restrict__ usage, int64_t begin,
+                                             int64_t end) {
+  const int64_t s = begin + int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (s >= end) return;
+  const int32_t old = id_of_slot[s];
+  if (old >= 0 && old < num_total) slot_of_id[old] = -1;
+  id_of_slot[s] = -1;
+  usage[s] = 0;
+}
+
+// Experts of one partition resident at or above `threshold`, compacted in expert order:
+// dst = buffer row (buffer_base + e), src = their slot; num = count.
+__global__ __launch_bounds__(LRU_THREADS) void prefill_hit_compact_kernel(
+    const int32_t* __restrict__ slot_row, int32_t* __restrict__ dst, int32_t* __restrict__ src,
+    int64_t* __restrict__ num, int64_t buffer_base, int64_t threshold, int E) {
+  __shared__ int red[LRU_THREADS / 64 + 1];
+  __shared__ int carry_lds;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) carry_lds = 0;
+  __syncthreads();
+  for (int e0 = 0; e0 < E; e0 += LRU_THREADS) {
+    const int e = e0 + tid;
+    const int32_t s = e < E ? slot_row[e] : -1;
+    const int hit = (e < E && s >= threshold) ? 1 : 0;
+    // inclusive scan within the wave, then across the 16 wave totals
+    int v = hit;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(v, o, 64);
+      if (lane >= o) v += t;
+    }
+    if (lane == 63) red[wave] = v;
+    __syncthreads();
+    int before = carry_lds;
+    for (int w = 0; w < wave; ++w) before += red[w];
+    if (hit) {
+      const int pos = before + v - 1;
+      dst[pos] = int32_t(buffer_base + e);
+      src[pos] = s;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int tot = 0;
+      for (int w = 0; w < LRU_THREADS / 64; ++w) tot += red[w];
+      carry_lds += tot;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) *num = carry_lds;
+}
+
+}  // namespace
+}  // namespace pia
+
+using namespace pia;
+
+extern "C" int pia_lru_ensure(const int32_t* query, int64_t num_queries, int32_t* slot_of_id,
+                              int64_t num_total, int32_t* id_of_slot, int64_t* lru_usage,
+                              int64_t num_cached, int64_t* lru_step, int32_t* out_indices,
+                              int32_t* src_indices, int32_t* dst_indices, int64_t* num_copy,
+                              int64_t* stats, int64_t id_base, void* stream) {
+  if (num_queries < 0 || num_total < 0 || num_cached < 0)
+    return fail(PIA_EINVAL, "lru_ensure: negative size");
+  if (num_queries > LRU_MAX_QUERY)
+    return fail(PIA_EUNSUPPORTED, "lru_ensure: more than 2048 queries per call");
+  if (num_cached < 1 || num_cached > LRU_MAX_CACHED)
+    return fail(PIA_EUNSUPPORTED, "lru_ensure: cache of 1..16384 slots supported");
+  if (num_total > 0x7fffffff) return fail(PIA_EINVAL, "lru_ensure: id space beyond int32");
+  if (!slot_of_id || !id_of_slot || !lru_usage || !lru_step || !num_copy ||
+      (num_queries > 0 && (!query || !out_indices)) || !src_indices || !dst_indices)
+    return fail(PIA_EINVAL, "lru_ensure: null pointer");
+  int c_pad = 2, slot_bits = 1;
+  while (c_pad < num_cached) {
+    c_pad <<= 1;
+    ++slot_bits;
+  }
+  hipLaunchKernelGGL(lru_ensure_kernel, dim3(1), dim3(LRU_THREADS), 0, as_stream(stream), query,
+                     int(num_queries), slot_of_id, num_total, id_of_slot, lru_usage,
+                     int(num_cached), c_pad, slot_bits, lru_step, out_indices, src_indices,
+                     dst_indices, num_copy, stats, id_base);
+  return check_launch("lru_ensure");
+}
+
+extern "C" int pia_slot_cache_reset(int32_t* slot_of_id, int64_t num_total, int32_t* id_of_slot,
+                                    int64_t* usage, int64_t num_cached, int64_t* step,
+                                    int32_t* active_mask, int num_experts,
+                                    int64_t* num_indices, void* stream) {
+  if (num_total < 0 || num_cached < 0 || num_experts < 0)
+    return fail(PIA_EINVAL, "slot_cache_reset: negative size");
+  if (!slot_of_id || !id_of_slot || !usage || !step)
+    return fail(PIA_EINVAL, "slot_cache_reset: null pointer");
+  const int64_t n = std::max<int64_t>({num_total, num_cached, int64_t(num_experts), 1});
+  const unsigned blocks = unsigned(std::min<int64_t>(ceil_div(n, 256), 1024));
+  hipLaunchKernelGGL(slot_cache_reset_kernel, dim3(blocks), dim3(256), 0, as_stream(stream),
+                     slot_of_id, num_total, id_of_slot, usage, num_cached, step, active_mask,
+                     num_experts, num_indices);
+  return check_launch("slot_cache_reset");
+}
+
+extern "C" int pia_slot_cache_materialize(int32_t* slot_of_id, int64_t num_total,
+                                          int32_t* id_of_slot, int64_t* usage,
+                                          int64_t num_cached, int64_t* step,
+                                          int32_t* evict_slots, int32_t* src_indices,
+                                          int64_t* num_indices, int layer_id, int num_experts,
+                                          void* stream) {
+  if (layer_id < 0 || num_experts <= 0 || num_cached < num_experts)
+    return fail(PIA_EINVAL, "slot_cache_materialize: need 0 <= layer and E <= cache size");
+  const int64_t base = int64_t(layer_id) * num_experts;
+  if (base + num_experts > num_total)
+    return fail(PIA_EINVAL, "slot_cache_materialize: layer outside the id space");
+  if (!slot_of_id || !id_of_slot || !usage || !step || !evict_slots || !src_indices ||
+      !num_indices)
+    return fail(PIA_EINVAL, "slot_cache_materialize: null pointer");
+  hipLaunchKernelGGL(slot_cache_materialize_kernel, dim3(1), dim3(LRU_THREADS), 0,
+                     as_stream(stream), slot_of_id, num_total, id_of_slot, usage, num_cached,
+                     step, evict_slots, src_indices, num_indices, base, num_experts);
+  return check_launch("slot_cache_materialize");
+}
+
+extern "C" int pia_slot_cache_invalidate(int32_t* slot_of_id, int64_t num_total,
+                                         int32_t* id_of_slot, int64_t* usage,
+                                         int64_t num_cached, int64_t slot_begin,
+                                         int64_t slot_end, void* stream) {
+  if (slot_begin < 0 || slot_end < slot_begin || slot_end > num_cached)
+    return fail(PIA_EINVAL, "slot_cache_invalidate: slot range outside the cache");
+  if (slot_end == slot_begin) return 0;
+  if (!slot_of_id || !id_of_slot || !usage)
+    return fail(PIA_EINVAL, "slot_cache_invalidate: null pointer");
+  hipLaunchKernelGGL(slot_cache_invalidate_kernel, dim3(unsigned(ceil_div(slot_end - slot_begin, 256))),
+                     dim3(256), 0, as_stream(stream), slot_of_id, num_total, id_of_slot, usage,
+                     slot_begin, slot_end);
+  return check_launch("slot_cache_invalidate");
+}
+
+extern "C" int pia_prefill_hit_compact(const int32_t* slot_row, int32_t* dst, int32_t* src,
+                                       int64_t* num, int64_t buffer_base, int64_t threshold,
+                                       int num_experts, void* stream) {
+  if (num_experts < 0) return fail(PIA_EINVAL, "prefill_hit_compact: negative size");
+  if (!num || (num_experts > 0 && (!slot_row || !dst || !src)))
+    return fail(PIA_EINVAL, "prefill_hit_compact: null pointer");
+  hipLaunchKernelGGL(prefill_hit_compact_kernel, dim3(1), dim3(LRU_THREADS), 0,
+                     as_stream(stream), slot_row, dst, src, num, buffer_base, threshold,
+                     num_experts);
+  return check_launch("prefill_hit_compact");
+}

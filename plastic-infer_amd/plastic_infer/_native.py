@@ -45,6 +45,11 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_index_copy_rows_multi": (_I, [_P, _P, _P, _I, _P, _P, _L, _P, _I, _P]),
     "pia_device_pointer": (_I, [_P, _P]),
     "pia_copy_rows_async": (_I, [_P, _P, _P, _P, _L, _L, _P, _P]),
+    "pia_lru_ensure": (_I, [_P, _L, _P, _L, _P, _P, _L, _P, _P, _P, _P, _P, _P, _L, _P]),
+    "pia_slot_cache_reset": (_I, [_P, _L, _P, _P, _L, _P, _P, _I, _P, _P]),
+    "pia_slot_cache_materialize": (_I, [_P, _L, _P, _P, _L, _P, _P, _P, _P, _I, _I, _P]),
+    "pia_slot_cache_invalidate": (_I, [_P, _L, _P, _P, _L, _L, _L, _P]),
+    "pia_prefill_hit_compact": (_I, [_P, _P, _P, _P, _L, _L, _I, _P]),
 }
 
 EXPECTED_ABI = 2

@@ -1,6 +1,7 @@
 """HIP kernel layer: batched entry points over libplastic_infer_amd.so (gfx950)."""
 
 from .index_copy import copy_rows_async, fast_index_copy, fast_index_copy_multi
+from .lru_ensure import lru_ensure
 from .moe_ops import (
     max_num_tokens_padded,
     moe_align_block_size,
@@ -19,7 +20,7 @@ from .paged_kv import (
 )
 
 __all__ = [
-    "copy_rows_async", "fast_index_copy", "fast_index_copy_multi",
+    "copy_rows_async", "fast_index_copy", "fast_index_copy_multi", "lru_ensure",
     "max_num_tokens_padded", "moe_align_block_size", "moe_permute", "moe_sum_reduce",
     "moe_topk", "moe_unpermute",
     "decode_workspace_bytes", "kv_gather", "kv_scatter", "paged_attention",

@@ -1,0 +1,254 @@
+"""GPU parity of the device slot cache (LRU admission, bookkeeping kernels) and of
+OffloadMoeCache's decode / prefill expert movement. Every check is bit-exact: maps, usage,
+clock, plan, stats against the oracle; slot-cache rows against the pinned host banks."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.slot_cache as SC
+from plastic_infer.kernel.fast_index_copy import fast_index_copy_jit, fast_index_copy_multi_jit
+from plastic_infer.kernel.lru_ensure import N_STATS, lru_ensure
+from plastic_infer.moe.offload_cache import OffloadMoeCache
+
+pytestmark = pytest.mark.gpu
+
+
+class DevState:
+    def __init__(self, dev, num_total: int, num_cached: int):
+        self.slot_of_id = torch.full((num_total,), -1, dtype=torch.int32, device=dev)
+        self.id_of_slot = torch.full((num_cached,), -1, dtype=torch.int32, device=dev)
+        self.usage = torch.zeros(num_cached, dtype=torch.int64, device=dev)
+        self.step = torch.zeros((), dtype=torch.int64, device=dev)
+        plan = num_cached
+        self.src = torch.full((plan,), -7, dtype=torch.int32, device=dev)
+        self.dst = torch.full((plan,), -7, dtype=torch.int32, device=dev)
+        self.num = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.stats = torch.zeros(N_STATS, dtype=torch.int64, device=dev)
+
+    def ensure(self, query: np.ndarray, id_base: int):
+        q = torch.tensor(query, dtype=torch.int32, device=self.slot_of_id.device)
+        lru_ensure(q, self.slot_of_id, self.id_of_slot, self.usage, self.step, q, self.src,
+                   self.dst, self.num, stats=self.stats, id_base=id_base)
+        return q.cpu().numpy()
+
+    def assert_equal(self, st: dict):
+        assert np.array_equal(self.slot_of_id.cpu().numpy(), st["slot_of_id"])
+        assert np.array_equal(self.id_of_slot.cpu().numpy(), st["id_of_slot"])
+        assert np.array_equal(self.usage.cpu().numpy(), st["usage"])
+        assert int(self.step) == st["step"]
+
+
+@pytest.mark.parametrize("seed,layers,experts,cached,k,calls", [
+    (0, 4, 16, 20, 12, 40),       # small cache, constant cross-layer eviction
+    (1, 48, 128, 3072, 512, 12),  # Qwen3-30B-A3B decode shape: B=64 x top-8 over 50% slots
+    (2, 2, 8, 8, 64, 30),         # many duplicates, cache exactly one layer
+    (3, 1, 2048, 2048, 2048, 4),  # the largest query
+    (4, 3, 1, 1, 3, 10),          # one slot
+])
+def test_lru_ensure_matches_oracle(dev, seed, layers, experts, cached, k, calls):
+    rng = np.random.default_rng(seed)
+    total = layers * experts
+    st, ds = SC.new_state(total, cached), DevState(dev, total, cached)
+    stats = np.zeros(3, np.int64)
+    for c in range(calls):
+        layer = int(rng.integers(0, layers))
+        distinct = int(rng.integers(1, min(experts, cached, k) + 1))
+        ids = rng.choice(experts, size=distinct, replace=False)
+        query = rng.choice(ids, size=k) if c % 3 else ids
+        print(f"call {c}: layer {layer}, {query.size} ids, {distinct} distinct", flush=True)
+        out, src, dst, n, dstats = SC.lru_ensure(st, query, id_base=layer * experts)
+        got = ds.ensure(query, layer * experts)
+        stats += np.asarray(dstats)
+        assert np.array_equal(got, out), c
+        assert int(ds.num) == n
+        assert np.array_equal(ds.src[:n].cpu().numpy(), src)
+        assert np.array_equal(ds.dst[:n].cpu().numpy(), dst)
+        ds.assert_equal(st)
+    assert np.array_equal(ds.stats.cpu().numpy(), stats)
+
+
+def test_lru_ensure_largest_cache_and_inert_ids(dev):
+    total, cached = 40000, 16384
+    st, ds = SC.new_state(total, cached), DevState(dev, total, cached)
+    rng = np.random.default_rng(7)
+    for c in range(6):
+        query = rng.choice(total, size=2048, replace=False)
+        out, src, dst, n, _ = SC.lru_ensure(st, query)
+        assert np.array_equal(ds.ensure(query, 0), out)
+        ds.assert_equal(st)
+    # ids outside [0, num_total) are inert: out -1, nothing admitted for them
+    q = np.array([5, -3, total + 10, 5], np.int64)
+    out, _, _, n, _ = SC.lru_ensure(st, q[[0, 3]])
+    got = ds.ensure(q, 0)
+    assert got.tolist() == [out[0], -1, -1, out[1]]
+    ds.assert_equal(st)
+
+
+def test_lru_ensure_more_misses_than_slots_admits_what_fits(dev):
+    ds = DevState(dev, 100, 4)
+    ds.ensure(np.array([1, 2]), 0)
+    got = ds.ensure(np.array([2, 9, 8, 7, 6]), 0)   # 2 hits; 4 misses, 3 evictable slots
+    assert got[0] == ds.slot_of_id[2].item() and int(ds.num) == 3
+    assert sorted(got[1:].tolist()) == [-1] + sorted(set(range(4)) - {got[0]})
+    assert got[1] == -1                               # the largest missing id is left out
+
+
+def test_materialize_reset_invalidate_compact_match_oracle(dev):
+    from plastic_infer import _native as N
+
+    L, E, C = 3, 8, 20
+    st, ds = SC.new_state(L * E, C), DevState(dev, L * E, C)
+    rng = np.random.default_rng(11)
+    for c in range(8):
+        layer = c % L
+        q = rng.choice(E, size=5, replace=False)
+        SC.lru_ensure(st, q, id_base=layer * E)
+        ds.ensure(q, layer * E)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    ev = torch.full((C,), -1, dtype=torch.int32, device=dev)
+    srci = torch.full((C,), -1, dtype=torch.int32, device=dev)
+    num = torch.zeros(1, dtype=torch.int64, device=dev)
+    ref_ev, ref_src, ref_n = SC.materialize(st, 1, E)
+    N.call("pia_slot_cache_materialize", ds.slot_of_id.data_ptr(), L * E, ds.id_of_slot.data_ptr(),
+           ds.usage.data_ptr(), C, ds.step.data_ptr(), ev.data_ptr(), srci.data_ptr(),
+           num.data_ptr(), 1, E, s)
+    ds.assert_equal(st)
+    assert ev[:E].cpu().tolist() == ref_ev.tolist() and srci[:E].cpu().tolist() == ref_src.tolist()
+    assert int(num) == ref_n
+    SC.invalidate(st, 2, 11)
+    N.call("pia_slot_cache_invalidate", ds.slot_of_id.data_ptr(), L * E, ds.id_of_slot.data_ptr(),
+           ds.usage.data_ptr(), C, 2, 11, s)
+    ds.assert_equal(st)
+    row = torch.tensor([3, -1, 25, 4, 19, 30, 0, 16], dtype=torch.int32, device=dev)
+    hd = torch.full((8,), -1, dtype=torch.int32, device=dev)
+    hs = torch.full((8,), -1, dtype=torch.int32, device=dev)
+    N.call("pia_prefill_hit_compact", row.data_ptr(), hd.data_ptr(), hs.data_ptr(), num.data_ptr(),
+           8, 16, 8, s)
+    rd, rs, rn = SC.prefill_hit_compact(row.cpu().numpy(), 8, 16)
+    assert int(num) == rn and hd[:rn].cpu().tolist() == rd.tolist()
+    assert hs[:rn].cpu().tolist() == rs.tolist()
+    SC.reset(st)
+    N.call("pia_slot_cache_reset", ds.slot_of_id.data_ptr(), L * E, ds.id_of_slot.data_ptr(),
+           ds.usage.data_ptr(), C, ds.step.data_ptr(), None, 0, num.data_ptr(), s)
+    ds.assert_equal(st)
+    assert int(num) == 0
+
+
+# ---- OffloadMoeCache --------------------------------------------------------------------------
+
+def _banks(L: int, E: int, H: int, I: int, seed: int):
+    g = torch.Generator().manual_seed(seed)
+    gate_up = [torch.randn(E, 2 * I, H, generator=g).to(torch.bfloat16).pin_memory()
+               for _ in range(L)]
+    down = [torch.randn(E, H, I, generator=g).to(torch.bfloat16).pin_memory() for _ in range(L)]
+    return {"gate_up": gate_up, "down": down}
+
+
+def _check_resident(cache, banks, layer: int, experts, slots):
+    gu, dn = cache.bank_caches["gate_up"], cache.bank_caches["down"]
+    for e, s in zip(experts, slots):
+        assert torch.equal(gu[s].cpu(), banks["gate_up"][layer][e]), (layer, e, s)
+        assert torch.equal(dn[s].cpu(), banks["down"][layer][e]), (layer, e, s)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_offload_cache_decode_steps(dev, fused, monkeypatch):
+    import plastic_infer.moe.offload_cache as OC
+
+    monkeypatch.setattr(OC, "_FUSED_COPY", fused)
+    L, E, H, I, B, K = 4, 16, 128, 64, 6, 4
+    banks = _banks(L, E, H, I, 3)
+    cache = OffloadMoeCache(num_layers=L, num_experts=E, cache_size=24, device=dev)
+    cache.collect_stats = True
+    cache.set_bank_sources(banks)
+    assert cache._copy_fused_ok == fused
+    st = SC.new_state(L * E, 24)
+    rng = np.random.default_rng(5)
+    stats = np.zeros((L, 3), np.int64)
+    for step in range(12):
+        for layer in range(L):
+            ids = np.stack([rng.choice(E, size=K, replace=False) for _ in range(B)])
+            out, _, _, _, dstats = SC.lru_ensure(st, ids.reshape(-1), id_base=layer * E)
+            stats[layer] += dstats
+            t = torch.tensor(ids, dtype=torch.int32, device=dev)
+            cache.ensure_experts(layer, t)
+            cache.copy_missing()
+            assert np.array_equal(t.cpu().numpy().reshape(-1), out)
+            _check_resident(cache, banks, layer, ids.reshape(-1), out)
+    assert np.array_equal(cache.slot_for_id.cpu().numpy().reshape(-1), st["slot_of_id"])
+    assert np.array_equal(cache.lru_stats.cpu().numpy(), stats)
+    m = cache.decode_miss_stats()
+    assert m["layer_calls"] == 12 * L and 0 < m["miss_rate"] <= 1
+    cache.materialize_layer(2)
+    cache.copy_missing()
+    _check_resident(cache, banks, 2, range(E), range(E))
+    views = cache.bank_views(E)
+    assert torch.equal(views[0].cpu(), banks["gate_up"][2])
+    cache.reset()
+    assert int((cache.slot_for_id >= 0).sum()) == 0 and int(cache.step) == 0
+
+
+@pytest.mark.parametrize("hit_d2d", [False, True])
+def test_offload_cache_prefill_double_buffer(dev, hit_d2d):
+    L, E, H, I = 5, 8, 256, 256       # gate_up rows 256 KiB (gathered), down rows 128 KiB
+    banks = _banks(L, E, H, I, 9)
+    cache = OffloadMoeCache(num_layers=L, num_experts=E, cache_size=3 * E, device=dev,
+                            prefill_overlap=True, prefill_hit_d2d=hit_d2d)
+    cache.set_bank_sources(banks)
+    # a decode step first: 4 experts x 5 layers fill slots 0..19, so the last layer's sit
+    # above the 2E = 16 slots the buffers own and are gathered device-side
+    for layer in range(L):
+        ids = torch.tensor([[0, 3], [5, 6]], dtype=torch.int32, device=dev)
+        cache.ensure_experts(layer, ids)
+        cache.copy_missing()
+    compute = torch.cuda.current_stream(dev)
+    for rep in range(2):
+        cache.begin_prefill()
+        cache.prefetch_prefill_layer(0)
+        for layer in range(L):
+            cache.prefetch_prefill_layer(layer + 1)        # next layer crosses PCIe meanwhile
+            gu, dn = cache.wait_prefill_layer(layer)
+            scratch = torch.empty_like(gu)
+            scratch.copy_(gu)                               # stand-in consumer on the compute stream
+            assert torch.equal(gu.cpu(), banks["gate_up"][layer]), (rep, layer)
+            assert torch.equal(dn.cpu(), banks["down"][layer]), (rep, layer)
+            cache.release_prefill_layer(layer)
+        compute.synchronize()
+    if hit_d2d:
+        assert cache.prefill_hit_rows == 2 * 4 and cache.prefill_total_rows == 2 * L * E
+    # decode after prefill: the buffers' slots were invalidated, residency stays consistent
+    ids = torch.tensor([[1, 2]], dtype=torch.int32, device=dev)
+    cache.ensure_experts(3, ids)
+    cache.copy_missing()
+    _check_resident(cache, banks, 3, [1, 2], ids.cpu().reshape(-1).tolist())
+    sid = cache.slot_for_id.cpu().numpy().reshape(-1)
+    ios = cache.id_of_slot.cpu().numpy()
+    res = np.nonzero(sid >= 0)[0]
+    assert np.array_equal(ios[sid[res]], res)
+
+
+def test_fast_index_copy_dropin_names(dev):
+    g = torch.Generator().manual_seed(2)
+    src = torch.randn(10, 64, generator=g).pin_memory()
+    dst = torch.zeros(6, 64, device=dev)
+    di = torch.tensor([4, 0, 2], dtype=torch.int32, device=dev)
+    si = torch.tensor([9, 1, 5], dtype=torch.int32, device=dev)
+    n = torch.tensor([2], dtype=torch.int64, device=dev)
+    fast_index_copy_jit(dst, di, src, si, n)
+    exp = torch.zeros(6, 64)
+    exp[4], exp[0] = src[9], src[1]
+    assert torch.equal(dst.cpu(), exp)
+    with pytest.raises(NotImplementedError):
+        fast_index_copy_jit(dst, di, src, si, priority="high")
+    from plastic_infer.kernel.pinned import device_ptr
+
+    dst2 = torch.zeros(6, 64, device=dev)
+    dp = torch.tensor([dst.data_ptr(), dst2.data_ptr()], dtype=torch.int64, device=dev)
+    sp = torch.tensor([device_ptr(src), device_ptr(src)], dtype=torch.int64, device=dev)
+    fb = torch.tensor([256, 256], dtype=torch.int64, device=dev)
+    fast_index_copy_multi_jit(dp, sp, fb, di, si)
+    exp[2] = src[5]
+    assert torch.equal(dst.cpu(), exp) and torch.equal(dst2.cpu(), exp)
