@@ -15,6 +15,12 @@ reference torch path on this host's cores, on a bounded sample of the same input
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-sample-seqs S] [--no-cpu-baseline]
   python bench.py --calibrate-copy     # 1 GiB read + 1 GiB write elementwise copy, three times:
                                        # the known-size reference for HBM byte counters
+  python bench.py --workload prefill-write   # ragged chunked-prefill KV write + gather back
+                                             # (8 sequences, S ~ U[256, 4096], seed 3)
+  python bench.py --workload moe-permute     # Qwen3-30B-A3B routing: top-8 of 128 experts,
+                                             # permute, identity expert, weighted unpermute
+                                             # (4096 tokens, hidden 2048, seed 4)
+The default workload (decode) is the headline; the others print their own JSON line.
 """
 
 from __future__ import annotations
@@ -150,6 +156,228 @@ def cpu_baseline(torch, inp, n_seqs):
     }
 
 
+def _phase_timer(torch, dev, step, n_phases, steps, warmup):
+    """Runs step(events) warmup + steps times; step records n_phases + 1 events on the launch
+    stream. Returns (ms per step over the timed region, mean ms of each phase, wall s)."""
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(warmup):
+        step(None)
+    torch.cuda.synchronize(dev)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(n_phases + 1)]
+           for _ in range(steps)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t0.record(stream)
+    for i in range(steps):
+        step(evs[i])
+    t1.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - wall0
+    phases = [statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs) for j in range(n_phases)]
+    return t0.elapsed_time(t1) / steps, phases, wall
+
+
+def _result(metric, value, unit, args, ms, dtype, config, extra, roofline, cpu=None):
+    r = {"metric": metric, "value": round(value, 2), "unit": unit, "n_gpus": 1,
+         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+         "data": "synthetic (seeded)", "config": config}
+    r.update(extra)
+    r["roofline"] = roofline
+    if cpu is not None:
+        r["cpu_baseline"] = cpu
+    return r
+
+
+PF_B, PF_LO, PF_HI, PF_SEED, PF_SPARE = 8, 256, 4096, 3, 1024
+
+
+def bench_prefill_write(torch, dev, args) -> dict:
+    """Ragged chunked-prefill KV write: packed [sum S, 8, 128] bf16 rows of 8 sequences with
+    S ~ U[256, 4096] scattered into a seeded random page allocation (partial last pages), then
+    gathered back. One step = kv_scatter + kv_gather; both bit-exact (checked once here)."""
+    from plastic_infer.kernel import kv_gather, kv_scatter
+
+    g = torch.Generator().manual_seed(PF_SEED)
+    lens = torch.randint(PF_LO, PF_HI + 1, (PF_B,), generator=g)
+    n_pages = (lens + P - 1) // P
+    num_pages = int(n_pages.sum()) + PF_SPARE
+    perm = torch.randperm(num_pages, generator=g)
+    max_pages = (PF_HI + P - 1) // P
+    bt = torch.zeros(PF_B, max_pages, dtype=torch.int32)
+    slots, off = [], 0
+    for b in range(PF_B):
+        n = int(n_pages[b])
+        bt[b, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+        pos = torch.arange(int(lens[b]))
+        slots.append(bt[b, pos // P].to(torch.int64) * P + pos % P)
+    total = int(lens.sum())
+    k = torch.randn(total, HKV, D, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(total, HKV, D, generator=g).to(torch.bfloat16).to(dev)
+    cu = torch.zeros(PF_B + 1, dtype=torch.int64)
+    cu[1:] = torch.cumsum(lens, 0)
+    slots_d, bt_d, cu_d = torch.cat(slots).to(dev), bt.to(dev), cu.to(dev)
+    kp = torch.zeros(num_pages, HKV, D, P, dtype=torch.bfloat16, device=dev)
+    vp = torch.zeros_like(kp)
+    kb, vb = torch.empty_like(k), torch.empty_like(v)
+
+    def step(ev):
+        if ev:
+            ev[0].record()
+        kv_scatter(k, v, kp, vp, slots_d)
+        if ev:
+            ev[1].record()
+        kv_gather(kp, vp, bt_d, cu_d, PF_HI, out=(kb, vb))
+        if ev:
+            ev[2].record()
+
+    ms, (sc_ms, ga_ms), wall = _phase_timer(torch, dev, step, 2, args.steps, args.warmup)
+    if not (torch.equal(kb, k) and torch.equal(vb, v)):
+        raise RuntimeError("prefill write: gather-back differs from the written rows")
+    row = HKV * D * 2                                   # one token's K (or V) bytes
+    scatter_bytes = total * row * 2 * 2 + total * 8     # K+V read and written, slots
+    gather_bytes = total * row * 2 * 2 + int(n_pages.sum()) * 4 + (PF_B + 1) * 8
+    step_bytes = scatter_bytes + gather_bytes
+    dom, dom_bytes, dom_ms = (("kv_scatter_kernel", scatter_bytes, sc_ms) if sc_ms >= ga_ms
+                              else ("kv_gather_kernel", gather_bytes, ga_ms))
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = _cpu_prefill_write(torch, k, v, slots, num_pages, total, scatter_bytes)
+    gbps = step_bytes / (ms / 1e3) / 1e9
+    return _result(
+        "ragged prefill KV write + gather-back GB/s", gbps, "GB/s", args, ms, "bf16",
+        {"workload": "ragged chunked-prefill kv write (8 seqs, S~U[256,4096], 8 kv heads x "
+                     "128, page 16) + gather back", "tokens": total, "pool_pages": num_pages},
+        {"tokens_per_s": round(total / (ms / 1e3), 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+         "bytes_per_step": step_bytes, "scatter_ms": round(sc_ms, 4), "gather_ms": round(ga_ms, 4),
+         "wall_s_timed": round(wall, 4)},
+        {"kernel": dom, "bound": "hbm", "achieved": round(dom_bytes / (dom_ms / 1e3) / 1e9, 2),
+         "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+         "frac": round(dom_bytes / (dom_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+         "algorithmic_bytes_per_launch": dom_bytes, "avg_launch_ms": round(dom_ms, 4)},
+        cpu)
+
+
+def _cpu_prefill_write(torch, k, v, slots, num_pages, total, scatter_bytes) -> dict:
+    """The oracle's per-token advanced-index store (the reference's _write_kv_layer loop) on
+    the first 2048 tokens of the same rows, 1 warm-up + median of 3; scaled per byte."""
+    import oracle.paged_kv as OP
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    n = min(2048, total)
+    kc, vc = k[:n].cpu(), v[:n].cpu()
+    sl = torch.cat(slots)[:n].tolist()
+    kp = torch.zeros(num_pages, HKV, D, P, dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    OP.scatter_slots(kc, vc, kp, vp, sl)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        OP.scatter_slots(kc, vc, kp, vp, sl)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    model, phys = cpu_info()
+    return {"value": round(scatter_bytes * n / total / t / 1e9, 3), "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"scatter of the first {n} of {total} tokens (same rows and slots), "
+                      f"1 warm-up + median of 3, {t * 1e3:.1f} ms",
+            "cpu_model": model, "physical_cores": phys}
+
+
+MOE_T, MOE_H, MOE_E, MOE_K, MOE_BS, MOE_SEED = 4096, 2048, 128, 8, 64, 4
+
+
+def bench_moe_permute(torch, dev, args) -> dict:
+    """Qwen3-30B-A3B MoE routing and permutation: router logits [4096, 128] fp32 N(0,1) ->
+    softmax top-8 renormalised -> align (block 64) -> permute hidden [4096, 2048] bf16 into
+    expert-contiguous rows -> identity expert -> weighted unpermute."""
+    from plastic_infer.kernel import moe_align_block_size, moe_permute, moe_topk, moe_unpermute
+
+    g = torch.Generator().manual_seed(MOE_SEED)
+    hidden = torch.randn(MOE_T, MOE_H, generator=g).to(torch.bfloat16).to(dev)
+    logits = torch.randn(MOE_T, MOE_E, generator=g, dtype=torch.float32).to(dev)
+    state = {}
+
+    def step(ev):
+        if ev:
+            ev[0].record()
+        w, ids = moe_topk(logits, MOE_K, True)
+        s, e, npp, pos = moe_align_block_size(ids, MOE_BS, MOE_E, return_route_pos=True)
+        if ev:
+            ev[1].record()
+        xp = moe_permute(hidden, s, npp, MOE_K, route_pos=pos)
+        if ev:
+            ev[2].record()
+        out = moe_unpermute(xp, pos, w, MOE_T, MOE_K)
+        if ev:
+            ev[3].record()
+        state["out"], state["w"] = out, w
+
+    ms, (route_ms, perm_ms, comb_ms), wall = _phase_timer(torch, dev, step, 3, args.steps,
+                                                          args.warmup)
+    closed = (hidden.double() * state["w"].double().sum(1, keepdim=True)).to(torch.bfloat16)
+    if (state["out"].float() - closed.float()).abs().max().item() > 2e-2:
+        raise RuntimeError("moe permute: identity-expert round trip is off")
+    T, H, K, E = MOE_T, MOE_H, MOE_K, MOE_E
+    route_bytes = T * E * 4 + T * K * 8
+    perm_bytes = T * H * 2 + T * K * H * 2 + T * K * 4
+    comb_bytes = T * K * H * 2 + T * H * 2 + T * K * 4 + T * K * 4
+    step_bytes = route_bytes + perm_bytes + comb_bytes
+    phases = [("moe_topk + moe_align", route_bytes, route_ms),
+              ("moe_permute_kernel", perm_bytes, perm_ms),
+              ("moe_combine_kernel", comb_bytes, comb_ms)]
+    dom, dom_bytes, dom_ms = max(phases, key=lambda x: x[2])
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = _cpu_moe(torch, hidden, logits, perm_bytes + comb_bytes + route_bytes)
+    gbps = step_bytes / (ms / 1e3) / 1e9
+    return _result(
+        "MoE route + permute + unpermute GB/s", gbps, "GB/s", args, ms, "bf16",
+        {"workload": "qwen3-30b-a3b moe routing/permute (4096 tokens, hidden 2048, 128 experts "
+                     "top-8, identity expert)", "tokens": T, "hidden": H, "experts": E, "topk": K},
+        {"tokens_per_s": round(T / (ms / 1e3), 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+         "bytes_per_step": step_bytes, "route_ms": round(route_ms, 4),
+         "permute_ms": round(perm_ms, 4), "combine_ms": round(comb_ms, 4),
+         "wall_s_timed": round(wall, 4)},
+        {"kernel": dom, "bound": "hbm", "achieved": round(dom_bytes / (dom_ms / 1e3) / 1e9, 2),
+         "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+         "frac": round(dom_bytes / (dom_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+         "algorithmic_bytes_per_launch": dom_bytes, "avg_launch_ms": round(dom_ms, 4)},
+        cpu)
+
+
+def _cpu_moe(torch, hidden, logits, step_bytes) -> dict:
+    """The oracle's restatement (softmax top-k, stable align, row gather, sequential fp32
+    combine) on the first 512 of the 4096 tokens, 1 warm-up + median of 3; scaled per token."""
+    import oracle.moe_route as OM
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    n = 512
+    h, lg = hidden[:n].cpu(), logits[:n].cpu()
+
+    def run():
+        w, ids = OM.fused_topk(lg, MOE_K, True)
+        s, _, npp, pos = OM.moe_align_block_size(ids.numpy(), MOE_BS, MOE_E)
+        xp = OM.permute(h, s, npp, MOE_K)
+        OM.unpermute(xp, pos, w.numpy(), n, MOE_K, torch.bfloat16)
+
+    run()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    model, phys = cpu_info()
+    return {"value": round(step_bytes * n / MOE_T / t / 1e9, 3), "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"first {n} of {MOE_T} tokens (same inputs), 1 warm-up + median of 3, "
+                      f"{t * 1e3:.1f} ms", "cpu_model": model, "physical_cores": phys}
+
+
 def calibrate_copy(torch, dev) -> int:
     """A plain elementwise copy of known size (2^30 bytes read, 2^30 written per launch) for
     scaling FETCH_SIZE / WRITE_SIZE readings of the attention kernel to bytes."""
@@ -172,6 +400,8 @@ def main() -> int:
     ap.add_argument("--cpu-sample-seqs", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--workload", choices=("decode", "prefill-write", "moe-permute"),
+                    default="decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the paged decode path on ONE GPU (per-GPU shard of a "
@@ -187,6 +417,11 @@ def main() -> int:
     torch.cuda.set_device(dev)
     if args.calibrate_copy:
         return calibrate_copy(torch, dev)
+    if args.workload != "decode":
+        run = bench_prefill_write if args.workload == "prefill-write" else bench_moe_permute
+        print(f"bench: workload {args.workload}", file=sys.stderr, flush=True)
+        print(json.dumps(run(torch, dev, args)), flush=True)
+        return 0
     print(f"bench: generating inputs (B={B}, pool={NUM_PAGES} pages)", file=sys.stderr, flush=True)
     inp = build_inputs(torch, dev)
     out = torch.empty(B, HQ, D, dtype=torch.bfloat16, device=dev)

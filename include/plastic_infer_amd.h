@@ -180,12 +180,16 @@ int pia_moe_align_block_size(int32_t* sorted_token_ids, int32_t* expert_ids,
  * Permute: x_perm[r, :] = hidden[sorted_token_ids[r] / topk, :] for r < *num_tokens_post_pad
  * and sorted_token_ids[r] < numel; padding rows (sentinel) are zero-filled; rows at or beyond
  * *num_tokens_post_pad are left untouched. Bit-exact row copy (row_bytes multiple of 4).
+ * route_pos (optional, the inverse map pia_moe_align_block_size writes): when given, each token
+ * row is read once and written to its routes' rows (same result, a quarter of the reads for
+ * top-8); NULL walks the destination rows in order.
  * (reference: the per-expert hidden[rows] gather of src/plastic_infer/exec/moe.py:150-153,
  * and the sorted_token_ids / topk A-row read of src/plastic_infer/kernel/triton/fused_moe.py:156-302)
  * ------------------------------------------------------------------------------------------- */
 int pia_moe_permute(void* x_perm, const void* hidden, const int32_t* sorted_token_ids,
-                    const int32_t* num_tokens_post_pad, int64_t max_rows, int64_t numel,
-                    int topk, int64_t row_bytes, int64_t hidden_row_stride_bytes, void* stream);
+                    const int32_t* route_pos, const int32_t* num_tokens_post_pad,
+                    int64_t max_rows, int64_t numel, int topk, int64_t row_bytes,
+                    int64_t hidden_row_stride_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Unpermute / combine: out[t, :] = cast( sum_{s<k} w[t,s] * y[route_pos[t*k+s], :] )

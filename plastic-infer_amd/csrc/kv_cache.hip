@@ -9,7 +9,8 @@ namespace pia {
 namespace {
 
 // ---------------------------------------------------------------------------------------------
-// Scatter
+// Generic scatter (any element size and page size; 16-bit elements with 16-token pages and
+// head_dim 64/128/256 take kv_scatter16_kernel below)
 // ---------------------------------------------------------------------------------------------
 // Full-page fast path: a block owns one destination page-run of up to P tokens. When the P
 // tokens i0..i0+P-1 land on one page at offsets 0..P-1 (the prefill case: a sequence's tokens
@@ -85,8 +86,8 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------
-// Gather: one block per (logical page, sequence); stage each head's [D][P] tile in LDS and write
-// rows [t][h][d] contiguously.
+// Generic gather: one block per (logical page, sequence); stage each head's [D][P] tile in LDS
+// and write rows [t][h][d] contiguously (16-bit / 16-token pages take kv_gather16_kernel).
 // ---------------------------------------------------------------------------------------------
 template <typename W>
 __global__ __launch_bounds__(256) void kv_gather_kernel(
@@ -122,6 +123,134 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(
       }
       __syncthreads();
     }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// 16-bit elements, 16-token pages (bf16 / fp16 pools with the reference's default page size):
+// one wave per (16 input tokens, kv head) for the scatter and per (sequence page, kv head) for
+// the gather. Both move the [16 tokens][D] <-> [D][16 tokens] transpose through LDS with
+// 16-byte global loads, and write whole 32-byte page rows (scatter) or 64-byte runs of token
+// rows (gather) per store instruction.
+// ---------------------------------------------------------------------------------------------
+constexpr int T16_P = 16;
+
+// Scatter. Input tokens form page segments: maximal runs whose slots advance by one inside one
+// page (a prefill chunk's page, a decode token alone, a padding slot alone). The wave of input
+// group g (tokens 16g .. 16g+15) owns every segment that STARTS in its group, including the
+// tokens of such a segment that spill into the next group (a segment has at most 16 tokens),
+// so each page row is written by one wave and its partial stores meet in L2 at once.
+// Owned tokens (at most 31) are staged in an LDS tile [32][D] (row pitch D + 8: the token
+// pairs read below fall in distinct banks) with 16-byte loads. Lane (pi = lane & 15,
+// dq = lane >> 4) writes owned tokens 2pi, 2pi + 1 for rows d = dq + 4j: one dword store when
+// the pair lands on an even offset and the next one of the same page, otherwise 16-bit stores;
+// padding or out-of-range slots store nothing.
+template <int D>
+__global__ __launch_bounds__(64) void kv_scatter16_kernel(
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, uint16_t* __restrict__ kp,
+    uint16_t* __restrict__ vp, const int64_t* __restrict__ slots, int64_t n, int64_t k_stride,
+    int64_t v_stride, int H, int64_t total_slots) {
+  constexpr int P = T16_P, PITCH = D + 8, CH = D / 8, MAXT = 32;
+  __shared__ __align__(16) uint16_t tile[MAXT * PITCH];
+  const int lane = threadIdx.x;
+  const int64_t i0 = int64_t(blockIdx.x) * P;
+  const int h = blockIdx.y;
+  // lane j < 33 looks at token i0 - 1 + j
+  const int64_t tj = i0 - 1 + lane;
+  long long s = -1;
+  if (lane < 33 && tj >= 0 && tj < n) {
+    s = slots[tj];
+    if (s < 0 || s >= total_slots) s = -1;
+  }
+  const long long sprev = __shfl_up(s, 1, 64);
+  const bool start = lane >= 1 && lane < 33 &&
+                     (s < 0 || sprev < 0 || s != sprev + 1 || (s % P) == 0 || tj >= n);
+  const uint64_t starts = __ballot(start);
+  // first segment start in the group (lanes 1..16) and the first one after it (lanes 17..32)
+  const int a = __builtin_ctzll(starts & 0x1fffeull);
+  const uint64_t after = starts & ~0x1ffffull;
+  const int b = after ? __builtin_ctzll(after) : 33;
+  const int m = max(0, min(b, int(min<int64_t>(n - i0 + 1, 33))) - a);  // owned tokens
+  const int64_t t0 = i0 - 1 + a;                                        // first owned token
+  if (m == 0) return;
+
+  const int pi = lane & 15, dq = lane >> 4;
+  const long long s0 = __shfl(s, (a + 2 * pi) & 63, 64), s1 = __shfl(s, (a + 2 * pi + 1) & 63, 64);
+  const bool has0 = 2 * pi < m && s0 >= 0, has1 = 2 * pi + 1 < m && s1 >= 0;
+  const bool pair = has0 && has1 && s1 == s0 + 1 && (s0 & 1) == 0;
+  const int64_t head_off = int64_t(h) * D * P;
+  const int64_t b0 = has0 ? (s0 / P) * H * D * P + head_off + (s0 % P) : 0;
+  const int64_t b1 = has1 ? (s1 / P) * H * D * P + head_off + (s1 % P) : 0;
+
+  for (int pass = 0; pass < 2; ++pass) {
+    const uint16_t* src = pass == 0 ? k : v;
+    const int64_t stride = pass == 0 ? k_stride : v_stride;
+    uint16_t* dst = pass == 0 ? kp : vp;
+    for (int it = lane; it < m * CH; it += 64) {
+      const int t = it / CH, c = it - t * CH;
+      *reinterpret_cast<uint4*>(&tile[t * PITCH + c * 8]) =
+          *reinterpret_cast<const uint4*>(src + (t0 + t) * stride + int64_t(h) * D + c * 8);
+    }
+    __syncthreads();
+    if (has0 || has1) {
+#pragma unroll 4
+      for (int d = dq; d < D; d += 4) {
+        const uint16_t x0 = tile[(2 * pi) * PITCH + d], x1 = tile[(2 * pi + 1) * PITCH + d];
+        if (pair) {
+          *reinterpret_cast<uint32_t*>(dst + b0 + int64_t(d) * P) =
+              uint32_t(x0) | (uint32_t(x1) << 16);
+        } else {
+          if (has0) dst[b0 + int64_t(d) * P] = x0;
+          if (has1) dst[b1 + int64_t(d) * P] = x1;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Gather: LDS tile [D][16 tokens] (row pitch 24: 16-byte aligned rows for the tile loads).
+// Lane (t = lane & 15, ci = lane >> 4) builds 16-byte chunks c = 4co + ci of token t's row, so
+// one store instruction writes 64 contiguous bytes of each of 16 token rows.
+template <int D>
+__global__ __launch_bounds__(64) void kv_gather16_kernel(
+    uint16_t* __restrict__ ko, uint16_t* __restrict__ vo, const uint16_t* __restrict__ kp,
+    const uint16_t* __restrict__ vp, const int32_t* __restrict__ bt, int64_t bt_stride,
+    const int64_t* __restrict__ cu, int H, int64_t num_pages) {
+  constexpr int P = T16_P, PITCH = 24, CH = D / 8;
+  __shared__ __align__(16) uint16_t tile[D * PITCH];
+  const int lane = threadIdx.x;
+  const int lp = blockIdx.x, b = blockIdx.y, h = blockIdx.z;
+  const int64_t row0 = cu[b];
+  const int64_t len = cu[b + 1] - row0;
+  if (int64_t(lp) * P >= len || lp >= bt_stride) return;
+  const int ntok = int(min<int64_t>(P, len - int64_t(lp) * P));
+  const int64_t phys = bt[int64_t(b) * bt_stride + lp];
+  const bool ok = phys >= 0 && phys < num_pages;
+  const int t = lane & 15, ci = lane >> 4;
+  for (int pass = 0; pass < 2; ++pass) {
+    const uint16_t* src = (pass == 0 ? kp : vp) + (phys * H + h) * int64_t(D) * P;
+    uint16_t* dst = pass == 0 ? ko : vo;
+    for (int q = lane; q < 2 * D; q += 64) {  // 16-byte chunk q: row d = q / 2, tokens 8(q&1)..
+      uint4 w = make_uint4(0u, 0u, 0u, 0u);
+      if (ok) w = *reinterpret_cast<const uint4*>(src + q * 8);
+      *reinterpret_cast<uint4*>(&tile[(q >> 1) * PITCH + (q & 1) * 8]) = w;
+    }
+    __syncthreads();
+    if (t < ntok) {
+      uint16_t* orow = dst + (row0 + int64_t(lp) * P + t) * int64_t(H) * D + int64_t(h) * D;
+#pragma unroll
+      for (int co = 0; co < CH / 4; ++co) {
+        const int c = 4 * co + ci;
+        uint32_t wv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          wv[j] = uint32_t(tile[(8 * c + 2 * j) * PITCH + t]) |
+                  (uint32_t(tile[(8 * c + 2 * j + 1) * PITCH + t]) << 16);
+        *reinterpret_cast<uint4*>(orow + 8 * c) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -185,6 +314,21 @@ extern "C" int pia_kv_scatter(const void* k, const void* v, void* k_pages, void*
   if (blocks > 0x7fffffff) return fail(PIA_EINVAL, "kv_scatter: too many tokens");
   const int64_t total_slots = num_pages * page_size;
   hipStream_t s = as_stream(stream);
+  if (elem_bytes == 2 && page_size == T16_P &&
+      (head_dim == 64 || head_dim == 128 || head_dim == 256) && aligned(k, 16) &&
+      aligned(v, 16) && k_token_stride % 8 == 0 && v_token_stride % 8 == 0 &&
+      aligned(k_pages, 4) && aligned(v_pages, 4) && num_kv_heads <= 65535) {
+    dim3 grid = dim3(unsigned(blocks), unsigned(num_kv_heads));
+#define PIA_SC16(DD)                                                                           \
+  hipLaunchKernelGGL(kv_scatter16_kernel<DD>, grid, dim3(64), 0, s, (const uint16_t*)k,        \
+                     (const uint16_t*)v, (uint16_t*)k_pages, (uint16_t*)v_pages, slot_mapping, \
+                     num_tokens, k_token_stride, v_token_stride, num_kv_heads, total_slots)
+    if (head_dim == 64) PIA_SC16(64);
+    else if (head_dim == 128) PIA_SC16(128);
+    else PIA_SC16(256);
+#undef PIA_SC16
+    return check_launch("kv_scatter");
+  }
   if (elem_bytes == 2)
     hipLaunchKernelGGL(kv_scatter_kernel<uint16_t>, dim3(unsigned(blocks), unsigned(page_size)),
                        dim3(256), smem, s,
@@ -217,6 +361,21 @@ extern "C" int pia_kv_gather(void* k_out, void* v_out, const void* k_pages, cons
   const int64_t pages = std::min<int64_t>(ceil_div(max_seq_len, page_size), bt_stride);
   if (pages > 0x7fffffff) return fail(PIA_EINVAL, "kv_gather: too many pages");
   hipStream_t s = as_stream(stream);
+  if (elem_bytes == 2 && page_size == T16_P &&
+      (head_dim == 64 || head_dim == 128 || head_dim == 256) && aligned(k_pages, 16) &&
+      aligned(v_pages, 16) && aligned(k_out, 16) && aligned(v_out, 16) &&
+      num_kv_heads <= 65535) {
+    dim3 grid16 = dim3(unsigned(pages), unsigned(num_seqs), unsigned(num_kv_heads));
+#define PIA_GA16(DD)                                                                           \
+  hipLaunchKernelGGL(kv_gather16_kernel<DD>, grid16, dim3(64), 0, s, (uint16_t*)k_out,         \
+                     (uint16_t*)v_out, (const uint16_t*)k_pages, (const uint16_t*)v_pages,     \
+                     block_tables, bt_stride, cu_seqlens, num_kv_heads, num_pages)
+    if (head_dim == 64) PIA_GA16(64);
+    else if (head_dim == 128) PIA_GA16(128);
+    else PIA_GA16(256);
+#undef PIA_GA16
+    return check_launch("kv_gather");
+  }
   dim3 grid = dim3(unsigned(pages), unsigned(num_seqs));
   if (elem_bytes == 2)
     hipLaunchKernelGGL(kv_gather_kernel<uint16_t>, grid, dim3(256), smem, s, (uint16_t*)k_out,

@@ -16,4 +16,4 @@ void set_error(const char* fmt, ...) {
 
 extern "C" const char* pia_last_error(void) { return pia::g_last_error; }
 
-extern "C" int pia_abi_version(void) { return 2; }
+extern "C" int pia_abi_version(void) { return 3; }

@@ -48,7 +48,7 @@ def moe_forward_sparse(hidden: torch.Tensor, experts: dict[int, ExpertWeights],
     # block_size 1: every expert's rows are exactly contiguous (no padding rows).
     sorted_ids, _, npp, route_pos = moe_align_block_size(ids32, 1, num_experts,
                                                         return_route_pos=True)
-    x_perm = moe_permute(hidden, sorted_ids, npp, k)
+    x_perm = moe_permute(hidden, sorted_ids, npp, k, route_pos=route_pos)
     # Per-expert row ranges: one host read of the routed ids (the plan itself stays on device).
     counts = torch.bincount(ids32.view(-1).clamp(min=-1).add(1), minlength=num_experts + 2)
     counts = counts[1:num_experts + 2].cpu().tolist()

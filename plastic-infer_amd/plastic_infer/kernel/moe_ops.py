@@ -81,12 +81,19 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: i
 
 def moe_permute(hidden: torch.Tensor, sorted_token_ids: torch.Tensor,
                 num_tokens_post_pad: torch.Tensor, topk: int,
-                out: torch.Tensor | None = None) -> torch.Tensor:
+                out: torch.Tensor | None = None,
+                route_pos: torch.Tensor | None = None) -> torch.Tensor:
     """x_perm[r] = hidden[sorted_token_ids[r] // topk] for r < num_tokens_post_pad; padding
     rows are zero. Output has sorted_token_ids.numel() rows (rows past num_tokens_post_pad are
-    left as allocated). Bit-exact."""
+    left as allocated). Bit-exact. With route_pos (moe_align_block_size's inverse map) every
+    token row is read once and written to all its routes."""
     dev = N.require_device(hidden, sorted_token_ids, num_tokens_post_pad,
                            names=("hidden", "sorted_token_ids", "num_tokens_post_pad"))
+    if route_pos is not None:
+        N.require_device(route_pos, names=("route_pos",))
+        if route_pos.dtype != torch.int32 or route_pos.numel() != hidden.shape[0] * topk:
+            raise ValueError("route_pos must be int32 [num_tokens * topk]")
+        route_pos = route_pos.contiguous()
     if hidden.dim() != 2 or hidden.stride(1) != 1:
         raise ValueError("hidden must be [T, H] with contiguous rows")
     T, H = hidden.shape
@@ -97,7 +104,7 @@ def moe_permute(hidden: torch.Tensor, sorted_token_ids: torch.Tensor,
         raise ValueError("out must be contiguous [len(sorted_token_ids), H] of hidden's dtype")
     eb = hidden.element_size()
     N.call("pia_moe_permute", out.data_ptr(), hidden.data_ptr(), sorted_token_ids.data_ptr(),
-           num_tokens_post_pad.data_ptr(), rows, T * topk, topk, H * eb,
+           N.ptr(route_pos), num_tokens_post_pad.data_ptr(), rows, T * topk, topk, H * eb,
            hidden.stride(0) * eb, N.stream_of(dev))
     return out
 

@@ -3,6 +3,7 @@ against the oracle — bit-exact (pure copies)."""
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -67,6 +68,55 @@ def test_scatter_strided_rows_and_tile_path(dev):
     gsrc = src.to(dev)
     kv_scatter(gsrc[:, 0], gsrc[:, 2], gk, gv, torch.tensor(slots, device=dev))
     assert torch.equal(gk.cpu(), ref_k) and torch.equal(gv.cpu(), ref_v)
+
+
+@pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (64, torch.float16),
+                                     (256, torch.bfloat16)])
+def test_scatter16_slot_patterns(dev, D, dtype):
+    """16-bit pools with 16-token pages: runs starting at odd offsets and crossing pages, a run
+    of whole pages, scattered decode slots, padding and out-of-range slots, a strided source."""
+    g = torch.Generator().manual_seed(15 + D)
+    H, P, N_ = 3, 16, 40
+    runs = (list(range(16 * 5 + 3, 16 * 5 + 3 + 37))      # offset 3, crosses three pages
+            + list(range(16 * 20, 16 * 22))               # two whole pages
+            + [16 * 30 + 7, -1, 16 * 31, N_ * P + 5, 16 * 33 + 15, 16 * 34 + 14, 16 * 34 + 15]
+            + list(range(16 * 36 + 1, 16 * 36 + 12)))     # odd start inside one page
+    n = len(runs)
+    src = torch.randn(n, 2, H, D, generator=g).to(dtype)
+    k, v = src[:, 0], src[:, 1]                        # token stride 2*H*D
+    kp = torch.randn(N_, H, D, P, generator=g).to(dtype)
+    vp = torch.randn(N_, H, D, P, generator=g).to(dtype)
+    ref_k, ref_v = kp.clone(), vp.clone()
+    OP.scatter_slots(k, v, ref_k, ref_v, [s if s < N_ * P else -1 for s in runs])
+    gk, gv, gsrc = kp.to(dev), vp.to(dev), src.to(dev)
+    kv_scatter(gsrc[:, 0], gsrc[:, 1], gk, gv, torch.tensor(runs, device=dev))
+    assert torch.equal(gk.cpu(), ref_k) and torch.equal(gv.cpu(), ref_v)
+
+
+def test_gather16_tables_with_invalid_pages(dev):
+    g = torch.Generator().manual_seed(16)
+    H, D, P = 4, 128, 16
+    kp = torch.randn(30, H, D, P, generator=g).to(torch.bfloat16)
+    vp = torch.randn(30, H, D, P, generator=g).to(torch.bfloat16)
+    tables = [[7, 3, 29], [12], [0, 5, -1, 8], []]
+    lens = [40, 16, 60, 0]
+    bt = torch.full((4, 4), -1, dtype=torch.int32)
+    for b, t in enumerate(tables):
+        bt[b, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    cu = torch.tensor([0] + list(np.cumsum(lens)))
+    k, v = kv_gather(kp.to(dev), vp.to(dev), bt.to(dev), cu.to(dev), 64)
+    for b, t in enumerate(tables):
+        if not lens[b]:
+            continue
+        ok = [p if p >= 0 else 0 for p in t]
+        rk, rv = OP.gather_paged_kv(kp, vp, ok, P, lens[b])
+        rk, rv = rk[0].clone(), rv[0].clone()
+        for i, p in enumerate(t):
+            if p < 0:                                   # an invalid page reads as zeros
+                rk[i * P:(i + 1) * P] = 0
+                rv[i * P:(i + 1) * P] = 0
+        assert torch.equal(k[cu[b]:cu[b + 1]].cpu(), rk)
+        assert torch.equal(v[cu[b]:cu[b + 1]].cpu(), rv)
 
 
 def test_gather_matches_oracle_and_empty(dev):

@@ -72,6 +72,23 @@ def test_align_random_bit_exact(dev, seed, T, k, E, bs):
     _check_align(dev, rng.integers(-1, E + 2, size=(T, k)).astype(np.int32), bs, E)
 
 
+@pytest.mark.parametrize("seed,T,k,E,bs,H,dtype", [(5, 300, 8, 16, 16, 100, torch.float32),
+                                                   (6, 77, 3, 5, 7, 2048, torch.bfloat16),
+                                                   (7, 64, 64, 100, 4, 24, torch.float16)])
+def test_permute_token_major_matches_row_major(dev, seed, T, k, E, bs, H, dtype):
+    rng = np.random.default_rng(seed)
+    ids = torch.tensor(rng.integers(-1, E + 1, size=(T, k)), dtype=torch.int32, device=dev)
+    hidden = torch.randn(T, H, generator=torch.Generator().manual_seed(seed)).to(dtype).to(dev)
+    s, _, npp, pos = moe_align_block_size(ids, bs, E, return_route_pos=True)
+    a = moe_permute(hidden, s, npp, k)
+    b = torch.full_like(a, 3.0)
+    moe_permute(hidden, s, npp, k, out=b, route_pos=pos)
+    n = int(npp.item())
+    assert torch.equal(a[:n], b[:n]) and bool((b[n:] == 3.0).all())
+    rs, _, rnpp, _ = OM.moe_align_block_size(ids.cpu().numpy(), bs, E)
+    assert torch.equal(b[:rnpp].cpu(), OM.permute(hidden.cpu(), rs, rnpp, k))
+
+
 def test_align_empty(dev):
     s, e, npp = moe_align_block_size(torch.empty(0, 8, dtype=torch.int32, device=dev), 16, 128)
     assert int(npp.item()) == 0 and s.numel() == 0
@@ -87,6 +104,11 @@ def test_permute_combine_config4(dev):
     rs, _, rnpp, rpos = OM.moe_align_block_size(ids.numpy(), 64, 128)
     ref_xp = OM.permute(wl.hidden, rs, rnpp, k)
     assert torch.equal(xp[:rnpp].cpu(), ref_xp)
+    # token-major path (each token row read once): same rows, and rows past npp untouched
+    xt = torch.full_like(xp, 7.0)
+    moe_permute(hidden, s, npp, k, out=xt, route_pos=pos)
+    assert torch.equal(xt[:rnpp].cpu(), ref_xp)
+    assert bool((xt[rnpp:] == 7.0).all())
     out = moe_unpermute(xp, pos, w.to(dev), T, k)              # identity expert stand-in
     ref = OM.unpermute(ref_xp, rpos, w.numpy(), T, k, torch.bfloat16)
     assert torch.equal(out.cpu(), ref)
