@@ -15,6 +15,8 @@ reference torch path on this host's cores, on a bounded sample of the same input
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-sample-seqs S] [--no-cpu-baseline]
   python bench.py --calibrate-copy     # 1 GiB read + 1 GiB write elementwise copy, three times:
                                        # the known-size reference for HBM byte counters
+  python bench.py --workload decode-gqa8     # Qwen3-30B-A3B attention layer: 64 x 4096 tokens,
+                                             # 32 q / 4 kv heads (GQA 8)
   python bench.py --workload prefill-write   # ragged chunked-prefill KV write + gather back
                                              # (8 sequences, S ~ U[256, 4096], seed 3)
   python bench.py --workload moe-permute     # Qwen3-30B-A3B routing: top-8 of 128 experts,
@@ -380,6 +382,61 @@ def _cpu_moe(torch, hidden, logits, step_bytes) -> dict:
                       f"{t * 1e3:.1f} ms", "cpu_model": model, "physical_cores": phys}
 
 
+def bench_decode_gqa8(torch, dev, args) -> dict:
+    """Qwen3-30B-A3B attention layer at its decode shape: 32 q heads over 4 kv heads (GQA 8),
+    head_dim 128, bf16, page 16; 64 sequences of 4096 tokens in a seeded random page
+    permutation of a 20,000-page pool. One step = kv_scatter of the 64 new rows + paged
+    decode attention."""
+    from plastic_infer.kernel import decode_workspace_bytes, kv_scatter, paged_decode_attention
+
+    b, hq, hkv, L, npool = 64, 32, 4, 4096, 20_000
+    g = torch.Generator().manual_seed(6)
+    lens = torch.full((b,), L, dtype=torch.int64)
+    n_pages = (lens + P - 1) // P
+    perm = torch.randperm(npool, generator=g)
+    bt = perm[: b * int(n_pages[0])].view(b, -1).to(torch.int32)
+    last = lens - 1
+    slots = bt[torch.arange(b), last // P].to(torch.int64) * P + last % P
+    gd = torch.Generator(device=dev).manual_seed(6)
+    kp = torch.randn(npool, hkv, D, P, generator=gd, device=dev).to(torch.bfloat16)
+    vp = torch.randn(npool, hkv, D, P, generator=gd, device=dev).to(torch.bfloat16)
+    kn = torch.randn(b, hkv, D, generator=gd, device=dev).to(torch.bfloat16)
+    vn = torch.randn(b, hkv, D, generator=gd, device=dev).to(torch.bfloat16)
+    q = torch.randn(b, hq, D, generator=gd, device=dev).to(torch.bfloat16)
+    out = torch.empty(b, hq, D, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(max(1, decode_workspace_bytes(b, hq, hkv, D, P, bt.shape[1])),
+                     dtype=torch.uint8, device=dev)
+    bt_d, lens_d, slots_d = bt.to(dev), lens.to(torch.int32).to(dev), slots.to(dev)
+
+    def step(ev):
+        if ev:
+            ev[0].record()
+        kv_scatter(kn, vn, kp, vp, slots_d)
+        if ev:
+            ev[1].record()
+        paged_decode_attention(q, kp, vp, bt_d, lens_d, out=out, workspace=ws)
+        if ev:
+            ev[2].record()
+
+    ms, (sc_ms, at_ms), wall = _phase_timer(torch, dev, step, 2, args.steps, args.warmup)
+    kv_row = 2 * hkv * D * 2
+    attn_bytes = b * L * kv_row + b * hq * D * 2 * 2 + int(n_pages.sum()) * 4 + b * 4
+    sc_bytes = b * kv_row * 2 + b * 8
+    gbps = (attn_bytes + sc_bytes) / (ms / 1e3) / 1e9
+    a_gbps = attn_bytes / (at_ms / 1e3) / 1e9
+    return _result(
+        "KV scatter + paged decode-attn GB/s (GQA 8)", gbps, "GB/s", args, ms, "bf16",
+        {"workload": "qwen3-30b-a3b attention layer decode: 64 seqs x 4096 tokens, 32 q / 4 kv "
+                     "heads, head_dim 128, page 16", "batch": b, "context_len": L},
+        {"tokens_per_s": round(b / (ms / 1e3), 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+         "bytes_per_step": attn_bytes + sc_bytes, "scatter_ms": round(sc_ms, 4),
+         "attention_ms": round(at_ms, 4), "wall_s_timed": round(wall, 4)},
+        {"kernel": "paged_decode_bf16_d128p16<8> + paged_decode_reduce (one attention call)",
+         "bound": "hbm", "achieved": round(a_gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+         "frac": round(a_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+         "algorithmic_bytes_per_launch": attn_bytes, "avg_launch_ms": round(at_ms, 4)})
+
+
 XS_L, XS_E, XS_H, XS_I, XS_B, XS_K, XS_SLOTS, XS_SEED = 48, 128, 2048, 768, 64, 8, 3072, 5
 _PINNED_KEEP = []
 
@@ -531,8 +588,8 @@ def main() -> int:
     ap.add_argument("--cpu-sample-seqs", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
-    ap.add_argument("--workload", choices=("decode", "prefill-write", "moe-permute",
-                                           "expert-stream"), default="decode")
+    ap.add_argument("--workload", choices=("decode", "decode-gqa8", "prefill-write",
+                                           "moe-permute", "expert-stream"), default="decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the paged decode path on ONE GPU (per-GPU shard of a "
@@ -549,8 +606,8 @@ def main() -> int:
     if args.calibrate_copy:
         return calibrate_copy(torch, dev)
     if args.workload != "decode":
-        run = {"prefill-write": bench_prefill_write, "moe-permute": bench_moe_permute,
-               "expert-stream": bench_expert_stream}[args.workload]
+        run = {"decode-gqa8": bench_decode_gqa8, "prefill-write": bench_prefill_write,
+               "moe-permute": bench_moe_permute, "expert-stream": bench_expert_stream}[args.workload]
         print(f"bench: workload {args.workload}", file=sys.stderr, flush=True)
         print(json.dumps(run(torch, dev, args)), flush=True)
         return 0
