@@ -70,7 +70,7 @@ int pia_kv_scatter(const void* k, const void* v, void* k_pages, void* v_pages,
                    int elem_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
- * (a5) Block-table gather into contiguous rows, batched over sequences.
+ * Block-table gather into contiguous rows, batched over sequences.
  * Replaces gather_paged_kv (reference: src/plastic_infer/exec/attention.py:103-148):
  *     k_out[cu_seqlens[b] + t, h, d] = k_pages[block_tables[b, t / P], h, d, t % P]
  * for t < cu_seqlens[b+1] - cu_seqlens[b]. max_seq_len bounds the grid (tokens beyond a row's
@@ -96,7 +96,7 @@ int pia_kv_pages_chunk_copy(void* chunk, void* pages, const int64_t* page_ids,
                             int elem_bytes, int to_chunk, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
- * (a6) Paged GQA decode attention, batched: one query row per sequence.
+ * Paged GQA decode attention, batched: one query row per sequence.
  * Per-row semantics of paged_attention_v1(q[b][None,None], ..., kv_num_tokens=L_b, causal=False)
  * (reference: src/plastic_infer/exec/attention.py:151-190, decode call
  * src/plastic_infer/exec/runner_paged.py:253-255): head hq reads kv head hq / (H / Hkv),
@@ -142,7 +142,7 @@ int pia_paged_attention(void* out, const void* q, const void* k_pages, const voi
                         int64_t num_pages, float scale, int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
- * (a8) Router: top-k expert selection per token.
+ * Router: top-k expert selection per token.
  * mode 0 = _torch_fused_topk (reference: src/plastic_infer/moe/fused.py:11-30):
  *     p = softmax(float(logits)); (w, ids) = topk(p, k); w /= sum(w) if renormalize.
  * mode 1 = topk_route (reference: src/plastic_infer/exec/moe.py:19-38):
@@ -156,7 +156,7 @@ int pia_moe_topk(float* topk_weights, int32_t* topk_ids, const void* logits, int
                  int64_t num_token_non_padded, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
- * (a9) Permute plan (moe_align_block_size, reference: src/plastic_infer/moe/fused.py:48-94,
+ * Permute plan (moe_align_block_size, reference: src/plastic_infer/moe/fused.py:48-94,
  * semantics src/plastic_infer/kernel/triton/moe_align.py:9-20,216-239).
  * effective_E = num_experts + 1 (ids in [0, num_experts] are routed, others dropped).
  *   count[e], padded cumsum in multiples of block_size, num_tokens_post_pad = cumsum[E+1],
@@ -209,7 +209,44 @@ int pia_moe_sum_reduce(void* out, const void* in, int64_t num_tokens, int topk, 
                        int dtype, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
- * (a14) Row index copy kernel (fast_index_copy, reference
+ * Grouped expert GEMM over a permute plan, one of the two GEMMs of the fused experts FFN
+ * (fused_experts_impl / fused_experts_decode_impl, reference src/plastic_infer/moe/fused.py:
+ * 169-359; kernels src/plastic_infer/kernel/triton/fused_moe.py:156-302 and
+ * src/plastic_infer/kernel/triton/decode_moe.py:6-75; the activation of
+ * src/plastic_infer/kernel/triton/activation.py:63-113 fused into the first GEMM).
+ * For every plan row p < min(*num_tokens_post_pad, max_num_tokens_padded) holding a route
+ * r = sorted_token_ids[p] < numel, with e = expert_ids[p / block_m] in [0, num_experts):
+ *     acc[n] = sum_k a[(r / a_div) * lda + k] * w[(e * n_rows + n) * k_dim + k]   (fp32)
+ *     activation PIA_ACT_NONE:  out[r * ldo + n] = round(acc[n] * w_r)          n < n_rows
+ *     activation X:             g = round(acc[n] * w_r), u = round(acc[n_rows/2 + n] * w_r),
+ *                               out[r * ldo + n] = round(X(g) * u)              n < n_rows / 2
+ * w_r = topk_weights[r] when mul_routed_weight != 0, else 1; round() is the storage dtype.
+ * Routes of a block whose expert is outside [0, num_experts) get zero rows. Storage: a, w, out
+ * bf16 or fp16 (dtype), topk_weights fp32 [numel]. k_dim and lda multiples of 8; a and w
+ * 16-byte aligned; block_m a multiple of 16. The first GEMM of the FFN is a_div = top_k
+ * (a = hidden [T, H]) with the activation; the second is a_div = 1 (a = the first GEMM's
+ * output [T*k, I]) without it, ldo = H, writing [T, k, H] for pia_moe_sum_reduce.
+ * ------------------------------------------------------------------------------------------- */
+#define PIA_ACT_NONE (-1)
+#define PIA_ACT_SILU 0
+#define PIA_ACT_GELU 1
+#define PIA_ACT_GELU_TANH 2
+int pia_moe_expert_gemm(void* out, const void* a, const void* w, const float* topk_weights,
+                        const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                        const int32_t* num_tokens_post_pad, int64_t max_num_tokens_padded,
+                        int block_m, int64_t numel, int a_div, int64_t lda, int num_experts,
+                        int n_rows, int k_dim, int64_t ldo, int activation,
+                        int mul_routed_weight, int dtype, void* stream);
+
+/* y[r, j] = round(act(x[r, j]) * x[r, d + j]) for x [rows, 2d], y [rows, d], bf16 or fp16
+ * (silu_and_mul / gelu_and_mul / gelu_tanh_and_mul, reference
+ * src/plastic_infer/kernel/triton/activation.py:63-150). activation: PIA_ACT_SILU, _GELU,
+ * _GELU_TANH. */
+int pia_act_and_mul(void* out, const void* x, int64_t rows, int64_t d, int activation, int dtype,
+                    void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Row index copy kernel (fast_index_copy, reference
  * src/plastic_infer/kernel/fast_index_copy.py:124-186, kernel .cuh:190-286):
  *     for i < n:  dst + dst_idx[i]*row_bytes  <-  src + src_idx[i]*row_bytes
  * n = min(*num_indices, length) when num_indices != NULL (device int64), else length.
@@ -252,7 +289,7 @@ int pia_copy_rows_async(void* dst, const int64_t* dst_rows, const void* src,
                         int64_t* copies_issued, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
- * (a15) Device-side LRU admission of a slot cache (lru_ensure, reference
+ * Device-side LRU admission of a slot cache (lru_ensure, reference
  * src/plastic_infer/kernel/lru_ensure.py:371-438, victim rule of its sequential kernel
  * :200-265; MoE use src/plastic_infer/moe/offload_kernels.py:19-40). Device arrays:
  *   slot_of_id [num_total] i32 (id -> slot or -1), id_of_slot [num_cached] i32 (-1 = empty),
@@ -272,7 +309,7 @@ int pia_lru_ensure(const int32_t* query, int64_t num_queries, int32_t* slot_of_i
                    int32_t* src_indices, int32_t* dst_indices, int64_t* num_copy,
                    int64_t* stats, int64_t id_base, void* stream);
 
-/* (a13) Slot-cache bookkeeping of OffloadMoeCache (reference
+/* Slot-cache bookkeeping of OffloadMoeCache (reference
  * src/plastic_infer/moe/offload_kernels.py:208-285, offload_cache.py:597-605):
  *   reset       every id non-resident, every slot empty with usage 0, step = 0, active_mask
  *               (NULL or i32[num_experts]) = 0, *num_indices = 0 (when non-NULL);
@@ -291,7 +328,7 @@ int pia_slot_cache_invalidate(int32_t* slot_of_id, int64_t num_total, int32_t* i
                               int64_t* usage, int64_t num_cached, int64_t slot_begin,
                               int64_t slot_end, void* stream);
 
-/* (a16) Prefill hit compaction (prefill_hit_compact, reference
+/* Prefill hit compaction (prefill_hit_compact, reference
  * src/plastic_infer/moe/offload_kernels.py:63-82,413-431): experts e < num_experts whose slot
  * slot_row[e] >= threshold, in expert order: dst[j] = buffer_base + e, src[j] = slot_row[e];
  * *num = count. */

@@ -1,6 +1,6 @@
-"""ORACLE (test infrastructure only): seeded synthetic inputs of the benchmark configurations.
+"""ORACLE (test infrastructure only): seeded synthetic inputs of the benchmark workloads.
 
-Generation rule: one torch.Generator('cpu') seeded with the configuration number; draws in the
+Generation rule: one torch.Generator("cpu") per workload with a fixed seed of its own; draws in the
 order lengths -> block permutation -> pools -> new K/V -> q, each drawn as fp32 N(0,1) and cast
 to bf16. Block tables are consecutive slices of one permutation of the pool's pages. Context
 lengths include the token written by this step.
@@ -59,7 +59,7 @@ def decode_workload(seed: int, num_pages: int, batch: int, len_lo: int, len_hi: 
                           page_size)
 
 
-def config1() -> DecodeWorkload:
+def decode_b32_small() -> DecodeWorkload:
     """4096-block pool, 32 sequences of 1..2048 tokens, 16 q heads / 8 kv heads, D 128."""
     return decode_workload(1, 4096, 32, 1, 2048, 16, 8)
 

@@ -1,0 +1,343 @@
+// Grouped expert GEMM of the routed MoE FFN and the *_and_mul activations (gfx950).
+//
+// pia_moe_expert_gemm computes, for every route r listed in a permute plan (sorted_token_ids,
+// expert_ids, num_tokens_post_pad of pia_moe_align_block_size):
+//     acc = A[r / a_div] . W[e]^T        e = expert of r's plan block, W[e] is [n_rows, K]
+// and stores one of two epilogues (w_r = topk_weights[r] when mul_routed_weight, else 1;
+// round() is the storage dtype, round to nearest even):
+//     act NONE   out[r, n] = round(acc[n] * w_r)                      n in [0, n_rows)
+//     act X      g = round(acc[n] * w_r), u = round(acc[n_rows/2 + n] * w_r)
+//                out[r, n] = round(X(g) * u)                          n in [0, n_rows/2)
+// These are the two GEMMs of the reference's fused experts
+// (src/plastic_infer/moe/fused.py:169-359; kernels src/plastic_infer/kernel/triton/fused_moe.py:
+// 156-302 and src/plastic_infer/kernel/triton/decode_moe.py:6-75), with the *_and_mul of
+// src/plastic_infer/kernel/triton/activation.py:63-113 fused into the first GEMM's epilogue at
+// the reference's rounding points: the GEMM output is rounded to the storage dtype before the
+// activation reads it, and the activation result is rounded again.
+//
+// Kernel: moe_gemm_splitk. A work item is (16 plan rows, one column tile): 64 W rows, which are
+// 64 output columns, or 32 gate rows plus the matching 32 up rows when the activation is fused.
+// The four waves of a workgroup split the K dimension in quarters; each wave runs
+// v_mfma_f32_16x16x32 (bf16 / f16) over its quarter with the operands loaded straight from
+// global memory into registers (lane l: plan row / W row l%16, K elements 8*(l/16) .. +7 of a
+// 32-wide chunk; A and B use the same K assignment, so every MFMA sums the same K set for both).
+// The four partial tiles meet in LDS and are summed in wave order (deterministic). Workgroups
+// are persistent over the items; W rows are streamed once per plan block, which is the HBM
+// bound at decode sizes (every expert's weights are read once per 16 routes it serves).
+#include "pia_internal.h"
+
+namespace pia {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int EG_ROWS = 16;       // plan rows per work item (MFMA M)
+constexpr int EG_WAVES = 4;       // waves per workgroup, one K quarter each
+constexpr int EG_U = 2;           // 32-wide K chunks per pipeline stage
+constexpr int EG_WGS_PER_CU = 4;  // persistent workgroups per compute unit
+
+// 16 bytes of zeros: the load source of masked-off lanes (plan padding, K tail, W row tail).
+__device__ __attribute__((aligned(16))) uint16_t g_zero8[8];
+
+template <int DT>
+__device__ __forceinline__ f32x4_t mfma_16x16x32(const uint4& a, const uint4& b, f32x4_t c) {
+  if constexpr (DT == PIA_DTYPE_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+template <int DT>
+__device__ __forceinline__ uint16_t to_dt(float v) {
+  if constexpr (DT == PIA_DTYPE_BF16) return f32_to_bf16(v);
+  else return f32_to_half(v);
+}
+template <int DT>
+__device__ __forceinline__ float from_dt(uint16_t x) {
+  if constexpr (DT == PIA_DTYPE_BF16) return bf16_to_f32(x);
+  else return half_to_f32(x);
+}
+
+// act(g) of the *_and_mul family: silu g/(1+e^-g); gelu 0.5g(1+erf(g/sqrt2));
+// gelu_tanh 0.5g(1+tanh(sqrt(2/pi)(g+0.044715g^3))).
+template <int ACT>
+__device__ __forceinline__ float act_fn(float g) {
+  if constexpr (ACT == PIA_ACT_SILU) {
+    return g / (1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+  } else if constexpr (ACT == PIA_ACT_GELU) {
+    return 0.5f * g * (1.0f + erff(g * 0.7071067811865476f));
+  } else {
+    return 0.5f * g * (1.0f + tanhf(0.7978845608028654f * (g + 0.044715f * g * g * g)));
+  }
+}
+
+template <int DT, int ACT>
+__global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_splitk(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ a, const uint16_t* __restrict__ w,
+    const float* __restrict__ topk_w, const int32_t* __restrict__ sorted,
+    const int32_t* __restrict__ expert_ids, const int32_t* __restrict__ npp, int64_t max_rows,
+    int64_t numel, int block_m, int a_div, int64_t lda, int num_experts, int n_rows, int K,
+    int64_t ldo, int n_tiles, int mulw) {
+  constexpr bool FUSED = ACT != PIA_ACT_NONE;
+  __shared__ float red[EG_WAVES][4][4][64];  // [wave][column block][row in quad][lane]
+  __shared__ int32_t blk_route[EG_ROWS];
+  __shared__ float blk_w[EG_ROWS];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int li = lane & 15, kg = lane >> 4;
+  const int64_t rows = min(max_rows, int64_t(npp[0]));
+  const int64_t items = ((rows + EG_ROWS - 1) / EG_ROWS) * n_tiles;
+  const int nch = (K + 31) >> 5;
+  const int cpw = (nch + EG_WAVES - 1) / EG_WAVES;
+  const int c0 = min(nch, wv * cpw), c1 = min(nch, c0 + cpw);
+  const int half = n_rows >> 1;
+  const uint16_t* zero = g_zero8;
+
+  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+    const int64_t mb = item / n_tiles;
+    const int t = int(item - mb * n_tiles);
+    const int e = expert_ids[(mb * EG_ROWS) / block_m];
+    const bool e_ok = e >= 0 && e < num_experts;
+    const int64_t p = mb * EG_ROWS + li;
+    const int64_t r = p < rows ? int64_t(sorted[p]) : numel;
+    const bool a_ok = r >= 0 && r < numel;
+    const uint16_t* arow = a + (a_ok ? (r / a_div) * lda : 0);
+    const uint16_t* wbase = w + (e_ok ? int64_t(e) * n_rows * K : 0);
+    const uint16_t* wrow[4];
+    bool w_ok[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      int n;
+      bool ok;
+      if constexpr (FUSED) {
+        const int col = t * 32 + (cb & 1) * 16 + li;
+        ok = col < half;
+        n = (cb < 2 ? 0 : half) + col;
+      } else {
+        n = t * 64 + cb * 16 + li;
+        ok = n < n_rows;
+      }
+      w_ok[cb] = ok;
+      wrow[cb] = wbase + int64_t(ok ? n : 0) * K;
+    }
+    f32x4_t acc[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    if (e_ok && c0 < c1) {
+      uint4 sa0[EG_U], sb0[EG_U][4], sa1[EG_U], sb1[EG_U][4];
+      // Masked lanes read the zero vector instead, so every load is issued unconditionally and
+      // the compiler can keep a whole stage in flight while the previous one is multiplied.
+      auto load = [&](uint4(&va)[EG_U], uint4(&vb)[EG_U][4], int c) {
+#pragma unroll
+        for (int u = 0; u < EG_U; ++u) {
+          const int cc = c + u;
+          const int k = cc * 32 + kg * 8;
+          const bool k_ok = cc < c1 && k < K;
+          va[u] = *reinterpret_cast<const uint4*>((k_ok && a_ok) ? arow + k : zero);
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb)
+            vb[u][cb] =
+                *reinterpret_cast<const uint4*>((k_ok && w_ok[cb]) ? wrow[cb] + k : zero);
+        }
+      };
+      auto mma = [&](const uint4(&va)[EG_U], const uint4(&vb)[EG_U][4]) {
+#pragma unroll
+        for (int u = 0; u < EG_U; ++u)
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma_16x16x32<DT>(va[u], vb[u][cb], acc[cb]);
+      };
+      load(sa0, sb0, c0);
+      for (int c = c0; c < c1; c += 2 * EG_U) {
+        load(sa1, sb1, c + EG_U);
+        mma(sa0, sb0);
+        load(sa0, sb0, c + 2 * EG_U);
+        mma(sa1, sb1);
+      }
+    }
+
+    __syncthreads();  // the previous item's epilogue has finished with red / blk_*
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[wv][cb][q][lane] = acc[cb][q];
+    if (tid < EG_ROWS) {
+      const int64_t pp = mb * EG_ROWS + tid;
+      const int64_t rr = pp < rows ? int64_t(sorted[pp]) : numel;
+      const bool ok = rr >= 0 && rr < numel;
+      blk_route[tid] = ok ? int32_t(rr) : -1;
+      blk_w[tid] = (mulw && ok) ? topk_w[rr] : 1.0f;
+    }
+    __syncthreads();
+
+    // MFMA output layout: lane l holds column l%16 of its block, rows 4*(l/16) + q.
+    if constexpr (!FUSED) {
+      const int cb = wv;
+      const int col = t * 64 + cb * 16 + li;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int row = kg * 4 + q;
+        float v = red[0][cb][q][lane];
+#pragma unroll
+        for (int x = 1; x < EG_WAVES; ++x) v += red[x][cb][q][lane];
+        const int32_t rr = blk_route[row];
+        if (rr >= 0 && col < n_rows) out[int64_t(rr) * ldo + col] = to_dt<DT>(v * blk_w[row]);
+      }
+    } else {
+      const int pb = wv & 1, qb = (wv >> 1) * 2;
+      const int col = t * 32 + pb * 16 + li;
+#pragma unroll
+      for (int q = qb; q < qb + 2; ++q) {
+        const int row = kg * 4 + q;
+        float g = red[0][pb][q][lane], u = red[0][pb + 2][q][lane];
+#pragma unroll
+        for (int x = 1; x < EG_WAVES; ++x) {
+          g += red[x][pb][q][lane];
+          u += red[x][pb + 2][q][lane];
+        }
+        const int32_t rr = blk_route[row];
+        if (rr >= 0 && col < half) {
+          const float wr = blk_w[row];
+          const float gr = from_dt<DT>(to_dt<DT>(g * wr));
+          const float ur = from_dt<DT>(to_dt<DT>(u * wr));
+          out[int64_t(rr) * ldo + col] = to_dt<DT>(act_fn<ACT>(gr) * ur);
+        }
+      }
+    }
+  }
+}
+
+// y[r, j] = round(act(x[r, j]) * x[r, d + j]) over [rows, 2d] -> [rows, d]; eight elements per
+// thread on 16-byte aligned rows, one otherwise.
+template <int DT, int ACT, int VEC>
+__global__ __launch_bounds__(256) void act_and_mul_kernel(uint16_t* __restrict__ y,
+                                                          const uint16_t* __restrict__ x,
+                                                          int64_t rows, int64_t d) {
+  const int64_t per_row = d / VEC;
+  const int64_t total = rows * per_row;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * 256) {
+    const int64_t r = i / per_row, j = (i - r * per_row) * VEC;
+    const uint16_t* xr = x + r * 2 * d;
+    uint16_t* yr = y + r * d;
+    if constexpr (VEC == 8) {
+      const uint4 gv = *reinterpret_cast<const uint4*>(xr + j);
+      const uint4 uv = *reinterpret_cast<const uint4*>(xr + d + j);
+      const uint16_t* g = reinterpret_cast<const uint16_t*>(&gv);
+      const uint16_t* u = reinterpret_cast<const uint16_t*>(&uv);
+      uint4 ov;
+      uint16_t* o = reinterpret_cast<uint16_t*>(&ov);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o[q] = to_dt<DT>(act_fn<ACT>(from_dt<DT>(g[q])) * from_dt<DT>(u[q]));
+      *reinterpret_cast<uint4*>(yr + j) = ov;
+    } else {
+      yr[j] = to_dt<DT>(act_fn<ACT>(from_dt<DT>(xr[j])) * from_dt<DT>(xr[d + j]));
+    }
+  }
+}
+
+}  // namespace
+}  // namespace pia
+
+using namespace pia;
+
+extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
+                                   const float* topk_weights, const int32_t* sorted_token_ids,
+                                   const int32_t* expert_ids, const int32_t* num_tokens_post_pad,
+                                   int64_t max_num_tokens_padded, int block_m, int64_t numel,
+                                   int a_div, int64_t lda, int num_experts, int n_rows, int k_dim,
+                                   int64_t ldo, int activation, int mul_routed_weight, int dtype,
+                                   void* stream) {
+  if (dtype != PIA_DTYPE_BF16 && dtype != PIA_DTYPE_F16)
+    return fail(PIA_EUNSUPPORTED, "moe_expert_gemm: dtype must be bf16 or fp16");
+  if (activation < PIA_ACT_NONE || activation > PIA_ACT_GELU_TANH)
+    return fail(PIA_EINVAL, "moe_expert_gemm: unknown activation");
+  if (max_num_tokens_padded < 0 || numel < 0 || a_div <= 0 || num_experts <= 0 || n_rows <= 0 ||
+      k_dim <= 0 || lda < k_dim || block_m <= 0)
+    return fail(PIA_EINVAL, "moe_expert_gemm: invalid size");
+  if (block_m % EG_ROWS)
+    return fail(PIA_EUNSUPPORTED, "moe_expert_gemm: block_m must be a multiple of 16");
+  if (k_dim % 8 || lda % 8)
+    return fail(PIA_EUNSUPPORTED, "moe_expert_gemm: K and the A row stride must be multiples of 8");
+  const bool fused = activation != PIA_ACT_NONE;
+  if (fused && n_rows % 2) return fail(PIA_EINVAL, "moe_expert_gemm: gate/up rows must be even");
+  const int out_cols = fused ? n_rows / 2 : n_rows;
+  if (ldo < out_cols) return fail(PIA_EINVAL, "moe_expert_gemm: output row stride too small");
+  if (max_num_tokens_padded == 0 || numel == 0) return 0;
+  if (max_num_tokens_padded >= 0x7fffffff || numel >= 0x7fffffff)
+    return fail(PIA_EINVAL, "moe_expert_gemm: sizes must fit int32");
+  if (!out || !a || !w || !sorted_token_ids || !expert_ids || !num_tokens_post_pad ||
+      (mul_routed_weight && !topk_weights))
+    return fail(PIA_EINVAL, "moe_expert_gemm: null pointer");
+  if (!aligned(a, 16) || !aligned(w, 16))
+    return fail(PIA_EINVAL, "moe_expert_gemm: A and W must be 16-byte aligned");
+  const int n_tiles = int(ceil_div(out_cols, fused ? 32 : 64));
+  const int64_t ub = ceil_div(max_num_tokens_padded, EG_ROWS) * n_tiles;
+  const unsigned grid = unsigned(std::min<int64_t>(ub, int64_t(device_cus()) * EG_WGS_PER_CU));
+  hipStream_t s = as_stream(stream);
+  uint16_t* o = reinterpret_cast<uint16_t*>(out);
+  const uint16_t* aa = reinterpret_cast<const uint16_t*>(a);
+  const uint16_t* ww = reinterpret_cast<const uint16_t*>(w);
+#define PIA_EG(DT, ACT)                                                                           \
+  hipLaunchKernelGGL((moe_gemm_splitk<DT, ACT>), dim3(grid), dim3(EG_WAVES * 64), 0, s, o, aa, ww, \
+                     topk_weights, sorted_token_ids, expert_ids, num_tokens_post_pad,             \
+                     max_num_tokens_padded, numel, block_m, a_div, lda, num_experts, n_rows,       \
+                     k_dim, ldo, n_tiles, mul_routed_weight ? 1 : 0)
+#define PIA_EG_ACT(DT)                                                                            \
+  switch (activation) {                                                                           \
+    case PIA_ACT_NONE: PIA_EG(DT, PIA_ACT_NONE); break;                                           \
+    case PIA_ACT_SILU: PIA_EG(DT, PIA_ACT_SILU); break;                                           \
+    case PIA_ACT_GELU: PIA_EG(DT, PIA_ACT_GELU); break;                                           \
+    default: PIA_EG(DT, PIA_ACT_GELU_TANH); break;                                                \
+  }
+  if (dtype == PIA_DTYPE_BF16) {
+    PIA_EG_ACT(PIA_DTYPE_BF16)
+  } else {
+    PIA_EG_ACT(PIA_DTYPE_F16)
+  }
+#undef PIA_EG_ACT
+#undef PIA_EG
+  return check_launch("moe_expert_gemm");
+}
+
+extern "C" int pia_act_and_mul(void* out, const void* x, int64_t rows, int64_t d, int activation,
+                               int dtype, void* stream) {
+  if (dtype != PIA_DTYPE_BF16 && dtype != PIA_DTYPE_F16)
+    return fail(PIA_EUNSUPPORTED, "act_and_mul: dtype must be bf16 or fp16");
+  if (activation < PIA_ACT_SILU || activation > PIA_ACT_GELU_TANH)
+    return fail(PIA_EINVAL, "act_and_mul: unknown activation");
+  if (rows < 0 || d < 0) return fail(PIA_EINVAL, "act_and_mul: invalid size");
+  if (rows == 0 || d == 0) return 0;
+  if (!out || !x) return fail(PIA_EINVAL, "act_and_mul: null pointer");
+  const bool vec = d % 8 == 0 && aligned(out, 16) && aligned(x, 16);
+  const int64_t work = rows * (vec ? d / 8 : d);
+  const unsigned grid =
+      unsigned(std::min<int64_t>(ceil_div(work, 256), int64_t(device_cus()) * 16));
+  hipStream_t s = as_stream(stream);
+  uint16_t* y = reinterpret_cast<uint16_t*>(out);
+  const uint16_t* xx = reinterpret_cast<const uint16_t*>(x);
+#define PIA_AM(DT, ACT)                                                                  \
+  if (vec)                                                                               \
+    hipLaunchKernelGGL((act_and_mul_kernel<DT, ACT, 8>), dim3(grid), dim3(256), 0, s, y, \
+                       xx, rows, d);                                                     \
+  else                                                                                   \
+    hipLaunchKernelGGL((act_and_mul_kernel<DT, ACT, 1>), dim3(grid), dim3(256), 0, s, y, \
+                       xx, rows, d)
+#define PIA_AM_ACT(DT)                                   \
+  switch (activation) {                                  \
+    case PIA_ACT_SILU: PIA_AM(DT, PIA_ACT_SILU); break;  \
+    case PIA_ACT_GELU: PIA_AM(DT, PIA_ACT_GELU); break;  \
+    default: PIA_AM(DT, PIA_ACT_GELU_TANH); break;       \
+  }
+  if (dtype == PIA_DTYPE_BF16) {
+    PIA_AM_ACT(PIA_DTYPE_BF16)
+  } else {
+    PIA_AM_ACT(PIA_DTYPE_F16)
+  }
+#undef PIA_AM_ACT
+#undef PIA_AM
+  return check_launch("act_and_mul");
+}

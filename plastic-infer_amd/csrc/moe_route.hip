@@ -296,6 +296,87 @@ __global__ __launch_bounds__(256) void moe_align_scatter(
   }
 }
 
+// Small plans (numel <= ALIGN_SMALL_MAX, the decode sizes) in one launch of one 1024-thread
+// block: ids and a per-expert count live in LDS; the exclusive scan and the fills are those of
+// moe_align_scan; a route's position is its expert's padded base plus the number of earlier
+// routes of that expert (ascending route index, the same plan as the three-launch path).
+constexpr int ALIGN_SMALL_MAX = 4096;
+constexpr int ALIGN_SMALL_MAX_E = 12288;  // cnt[] of 48 KiB next to the 16 KiB of ids
+
+__global__ __launch_bounds__(1024) void moe_align_small(
+    int32_t* __restrict__ sorted, int32_t* __restrict__ expert_ids, int32_t* __restrict__ npp_out,
+    int32_t* __restrict__ route_pos, const int32_t* __restrict__ ids, int numel, int E_eff, int bs,
+    int64_t max_padded) {
+  __shared__ __attribute__((aligned(16))) int32_t ids_lds[ALIGN_SMALL_MAX];
+  __shared__ int32_t wsum[16];
+  __shared__ int32_t total_lds;
+  extern __shared__ int32_t cnt[];  // [E_eff]: count, then the padded base plus routes placed
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < E_eff; e += 1024) cnt[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < numel; i += 1024) {
+    const int e = ids[i];
+    const bool ok = e >= 0 && e < E_eff;
+    ids_lds[i] = ok ? e : -1;
+    if (ok)
+      atomicAdd(&cnt[e], 1);
+    else if (route_pos)
+      route_pos[i] = -1;
+  }
+  __syncthreads();
+  const int per = (E_eff + 1023) / 1024;
+  const int e0 = min(E_eff, tid * per), e1 = min(E_eff, e0 + per);
+  int32_t mine = 0;
+  for (int e = e0; e < e1; ++e) mine += ((cnt[e] + bs - 1) / bs) * bs;
+  int32_t incl = mine;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int32_t t = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += t;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int32_t off = incl - mine;
+  for (int w = 0; w < wave; ++w) off += wsum[w];
+  if (tid == 1023) total_lds = off + mine;
+  __syncthreads();
+  const int32_t npp = total_lds;
+  for (int e = e0; e < e1; ++e) {
+    const int32_t c = cnt[e];
+    const int32_t padded = ((c + bs - 1) / bs) * bs;
+    for (int b = 0; b < padded / bs; ++b) expert_ids[off / bs + b] = e;
+    for (int i = c; i < padded; ++i) sorted[off + i] = numel;
+    cnt[e] = off;
+    off += padded;
+  }
+  if (tid == 0) npp_out[0] = npp;
+  for (int64_t i = npp + tid; i < max_padded; i += 1024) sorted[i] = numel;
+  const int64_t max_blocks = (max_padded + bs - 1) / bs;
+  for (int64_t i = npp / bs + tid; i < max_blocks; i += 1024) expert_ids[i] = -1;
+  __syncthreads();
+  for (int s0 = 0; s0 < numel; s0 += 1024) {
+    const int i = s0 + tid;
+    const int e = i < numel ? ids_lds[i] : -1;
+    int rank = 0;
+    if (e >= 0) {
+      // earlier routes of this round, four ids per LDS read (s0 is a multiple of 4)
+      const int4* v4 = reinterpret_cast<const int4*>(ids_lds + s0);
+      const int n = i - s0;
+      for (int j = 0; j < n; j += 4) {
+        const int4 v = v4[j >> 2];
+        rank += (v.x == e) + (j + 1 < n && v.y == e) + (j + 2 < n && v.z == e) +
+                (j + 3 < n && v.w == e);
+      }
+      const int32_t pos = cnt[e] + rank;
+      sorted[pos] = i;
+      if (route_pos) route_pos[i] = pos;
+    }
+    __syncthreads();
+    if (e >= 0) atomicAdd(&cnt[e], 1);
+    __syncthreads();
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Permute: a wave moves four destination rows (sixteen per 256-thread block) with the loads of
 // all four issued before their stores; 16-byte words when the row allows it. Rows past
@@ -559,6 +640,12 @@ extern "C" int pia_moe_align_block_size(int32_t* sorted_token_ids, int32_t* expe
                                                 numel * block_size))
     return fail(PIA_EINVAL, "moe_align: max_num_tokens_padded below the padded worst case");
   hipStream_t s = as_stream(stream);
+  if (numel <= ALIGN_SMALL_MAX && E_eff <= ALIGN_SMALL_MAX_E) {
+    hipLaunchKernelGGL(moe_align_small, dim3(1), dim3(1024), size_t(E_eff) * sizeof(int32_t), s,
+                       sorted_token_ids, expert_ids, num_tokens_post_pad, route_pos, topk_ids,
+                       int(numel), E_eff, block_size, max_num_tokens_padded);
+    return check_launch("moe_align_small");
+  }
   int32_t* chunk_off = reinterpret_cast<int32_t*>(workspace);
   int32_t* base = chunk_off + int64_t(ALIGN_MAX_CHUNKS) * E_eff;
   const int64_t csz = std::max<int64_t>(256, ceil_div(ceil_div(numel, ALIGN_MAX_CHUNKS), 256) * 256);

@@ -19,7 +19,6 @@
 //    rows per sequence with optional causal offsets. One wave per (query row, head); keys are
 //    processed 64 at a time (lane = key for QK, lane = head-dim element for PV).
 #include <algorithm>
-#include <atomic>
 
 #include "pia_internal.h"
 
@@ -956,19 +955,7 @@ bool fast_path(int dtype, int Hq, int Hkv, int D, int P) {
 
 // Waves of a stream launch: every CU at two single-wave workgroups per SIMD (CU count cached
 // per device), capped by the partial slots the workspace holds.
-int stream_waves() {
-  static std::atomic<int> cus_of[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  int cus = cus_of[dev].load(std::memory_order_relaxed);
-  if (cus <= 0) {
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-    cus_of[dev].store(cus, std::memory_order_relaxed);
-  }
-  return std::min(cus * SD_WAVES_PER_CU, SD_MAX_WAVES);
-}
+int stream_waves() { return std::min(device_cus() * SD_WAVES_PER_CU, SD_MAX_WAVES); }
 
 }  // namespace
 }  // namespace pia

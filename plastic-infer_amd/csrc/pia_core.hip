@@ -1,4 +1,6 @@
 // Library-level entry points: error reporting and ABI version.
+#include <atomic>
+
 #include "pia_internal.h"
 
 namespace pia {
@@ -12,8 +14,22 @@ void set_error(const char* fmt, ...) {
   va_end(ap);
 }
 
+int device_cus() {
+  static std::atomic<int> cus_of[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int cus = cus_of[dev].load(std::memory_order_relaxed);
+  if (cus <= 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cus_of[dev].store(cus, std::memory_order_relaxed);
+  }
+  return cus;
+}
+
 }  // namespace pia
 
 extern "C" const char* pia_last_error(void) { return pia::g_last_error; }
 
-extern "C" int pia_abi_version(void) { return 3; }
+extern "C" int pia_abi_version(void) { return 4; }

@@ -25,6 +25,9 @@ inline int check_hip(hipError_t e, const char* where) {
   return (int)e;
 }
 
+// Compute units of the current device (cached per device; 256 if the query fails).
+int device_cus();
+
 inline int check_launch(const char* where) { return check_hip(hipGetLastError(), where); }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

@@ -41,6 +41,9 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_moe_permute": (_I, [_P, _P, _P, _P, _P, _L, _L, _I, _L, _L, _P]),
     "pia_moe_unpermute": (_I, [_P, _P, _L, _P, _P, _L, _I, _I, _I, _P]),
     "pia_moe_sum_reduce": (_I, [_P, _P, _L, _I, _I, _I, _P]),
+    "pia_moe_expert_gemm": (_I, [_P, _P, _P, _P, _P, _P, _P, _L, _I, _L, _I, _L, _I, _I, _I, _L,
+                                 _I, _I, _I, _P]),
+    "pia_act_and_mul": (_I, [_P, _P, _L, _L, _I, _I, _P]),
     "pia_index_copy_rows": (_I, [_P, _P, _L, _P, _P, _L, _L, _P, _L, _I, _P]),
     "pia_index_copy_rows_multi": (_I, [_P, _P, _P, _I, _P, _P, _L, _P, _I, _P]),
     "pia_device_pointer": (_I, [_P, _P]),
@@ -52,7 +55,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_prefill_hit_compact": (_I, [_P, _P, _P, _P, _L, _L, _I, _P]),
 }
 
-EXPECTED_ABI = 3
+EXPECTED_ABI = 4
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

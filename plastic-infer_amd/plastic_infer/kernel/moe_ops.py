@@ -142,3 +142,57 @@ def moe_sum_reduce(input: torch.Tensor, output: torch.Tensor) -> None:
         raise ValueError("output must be [T, H] of input's dtype")
     N.call("pia_moe_sum_reduce", output.data_ptr(), input.data_ptr(), T, k, H,
            N.dtype_code(input.dtype), N.stream_of(dev))
+
+
+ACTIVATION_CODES = {"silu": 0, "gelu": 1, "gelu_tanh": 2}
+
+
+def moe_expert_gemm(a: torch.Tensor, w: torch.Tensor, topk_weights: torch.Tensor | None,
+                    sorted_token_ids: torch.Tensor, expert_ids: torch.Tensor,
+                    num_tokens_post_pad: torch.Tensor, block_m: int, numel: int, a_div: int,
+                    activation: str | None = None, mul_routed_weight: bool = False,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """One GEMM of the fused experts FFN over a permute plan (block_m a multiple of 16).
+
+    For every planned route r < numel of expert e: acc = a[r // a_div] . w[e]^T (fp32), then
+    activation None: out[r] = round(acc * w_r); activation X: out[r, n] =
+    round(X(round(acc[n] * w_r)) * round(acc[I + n] * w_r)) with I = w.shape[1] // 2.
+    w_r = topk_weights.flat[r] when mul_routed_weight, else 1. out is [numel, N or I] unless given
+    (a [*, N or I] view with unit column stride)."""
+    dev = N.require_device(a, w, sorted_token_ids, expert_ids, num_tokens_post_pad,
+                           names=("a", "w", "sorted_token_ids", "expert_ids",
+                                  "num_tokens_post_pad"))
+    if a.dim() != 2 or a.stride(1) != 1:
+        raise ValueError("a must be [rows, K] with contiguous rows")
+    if w.dim() != 3 or not w.is_contiguous():
+        raise ValueError("w must be contiguous [E, N, K]")
+    if a.dtype != w.dtype:
+        raise ValueError("a and w must share a dtype")
+    E, n_rows, K = w.shape
+    if a.shape[1] != K:
+        raise ValueError(f"a has {a.shape[1]} columns, w expects K = {K}")
+    if a_div <= 0 or a.shape[0] * a_div < numel:
+        raise ValueError(f"a needs ceil(numel / a_div) = {-(-numel // max(a_div, 1))} rows")
+    act = -1 if activation is None else ACTIVATION_CODES.get(activation)
+    if act is None:
+        raise ValueError(f"Unsupported activation: {activation}")
+    out_cols = n_rows if act < 0 else n_rows // 2
+    if out is None:
+        out = torch.empty(numel, out_cols, dtype=a.dtype, device=dev)
+    elif out.dim() != 2 or out.stride(1) != 1 or out.shape[1] != out_cols or \
+            out.shape[0] < numel or out.dtype != a.dtype:
+        raise ValueError(f"out must be [>= {numel}, {out_cols}] of a's dtype with unit column stride")
+    if mul_routed_weight:
+        if topk_weights is None or topk_weights.dtype != torch.float32 or \
+                not topk_weights.is_contiguous() or topk_weights.numel() != numel:
+            raise ValueError("topk_weights must be contiguous float32 with one weight per route")
+        N.require_device(topk_weights, names=("topk_weights",))
+    for name, t in (("sorted_token_ids", sorted_token_ids), ("expert_ids", expert_ids)):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous int32")
+    N.call("pia_moe_expert_gemm", out.data_ptr(), a.data_ptr(), w.data_ptr(),
+           N.ptr(topk_weights) if mul_routed_weight else None, sorted_token_ids.data_ptr(),
+           expert_ids.data_ptr(), num_tokens_post_pad.data_ptr(), sorted_token_ids.numel(),
+           block_m, numel, a_div, a.stride(0), E, n_rows, K, out.stride(0), act,
+           1 if mul_routed_weight else 0, N.dtype_code(a.dtype), N.stream_of(dev))
+    return out

@@ -48,8 +48,8 @@ def _oracle_decode_step(wl: W.DecodeWorkload, seqs=None):
                            wl.page_size)
 
 
-def test_decode_config1_fast_path(dev):
-    wl = W.config1()
+def test_decode_b32_fast_path(dev):
+    wl = W.decode_b32_small()
     got = _run_decode_step(wl, dev)
     ref = _oracle_decode_step(wl)
     err = (got.float() - ref.float()).abs().max().item()
@@ -134,7 +134,7 @@ def test_decode_stream_batch_over_one_launch(dev):
     assert err <= BF16_TOL, err
 
 
-def test_decode_config2_full_shape(dev):
+def test_decode_qwen3_8b_b256_full_shape(dev):
     """Qwen3-8B decode at full size (B = 256, L ~ U[512, 8192], 160k-page pool) generated on
     the device; five sequences (the longest, shortest and three seeded picks) are checked
     against the oracle from their own pages."""

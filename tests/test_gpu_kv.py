@@ -15,8 +15,8 @@ from plastic_infer.kv.kv_store import KVConfig, KVStore
 pytestmark = pytest.mark.gpu
 
 
-def test_decode_scatter_config1(dev):
-    wl = W.config1()
+def test_decode_scatter_b32(dev):
+    wl = W.decode_b32_small()
     kp, vp = wl.k_pages.clone(), wl.v_pages.clone()
     OP.scatter_slots(wl.k_new, wl.v_new, kp, vp, wl.slot_mapping.tolist())
     gk, gv = wl.k_pages.to(dev), wl.v_pages.to(dev)
@@ -24,7 +24,7 @@ def test_decode_scatter_config1(dev):
     assert torch.equal(gk.cpu(), kp) and torch.equal(gv.cpu(), vp)
 
 
-def test_prefill_scatter_and_gather_round_trip_config3(dev):
+def test_prefill_scatter_and_gather_round_trip_8seq(dev):
     wl = W.prefill_write_workload()
     H, D, P = wl.k.shape[1], wl.k.shape[2], wl.page_size
     kp = torch.zeros(wl.num_pages, H, D, P, dtype=torch.bfloat16)

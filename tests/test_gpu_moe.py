@@ -22,7 +22,7 @@ from plastic_infer.store.experts import ExpertWeights
 pytestmark = pytest.mark.gpu
 
 
-def test_router_config4_indices_bit_exact(dev):
+def test_router_t4096_e128_indices_bit_exact(dev):
     wl = W.moe_workload()
     w, ids = fused_topk(wl.hidden.to(dev), wl.logits.to(dev), wl.topk, True)
     rw, rids = OM.fused_topk(wl.logits, wl.topk, True)
@@ -66,7 +66,11 @@ def test_align_reference_docstring_example(dev):
 
 @pytest.mark.parametrize("seed,T,k,E,bs", [(0, 4096, 8, 128, 64), (1, 1, 8, 128, 16),
                                            (2, 300, 8, 128, 1), (3, 77, 3, 5, 7),
-                                           (4, 2000, 2, 1023, 16)])
+                                           (4, 2000, 2, 1023, 16),
+                                           # one-launch path at its limits and just past them
+                                           (5, 512, 8, 128, 16), (6, 513, 8, 128, 16),
+                                           (7, 64, 8, 3072, 16), (8, 64, 8, 12287, 16),
+                                           (9, 64, 8, 12288, 16)])
 def test_align_random_bit_exact(dev, seed, T, k, E, bs):
     rng = np.random.default_rng(seed)
     _check_align(dev, rng.integers(-1, E + 2, size=(T, k)).astype(np.int32), bs, E)
@@ -94,7 +98,7 @@ def test_align_empty(dev):
     assert int(npp.item()) == 0 and s.numel() == 0
 
 
-def test_permute_combine_config4(dev):
+def test_permute_combine_t4096(dev):
     wl = W.moe_workload()
     w, ids = OM.fused_topk(wl.logits, wl.topk, True)
     T, k = ids.shape
