@@ -54,7 +54,7 @@ const char* pia_last_error(void);
 int pia_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------
- * (a3/a4) Slot-mapped KV scatter.
+ * Slot-mapped KV scatter.
  * Replaces the per-token advanced-index store of _write_kv_layer
  * (reference: src/plastic_infer/exec/runner_paged.py:112-129) and of KVRequestCache.append_token
  * (src/plastic_infer/kv/kv_store.py:124-143):  for i < num_tokens with slot = slot_mapping[i],
@@ -126,7 +126,7 @@ int pia_paged_decode_attention(void* out, const void* q, int64_t q_seq_stride,
                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
- * (a6/a7) General paged attention over several query rows per sequence (prefill / chunked
+ * General paged attention over several query rows per sequence (prefill / chunked
  * prefill / the drop-in paged_attention_v1 and _attn_paged paths).
  * Rows of sequence b are q[cu_q[b] .. cu_q[b+1]) (cu_q NULL: one row per sequence). Row s of b
  * attends keys j < kv_lens[b]; when q_pos_offsets != NULL additionally j <= q_pos_offsets[b] + s
@@ -223,7 +223,10 @@ int pia_moe_sum_reduce(void* out, const void* in, int64_t num_tokens, int topk, 
  * w_r = topk_weights[r] when mul_routed_weight != 0, else 1; round() is the storage dtype.
  * Routes of a block whose expert is outside [0, num_experts) get zero rows. Storage: a, w, out
  * bf16 or fp16 (dtype), topk_weights fp32 [numel]. k_dim and lda multiples of 8; a and w
- * 16-byte aligned; block_m a multiple of 16. The first GEMM of the FFN is a_div = top_k
+ * 16-byte aligned; block_m a multiple of 16; a holds ceil(numel / a_div) rows. Small calls
+ * (decode: fewer than 4096 routes) run a split-K kernel over 16-row plan blocks that streams
+ * each expert's W once per block; larger calls run an LDS-tiled kernel over the experts present
+ * in the plan (128 x 128 tiles). The first GEMM of the FFN is a_div = top_k
  * (a = hidden [T, H]) with the activation; the second is a_div = 1 (a = the first GEMM's
  * output [T*k, I]) without it, ldo = H, writing [T, k, H] for pia_moe_sum_reduce.
  * ------------------------------------------------------------------------------------------- */
@@ -236,7 +239,12 @@ int pia_moe_expert_gemm(void* out, const void* a, const void* w, const float* to
                         const int32_t* num_tokens_post_pad, int64_t max_num_tokens_padded,
                         int block_m, int64_t numel, int a_div, int64_t lda, int num_experts,
                         int n_rows, int k_dim, int64_t ldo, int activation,
-                        int mul_routed_weight, int dtype, void* stream);
+                        int mul_routed_weight, int dtype, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
+/* Workspace of pia_moe_expert_gemm in bytes (4-byte aligned; holds the work list built from
+ * the plan on every call): (2 * ceil(max_num_tokens_padded / block_m) + 10) * 4. */
+int64_t pia_moe_expert_gemm_workspace_bytes(int64_t max_num_tokens_padded, int block_m);
 
 /* y[r, j] = round(act(x[r, j]) * x[r, d + j]) for x [rows, 2d], y [rows, d], bf16 or fp16
  * (silu_and_mul / gelu_and_mul / gelu_tanh_and_mul, reference

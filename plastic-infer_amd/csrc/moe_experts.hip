@@ -210,6 +210,297 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_splitk(
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// moe_gemm_tiled: the many-routes-per-expert case (prefill). A work item is one 128-row tile of
+// an expert's plan rows against one column tile of 256 W rows. Every item of one expert lands
+// on the same XCD (workgroup g runs on XCD g % 8 and the grid is a multiple of 8) and the
+// expert's items are adjacent in that XCD's list, row tiles of one column tile next to each
+// other: the row tiles that share a W tile run side by side, the column tiles that share the
+// expert's A rows run together, and both are fetched from HBM about once and shared through
+// that XCD's L2 (a compact per-XCD work list from moe_plan_segments, so no item is empty).
+// Per K step (64): A [128 plan rows x 64] gathered through the plan and B [256 W rows x 64] go
+// global -> registers -> LDS (16-byte chunks, eight threads per 128-byte row; XOR-swizzled LDS
+// rows), double buffered with one barrier per step and the global loads two steps ahead; eight
+// waves in a 2 x 4 arrangement each multiply 64 x 64 with v_mfma_f32_16x16x32 from LDS.
+// 16-row fragments past the tile's last real route are skipped. With the activation fused, the
+// W tile holds 128 gate and the matching 128 up rows, arranged so that each wave owns gate and
+// up of the same 32 columns.
+// ---------------------------------------------------------------------------------------------
+constexpr int TG_BM = 128, TG_BN = 256, TG_BK = 64;
+constexpr int TG_WM = 2, TG_WN = 4, TG_THREADS = 64 * TG_WM * TG_WN;  // 8 waves, 64 x 64 each
+constexpr int TG_XCDS = 8;
+// Buffer resources: word 3 of a raw (stride 0) buffer descriptor on gfx9 parts; a load whose
+// offset is at or past the descriptor's byte count returns zeros, which masks plan padding, the
+// K tail and the column tail without branches. TG_OOB is such an offset for every buffer here
+// (the host keeps A and each expert's W below 2 GiB).
+constexpr int TG_RSRC_WORD3 = 0x00020000;
+constexpr uint32_t TG_OOB = 0x80000000u;
+#ifndef PIA_EG_TILED_MIN_ROUTES
+#define PIA_EG_TILED_MIN_ROUTES 2048  // routes per call from which the tiled kernel is used
+#endif
+
+// Work list of moe_gemm_tiled from a plan (expert_ids of the used blocks ascend):
+//   seg_block[s]   first plan block of the s-th expert present, seg_block[n_seg] = used blocks
+//   seg_count[0]   n_seg
+//   seg_xstart[s]  items of the segments before s on s's XCD lane (segments s' = s mod 8)
+//   xcd_items[x]   items on XCD lane x
+// where a segment has ceil(rows / 128) row tiles times n_tiles column tiles of items.
+// One 1024-thread block: a compaction over the plan blocks, then waves 0..7 scan lanes 0..7.
+__global__ __launch_bounds__(1024) void moe_plan_segments(
+    int32_t* __restrict__ seg_block, int32_t* __restrict__ seg_count,
+    int32_t* __restrict__ seg_xstart, int32_t* __restrict__ xcd_items,
+    const int32_t* __restrict__ expert_ids, const int32_t* __restrict__ npp, int block_m,
+    int64_t max_rows, int n_tiles) {
+  __shared__ int32_t wsum[16];
+  __shared__ int32_t base_lds;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nblk = int(min(max_rows, int64_t(npp[0])) / block_m);
+  if (tid == 0) base_lds = 0;
+  __syncthreads();
+  for (int c0 = 0; c0 < nblk; c0 += 1024) {
+    const int b = c0 + tid;
+    const int first = (b < nblk && (b == 0 || expert_ids[b] != expert_ids[b - 1])) ? 1 : 0;
+    int incl = first;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += t;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int excl = base_lds + incl - first;
+    for (int w = 0; w < wave; ++w) excl += wsum[w];
+    if (first) seg_block[excl] = b;
+    __syncthreads();
+    if (tid == 1023) base_lds = excl + first;
+    __syncthreads();
+  }
+  const int n_seg = base_lds;
+  if (tid == 0) {
+    seg_block[n_seg] = nblk;
+    seg_count[0] = n_seg;
+  }
+  __syncthreads();  // seg_block (global, this block's writes) is complete and visible
+  if (wave < TG_XCDS) {
+    int carry = 0;
+    for (int i0 = 0; wave + TG_XCDS * i0 < n_seg; i0 += 64) {
+      const int sg = wave + TG_XCDS * (i0 + lane);
+      int items = 0;
+      if (sg < n_seg) {
+        const int64_t rows = int64_t(seg_block[sg + 1] - seg_block[sg]) * block_m;
+        items = int((rows + TG_BM - 1) / TG_BM) * n_tiles;
+      }
+      int incl = items;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
+      }
+      if (sg < n_seg) seg_xstart[sg] = carry + incl - items;
+      carry += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) xcd_items[wave] = carry;
+  }
+}
+
+// LDS tile rows are 64 elements (128 bytes, eight 16-byte chunks); chunk c of row r is stored
+// at chunk c ^ ((r >> 1) & 7), so that a 16-byte store of two rows by sixteen lanes and a
+// 16-byte MFMA operand read of sixteen rows each touch all 64 banks once.
+__device__ __forceinline__ int tg_swz(int r, int c) { return r * TG_BK + ((c ^ ((r >> 1) & 7)) << 3); }
+
+template <int DT, int ACT>
+__global__ __launch_bounds__(TG_THREADS, 1) void moe_gemm_tiled(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ a, const uint16_t* __restrict__ w,
+    const float* __restrict__ topk_w, const int32_t* __restrict__ sorted,
+    const int32_t* __restrict__ expert_ids, const int32_t* __restrict__ seg_block,
+    const int32_t* __restrict__ seg_count, const int32_t* __restrict__ seg_xstart,
+    const int32_t* __restrict__ xcd_items, int64_t numel, int block_m, int a_div, int64_t lda,
+    int num_experts, int n_rows, int K, int64_t ldo, int n_tiles, int mulw, uint32_t a_bytes) {
+  constexpr bool FUSED = ACT != PIA_ACT_NONE;
+  constexpr int AQ = TG_BM * 8 / TG_THREADS, BQ = TG_BN * 8 / TG_THREADS;  // chunks per thread
+  constexpr int RSTEP = TG_THREADS / 8;                                     // rows per pass
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][TG_BM * TG_BK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][TG_BN * TG_BK];
+  __shared__ int32_t tile_route[TG_BM];
+  __shared__ float tile_w[TG_BM];
+  const int tid = threadIdx.x, lane = tid & 63;
+  // wave index as a scalar, so that per-wave decisions compile to scalar branches
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wv / TG_WN, wn = wv % TG_WN;
+  const int li = lane & 15, kg = lane >> 4;
+  const int n_seg = seg_count[0];
+  const int half = n_rows >> 1;
+  // K steps, rounded up to even (a trailing step past K reads zeros)
+  const int nk = ((K + 2 * TG_BK - 1) / (2 * TG_BK)) * 2;
+  const __amdgpu_buffer_rsrc_t ares =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a), 0, int(a_bytes), TG_RSRC_WORD3);
+  // loader: 16-byte chunk (row lrow + RSTEP q, K chunk lc) of a tile
+  const int lrow = tid >> 3, lc = tid & 7, lk = lc * 8;
+  // this workgroup's XCD lane (workgroups are dealt to XCDs round robin; the grid is a
+  // multiple of 8) and its segments x, x + 8, ...
+  const int x = blockIdx.x % TG_XCDS;
+  const int nx = (n_seg - x + TG_XCDS - 1) / TG_XCDS;
+  const int total = xcd_items[x];
+
+  for (int p = blockIdx.x / TG_XCDS; p < total; p += gridDim.x / TG_XCDS) {
+    // segment of item p: the last of this lane's segments starting at or before p
+    int lo = 0, hi = nx - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (seg_xstart[x + TG_XCDS * mid] <= p) lo = mid;
+      else hi = mid - 1;
+    }
+    const int sg = x + TG_XCDS * lo;
+    const int b0 = seg_block[sg], b1 = seg_block[sg + 1];
+    const int64_t seg0 = int64_t(b0) * block_m, seg1 = int64_t(b1) * block_m;
+    const int mts = int((seg1 - seg0 + TG_BM - 1) / TG_BM);
+    const int local = p - seg_xstart[sg];
+    const int t = local / mts, mt = local - t * mts;  // row tiles of one column tile adjacent
+    const int e = expert_ids[b0];
+    const bool e_ok = e >= 0 && e < num_experts;  // else zero rows, as in moe_gemm_splitk
+    const int64_t m0 = seg0 + int64_t(mt) * TG_BM;
+
+    // this thread's W rows of the tile as byte offsets into the expert's W; rows past the
+    // tile's end read as zeros (offset beyond the buffer's range)
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(w + (e_ok ? int64_t(e) * n_rows * K : 0)), 0,
+        e_ok ? n_rows * K * 2 : 0, TG_RSRC_WORD3);
+    uint32_t boff[BQ];
+#pragma unroll
+    for (int q = 0; q < BQ; ++q) {
+      const int r = lrow + RSTEP * q;
+      int n;
+      bool ok;
+      if constexpr (FUSED) {
+        // each wave column owns 64 W rows: 32 gate rows and the matching 32 up rows
+        const int rw = r & 63, jj = rw >> 4;
+        const int col = t * (TG_BN / 2) + (r >> 6) * 32 + (jj & 1) * 16 + (rw & 15);
+        ok = col < half;
+        n = (jj < 2 ? 0 : half) + col;
+      } else {
+        n = t * TG_BN + r;
+        ok = n < n_rows;
+      }
+      boff[q] = ok ? uint32_t(n) * uint32_t(K) * 2u + uint32_t(lk) * 2u : TG_OOB;
+    }
+
+    __syncthreads();  // the previous tile's epilogue is done with tile_route / tile_w
+    bool live = false;
+    if (tid < TG_BM) {
+      const int64_t pr = m0 + tid;
+      const int64_t rr = pr < seg1 ? int64_t(sorted[pr]) : numel;
+      live = rr >= 0 && rr < numel;
+      tile_route[tid] = live ? int32_t(rr) : -1;
+      tile_w[tid] = (mulw && live) ? topk_w[rr] : 1.0f;
+    }
+    // real routes come first in an expert's plan rows, so the live rows are a prefix
+    const int nlive = __builtin_amdgcn_readfirstlane(__syncthreads_count(live));
+    uint32_t aoff[AQ];
+#pragma unroll
+    for (int q = 0; q < AQ; ++q) {
+      const int32_t rr = tile_route[lrow + RSTEP * q];
+      aoff[q] = rr >= 0 ? uint32_t(rr / a_div) * uint32_t(lda) * 2u + uint32_t(lk) * 2u : TG_OOB;
+    }
+    // K steps of 64: two register sets in flight ahead of the LDS buffer being multiplied
+    // (loads for step kt + 2 are issued while step kt is multiplied and kt + 1 is stored).
+    // Loads past K read as zeros (offset beyond the buffer), so every load is unconditional.
+    auto gload = [&](uint4(&ra)[AQ], uint4(&rb)[BQ], int k0) __attribute__((always_inline)) {
+      const bool k_ok = k0 + lk < K;
+      const uint32_t kb = uint32_t(k0) * 2u;
+#pragma unroll
+      for (int q = 0; q < AQ; ++q)
+        ra[q] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(ares, k_ok ? aoff[q] + kb : TG_OOB, 0, 0));
+#pragma unroll
+      for (int q = 0; q < BQ; ++q)
+        rb[q] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, k_ok ? boff[q] + kb : TG_OOB, 0, 0));
+    };
+    auto sstore = [&](const uint4(&ra)[AQ], const uint4(&rb)[BQ], int buf)
+                      __attribute__((always_inline)) {
+#pragma unroll
+      for (int q = 0; q < AQ; ++q)
+        *reinterpret_cast<uint4*>(&As[buf][tg_swz(lrow + RSTEP * q, lc)]) = ra[q];
+#pragma unroll
+      for (int q = 0; q < BQ; ++q)
+        *reinterpret_cast<uint4*>(&Bs[buf][tg_swz(lrow + RSTEP * q, lc)]) = rb[q];
+    };
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) acc[i][jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    bool frag_live[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) frag_live[i] = wm * 64 + i * 16 < nlive;
+    auto mma = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int s = 0; s < TG_BK / 32; ++s) {
+        const int c = s * 4 + kg;  // this lane's 16-byte K chunk of the step
+        uint4 fb[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          fb[jj] = *reinterpret_cast<const uint4*>(&Bs[buf][tg_swz(wn * 64 + jj * 16 + li, c)]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (!frag_live[i]) continue;
+          const uint4 fa =
+              *reinterpret_cast<const uint4*>(&As[buf][tg_swz(wm * 64 + i * 16 + li, c)]);
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) acc[i][jj] = mfma_16x16x32<DT>(fa, fb[jj], acc[i][jj]);
+        }
+      }
+    };
+
+    uint4 ra0[AQ], rb0[BQ], ra1[AQ], rb1[BQ];
+    gload(ra0, rb0, 0);
+    gload(ra1, rb1, TG_BK);
+    sstore(ra0, rb0, 0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+      gload(ra0, rb0, (kt + 2) * TG_BK);
+      mma(0);
+      sstore(ra1, rb1, 1);
+      __syncthreads();
+      gload(ra1, rb1, (kt + 3) * TG_BK);
+      mma(1);
+      sstore(ra0, rb0, 0);
+      __syncthreads();
+    }
+
+    // epilogue: lane holds column li of each 16-column fragment, rows 4 kg + q
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!frag_live[i]) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int row = wm * 64 + i * 16 + kg * 4 + q;
+        const int32_t rr = tile_route[row];
+        if (rr < 0) continue;
+        const float wr = tile_w[row];
+        uint16_t* orow = out + int64_t(rr) * ldo;
+        if constexpr (FUSED) {
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) {
+            const int col = t * (TG_BN / 2) + wn * 32 + jj * 16 + li;
+            if (col < half) {
+              const float gr = from_dt<DT>(to_dt<DT>(acc[i][jj][q] * wr));
+              const float ur = from_dt<DT>(to_dt<DT>(acc[i][jj + 2][q] * wr));
+              orow[col] = to_dt<DT>(act_fn<ACT>(gr) * ur);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int col = t * TG_BN + wn * 64 + jj * 16 + li;
+            if (col < n_rows) orow[col] = to_dt<DT>(acc[i][jj][q] * wr);
+          }
+        }
+      }
+    }
+  }
+}
+
 // y[r, j] = round(act(x[r, j]) * x[r, d + j]) over [rows, 2d] -> [rows, d]; eight elements per
 // thread on 16-byte aligned rows, one otherwise.
 template <int DT, int ACT, int VEC>
@@ -244,13 +535,19 @@ __global__ __launch_bounds__(256) void act_and_mul_kernel(uint16_t* __restrict__
 
 using namespace pia;
 
+extern "C" int64_t pia_moe_expert_gemm_workspace_bytes(int64_t max_num_tokens_padded,
+                                                       int block_m) {
+  if (max_num_tokens_padded < 0 || block_m <= 0) return 0;
+  return (2 * ceil_div(max_num_tokens_padded, block_m) + 2 + TG_XCDS) * int64_t(sizeof(int32_t));
+}
+
 extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
                                    const float* topk_weights, const int32_t* sorted_token_ids,
                                    const int32_t* expert_ids, const int32_t* num_tokens_post_pad,
                                    int64_t max_num_tokens_padded, int block_m, int64_t numel,
                                    int a_div, int64_t lda, int num_experts, int n_rows, int k_dim,
                                    int64_t ldo, int activation, int mul_routed_weight, int dtype,
-                                   void* stream) {
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
   if (dtype != PIA_DTYPE_BF16 && dtype != PIA_DTYPE_F16)
     return fail(PIA_EUNSUPPORTED, "moe_expert_gemm: dtype must be bf16 or fp16");
   if (activation < PIA_ACT_NONE || activation > PIA_ACT_GELU_TANH)
@@ -270,22 +567,68 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
   if (max_num_tokens_padded >= 0x7fffffff || numel >= 0x7fffffff)
     return fail(PIA_EINVAL, "moe_expert_gemm: sizes must fit int32");
   if (!out || !a || !w || !sorted_token_ids || !expert_ids || !num_tokens_post_pad ||
-      (mul_routed_weight && !topk_weights))
+      (mul_routed_weight && !topk_weights) || !workspace)
     return fail(PIA_EINVAL, "moe_expert_gemm: null pointer");
-  if (!aligned(a, 16) || !aligned(w, 16))
-    return fail(PIA_EINVAL, "moe_expert_gemm: A and W must be 16-byte aligned");
-  const int n_tiles = int(ceil_div(out_cols, fused ? 32 : 64));
-  const int64_t ub = ceil_div(max_num_tokens_padded, EG_ROWS) * n_tiles;
-  const unsigned grid = unsigned(std::min<int64_t>(ub, int64_t(device_cus()) * EG_WGS_PER_CU));
+  if (workspace_bytes < pia_moe_expert_gemm_workspace_bytes(max_num_tokens_padded, block_m))
+    return fail(PIA_EINVAL, "moe_expert_gemm: workspace too small");
+  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(workspace, 4))
+    return fail(PIA_EINVAL, "moe_expert_gemm: A and W must be 16-byte aligned, workspace 4");
   hipStream_t s = as_stream(stream);
   uint16_t* o = reinterpret_cast<uint16_t*>(out);
   const uint16_t* aa = reinterpret_cast<const uint16_t*>(a);
   const uint16_t* ww = reinterpret_cast<const uint16_t*>(w);
+  const int mulw = mul_routed_weight ? 1 : 0;
+  const int cus = device_cus();
+  // bytes of A the plan can reach: rows ceil(numel / a_div), the last one k_dim long
+  const int64_t a_bytes = ((ceil_div(numel, a_div) - 1) * lda + k_dim) * 2;
+  const int64_t w_bytes = int64_t(n_rows) * k_dim * 2;
+  if (numel >= PIA_EG_TILED_MIN_ROUTES && a_bytes < (int64_t(1) << 31) &&
+      w_bytes < (int64_t(1) << 31)) {
+    const int64_t max_blocks = ceil_div(max_num_tokens_padded, block_m);
+    int32_t* seg_block = reinterpret_cast<int32_t*>(workspace);  // [max_blocks + 1]
+    int32_t* seg_count = seg_block + max_blocks + 1;                // [1]
+    int32_t* seg_xstart = seg_count + 1;                             // [max_blocks]
+    int32_t* xcd_items = seg_xstart + max_blocks;                   // [8]
+    const int n_tiles = int(ceil_div(out_cols, fused ? TG_BN / 2 : TG_BN));
+    hipLaunchKernelGGL(moe_plan_segments, dim3(1), dim3(1024), 0, s, seg_block, seg_count,
+                       seg_xstart, xcd_items, expert_ids, num_tokens_post_pad, block_m,
+                       max_num_tokens_padded, n_tiles);
+    if (int rc = check_launch("moe_plan_segments")) return rc;
+    // items: at most (used blocks * block_m / 128 + experts present) row tiles per column tile
+    const int64_t max_seg = std::min<int64_t>(max_blocks, int64_t(num_experts) + 1);
+    const int64_t ub = (ceil_div(max_num_tokens_padded, TG_BM) + max_seg) * n_tiles;
+    const int64_t g = std::min<int64_t>(ub, int64_t(cus));
+    const unsigned grid = unsigned(std::max<int64_t>(TG_XCDS, g / TG_XCDS * TG_XCDS));
+#define PIA_TG(DT, ACT)                                                                        \
+  hipLaunchKernelGGL((moe_gemm_tiled<DT, ACT>), dim3(grid), dim3(TG_THREADS), 0, s, o, aa, ww, \
+                     topk_weights, sorted_token_ids, expert_ids, seg_block, seg_count,         \
+                     seg_xstart, xcd_items, numel,                                             \
+                     block_m, a_div, lda, num_experts, n_rows, k_dim, ldo, n_tiles, mulw,      \
+                     uint32_t(a_bytes))
+#define PIA_TG_ACT(DT)                                                                         \
+  switch (activation) {                                                                        \
+    case PIA_ACT_NONE: PIA_TG(DT, PIA_ACT_NONE); break;                                        \
+    case PIA_ACT_SILU: PIA_TG(DT, PIA_ACT_SILU); break;                                        \
+    case PIA_ACT_GELU: PIA_TG(DT, PIA_ACT_GELU); break;                                        \
+    default: PIA_TG(DT, PIA_ACT_GELU_TANH); break;                                             \
+  }
+    if (dtype == PIA_DTYPE_BF16) {
+      PIA_TG_ACT(PIA_DTYPE_BF16)
+    } else {
+      PIA_TG_ACT(PIA_DTYPE_F16)
+    }
+#undef PIA_TG_ACT
+#undef PIA_TG
+    return check_launch("moe_gemm_tiled");
+  }
+  const int n_tiles = int(ceil_div(out_cols, fused ? 32 : 64));
+  const int64_t ub = ceil_div(max_num_tokens_padded, EG_ROWS) * n_tiles;
+  const unsigned grid = unsigned(std::min<int64_t>(ub, int64_t(cus) * EG_WGS_PER_CU));
 #define PIA_EG(DT, ACT)                                                                           \
   hipLaunchKernelGGL((moe_gemm_splitk<DT, ACT>), dim3(grid), dim3(EG_WAVES * 64), 0, s, o, aa, ww, \
                      topk_weights, sorted_token_ids, expert_ids, num_tokens_post_pad,             \
                      max_num_tokens_padded, numel, block_m, a_div, lda, num_experts, n_rows,       \
-                     k_dim, ldo, n_tiles, mul_routed_weight ? 1 : 0)
+                     k_dim, ldo, n_tiles, mulw)
 #define PIA_EG_ACT(DT)                                                                            \
   switch (activation) {                                                                           \
     case PIA_ACT_NONE: PIA_EG(DT, PIA_ACT_NONE); break;                                           \
@@ -300,7 +643,7 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
   }
 #undef PIA_EG_ACT
 #undef PIA_EG
-  return check_launch("moe_expert_gemm");
+  return check_launch("moe_gemm_splitk");
 }
 
 extern "C" int pia_act_and_mul(void* out, const void* x, int64_t rows, int64_t d, int activation,

@@ -354,26 +354,28 @@ __global__ __launch_bounds__(1024) void moe_align_small(
   const int64_t max_blocks = (max_padded + bs - 1) / bs;
   for (int64_t i = npp / bs + tid; i < max_blocks; i += 1024) expert_ids[i] = -1;
   __syncthreads();
-  for (int s0 = 0; s0 < numel; s0 += 1024) {
-    const int i = s0 + tid;
+  // Routes go in 64-route groups, one per wave, in group order: a wave reads the running count
+  // of its experts, adds the rank among its own lower lanes (readlane loop), writes, then adds
+  // its counts; one barrier per group keeps the groups in order.
+  for (int g0 = 0; g0 < numel; g0 += 64 * 16) {
+    const int i = g0 + tid;
     const int e = i < numel ? ids_lds[i] : -1;
     int rank = 0;
-    if (e >= 0) {
-      // earlier routes of this round, four ids per LDS read (s0 is a multiple of 4)
-      const int4* v4 = reinterpret_cast<const int4*>(ids_lds + s0);
-      const int n = i - s0;
-      for (int j = 0; j < n; j += 4) {
-        const int4 v = v4[j >> 2];
-        rank += (v.x == e) + (j + 1 < n && v.y == e) + (j + 2 < n && v.z == e) +
-                (j + 3 < n && v.w == e);
-      }
-      const int32_t pos = cnt[e] + rank;
-      sorted[pos] = i;
-      if (route_pos) route_pos[i] = pos;
+#pragma unroll 8
+    for (int j = 0; j < 64; ++j) {
+      const int ej = __builtin_amdgcn_readlane(e, j);
+      rank += (j < lane && ej == e) ? 1 : 0;
     }
-    __syncthreads();
-    if (e >= 0) atomicAdd(&cnt[e], 1);
-    __syncthreads();
+    const int groups = min(16, (numel - g0 + 63) / 64);
+    for (int w = 0; w < groups; ++w) {
+      if (wave == w && e >= 0) {
+        const int32_t pos = cnt[e] + rank;
+        sorted[pos] = i;
+        if (route_pos) route_pos[i] = pos;
+        atomicAdd(&cnt[e], 1);
+      }
+      __syncthreads();
+    }
   }
 }
 

@@ -42,7 +42,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_moe_unpermute": (_I, [_P, _P, _L, _P, _P, _L, _I, _I, _I, _P]),
     "pia_moe_sum_reduce": (_I, [_P, _P, _L, _I, _I, _I, _P]),
     "pia_moe_expert_gemm": (_I, [_P, _P, _P, _P, _P, _P, _P, _L, _I, _L, _I, _L, _I, _I, _I, _L,
-                                 _I, _I, _I, _P]),
+                                 _I, _I, _I, _P, _L, _P]),
+    "pia_moe_expert_gemm_workspace_bytes": (_L, [_L, _I]),
     "pia_act_and_mul": (_I, [_P, _P, _L, _L, _I, _I, _P]),
     "pia_index_copy_rows": (_I, [_P, _P, _L, _P, _P, _L, _L, _P, _L, _I, _P]),
     "pia_index_copy_rows_multi": (_I, [_P, _P, _P, _I, _P, _P, _L, _P, _I, _P]),

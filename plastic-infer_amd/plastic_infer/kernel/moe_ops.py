@@ -151,14 +151,16 @@ def moe_expert_gemm(a: torch.Tensor, w: torch.Tensor, topk_weights: torch.Tensor
                     sorted_token_ids: torch.Tensor, expert_ids: torch.Tensor,
                     num_tokens_post_pad: torch.Tensor, block_m: int, numel: int, a_div: int,
                     activation: str | None = None, mul_routed_weight: bool = False,
-                    out: torch.Tensor | None = None) -> torch.Tensor:
+                    out: torch.Tensor | None = None,
+                    workspace: torch.Tensor | None = None) -> torch.Tensor:
     """One GEMM of the fused experts FFN over a permute plan (block_m a multiple of 16).
 
     For every planned route r < numel of expert e: acc = a[r // a_div] . w[e]^T (fp32), then
     activation None: out[r] = round(acc * w_r); activation X: out[r, n] =
     round(X(round(acc[n] * w_r)) * round(acc[I + n] * w_r)) with I = w.shape[1] // 2.
     w_r = topk_weights.flat[r] when mul_routed_weight, else 1. out is [numel, N or I] unless given
-    (a [*, N or I] view with unit column stride)."""
+    (a [*, N or I] view with unit column stride). workspace: optional device buffer reused
+    across calls (pia_moe_expert_gemm_workspace_bytes of the plan)."""
     dev = N.require_device(a, w, sorted_token_ids, expert_ids, num_tokens_post_pad,
                            names=("a", "w", "sorted_token_ids", "expert_ids",
                                   "num_tokens_post_pad"))
@@ -190,9 +192,14 @@ def moe_expert_gemm(a: torch.Tensor, w: torch.Tensor, topk_weights: torch.Tensor
     for name, t in (("sorted_token_ids", sorted_token_ids), ("expert_ids", expert_ids)):
         if t.dtype != torch.int32 or not t.is_contiguous():
             raise ValueError(f"{name} must be contiguous int32")
+    mpad = sorted_token_ids.numel()
+    ws_bytes = N.query("pia_moe_expert_gemm_workspace_bytes", mpad, block_m)
+    if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
+        workspace = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=dev)
     N.call("pia_moe_expert_gemm", out.data_ptr(), a.data_ptr(), w.data_ptr(),
            N.ptr(topk_weights) if mul_routed_weight else None, sorted_token_ids.data_ptr(),
-           expert_ids.data_ptr(), num_tokens_post_pad.data_ptr(), sorted_token_ids.numel(),
-           block_m, numel, a_div, a.stride(0), E, n_rows, K, out.stride(0), act,
-           1 if mul_routed_weight else 0, N.dtype_code(a.dtype), N.stream_of(dev))
+           expert_ids.data_ptr(), num_tokens_post_pad.data_ptr(), mpad, block_m, numel, a_div,
+           a.stride(0), E, n_rows, K, out.stride(0), act, 1 if mul_routed_weight else 0,
+           N.dtype_code(a.dtype), workspace.data_ptr(),
+           workspace.numel() * workspace.element_size(), N.stream_of(dev))
     return out

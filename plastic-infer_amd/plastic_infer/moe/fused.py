@@ -83,14 +83,16 @@ def _routed_ffn(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
     weights = topk_weights.to(torch.float32).contiguous()
     sorted_ids, expert_ids, npp = _align(ids, EXPERT_BLOCK_M, E)
     dev = hidden_states.device
+    ws = torch.empty(N.query("pia_moe_expert_gemm_workspace_bytes", sorted_ids.numel(),
+                             EXPERT_BLOCK_M), dtype=torch.uint8, device=dev)
     cache2 = torch.empty(numel, two_i // 2, dtype=hidden_states.dtype, device=dev)
     moe_expert_gemm(hidden_states, w1, weights, sorted_ids, expert_ids, npp, EXPERT_BLOCK_M,
                     numel, k, activation=activation,
-                    mul_routed_weight=apply_router_weight_on_input, out=cache2)
+                    mul_routed_weight=apply_router_weight_on_input, out=cache2, workspace=ws)
     cache3 = torch.empty(M, k, H, dtype=hidden_states.dtype, device=dev)
     moe_expert_gemm(cache2, w2, weights, sorted_ids, expert_ids, npp, EXPERT_BLOCK_M, numel, 1,
                     activation=None, mul_routed_weight=not apply_router_weight_on_input,
-                    out=cache3.view(numel, H))
+                    out=cache3.view(numel, H), workspace=ws)
     moe_sum_reduce(cache3, out)
     return out
 

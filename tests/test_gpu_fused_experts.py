@@ -73,6 +73,10 @@ def test_act_and_mul(dev, activation, dtype, rows, d):
     (0, 64, 2048, 768, 128, 8, torch.bfloat16, "silu", False),   # Qwen3-30B-A3B decode layer
     (1, 5, 200, 40, 7, 3, torch.float16, "gelu", True),          # K, N tails; weight on input
     (2, 100, 128, 64, 4, 2, torch.bfloat16, "gelu_tanh", False), # ~50 routes per expert
+    # from 4096 routes per call the LDS-tiled kernel runs
+    (10, 1024, 512, 256, 8, 4, torch.bfloat16, "silu", False),   # 512 routes per expert
+    (11, 700, 200, 40, 7, 6, torch.float16, "gelu", True),       # K tail, column tail
+    (12, 512, 2048, 768, 128, 8, torch.bfloat16, "silu", False), # Qwen3-30B-A3B prefill chunk
 ])
 def test_expert_gemms_match_oracle_intermediates(dev, seed, T, H, I, E, k, dtype, activation,
                                                  on_input):
@@ -109,8 +113,9 @@ def test_fused_experts_decode_matches_oracle(dev, seed, T, H, I, E, k, dtype, ac
     _mostly_equal(got, ref, "decode FFN", frac_max=0.02, steps=None)
 
 
-def test_fused_experts_impl_overwrites_hidden(dev):
-    x, w1, w2, tw, ids = _problem(6, 300, 512, 128, 32, 4, torch.bfloat16)
+@pytest.mark.parametrize("T", [300, 1100])
+def test_fused_experts_impl_overwrites_hidden(dev, T):
+    x, w1, w2, tw, ids = _problem(6, T, 512, 128, 32, 4, torch.bfloat16)
     ref = OF.fused_experts(x, w1, w2, tw, ids)
     xd = x.to(dev)
     got = fused_experts_impl(xd, w1.to(dev), w2.to(dev), tw.to(dev), ids.to(dev))
