@@ -24,6 +24,9 @@ reference torch path on this host's cores, on a bounded sample of the same input
                                              # (4096 tokens, hidden 2048, seed 4)
   python bench.py --workload expert-stream   # Qwen3-30B-A3B expert streaming: 48 layers of
                                              # pinned banks (54 GiB), 3072 HBM slots, LRU
+  python bench.py --workload moe-experts     # Qwen3-30B-A3B routed expert FFN, one layer,
+                                             # 64 decode tokens, 128 resident experts top-8
+  python bench.py --workload moe-experts-prefill   # the same FFN over 4096 prefill tokens
 The default workload (decode) is the headline; the others print their own JSON line.
 """
 
@@ -566,6 +569,145 @@ def bench_expert_stream(torch, dev, args) -> dict:
          "algorithmic_bytes_per_launch": int(streamed / L), "avg_launch_ms": round(ms / L, 4)})
 
 
+EXP_H, EXP_I, EXP_E, EXP_K, EXP_BM, EXP_SEED = 2048, 768, 128, 8, 16, 6
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def bench_moe_experts(torch, dev, args, tokens: int) -> dict:
+    """Qwen3-30B-A3B routed expert FFN, one layer, experts resident in HBM: gate_up
+    [128, 1536, 2048] and down [128, 2048, 768] bf16 ~ N(0, 0.02); hidden [tokens, 2048] bf16
+    ~ N(0,1); router logits fp32 N(0,1) -> softmax top-8 renormalised (outside the step). One
+    step = moe_align_block_size (block 16) + first expert GEMM with SiLU-and-mul fused +
+    second expert GEMM with the routing weight + sum over the 8 routes (fused_experts)."""
+    from plastic_infer import _native as N
+    from plastic_infer.kernel import moe_align_block_size, moe_expert_gemm, moe_sum_reduce, moe_topk
+
+    H, I, E, K = EXP_H, EXP_I, EXP_E, EXP_K
+    g = torch.Generator(device=dev).manual_seed(EXP_SEED)
+    x = torch.randn(tokens, H, generator=g, device=dev).to(torch.bfloat16)
+    w1 = (torch.randn(E, 2 * I, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, H, I, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    logits = torch.randn(tokens, E, generator=g, device=dev)
+    tw, ids = moe_topk(logits, K, True)
+    numel = tokens * K
+    mpad = numel + (E + 1) * (EXP_BM - 1) if numel >= E + 1 else numel * EXP_BM
+    ws = torch.empty(N.query("pia_moe_expert_gemm_workspace_bytes", mpad, EXP_BM),
+                     dtype=torch.uint8, device=dev)
+    c2 = torch.empty(numel, I, dtype=torch.bfloat16, device=dev)
+    c3 = torch.empty(tokens, K, H, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(tokens, H, dtype=torch.bfloat16, device=dev)
+
+    def step(ev):
+        if ev:
+            ev[0].record()
+        s, e, npp = moe_align_block_size(ids, EXP_BM, E)
+        if ev:
+            ev[1].record()
+        moe_expert_gemm(x, w1, tw, s, e, npp, EXP_BM, numel, K, activation="silu", out=c2,
+                        workspace=ws)
+        if ev:
+            ev[2].record()
+        moe_expert_gemm(c2, w2, tw, s, e, npp, EXP_BM, numel, 1, mul_routed_weight=True,
+                        out=c3.view(numel, H), workspace=ws)
+        if ev:
+            ev[3].record()
+        moe_sum_reduce(c3, out)
+        if ev:
+            ev[4].record()
+
+    ms, (align_ms, g1_ms, g2_ms, sum_ms), wall = _phase_timer(torch, dev, step, 4, args.steps,
+                                                              args.warmup)
+    distinct = int(torch.unique(ids).numel())
+    w1_bytes, w2_bytes = distinct * 2 * I * H * 2, distinct * H * I * 2
+    g1_bytes = w1_bytes + tokens * H * 2 + numel * I * 2
+    g2_bytes = w2_bytes + numel * I * 2 + numel * H * 2 + numel * 4
+    sum_bytes = numel * H * 2 + tokens * H * 2
+    g1_flops, g2_flops = numel * 2 * I * H * 2, numel * H * I * 2
+    step_bytes = g1_bytes + g2_bytes + sum_bytes
+    step_flops = g1_flops + g2_flops
+    # the dominant kernel's bound: the larger of its HBM time and its MFMA time at peak
+    dom_name = "moe_gemm_splitk" if numel < 2048 else "moe_gemm_tiled"
+    dom_name += "<bf16, silu> (first expert GEMM)"
+    t_hbm = g1_bytes / (HBM_PEAK_GBPS * 1e9)
+    t_mfma = g1_flops / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+    if t_hbm >= t_mfma:
+        achieved, peak, unit, bound = g1_bytes / (g1_ms / 1e3) / 1e9, HBM_PEAK_GBPS, "GB/s", "hbm"
+    else:
+        achieved, peak, unit, bound = (g1_flops / (g1_ms / 1e3) / 1e12, MFMA_BF16_PEAK_TFLOPS,
+                                       "TFLOP/s", "mfma")
+    traffic = None
+    pmc = ROOT / "profiles" / f"moe_experts_t{tokens}_pmc.json"
+    if pmc.exists():
+        try:
+            traffic = json.loads(pmc.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    decode = tokens < 512
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = _cpu_experts(torch, x, w1, w2, tw, ids, out, decode)
+    if decode:
+        value, unit_v, metric = step_bytes / (ms / 1e3) / 1e9, "GB/s", \
+            "routed expert FFN GB/s (weights of the experts hit + activations); tokens/s"
+    else:
+        value, unit_v, metric = step_flops / (ms / 1e3) / 1e12, "TFLOP/s", \
+            "routed expert FFN TFLOP/s; tokens/s"
+    return _result(
+        metric, value, unit_v, args, ms, "bf16",
+        {"workload": f"qwen3-30b-a3b routed expert FFN, one layer, experts resident "
+                     f"({tokens} tokens, hidden 2048, moe_intermediate 768, 128 experts top-8)",
+         "tokens": tokens, "hidden": H, "intermediate": I, "experts": E, "topk": K},
+        {"tokens_per_s": round(tokens / (ms / 1e3), 1), "distinct_experts": distinct,
+         "bytes_per_step": step_bytes, "flops_per_step": step_flops,
+         "hbm_frac": round(step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+         "align_ms": round(align_ms, 4), "gemm1_ms": round(g1_ms, 4),
+         "gemm2_ms": round(g2_ms, 4), "sum_ms": round(sum_ms, 4),
+         "wall_s_timed": round(wall, 4)},
+        {"kernel": dom_name, "bound": bound, "achieved": round(achieved, 2), "peak": peak,
+         "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic,
+         "algorithmic_bytes_per_launch": g1_bytes, "flops_per_launch": g1_flops,
+         "avg_launch_ms": round(g1_ms, 4)},
+        cpu)
+
+
+def _cpu_experts(torch, x, w1, w2, tw, ids, out, decode: bool) -> dict:
+    """The oracle's fused experts (float64 dot products, the reference's rounding points) on the
+    first 8 tokens, with only the experts they route to; 1 warm-up + median of 3. Scaled to
+    the workload's unit (weight + activation bytes per second for decode, FLOP/s for
+    prefill). Its result also checks the GPU output of those tokens (1e-2 of the largest
+    magnitude, the parity bar of the expert GEMM tests)."""
+    import oracle.fused_experts as OF
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    n = 8
+    sub = ids[:n]
+    used = torch.unique(sub)
+    remap = torch.full((w1.shape[0],), -1, dtype=torch.int32, device=ids.device)
+    remap[used.long()] = torch.arange(used.numel(), dtype=torch.int32, device=ids.device)
+    xs, a, b = x[:n].cpu(), w1[used.long()].cpu(), w2[used.long()].cpu()
+    ws, rs = tw[:n].cpu(), remap[sub.long()].cpu()
+    ref = OF.fused_experts(xs, a, b, ws, rs)
+    err = (out[:n].float().cpu() - ref.float()).abs().max().item()
+    if err > 1e-2 * max(ref.float().abs().max().item(), 1e-6):
+        raise RuntimeError(f"moe experts: GPU output differs from the oracle ({err})")
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        OF.fused_experts(xs, a, b, ws, rs)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    H, I, K = EXP_H, EXP_I, EXP_K
+    nb = used.numel() * 3 * I * H * 2 + n * H * 2 * 2 + n * K * (I + H) * 2 * 2
+    fl = n * K * 3 * I * H * 2
+    model, phys = cpu_info()
+    value, unit = (nb / t / 1e9, "GB/s") if decode else (fl / t / 1e12, "TFLOP/s")
+    return {"value": round(value, 4), "unit": unit, "cores": threads, "kind": "port",
+            "sample": f"first {n} of the step's tokens with their {used.numel()} experts (same "
+                      f"inputs), 1 warm-up + median of 3, {t * 1e3:.1f} ms",
+            "cpu_model": model, "physical_cores": phys}
+
+
 def calibrate_copy(torch, dev) -> int:
     """A plain elementwise copy of known size (2^30 bytes read, 2^30 written per launch) for
     scaling FETCH_SIZE / WRITE_SIZE readings of the attention kernel to bytes."""
@@ -589,7 +731,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--workload", choices=("decode", "decode-gqa8", "prefill-write",
-                                           "moe-permute", "expert-stream"), default="decode")
+                                           "moe-permute", "expert-stream", "moe-experts",
+                                           "moe-experts-prefill"), default="decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the paged decode path on ONE GPU (per-GPU shard of a "
@@ -607,7 +750,10 @@ def main() -> int:
         return calibrate_copy(torch, dev)
     if args.workload != "decode":
         run = {"decode-gqa8": bench_decode_gqa8, "prefill-write": bench_prefill_write,
-               "moe-permute": bench_moe_permute, "expert-stream": bench_expert_stream}[args.workload]
+               "moe-permute": bench_moe_permute, "expert-stream": bench_expert_stream,
+               "moe-experts": lambda t, d, a: bench_moe_experts(t, d, a, 64),
+               "moe-experts-prefill": lambda t, d, a: bench_moe_experts(t, d, a, 4096),
+               }[args.workload]
         print(f"bench: workload {args.workload}", file=sys.stderr, flush=True)
         print(json.dumps(run(torch, dev, args)), flush=True)
         return 0
