@@ -22,11 +22,14 @@ reference torch path on this host's cores, on a bounded sample of the same input
   python bench.py --workload moe-permute     # Qwen3-30B-A3B routing: top-8 of 128 experts,
                                              # permute, identity expert, weighted unpermute
                                              # (4096 tokens, hidden 2048, seed 4)
-  python bench.py --workload expert-stream   # Qwen3-30B-A3B expert streaming: 48 layers of
-                                             # pinned banks (54 GiB), 3072 HBM slots, LRU
+  python bench.py --workload expert-stream   # Qwen3-30B-A3B routed experts of a decode step:
+                                             # 48 layers of pinned banks (54 GiB), 3072 HBM
+                                             # slots, LRU, expert FFN on the slots
   python bench.py --workload moe-experts     # Qwen3-30B-A3B routed expert FFN, one layer,
                                              # 64 decode tokens, 128 resident experts top-8
   python bench.py --workload moe-experts-prefill   # the same FFN over 4096 prefill tokens
+  python bench.py --workload prefill-stream  # Qwen3-30B-A3B prefill of 4096 tokens through the
+                                             # expert double buffer, 48 layers of pinned banks
 The default workload (decode) is the headline; the others print their own JSON line.
 """
 
@@ -461,6 +464,34 @@ def _pinned_exact(torch, shape):
     return torch.frombuffer(buf, dtype=torch.bfloat16).view(shape)
 
 
+def _pin_expert_banks(torch, markers: bool):
+    """48 layers of pinned gate_up [128, 1536, 2048] / down [128, 2048, 768] bf16 banks.
+    markers: layer l holds l / -l with row markers (expert index at [e, 0, 0]) for slot checks;
+    else layer l holds (l + 1) / 64 and -(l + 1) / 64 everywhere (exact in bf16), which gives the
+    expert FFN a closed form."""
+    L, E, H, I = XS_L, XS_E, XS_H, XS_I
+    row_bytes = 2 * I * H * 2 + H * I * 2
+    print(f"bench: pinning {L * E * row_bytes / 2**30:.1f} GiB of expert banks", file=sys.stderr,
+          flush=True)
+    banks = {"gate_up": [], "down": []}
+    for l in range(L):
+        gu = _pinned_exact(torch, (E, 2 * I, H))
+        dn = _pinned_exact(torch, (E, H, I))
+        if markers:
+            gu.fill_(float(l))
+            dn.fill_(float(-l))
+            gu[:, 0, 0] = torch.arange(E, dtype=torch.bfloat16)
+            dn[:, 0, 0] = torch.arange(E, dtype=torch.bfloat16)
+        else:
+            gu.fill_((l + 1) / 64.0)
+            dn.fill_(-(l + 1) / 64.0)
+        banks["gate_up"].append(gu)
+        banks["down"].append(dn)
+        if l % 8 == 7:
+            print(f"bench: {l + 1}/{L} layers pinned", file=sys.stderr, flush=True)
+    return banks
+
+
 def bench_expert_stream(torch, dev, args) -> dict:
     """Qwen3-30B-A3B expert streaming through the GPU slot cache: 48 layers x 128 experts,
     gate_up [1536, 2048] + down [2048, 768] bf16 = 9 MiB per expert (54 GiB of pinned host
@@ -469,24 +500,12 @@ def bench_expert_stream(torch, dev, args) -> dict:
     uniform top-8 routing of 64 decode tokens, then copy_missing of the admitted experts (one
     multi-bank launch reading the pinned banks over the host link)."""
     from plastic_infer.kernel import copy_rows_async
+    from plastic_infer.moe.fused import fused_experts_decode_impl
     from plastic_infer.moe.offload_cache import OffloadMoeCache
 
     L, E, H, I, B, K = XS_L, XS_E, XS_H, XS_I, XS_B, XS_K
     row_bytes = 2 * I * H * 2 + H * I * 2
-    print(f"bench: pinning {L * E * row_bytes / 2**30:.1f} GiB of expert banks", file=sys.stderr,
-          flush=True)
-    banks = {"gate_up": [], "down": []}
-    for l in range(L):
-        gu = _pinned_exact(torch, (E, 2 * I, H))
-        dn = _pinned_exact(torch, (E, H, I))
-        gu.fill_(float(l))
-        dn.fill_(float(-l))
-        gu[:, 0, 0] = torch.arange(E, dtype=torch.bfloat16)   # row markers for the spot check
-        dn[:, 0, 0] = torch.arange(E, dtype=torch.bfloat16)
-        banks["gate_up"].append(gu)
-        banks["down"].append(dn)
-        if l % 8 == 7:
-            print(f"bench: {l + 1}/{L} layers pinned", file=sys.stderr, flush=True)
+    banks = _pin_expert_banks(torch, markers=True)
     cache = OffloadMoeCache(num_layers=L, num_experts=E, cache_size=XS_SLOTS, device=dev)
     cache.collect_stats = True
     cache.set_bank_sources(banks)
@@ -517,12 +536,24 @@ def bench_expert_stream(torch, dev, args) -> dict:
     g = torch.Generator(device=dev).manual_seed(XS_SEED)
     routing = torch.rand(steps + warmup, L, B, E, generator=g, device=dev).argsort(dim=3)[..., :K]
     routing = routing.to(torch.int32).contiguous()
+    rw = torch.rand(L, B, K, generator=g, device=dev)
+    rw = (rw / rw.sum(-1, keepdim=True)).contiguous()
+    x = torch.randn(B, H, generator=g, device=dev).to(torch.bfloat16)
+    gu_cache, dn_cache = cache.bank_caches["gate_up"], cache.bank_caches["down"]
+    ffn_ev = []
 
-    def step(i):
+    def step(i, timed=False):
         for l in range(L):
             ids = routing[i, l].clone()
-            cache.ensure_experts(l, ids)
+            cache.ensure_experts(l, ids)          # ids become slot ids, in place
             cache.copy_missing()
+            if timed:
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+            fused_experts_decode_impl(x, gu_cache, dn_cache, rw[l], ids)
+            if timed:
+                b.record()
+                ffn_ev.append((a, b))
 
     for i in range(warmup):
         step(i)
@@ -533,13 +564,14 @@ def bench_expert_stream(torch, dev, args) -> dict:
     wall0 = time.perf_counter()
     t0.record()
     for i in range(steps):
-        step(warmup + i)
+        step(warmup + i, timed=True)
         print(f"bench: step {i + 1}/{steps}", file=sys.stderr, flush=True)
     t1.record()
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - wall0
     ms = t0.elapsed_time(t1) / steps
-    active, missing, calls = (int(x) for x in cache.lru_stats.sum(0))
+    ffn_ms = sum(a.elapsed_time(b) for a, b in ffn_ev) / steps
+    active, missing, calls = (int(v) for v in cache.lru_stats.sum(0))
     streamed = missing * row_bytes / steps
     # spot check: the last step's slots hold the right layer's rows
     gu_cache = cache.bank_caches["gate_up"]
@@ -553,10 +585,12 @@ def bench_expert_stream(torch, dev, args) -> dict:
     return _result(
         "MoE expert streaming GB/s over the host link; decode tokens/s", gbps, "GB/s", args, ms,
         "bf16",
-        {"workload": "qwen3-30b-a3b expert streaming (48 layers x 128 experts, 9 MiB each, 3072 "
-                     "HBM slots, global LRU, 64 decode tokens top-8)", "layers": L,
-         "experts": E, "slots": XS_SLOTS, "batch": B, "topk": K},
-        {"tokens_per_s": round(B / (ms / 1e3), 2), "hit_rate": round(1 - missing / max(active, 1), 4),
+        {"workload": "qwen3-30b-a3b routed experts of a decode step over the slot cache (48 layers "
+                     "x 128 experts, 9 MiB each, 3072 HBM slots, global LRU, 64 decode tokens "
+                     "top-8): admission, streaming of the misses, expert FFN on the slots",
+         "layers": L, "experts": E, "slots": XS_SLOTS, "batch": B, "topk": K},
+        {"tokens_per_s": round(B / (ms / 1e3), 2), "ffn_ms_per_step": round(ffn_ms, 3),
+         "hit_rate": round(1 - missing / max(active, 1), 4),
          "experts_per_layer_step": round(active / max(calls, 1), 2),
          "streamed_bytes_per_step": int(streamed), "dma_copy_gbps": round(dma_gbps, 2),
          "kernel_copy_gbps": round(kern_gbps, 2), "wall_s_timed": round(wall, 3),
@@ -567,6 +601,120 @@ def bench_expert_stream(torch, dev, args) -> dict:
          "achieved": round(gbps, 2), "peak": 64.0, "unit": "GB/s",
          "frac": round(gbps / 64.0, 4), "traffic": None,
          "algorithmic_bytes_per_launch": int(streamed / L), "avg_launch_ms": round(ms / L, 4)})
+
+
+PS_T, PS_SEED = 4096, 7
+
+
+def bench_prefill_stream(torch, dev, args) -> dict:
+    """Qwen3-30B-A3B prefill through the expert double buffer (the reference's OffloadMoeCache
+    prefill overlap): 48 layers of pinned banks (54 GiB), one 4096-token prefill chunk. Layer
+    l's experts stream host -> one of two HBM layer buffers on the cache's copy stream while
+    layer l - 1's routed expert FFN (fused_experts_impl over the buffer views, position ==
+    expert id) runs on the compute stream; a buffer is refilled once the FFN that read it has
+    finished. One step = the 48 layers (router logits fp32 N(0,1), top-8 renormalised,
+    computed before timing)."""
+    from plastic_infer.kernel import copy_rows_async, moe_topk
+    from plastic_infer.moe.fused import fused_experts_impl
+    from plastic_infer.moe.offload_cache import OffloadMoeCache
+
+    L, E, H, I, K, T = XS_L, XS_E, XS_H, XS_I, XS_K, PS_T
+    row_bytes = 2 * I * H * 2 + H * I * 2
+    banks = _pin_expert_banks(torch, markers=False)
+    cache = OffloadMoeCache(num_layers=L, num_experts=E, cache_size=XS_SLOTS, device=dev,
+                            prefill_overlap=True)
+    cache.set_bank_sources(banks)
+    g = torch.Generator(device=dev).manual_seed(PS_SEED)
+    x = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+    routes = [moe_topk(torch.randn(T, E, generator=g, device=dev), K, True) for _ in range(L)]
+    work = torch.empty_like(x)
+
+    # host-link rate of the DMA engines on one whole layer (both banks), alone
+    scratch = [torch.empty(E, 2 * I, H, dtype=torch.bfloat16, device=dev),
+               torch.empty(E, H, I, dtype=torch.bfloat16, device=dev)]
+    rows = list(range(E))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for rep in range(2):
+        e0.record()
+        copy_rows_async(scratch[0], rows, banks["gate_up"][1], rows)
+        copy_rows_async(scratch[1], rows, banks["down"][1], rows)
+        e1.record()
+        torch.cuda.synchronize(dev)
+    dma_gbps = E * row_bytes / (e0.elapsed_time(e1) / 1e3) / 1e9
+    del scratch
+    ffn_ev = []
+
+    def step(timed):
+        for l in range(L):
+            if l == 0:
+                cache.begin_prefill()
+            cache.prefetch_prefill_layer(l)
+            cache.prefetch_prefill_layer(l + 1)
+            gu, dn = cache.wait_prefill_layer(l)
+            work.copy_(x)
+            tw, ids = routes[l]
+            if timed:
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+            fused_experts_impl(work, gu, dn, tw, ids)
+            if timed:
+                b.record()
+                ffn_ev.append((a, b))
+            cache.release_prefill_layer(l)
+
+    for i in range(args.warmup):
+        step(False)
+        print(f"bench: warm-up step {i + 1}/{args.warmup}", file=sys.stderr, flush=True)
+    torch.cuda.synchronize(dev)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t0.record()
+    for i in range(args.steps):
+        step(True)
+        print(f"bench: step {i + 1}/{args.steps}", file=sys.stderr, flush=True)
+    t1.record()
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - wall0
+    ms = t0.elapsed_time(t1) / args.steps
+    ffn_ms = sum(a.elapsed_time(b) for a, b in ffn_ev) / args.steps
+    # closed form of the last layer (all gate/up weights c, all down weights d): every gate and
+    # up value of token t is R(c * sum(x_t)), the activation a = R(silu(g) * g) is the same in
+    # all I columns, route j's output is R(I * a * d * w_j), the FFN output R(sum_j of those)
+    c, d = L / 64.0, -L / 64.0
+    n = 4
+    xs = x[:n].double().sum(1).cpu()
+    bf = lambda v: v.to(torch.bfloat16).double()
+    gsum = bf((c * xs).float())
+    act = bf((gsum / (1 + torch.exp(-gsum)) * gsum).float())
+    tw, _ = routes[L - 1]
+    c3 = bf(((I * act * d).float()[:, None] * tw[:n].cpu()).float())
+    exp = bf(c3.float().sum(1))
+    got = work[:n].double().cpu()
+    err = (got - exp[:, None]).abs().max().item()
+    if not err <= 2e-2 * max(exp.abs().max().item(), 1e-6):
+        raise RuntimeError(f"prefill stream: last layer's output is off its closed form ({err})")
+    layer_bytes = E * row_bytes
+    copy_ms = L * layer_bytes / (dma_gbps * 1e9) * 1e3
+    exposed_ms = max(0.0, ms - ffn_ms)
+    overlap = max(0.0, 1.0 - exposed_ms / copy_ms)
+    gbps = L * layer_bytes / (ms / 1e3) / 1e9
+    return _result(
+        "prefill expert streaming GB/s over the host link (double buffer); prefill tokens/s",
+        gbps, "GB/s", args, ms, "bf16",
+        {"workload": "qwen3-30b-a3b prefill, 48 layers of pinned expert banks (54 GiB) through "
+                     "the two-buffer overlap, 4096 tokens, 128 experts top-8",
+         "layers": L, "experts": E, "tokens": T, "topk": K},
+        {"tokens_per_s": round(T / (ms / 1e3), 1), "ffn_ms_per_step": round(ffn_ms, 3),
+         "dma_copy_gbps": round(dma_gbps, 2), "copy_ms_per_step_at_dma_rate": round(copy_ms, 2),
+         "exposed_copy_ms": round(exposed_ms, 2), "overlap_fraction": round(overlap, 4),
+         "ffn_hidden_fraction": round(min(1.0, max(0.0, (copy_ms + ffn_ms - ms) / ffn_ms)), 4),
+         "overlap_note": "1 - (step time - expert FFN time) / (the step's bytes at the measured "
+                         "DMA rate); the FFN of a layer hides under the next layer's copy",
+         "streamed_bytes_per_step": L * layer_bytes, "wall_s_timed": round(wall, 3)},
+        {"kernel": "hipMemcpyAsync runs (copy_rows_async) on the copy stream", "bound": "host-link",
+         "achieved": round(gbps, 2), "peak": 64.0, "unit": "GB/s", "frac": round(gbps / 64.0, 4),
+         "traffic": None, "algorithmic_bytes_per_launch": layer_bytes,
+         "avg_launch_ms": round(ms / L, 4)})
 
 
 EXP_H, EXP_I, EXP_E, EXP_K, EXP_BM, EXP_SEED = 2048, 768, 128, 8, 16, 6
@@ -732,7 +880,8 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--workload", choices=("decode", "decode-gqa8", "prefill-write",
                                            "moe-permute", "expert-stream", "moe-experts",
-                                           "moe-experts-prefill"), default="decode")
+                                           "moe-experts-prefill", "prefill-stream"),
+                    default="decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the paged decode path on ONE GPU (per-GPU shard of a "
@@ -753,6 +902,7 @@ def main() -> int:
                "moe-permute": bench_moe_permute, "expert-stream": bench_expert_stream,
                "moe-experts": lambda t, d, a: bench_moe_experts(t, d, a, 64),
                "moe-experts-prefill": lambda t, d, a: bench_moe_experts(t, d, a, 4096),
+               "prefill-stream": bench_prefill_stream,
                }[args.workload]
         print(f"bench: workload {args.workload}", file=sys.stderr, flush=True)
         print(json.dumps(run(torch, dev, args)), flush=True)
