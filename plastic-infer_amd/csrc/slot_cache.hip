@@ -13,9 +13,13 @@
 // lru_ensure_kernel is one 1024-thread workgroup: admission is a small sequential decision
 // (a few hundred ids against a few thousand slots), so the whole state of a call lives in LDS
 // and every phase is a barrier-separated parallel pass:
-//   1. dedup the query, split hits and misses, rank the distinct misses by id, bump hits;
-//   2. victims: the evictable slots (not touched by this call) sorted by (usage, slot) with a
-//      bitonic sort of packed 64-bit keys in LDS;
+//   1. dedup the query, split hits and misses, rank the distinct misses by id, bump hits
+//      (match counts over the query read four ids at a time);
+//   2. victims in ascending (usage, slot) order among the slots not touched by this call:
+//      rounds that take every remaining slot holding the smallest usage, in slot order (each
+//      thread owns consecutive slots: a block min, an exclusive scan); an LRU cache fed by
+//      calls that each touch many slots needs two or three rounds. After 8 rounds the call
+//      falls back to a bitonic sort of packed (usage << bits | slot) keys in LDS;
 //   3. the i-th smallest missing id takes the i-th victim: maps, usage and the copy plan.
 #include <algorithm>
 
@@ -47,20 +51,92 @@ __device__ __forceinline__ int block_sum(int v, int* red) {
   return red[LRU_THREADS / 64];
 }
 
+__device__ __forceinline__ long long block_min64(long long v, long long* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  long long t = red[0];
+#pragma unroll
+  for (int w = 1; w < LRU_THREADS / 64; ++w) t = min(t, red[w]);
+  return t;
+}
+
+// exclusive prefix of v over threads in index order; *total gets the sum
+__device__ __forceinline__ int block_excl_scan(int v, int* red, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += t;
+  }
+  __syncthreads();
+  if (lane == 63) red[wave] = incl;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < LRU_THREADS / 64; ++w) {
+    const int t = red[w];
+    before += w < wave ? t : 0;
+    all += t;
+  }
+  *total = all;
+  return before + incl - v;
+}
+
+// number of j < n with q[j] == v (q 16-byte aligned)
+__device__ __forceinline__ int count_equal(const int32_t* q, int n, int v) {
+  const int4* q4 = reinterpret_cast<const int4*>(q);
+  int c = 0;
+  const int full = n >> 2;
+#pragma unroll 4
+  for (int j = 0; j < full; ++j) {
+    const int4 x = q4[j];
+    c += (x.x == v) + (x.y == v) + (x.z == v) + (x.w == v);
+  }
+  for (int j = full * 4; j < n; ++j) c += q[j] == v;
+  return c;
+}
+
+// number of j < n with q[j] < v (q 16-byte aligned)
+__device__ __forceinline__ int count_below(const int32_t* q, int n, int v) {
+  const int4* q4 = reinterpret_cast<const int4*>(q);
+  int c = 0;
+  const int full = n >> 2;
+#pragma unroll 4
+  for (int j = 0; j < full; ++j) {
+    const int4 x = q4[j];
+    c += (x.x < v) + (x.y < v) + (x.z < v) + (x.w < v);
+  }
+  for (int j = full * 4; j < n; ++j) c += q[j] < v;
+  return c;
+}
+
+constexpr int LRU_SPT = LRU_MAX_CACHED / LRU_THREADS;  // slots per thread in the victim rounds
+constexpr int LRU_MAX_ROUNDS = 8;
+constexpr long long kUsageNone = 0x7fffffffffffffffll;
+
 __global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
     const int32_t* __restrict__ query, int K, int32_t* __restrict__ slot_of_id,
     int64_t num_total, int32_t* __restrict__ id_of_slot, int64_t* __restrict__ usage,
     int C, int c_pad, int slot_bits, int64_t* __restrict__ step_ptr,
     int32_t* __restrict__ out, int32_t* __restrict__ src_plan, int32_t* __restrict__ dst_plan,
     int64_t* __restrict__ num_copy, int64_t* __restrict__ stats, int64_t id_base) {
-  __shared__ unsigned long long keys[LRU_MAX_CACHED];
-  __shared__ int32_t q_lds[LRU_MAX_QUERY];
+  // keys: the fallback sort; its first 8 KiB hold the round victims otherwise
+  __shared__ __attribute__((aligned(16))) unsigned long long keys[LRU_MAX_CACHED];
+  __shared__ __attribute__((aligned(16))) int32_t q_lds[LRU_MAX_QUERY];
+  __shared__ __attribute__((aligned(16))) int32_t fm_ids[LRU_MAX_QUERY];  // first misses' ids
   __shared__ int32_t miss_ids[LRU_MAX_QUERY];
-  __shared__ uint8_t first_miss[LRU_MAX_QUERY];
   __shared__ int red[LRU_THREADS / 64 + 1];
+  __shared__ long long red64[LRU_THREADS / 64];
   __shared__ int64_t step_lds;
+  int32_t* victims = reinterpret_cast<int32_t*>(keys);
   const int tid = threadIdx.x;
   constexpr int QPT = LRU_MAX_QUERY / LRU_THREADS;  // queries per thread
+  constexpr int kIdNone = 0x7fffffff;
 
   if (tid == 0) {
     const int64_t s = *step_ptr + 1;
@@ -82,8 +158,8 @@ __global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
         si[r] = slot_of_id[g];
         if (si[r] >= C) si[r] = -1;  // a map entry past the cache is not a hit
       }
-      q_lds[i] = qi[r];
     }
+    if (i < LRU_MAX_QUERY) q_lds[i] = i < K ? qi[r] : -1;
   }
   __syncthreads();
   const int64_t step = step_lds;
@@ -94,16 +170,15 @@ __global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
   for (int r = 0; r < QPT; ++r) {
     const int i = tid + r * LRU_THREADS;
     if (i >= K) continue;
-    bool first = qi[r] >= 0;
-    for (int j = 0; j < i && first; ++j) first = q_lds[j] != qi[r];
+    const bool first = qi[r] >= 0 && count_equal(q_lds, i, qi[r]) == 0;
     const bool fm = first && si[r] < 0;
-    first_miss[i] = fm ? 1 : 0;
+    fm_ids[i] = fm ? qi[r] : kIdNone;
     nfirst += first ? 1 : 0;
     nfm += fm ? 1 : 0;
     if (si[r] >= 0) usage[si[r]] = step;  // duplicated hits store the same value
   }
   const int distinct = block_sum(nfirst, red);
-  const int M = block_sum(nfm, red);  // barriers inside also publish first_miss[]
+  const int M = block_sum(nfm, red);  // barriers inside also publish fm_ids[]
 
   // Phase 1c: rank of every missing position = number of distinct missing ids below it
   // (a duplicate shares its first occurrence's rank); the distinct ones list their id.
@@ -113,52 +188,94 @@ __global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
     const int i = tid + r * LRU_THREADS;
     rank[r] = -1;
     if (i >= K || qi[r] < 0 || si[r] >= 0) continue;
-    int rk = 0;
-    for (int j = 0; j < K; ++j) rk += (first_miss[j] && q_lds[j] < qi[r]) ? 1 : 0;
+    const int rk = count_below(fm_ids, K, qi[r]);
     rank[r] = rk;
-    if (first_miss[i]) miss_ids[rk] = qi[r];
+    if (fm_ids[i] != kIdNone) miss_ids[rk] = qi[r];
   }
   __syncthreads();  // also orders the hit bumps before the usage reload below
 
   int admitted = 0;
+  bool sorted_path = false;
+  const unsigned long long slot_mask = (1ull << slot_bits) - 1;
   if (M > 0) {
-    // Phase 2: packed (usage, slot) keys of evictable slots, ascending.
-    for (int c = tid; c < c_pad; c += LRU_THREADS) {
-      unsigned long long k = kKeyNone;
+    // Phase 2: victims. This thread's slots are c0 .. c0 + LRU_SPT - 1.
+    const int c0 = tid * LRU_SPT;
+    long long u[LRU_SPT];
+#pragma unroll
+    for (int s = 0; s < LRU_SPT; ++s) {
+      const int c = c0 + s;
+      u[s] = kUsageNone;
       if (c < C) {
-        const int64_t u = usage[c];
-        if (u != step) k = (static_cast<unsigned long long>(u) << slot_bits) | unsigned(c);
+        const int64_t v = usage[c];
+        if (v != step) u[s] = v;
       }
-      keys[c] = k;
     }
-    __syncthreads();
-    for (int size = 2; size <= c_pad; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int t = tid; t < c_pad / 2; t += LRU_THREADS) {
-          const int lo = 2 * t - (t & (stride - 1));
-          const int hi = lo + stride;
-          const bool up = (lo & size) == 0;
-          const unsigned long long a = keys[lo], b = keys[hi];
-          if ((a > b) == up) {
-            keys[lo] = b;
-            keys[hi] = a;
-          }
-        }
-        __syncthreads();
+    int taken = 0, rounds = 0;
+    while (taken < M) {
+      long long lmin = kUsageNone;
+#pragma unroll
+      for (int s = 0; s < LRU_SPT; ++s) lmin = min(lmin, u[s]);
+      const long long umin = block_min64(lmin, red64);
+      if (umin == kUsageNone) break;  // no evictable slot left
+      if (++rounds > LRU_MAX_ROUNDS) {
+        sorted_path = true;
+        break;
       }
+      int cnt = 0;
+#pragma unroll
+      for (int s = 0; s < LRU_SPT; ++s) cnt += u[s] == umin ? 1 : 0;
+      int total;
+      int pos = taken + block_excl_scan(cnt, red, &total);
+#pragma unroll
+      for (int s = 0; s < LRU_SPT; ++s)
+        if (u[s] == umin) {
+          if (pos < M) victims[pos] = c0 + s;
+          ++pos;
+          u[s] = kUsageNone;
+        }
+      taken += min(total, M - taken);
+    }
+    if (sorted_path) {
+      __syncthreads();  // victims (aliasing keys) are no longer read
+      // packed (usage, slot) keys of evictable slots, ascending
+      for (int c = tid; c < c_pad; c += LRU_THREADS) {
+        unsigned long long k = kKeyNone;
+        if (c < C) {
+          const int64_t v = usage[c];
+          if (v != step) k = (static_cast<unsigned long long>(v) << slot_bits) | unsigned(c);
+        }
+        keys[c] = k;
+      }
+      __syncthreads();
+      for (int size = 2; size <= c_pad; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          for (int t = tid; t < c_pad / 2; t += LRU_THREADS) {
+            const int lo = 2 * t - (t & (stride - 1));
+            const int hi = lo + stride;
+            const bool up = (lo & size) == 0;
+            const unsigned long long a = keys[lo], b = keys[hi];
+            if ((a > b) == up) {
+              keys[lo] = b;
+              keys[hi] = a;
+            }
+          }
+          __syncthreads();
+        }
+      }
+      int nev = 0;
+      for (int c = tid; c < C; c += LRU_THREADS) nev += keys[c] != kKeyNone ? 1 : 0;
+      taken = min(M, block_sum(nev, red));
+    } else {
+      __syncthreads();  // victims[] complete
     }
     // Misses beyond the evictable slots (a caller breaking |distinct(query)| <= cache size)
     // are left unadmitted: out = -1 and no plan entry.
-    int nev = 0;
-    for (int c = tid; c < C; c += LRU_THREADS) nev += keys[c] != kKeyNone ? 1 : 0;
-    const int evictable = block_sum(nev, red);
-    admitted = min(M, evictable);
+    admitted = taken;
 
     // Phase 3: install. Victims are distinct slots and the evicted ids (resident) never
     // equal the admitted ones (not resident), so the map writes of different i never meet.
-    const unsigned long long slot_mask = (1ull << slot_bits) - 1;
     for (int i = tid; i < admitted; i += LRU_THREADS) {
-      const int victim = int(keys[i] & slot_mask);
+      const int victim = sorted_path ? int(keys[i] & slot_mask) : victims[i];
       const int32_t e = miss_ids[i];
       const int32_t old = id_of_slot[victim];
       if (old >= 0 && old < num_total) slot_of_id[old] = -1;
@@ -170,13 +287,15 @@ __global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
     }
   }
   // out may alias query: every query read happened before the barriers above.
-  const unsigned long long slot_mask = (1ull << slot_bits) - 1;
 #pragma unroll
   for (int r = 0; r < QPT; ++r) {
     const int i = tid + r * LRU_THREADS;
     if (i >= K) continue;
     int32_t o = si[r];
-    if (rank[r] >= 0) o = rank[r] < admitted ? int32_t(keys[rank[r]] & slot_mask) : -1;
+    if (rank[r] >= 0)
+      o = rank[r] < admitted ? (sorted_path ? int32_t(keys[rank[r]] & slot_mask)
+                                            : victims[rank[r]])
+                             : -1;
     out[i] = o;
   }
   if (tid == 0) {

@@ -87,6 +87,34 @@ def test_lru_ensure_largest_cache_and_inert_ids(dev):
     ds.assert_equal(st)
 
 
+def test_lru_ensure_fragmented_usage_rounds_and_sorted_path(dev):
+    """Victims come in rounds of equal usage; a call needing more than 8 rounds takes the
+    sorted path. Single-id calls give every slot its own usage value, so a call with m misses
+    needs m rounds: 8 stays on the rounds, 9 and 40 take the sorted path."""
+    total, cached = 1000, 64
+    st, ds = SC.new_state(total, cached), DevState(dev, total, cached)
+    nxt = 0
+
+    def call(query):
+        out, src, dst, n, _ = SC.lru_ensure(st, np.asarray(query, np.int64))
+        got = ds.ensure(np.asarray(query, np.int64), 0)
+        assert np.array_equal(got, out)
+        assert int(ds.num) == n
+        assert np.array_equal(ds.src[:n].cpu().numpy(), src)
+        assert np.array_equal(ds.dst[:n].cpu().numpy(), dst)
+        ds.assert_equal(st)
+
+    for _ in range(cached):                 # one new id per call: 64 distinct usage values
+        call([nxt])
+        nxt += 1
+    for m in (40, 8, 9, 3, 1, 16):
+        call(list(range(nxt, nxt + m))[::-1])
+        nxt += m
+        for _ in range(5):                  # re-fragment a few slots
+            call([nxt])
+            nxt += 1
+
+
 def test_lru_ensure_more_misses_than_slots_admits_what_fits(dev):
     ds = DevState(dev, 100, 4)
     ds.ensure(np.array([1, 2]), 0)
