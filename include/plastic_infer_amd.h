@@ -109,10 +109,9 @@ int pia_kv_pages_chunk_copy(void* chunk, void* pages, const int64_t* page_ids,
  *                                      bt_stride)
  * bytes, 4-byte aligned (may be NULL when that query returns 0). Calls that share a workspace
  * must be ordered (same stream): the kernels keep partials in it between their two launches.
- * bf16 with head_dim 128 and page_size 16 and Hq/Hkv in {1, 2, 4, 8} takes the fast kernels
- * (an even split of the batch's KV steps over persistent waves for Hq/Hkv <= 4, split-context
- * partitions for 8); every other supported combination (f32/f16/bf16, head_dim <= 512, any
- * page_size) takes the general kernel.
+ * bf16 with head_dim 128 and page_size 16 and Hq/Hkv in {1, 2, 4, 8} takes the fast kernel
+ * (an even split of the batch's KV steps over persistent waves); every other supported
+ * combination (f32/f16/bf16, head_dim <= 512, any page_size) takes the general kernel.
  * ------------------------------------------------------------------------------------------- */
 int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_heads,
                                          int head_dim, int page_size, int64_t bt_stride);

@@ -1,9 +1,10 @@
 // Paged GQA attention over the KV pool layout [num_pages, Hkv, D, P] (token innermost).
 //
-// 1. paged_decode_stream<G> (G = Hq/Hkv in {1,2,4}) and paged_decode_bf16_d128p16<8>: the
-//    decode hot path for bf16, D = 128, P = 16. The stream kernel (described where it is
-//    defined) spreads the batch's 128-token steps evenly over persistent single waves; the
-//    G = 8 kernel is split-context: one 256-thread workgroup per (512-token partition, kv head,
+// 1. paged_decode_stream<G> (G = Hq/Hkv in {1,2,4,8}): the decode hot path for bf16, D = 128,
+//    P = 16 (described where it is defined): the batch's 128-token steps spread evenly over
+//    persistent single waves, two per SIMD (one for G = 8, whose accumulators need the
+//    registers). paged_decode_bf16_d128p16<8> is the earlier split-context G = 8 kernel, kept
+//    behind PIA_G8_STREAM=0: one 256-thread workgroup per (512-token partition, kv head,
 //    sequence); each of its 4 waves owns 8 pages (128 tokens) of the partition. Both use:
 //      K tile loads: lane l reads page l/8, rows d = 4i + (l&3), token half (l>>2)&1, so load i
 //        of the wave covers one whole 128-byte line of each of the 8 pages (32 loads / 8 pages).
@@ -405,7 +406,7 @@ __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 template <int G>
-__global__ __launch_bounds__(64, 2) void paged_decode_stream(
+__global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
     const uint16_t* __restrict__ kpool, const uint16_t* __restrict__ vpool,
     const int32_t* __restrict__ block_tables, int64_t bt_stride,
@@ -498,23 +499,32 @@ __global__ __launch_bounds__(64, 2) void paged_decode_stream(
   };
   // q rows of a segment: lane l < 16G holds q[g][8pp .. 8pp+7], g = l/16, pp = l%16 (four dword
   // loads: q is only 4-byte aligned); staged as the (d, d+4) pairs of row-pair pp.
-  auto load_q = [&](const StreamCursor& c) -> uint4 {
-    uint4 r = make_uint4(0u, 0u, 0u, 0u);
-    if (lane < 16 * G) {
-      const uint32_t* qw = reinterpret_cast<const uint32_t*>(
-          q + int64_t(c.b) * q_seq_stride + int64_t(c.h) * G * D + (lane >> 4) * D +
-          8 * (lane & 15));
-      r = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+  // (G = 8: lane l also holds row g + 4 in the second word group)
+  constexpr int QW = (G + 3) / 4;
+  using QRows = uint4[QW];
+  auto load_q = [&](const StreamCursor& c, QRows& r) {
+#pragma unroll
+    for (int k = 0; k < QW; ++k) {
+      r[k] = make_uint4(0u, 0u, 0u, 0u);
+      const int g = (lane >> 4) + 4 * k;
+      if (g < G) {
+        const uint32_t* qw = reinterpret_cast<const uint32_t*>(
+            q + int64_t(c.b) * q_seq_stride + int64_t(c.h) * G * D + g * D + 8 * (lane & 15));
+        r[k] = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+      }
     }
-    return r;
   };
-  auto stage_q = [&](const uint4 wq) {
-    if (lane < 16 * G) {
-      const int g = lane >> 4, pp = lane & 15;
-      q_lds[0][pp][g] = pack_lo(wq.x, wq.z);
-      q_lds[1][pp][g] = pack_hi(wq.x, wq.z);
-      q_lds[2][pp][g] = pack_lo(wq.y, wq.w);
-      q_lds[3][pp][g] = pack_hi(wq.y, wq.w);
+  auto stage_q = [&](const QRows& wr) {
+#pragma unroll
+    for (int k = 0; k < QW; ++k) {
+      const int g = (lane >> 4) + 4 * k, pp = lane & 15;
+      if (g < G) {
+        const uint4 wq = wr[k];
+        q_lds[0][pp][g] = pack_lo(wq.x, wq.z);
+        q_lds[1][pp][g] = pack_hi(wq.x, wq.z);
+        q_lds[2][pp][g] = pack_lo(wq.y, wq.w);
+        q_lds[3][pp][g] = pack_hi(wq.y, wq.w);
+      }
     }
   };
 
@@ -540,7 +550,8 @@ __global__ __launch_bounds__(64, 2) void paged_decode_stream(
   //   B: K rows 64..127 -> V pages 4..7 -> next step's K rows 64..127
   uint4 bufA[16], bufB[16];
   {
-    const uint4 q0 = load_q(cur);
+    QRows q0;
+    load_q(cur, q0);
     bt_cur = load_bt(cur);
     const uint16_t* kp = kbase + int64_t(cur.h) * TILE + page_ok(bt_cur) * page_stride;
 #pragma unroll
@@ -632,8 +643,10 @@ __global__ __launch_bounds__(64, 2) void paged_decode_stream(
     const StreamCursor nxt = has_next ? next_of(cur) : cur;
     const bool nxt_opens = has_next && nxt.ls == 0;
     const int bt_nxt = load_bt(nxt);
-    uint4 q_nxt = make_uint4(0u, 0u, 0u, 0u);
-    if (nxt_opens) q_nxt = load_q(nxt);
+    QRows q_nxt;
+#pragma unroll
+    for (int k = 0; k < QW; ++k) q_nxt[k] = make_uint4(0u, 0u, 0u, 0u);
+    if (nxt_opens) load_q(nxt, q_nxt);
     const int valid = min(SD_STEP_TOKENS, cur.L - cur.ls * SD_STEP_TOKENS);
     const uint16_t* head_v = vbase + int64_t(cur.h) * TILE;
 
@@ -955,7 +968,14 @@ bool fast_path(int dtype, int Hq, int Hkv, int D, int P) {
 
 // Waves of a stream launch: every CU at two single-wave workgroups per SIMD (CU count cached
 // per device), capped by the partial slots the workspace holds.
-int stream_waves() { return std::min(device_cus() * SD_WAVES_PER_CU, SD_MAX_WAVES); }
+// persistent waves of the stream kernel: two per SIMD, or one for G = 8 (its registers)
+int stream_waves(int G) {
+  return std::min(device_cus() * (G > 4 ? SD_WAVES_PER_CU / 2 : SD_WAVES_PER_CU), SD_MAX_WAVES);
+}
+
+#ifndef PIA_G8_STREAM
+#define PIA_G8_STREAM 1  // G = 8 on the stream kernel (else the split-context partitions)
+#endif
 
 }  // namespace
 }  // namespace pia
@@ -969,10 +989,10 @@ extern "C" int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads,
       num_kv_heads <= 0 || num_heads % num_kv_heads || bt_stride <= 0)
     return 0;
   const int G = num_heads / num_kv_heads;
-  if (G == 8)  // partition partials: (acc[128], max, sum) per (sequence, q head, partition)
+  if (G == 8 && !PIA_G8_STREAM)  // partition partials: (acc[128], max, sum) per (seq, head, part)
     return int64_t(num_seqs) * num_heads * ceil_div(bt_stride, FD_PART_PAGES) * (FD_D + 2) *
            int64_t(sizeof(float));
-  if (G == 1 || G == 2 || G == 4)  // two partial slots per wave + the step-prefix table
+  if (G == 1 || G == 2 || G == 4 || G == 8)  // two partial slots per wave + step-prefix table
     return int64_t(SD_MAX_WAVES) * 2 * G * (FD_D + 2) * int64_t(sizeof(float)) +
            int64_t(SD_META_INTS) * int64_t(sizeof(int32_t));
   return 0;
@@ -1011,7 +1031,7 @@ extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_se
       return fail(PIA_EINVAL, "paged_decode: q and workspace must be 4-byte and pools "
                               "16-byte aligned");
     const int G = num_heads / num_kv_heads;
-    if (G == 8) {
+    if (G == 8 && !PIA_G8_STREAM) {
       const int max_parts = int(ceil_div(bt_stride, FD_PART_PAGES));
       float* ws_acc = reinterpret_cast<float*>(workspace);
       float* ws_ml = ws_acc + int64_t(num_seqs) * num_heads * max_parts * FD_D;
@@ -1031,7 +1051,7 @@ extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_se
     }
     // Stream kernel, in launches of up to SD_MAX_SEQS sequences. Its step arithmetic is int32:
     // Hkv * (sequences) * (steps per sequence) plus a wave count must stay below 2^31.
-    const int NW = stream_waves();
+    const int NW = stream_waves(G);
     if (int64_t(num_kv_heads) * std::min(num_seqs, SD_MAX_SEQS) * ceil_div(bt_stride, 8) +
             2 * int64_t(NW) >= (int64_t(1) << 31))
       return fail(PIA_EUNSUPPORTED, "paged_decode: batch too large for int32 step indices");
@@ -1052,7 +1072,8 @@ extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_se
       switch (G) {
         case 1: PIA_SD(1); break;
         case 2: PIA_SD(2); break;
-        default: PIA_SD(4); break;
+        case 4: PIA_SD(4); break;
+        default: PIA_SD(8); break;
       }
 #undef PIA_SD
       if (int rc = check_launch("paged_decode_stream")) return rc;

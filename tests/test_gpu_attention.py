@@ -100,6 +100,8 @@ def _decode_case(seed: int, lens: list[int], Hq: int, Hkv: int, num_pages: int):
     (4, [8192]),                 # one segment per kv head, cut into one-step wave ranges
     (1, [8191, 3]),
     (2, [0, 4097, 0, 129, 0]),   # empty sequences between and around long ones
+    (8, [8192]),                 # GQA 8: one wave per SIMD, eight q rows per partial
+    (8, [0, 4097, 0, 129, 0]),
 ])
 def test_decode_stream_few_long_sequences(dev, G, lens):
     """Few long sequences: every segment is split across many waves and merged from partials."""
@@ -114,13 +116,15 @@ def test_decode_stream_few_long_sequences(dev, G, lens):
     assert err <= BF16_TOL, err
 
 
-def test_decode_stream_batch_over_one_launch(dev):
-    """1100 sequences (more than one launch's 1024), a third of them empty, short lengths."""
+@pytest.mark.parametrize("Hq", [8, 16])
+def test_decode_stream_batch_over_one_launch(dev, Hq):
+    """1100 sequences (more than one launch's 1024), a third of them empty, short lengths;
+    GQA 4 and 8 over two kv heads."""
     g = torch.Generator().manual_seed(44)
     lens = torch.randint(1, 300, (1100,), generator=g)
     lens[torch.randperm(1100, generator=g)[:370]] = 0
-    q, kp, vp, bt, lens_t = _decode_case(45, lens.tolist(), 8, 2, 14000)
-    ws_dev = torch.empty(decode_workspace_bytes(1100, 8, 2, 128, 16, bt.shape[1]),
+    q, kp, vp, bt, lens_t = _decode_case(45, lens.tolist(), Hq, 2, 14000)
+    ws_dev = torch.empty(decode_workspace_bytes(1100, Hq, 2, 128, 16, bt.shape[1]),
                          dtype=torch.uint8, device=dev)
     outs = []
     for _ in range(2):   # the same workspace twice in a row

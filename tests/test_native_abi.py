@@ -57,9 +57,9 @@ def test_invalid_arguments_are_rejected_without_device_work():
         4096 * 2 * 4 * 130 * 4 + 1028 * 4
     assert N.query("pia_paged_decode_workspace_bytes", 1, 32, 8, 128, 16, 4) == \
         4096 * 2 * 4 * 130 * 4 + 1028 * 4
-    # G = 8: one partial per (sequence, q head, 32-page partition)
+    # G = 8: the same layout with eight q rows per partial slot
     assert N.query("pia_paged_decode_workspace_bytes", 256, 64, 8, 128, 16, 512) == \
-        256 * 64 * 16 * 130 * 4
+        4096 * 2 * 8 * 130 * 4 + 1028 * 4
     # general kernel (head_dim 64, or G = 3): no workspace
     assert N.query("pia_paged_decode_workspace_bytes", 4, 4, 4, 64, 16, 8) == 0
     assert N.query("pia_paged_decode_workspace_bytes", 4, 24, 8, 128, 16, 8) == 0
