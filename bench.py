@@ -856,6 +856,152 @@ def _cpu_experts(torch, x, w1, w2, tw, ids, out, decode: bool) -> dict:
             "cpu_model": model, "physical_cores": phys}
 
 
+KS_L, KS_H, KS_D, KS_P, KS_PPC, KS_T, KS_SEED = 36, 8, 128, 16, 16, 16384, 9
+
+
+def bench_kv_sink(torch, dev, args) -> dict:
+    """KV chunk sink and prefix load of the reference's KVStore on a Qwen3-8B KV cache (36
+    layers x 8 KV heads x 128 dims, bf16, 16-token pages, 256-token chunks = 37.7 MB of K+V per
+    chunk). One step = a finished 16384-token request sinks its 64 chunks to the host cache
+    (evicting the previous step's 64, LRU) and is freed, then a new request with the same
+    tokens loads the 64-chunk prefix back into fresh pages. Each direction is one page<->chunk
+    launch per pool over device-mapped pinned host chunks."""
+    from plastic_infer.kernel import pages_chunks_copy
+    from plastic_infer.kv.kv_store import KVConfig, KVStore
+
+    L, H, D, P, ppc, T = KS_L, KS_H, KS_D, KS_P, KS_PPC, KS_T
+    C = P * ppc
+    n_chunks = T // C
+    cfg = KVConfig(n_layers=L, n_kv_heads=H, head_dim=D, page_size=P, pages_per_chunk=ppc,
+                   max_pages=T // P * L + 1024, max_host_chunks=n_chunks, dtype=torch.bfloat16,
+                   device=dev)
+    store = KVStore(cfg)
+    g = torch.Generator(device=dev).manual_seed(KS_SEED)
+    for pool in (store.gpu.k_pages, store.gpu.v_pages):
+        pool.copy_(torch.randn(pool.shape, generator=g, device=dev).to(torch.bfloat16))
+    chunk_bytes = 2 * L * H * D * C * 2
+    dir_bytes = n_chunks * chunk_bytes
+
+    # kernel-only and DMA rates of one direction's bytes (K pool, all chunks)
+    host = [torch.empty(L, H, D, C, dtype=torch.bfloat16, pin_memory=True) for _ in range(n_chunks)]
+    ids = torch.randperm(cfg.max_pages, generator=g, device=dev)[:n_chunks * L * ppc]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    rates = {}
+    for name, to_chunk in (("d2h", True), ("h2d", False)):
+        pages_chunks_copy(host, store.gpu.k_pages, ids, to_chunk=to_chunk)
+        e0.record()
+        pages_chunks_copy(host, store.gpu.k_pages, ids, to_chunk=to_chunk)
+        e1.record()
+        torch.cuda.synchronize(dev)
+        rates[f"kernel_{name}_gbps"] = round(dir_bytes / 2 / (e0.elapsed_time(e1) / 1e3) / 1e9, 2)
+    flat = torch.empty(n_chunks * L * H * D * C, dtype=torch.bfloat16, pin_memory=True)
+    dflat = torch.empty(flat.shape, dtype=torch.bfloat16, device=dev)
+    for name, (dst, src) in (("d2h", (flat, dflat)), ("h2d", (dflat, flat))):
+        dst.copy_(src, non_blocking=True)
+        e0.record()
+        dst.copy_(src, non_blocking=True)
+        e1.record()
+        torch.cuda.synchronize(dev)
+        rates[f"dma_{name}_gbps"] = round(dir_bytes / 2 / (e0.elapsed_time(e1) / 1e3) / 1e9, 2)
+    del host, flat, dflat
+
+    def step(i, snapshot=False):
+        toks = list(range(i * T, (i + 1) * T))
+        a = store.new_request()
+        a._ensure_pages(T)
+        a._length = T
+        a.set_token_ids(toks)
+        t0 = time.perf_counter()
+        sunk = store.sink_completed_chunks(a)
+        t1 = time.perf_counter()
+        if sunk != n_chunks:
+            raise RuntimeError(f"kv sink: {sunk} chunks sunk, expected {n_chunks}")
+        old = [list(a.block_table.pages[l]) for l in range(L)]
+        snap = (store.gpu.k_pages.clone(), store.gpu.v_pages.clone()) if snapshot else None
+        store.free_request(a)
+        b = store.new_request()
+        t2 = time.perf_counter()
+        matched, _ = store.load_prefix(b, toks)
+        torch.cuda.synchronize(dev)
+        t3 = time.perf_counter()
+        if matched != T:
+            raise RuntimeError(f"kv load: {matched} tokens matched, expected {T}")
+        new = [list(b.block_table.pages[l]) for l in range(L)]
+        store.free_request(b)
+        return t1 - t0, t3 - t2, old, new, snap
+
+    for i in range(args.warmup):
+        step(i)
+        print(f"bench: warm-up step {i + 1}/{args.warmup}", file=sys.stderr, flush=True)
+    sink_s, load_s = [], []
+    wall0 = time.perf_counter()
+    for i in range(args.steps):
+        last = i == args.steps - 1
+        s_t, l_t, old, new, snap = step(args.warmup + i, snapshot=last)
+        sink_s.append(s_t)
+        load_s.append(l_t)
+        print(f"bench: step {i + 1}/{args.steps}", file=sys.stderr, flush=True)
+    wall = time.perf_counter() - wall0
+    # round trip: every page of the loaded request equals the page it was sunk from
+    old_t = torch.tensor(old, dtype=torch.int64, device=dev).reshape(-1)
+    new_t = torch.tensor(new, dtype=torch.int64, device=dev).reshape(-1)
+    for pool, ref in zip((store.gpu.k_pages, store.gpu.v_pages), snap):
+        if not torch.equal(pool[new_t], ref[old_t]):
+            raise RuntimeError("kv sink/load: loaded pages differ from the sunk pages")
+    sink_ms = statistics.mean(sink_s) * 1e3
+    load_ms = statistics.mean(load_s) * 1e3
+    ms = sink_ms + load_ms
+    gbps = 2 * dir_bytes / (ms / 1e3) / 1e9
+    sink_gbps = dir_bytes / (sink_ms / 1e3) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = _cpu_kv_sink(torch, store, snap, old)
+    return _result(
+        "KV chunk sink + prefix load GB/s over the host link", gbps, "GB/s", args, ms, "bf16",
+        {"workload": "qwen3-8b kv cache (36 layers x 8 kv heads x 128, bf16, 16-token pages, "
+                     "256-token chunks): sink a 16384-token request's 64 chunks to pinned host "
+                     "memory, then load them back as a prefix",
+         "layers": L, "kv_heads": H, "head_dim": D, "page_size": P, "pages_per_chunk": ppc,
+         "tokens": T},
+        {"sink_ms": round(sink_ms, 3), "load_ms": round(load_ms, 3),
+         "sink_gbps": round(sink_gbps, 2), "load_gbps": round(dir_bytes / (load_ms / 1e3) / 1e9, 2),
+         "bytes_per_direction": dir_bytes, **rates, "wall_s_timed": round(wall, 3)},
+        {"kernel": "kv_chunks_copy_kernel<uint4> (sink, pages -> pinned host chunks)",
+         "bound": "host-link", "achieved": round(sink_gbps, 2), "peak": 64.0, "unit": "GB/s",
+         "frac": round(sink_gbps / 64.0, 4), "traffic": None,
+         "algorithmic_bytes_per_launch": dir_bytes // 2,
+         "avg_launch_ms": round(sink_ms / 2, 4)}, cpu)
+
+
+def _cpu_kv_sink(torch, store, snap, old) -> dict:
+    """The oracle's page -> chunk copy (the reference's per-page slice copies) on the host
+    cores over the K side of all chunks of the last step, from a host copy of the pool; its
+    result also checks those chunks' host tensors bit for bit."""
+    import oracle.paged_kv as OP
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    cfg = store.config
+    n = len(store._host_cache)
+    kp = snap[0].cpu()
+    ppc = cfg.pages_per_chunk
+    ids = [[old[l][c * ppc + p] for l in range(cfg.n_layers) for p in range(ppc)]
+           for c in range(n)]
+    t0 = time.perf_counter()
+    chunks = [OP.pages_to_chunk(kp, ids[c], cfg.n_layers, ppc) for c in range(n)]
+    t = time.perf_counter() - t0
+    keys = list(store._host_cache)
+    for c in range(n):
+        if not torch.equal(store._host_cache[keys[c]][0], chunks[c]):
+            raise RuntimeError("kv sink: host chunk differs from the oracle's page -> chunk copy")
+    nbytes = n * chunks[0].numel() * 2
+    model, phys = cpu_info()
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "sample": f"K of all {n} chunks of the last step "
+                                      f"({nbytes / 1e6:.1f} MB), {t * 1e3:.1f} ms",
+            "cpu_model": model, "physical_cores": phys}
+
+
 def calibrate_copy(torch, dev) -> int:
     """A plain elementwise copy of known size (2^30 bytes read, 2^30 written per launch) for
     scaling FETCH_SIZE / WRITE_SIZE readings of the attention kernel to bytes."""
@@ -880,7 +1026,7 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--workload", choices=("decode", "decode-gqa8", "prefill-write",
                                            "moe-permute", "expert-stream", "moe-experts",
-                                           "moe-experts-prefill", "prefill-stream"),
+                                           "moe-experts-prefill", "prefill-stream", "kv-sink"),
                     default="decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -902,7 +1048,7 @@ def main() -> int:
                "moe-permute": bench_moe_permute, "expert-stream": bench_expert_stream,
                "moe-experts": lambda t, d, a: bench_moe_experts(t, d, a, 64),
                "moe-experts-prefill": lambda t, d, a: bench_moe_experts(t, d, a, 4096),
-               "prefill-stream": bench_prefill_stream,
+               "prefill-stream": bench_prefill_stream, "kv-sink": bench_kv_sink,
                }[args.workload]
         print(f"bench: workload {args.workload}", file=sys.stderr, flush=True)
         print(json.dumps(run(torch, dev, args)), flush=True)

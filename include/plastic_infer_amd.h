@@ -95,6 +95,18 @@ int pia_kv_pages_chunk_copy(void* chunk, void* pages, const int64_t* page_ids,
                             int num_kv_heads, int head_dim, int page_size, int64_t num_pages,
                             int elem_bytes, int to_chunk, void* stream);
 
+/* The same copy for num_chunks chunks in one launch, in 16-byte words where page_size *
+ * elem_bytes allows: chunks is a device-readable array of num_chunks chunk base addresses
+ * (device memory, or pinned host memory through its device mapping, pia_device_pointer;
+ * 16-byte aligned), page_ids int64
+ * [num_chunks * num_layers * pages_per_chunk] (chunk-major, then layer-major). Batches the
+ * per-page .to() loops of KVStore.sink_completed_chunks / load_prefix (reference
+ * src/plastic_infer/kv/kv_store.py:230-334) into one transfer over the host link. */
+int pia_kv_pages_chunks_copy(void* const* chunks, int num_chunks, void* pages,
+                             const int64_t* page_ids, int num_layers, int pages_per_chunk,
+                             int num_kv_heads, int head_dim, int page_size, int64_t num_pages,
+                             int elem_bytes, int to_chunk, void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Paged GQA decode attention, batched: one query row per sequence.
  * Per-row semantics of paged_attention_v1(q[b][None,None], ..., kv_num_tokens=L_b, causal=False)
@@ -139,6 +151,36 @@ int pia_paged_attention(void* out, const void* q, const void* k_pages, const voi
                         int num_seqs, int64_t total_q_rows,
                         int num_heads, int num_kv_heads, int head_dim, int page_size,
                         int64_t num_pages, float scale, int dtype, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Host-stream attention: q rows over KV split into host chunks and a device-resident tail,
+ * read in place (reference host_stream_attention_v1, src/plastic_infer/exec/attention.py:193-250,
+ * which concatenates both on the device before SDPA).
+ * q, out: [q_len, num_heads, head_dim] contiguous. Chunk c covers KV positions
+ * [c*chunk_tokens, ...) and is [num_kv_heads, head_dim, len_c] (token innermost) with
+ * len_c = chunk_tokens except the last, len = host_len - (num_chunks-1)*chunk_tokens in
+ * [1, chunk_tokens]. chunk_k / chunk_v: device-readable arrays of num_chunks 16-byte-aligned chunk
+ * addresses: HBM, or pinned host memory through its device mapping (pia_device_pointer), which
+ * the kernel then streams over the host link without staging. The tail (positions host_len ..
+ * host_len + resident_len) is token-major: row t at resident_k + t*resident_token_stride elements
+ * holds [num_kv_heads, head_dim]. Query row i sits at position q_start_pos + i; causal != 0 lets it
+ * see keys at positions <= q_start_pos + i (the reference's mask, and SDPA is_causal when
+ * q_start_pos == 0 and q_len == kv_len), causal == 0 sees all keys. Softmax in fp32; a row that
+ * sees no key writes zeros. head_dim <= 256 (fp32: <= 128). workspace: at least
+ * pia_host_stream_attention_workspace_bytes(...) bytes of device memory (4-byte aligned).
+ * ------------------------------------------------------------------------------------------- */
+int64_t pia_host_stream_attention_workspace_bytes(int64_t q_len, int num_heads, int num_kv_heads,
+                                                  int head_dim, int num_chunks,
+                                                  int64_t chunk_tokens, int64_t host_len,
+                                                  int64_t resident_len);
+int pia_host_stream_attention(void* out, const void* q, int64_t q_len, int num_heads,
+                              const void* const* chunk_k, const void* const* chunk_v,
+                              int num_chunks, int64_t chunk_tokens, int64_t host_len,
+                              const void* resident_k, const void* resident_v,
+                              int64_t resident_len, int64_t resident_token_stride,
+                              int num_kv_heads, int head_dim, int64_t q_start_pos, int causal,
+                              float scale, int dtype, void* workspace, int64_t workspace_bytes,
+                              void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Router: top-k expert selection per token.

@@ -280,6 +280,36 @@ __global__ __launch_bounds__(256) void kv_chunk_copy_kernel(
   }
 }
 
+// Many chunks in one launch, one Word (16 bytes where the page row allows) per thread: chunk c
+// (its own base address, device memory or device-mapped pinned host memory) row (l, h, d) is
+// assembled from the ppc pages of page_ids[(c * L + l) * ppc .. +ppc). Consecutive threads take
+// consecutive words of a chunk row, so the chunk side moves whole rows (tokens_per_chunk * elem
+// bytes) contiguously, the page side vpr words of each page row.
+template <typename Word>
+__global__ __launch_bounds__(256) void kv_chunks_copy_kernel(
+    Word* const* __restrict__ chunks, Word* __restrict__ pages, const int64_t* __restrict__ ids,
+    int L, int ppc, int H, int D, int vpr, int64_t num_pages, int to_chunk, int64_t total) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    int64_t r = i;
+    const int v = int(r % vpr); r /= vpr;
+    const int p = int(r % ppc); r /= ppc;
+    const int d = int(r % D); r /= D;
+    const int h = int(r % H); r /= H;
+    const int l = int(r % L);
+    const int64_t c = r / L;
+    const int64_t phys = ids[(c * L + l) * ppc + p];
+    if (phys < 0 || phys >= num_pages) continue;
+    Word* chunk = chunks[c];
+    const int64_t ci = (((int64_t(l) * H + h) * D + d) * ppc + p) * vpr + v;
+    const int64_t pi = ((phys * H + h) * D + d) * vpr + v;
+    if (to_chunk)
+      chunk[ci] = pages[pi];
+    else
+      pages[pi] = chunk[ci];
+  }
+}
+
 int check_common(int H, int D, int P, int64_t num_pages, int eb) {
   if (H <= 0 || D <= 0 || P <= 0 || P > 1024 || num_pages <= 0)
     return fail(PIA_EINVAL, "kv: num_kv_heads, head_dim, num_pages must be > 0 and page_size "
@@ -388,6 +418,40 @@ extern "C" int pia_kv_gather(void* k_out, void* v_out, const void* k_pages, cons
                        block_tables, bt_stride, cu_seqlens, num_kv_heads, head_dim, page_size,
                        num_pages);
   return check_launch("kv_gather");
+}
+
+extern "C" int pia_kv_pages_chunks_copy(void* const* chunks, int num_chunks, void* pages,
+                                        const int64_t* page_ids, int num_layers,
+                                        int pages_per_chunk, int num_kv_heads, int head_dim,
+                                        int page_size, int64_t num_pages, int elem_bytes,
+                                        int to_chunk, void* stream) {
+  if (int rc = check_common(num_kv_heads, head_dim, page_size, num_pages, elem_bytes)) return rc;
+  if (num_chunks < 0 || num_layers < 0 || pages_per_chunk < 0)
+    return fail(PIA_EINVAL, "kv_chunks_copy: negative size");
+  const int row_bytes = page_size * elem_bytes;
+  int word = 16;
+  while (word > 1 && (row_bytes % word || !aligned(pages, word))) word >>= 1;
+  const int vpr = row_bytes / word;
+  const int64_t total = int64_t(num_chunks) * num_layers * pages_per_chunk * num_kv_heads *
+                        head_dim * vpr;
+  if (total == 0) return 0;
+  if (!chunks || !pages || !page_ids) return fail(PIA_EINVAL, "kv_chunks_copy: null pointer");
+  const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), int64_t(device_cus()) * 16);
+  auto launch = [&](auto tag) {
+    using Word = decltype(tag);
+    hipLaunchKernelGGL(kv_chunks_copy_kernel<Word>, dim3(unsigned(blocks)), dim3(256), 0,
+                       as_stream(stream), reinterpret_cast<Word* const*>(chunks),
+                       reinterpret_cast<Word*>(pages), page_ids, num_layers, pages_per_chunk,
+                       num_kv_heads, head_dim, vpr, num_pages, to_chunk, total);
+  };
+  switch (word) {
+    case 16: launch(uint4{}); break;
+    case 8: launch(uint2{}); break;
+    case 4: launch(uint32_t{}); break;
+    case 2: launch(uint16_t{}); break;
+    default: launch(uint8_t{}); break;
+  }
+  return check_launch("kv_chunks_copy");
 }
 
 extern "C" int pia_kv_pages_chunk_copy(void* chunk, void* pages, const int64_t* page_ids,

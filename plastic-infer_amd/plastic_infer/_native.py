@@ -30,11 +30,16 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_kv_scatter": (_I, [_P, _P, _P, _P, _P, _L, _L, _L, _I, _I, _I, _L, _I, _P]),
     "pia_kv_gather": (_I, [_P, _P, _P, _P, _P, _L, _P, _I, _L, _I, _I, _I, _L, _I, _P]),
     "pia_kv_pages_chunk_copy": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _L, _I, _I, _P]),
+    "pia_kv_pages_chunks_copy": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _L, _I, _I, _P]),
     "pia_paged_decode_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _L]),
     "pia_paged_decode_attention": (
         _I, [_P, _P, _L, _P, _P, _P, _L, _P, _I, _I, _I, _I, _I, _L, _F, _I, _P, _L, _P]),
     "pia_paged_attention": (
         _I, [_P, _P, _P, _P, _P, _L, _P, _P, _P, _I, _L, _I, _I, _I, _I, _L, _F, _I, _P]),
+    "pia_host_stream_attention_workspace_bytes": (_L, [_L, _I, _I, _I, _I, _L, _L, _L]),
+    "pia_host_stream_attention": (
+        _I, [_P, _P, _L, _I, _P, _P, _I, _L, _L, _P, _P, _L, _L, _I, _I, _L, _I, _F, _I, _P, _L,
+             _P]),
     "pia_moe_topk": (_I, [_P, _P, _P, _I, _L, _I, _I, _I, _I, _L, _P]),
     "pia_moe_align_workspace_bytes": (_L, [_I]),
     "pia_moe_align_block_size": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _L, _P, _L, _P]),
@@ -56,7 +61,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_prefill_hit_compact": (_I, [_P, _P, _P, _P, _L, _L, _I, _P]),
 }
 
-EXPECTED_ABI = 4
+EXPECTED_ABI = 5
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

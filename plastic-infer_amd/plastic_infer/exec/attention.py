@@ -25,6 +25,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native as N
+from ..kernel.host_stream import host_stream_attention
 from ..kernel.paged_kv import kv_gather, paged_attention, paged_decode_attention
 
 
@@ -89,30 +90,16 @@ def host_stream_attention_v1(q: torch.Tensor,
                              resident_k: torch.Tensor, resident_v: torch.Tensor,
                              q_start_pos: int = 0, causal: bool = True) -> torch.Tensor:
     """Attention over KV split into host chunks ([H_kv, D, C] each, oldest first) and a device
-    resident tail [1, R, H_kv, D]. The chunks are streamed to the device and laid out with the
-    tail as a one-token-per-page pool ([T, H_kv, D, 1] is the memory of [T, H_kv, D]), which
-    the paged kernel reads directly."""
-    dev = N.require_device(q, resident_k, resident_v, names=("q", "resident_k", "resident_v"))
-    if q.dim() != 4 or q.shape[0] != 1:
-        raise ValueError("q must be [1, q_len, n_heads, head_dim]")
-    _, Sq, Hq, D = q.shape
-    Hkv = resident_k.shape[2]
-    parts_k = [k_c.to(dev, non_blocking=True).permute(2, 0, 1) for k_c, _ in host_chunks]
-    parts_v = [v_c.to(dev, non_blocking=True).permute(2, 0, 1) for _, v_c in host_chunks]
-    k_all = torch.cat(parts_k + [resident_k[0]], dim=0).contiguous()   # [T, H_kv, D]
-    v_all = torch.cat(parts_v + [resident_v[0]], dim=0).contiguous()
-    T = k_all.shape[0]
-    if Sq == 0:
-        return torch.empty_like(q)
-    if T == 0:
-        return torch.zeros_like(q)
-    k_pool = k_all.view(T, Hkv, D, 1)
-    v_pool = v_all.view(T, Hkv, D, 1)
-    bt = torch.arange(T, dtype=torch.int32, device=dev).view(1, T)
-    lens = torch.tensor([T], dtype=torch.int32).to(dev, non_blocking=True)
-    cu = torch.tensor([0, Sq], dtype=torch.int32).to(dev, non_blocking=True)
-    offs = torch.tensor([q_start_pos], dtype=torch.int32).to(dev, non_blocking=True) if causal else None
-    out = paged_attention(q[0], k_pool, v_pool, bt, lens, cu_q=cu, q_pos_offsets=offs)
+    resident tail [1, R, H_kv, D]; q [1, q_len, H, D] at positions q_start_pos.. (reference
+    src/plastic_infer/exec/attention.py:193-250, same mask rule). The chunks are not
+    concatenated: the HIP kernel reads pinned host chunks in place over the host link (decode
+    shapes) and device chunks where they are, merging per-split online-softmax partials."""
+    N.require_device(q, resident_k, resident_v, names=("q", "resident_k", "resident_v"))
+    if q.dim() != 4 or q.shape[0] != 1 or resident_k.dim() != 4 or resident_k.shape[0] != 1:
+        raise ValueError("q must be [1, q_len, n_heads, head_dim] and the resident tail "
+                         "[1, R, n_kv_heads, head_dim]")
+    out = host_stream_attention(q[0], list(host_chunks), resident_k[0], resident_v[0],
+                                q_start_pos=q_start_pos, causal=causal)
     return out.unsqueeze(0)
 
 

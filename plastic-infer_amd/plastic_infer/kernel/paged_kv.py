@@ -217,3 +217,48 @@ def pages_chunk_copy(chunk: torch.Tensor, pages: torch.Tensor, page_ids: torch.T
     N.call("pia_kv_pages_chunk_copy", chunk.data_ptr(), pages.data_ptr(),
            page_ids.contiguous().data_ptr(), L, ppc, H, D, P, num_pages, pages.element_size(),
            1 if to_chunk else 0, N.stream_of(dev))
+
+
+def pages_chunks_copy(chunks: list[torch.Tensor], pages: torch.Tensor, page_ids: torch.Tensor,
+                      to_chunk: bool) -> None:
+    """pages_chunk_copy for many chunks in one launch. chunks: [L, H, D, ppc*P] contiguous
+    tensors of the pool's dtype, each on the pool's device or pinned on the host (reached
+    through its device mapping, so a sink writes host memory directly and a prefix load reads
+    it, with no device staging); page_ids int64 [len(chunks) * L * ppc] on the pool's device,
+    chunk-major then layer-major, -1 = absent. Asynchronous on the current stream: host chunks
+    hold the result only after that stream is synchronized."""
+    from .index_copy import device_ptr
+
+    dev = N.require_device(pages, page_ids, names=("pages", "page_ids"))
+    num_pages, H, D, P = pages.shape
+    if not chunks:
+        return
+    L, _, _, T = chunks[0].shape if chunks[0].dim() == 4 else (0, 0, 0, 0)
+    if T % P or T == 0:
+        raise ValueError(f"chunks must be [L, {H}, {D}, ppc*{P}], got {tuple(chunks[0].shape)}")
+    ptrs = []
+    for i, c in enumerate(chunks):
+        if c.dim() != 4 or tuple(c.shape) != (L, H, D, T):
+            raise ValueError(f"chunk {i} must be [{L}, {H}, {D}, {T}], got {tuple(c.shape)}")
+        if c.dtype != pages.dtype or not c.is_contiguous():
+            raise ValueError(f"chunk {i} must be contiguous {pages.dtype}")
+        if c.device.type == "cpu":
+            if not c.is_pinned():
+                raise ValueError(f"chunk {i} is a pageable host tensor; host chunks must be pinned")
+        elif c.device != dev:
+            raise ValueError(f"chunk {i} is on {c.device}, the pool on {dev}")
+        ptr = device_ptr(c)
+        if ptr % 16:
+            raise ValueError(f"chunk {i} is not 16-byte aligned")
+        ptrs.append(ptr)
+    ppc = T // P
+    if page_ids.dtype != torch.int64 or page_ids.numel() != len(chunks) * L * ppc:
+        raise ValueError(f"page_ids must be int64 [{len(chunks) * L * ppc}]")
+    if not pages.is_contiguous():
+        raise ValueError("pages must be contiguous")
+    table = torch.tensor(ptrs, dtype=torch.int64).to(dev)
+    N.call("pia_kv_pages_chunks_copy", table.data_ptr(), len(chunks), pages.data_ptr(),
+           page_ids.contiguous().data_ptr(), L, ppc, H, D, P, num_pages, pages.element_size(),
+           1 if to_chunk else 0, N.stream_of(dev))
+    # The table is read by the launch: keep it alive until the stream has passed it.
+    table.record_stream(torch.cuda.current_stream(dev))

@@ -4,11 +4,13 @@ Same API and bookkeeping as the reference (src/plastic_infer/kv/kv_store.py:46-4
 movement is the HIP library's:
   * append_token writes one token of every layer with ONE slot-mapped scatter launch
     (reference: per-layer advanced-index stores, kv_store.py:134-143);
-  * sink_completed_chunks gathers a chunk's pages of all layers into a device staging buffer
-    with one page->chunk kernel per pool and copies it to host once
-    (reference: one blocking .to("cpu") per page, kv_store.py:230-276);
-  * load_prefix copies a host chunk to the device once and scatters it into freshly allocated
-    pages with one chunk->page kernel per pool (reference: per-page .to(device), :282-334).
+  * sink_completed_chunks gathers the pages of all new chunks, all layers, with one
+    page->chunk kernel per pool that writes their pinned host tensors directly (no device
+    staging) and synchronizes once (reference: one blocking .to("cpu") per page,
+    kv_store.py:230-276);
+  * load_prefix scatters all matched host chunks into freshly allocated pages with one
+    chunk->page kernel per pool reading the pinned host tensors directly (reference: per-page
+    .to(device), :282-334).
 The pools live on a HIP device; a non-HIP device is rejected at construction.
 Storage layout: k_pages / v_pages = [total_pages, n_kv_heads, head_dim, page_size].
 Host chunks: [n_layers, n_kv_heads, head_dim, tokens_per_chunk] CPU tensors (pinned).
@@ -16,6 +18,7 @@ Host chunks: [n_layers, n_kv_heads, head_dim, tokens_per_chunk] CPU tensors (pin
 
 from __future__ import annotations
 
+import array
 from collections import OrderedDict
 from dataclasses import dataclass, field
 from typing import Optional
@@ -23,9 +26,17 @@ from typing import Optional
 import torch
 
 from .. import _native as N
-from ..kernel.paged_kv import kv_scatter, pages_chunk_copy
+from ..kernel.paged_kv import kv_scatter, pages_chunks_copy
 from .chunk import ChunkKey, compute_prefix_hashes_and_final, longest_prefix_hits
 from .paged import DEFAULT_CHUNK_PAGES, DEFAULT_PAGE_SIZE, BlockTable, PageAllocator
+
+
+def _ids_tensor(ids: list[int], dev: torch.device) -> torch.Tensor:
+    """int64 device tensor of a page-id list (through a packed host buffer: several times
+    faster than torch.tensor on a list of tens of thousands of ints)."""
+    buf = array.array("q", ids)
+    return torch.frombuffer(buf, dtype=torch.int64).to(dev) if ids else \
+        torch.empty(0, dtype=torch.int64, device=dev)
 
 
 def _default_device() -> torch.device:
@@ -163,6 +174,7 @@ class KVStore:
         self._host_lru: OrderedDict[bytes, None] = OrderedDict()
         self._max_host_chunks = config.max_host_chunks
         self._prefix_index: dict[bytes, ChunkKey] = {}
+        self._host_reads: Optional[torch.cuda.Event] = None
 
     # -- request lifecycle --------------------------------------------------------------------
 
@@ -189,9 +201,15 @@ class KVStore:
         return (cfg.n_layers, cfg.n_kv_heads, cfg.head_dim, cfg.tokens_per_chunk)
 
     def sink_completed_chunks(self, cache: KVRequestCache) -> int:
-        """Copy every complete chunk not yet cached to host. Returns the number newly sunk."""
+        """Copy every complete chunk not yet cached to host. Returns the number newly sunk.
+
+        The host-cache bookkeeping runs chunk by chunk in the reference's order (a cached chunk
+        is touched; a new one first evicts the LRU entries it needs room for); the data of all
+        new chunks that are still cached at the end then moves in ONE page->chunk launch per
+        pool, written straight into their pinned host tensors, followed by one synchronize."""
         dev = self.gpu.device
         sunk = 0
+        new: list[tuple[int, bytes]] = []
         for chunk_idx, key in enumerate(cache.chunk_keys):
             full_key = key.full_key
             if full_key in self._host_cache:
@@ -199,19 +217,25 @@ class KVStore:
                 continue
             while len(self._host_cache) >= self._max_host_chunks:
                 self._evict_host_lru()
-            ids = torch.tensor(self._chunk_page_ids(cache, chunk_idx), dtype=torch.int64).to(dev)
-            staged = []
-            for pool in (self.gpu.k_pages, self.gpu.v_pages):
-                buf = torch.zeros(self._chunk_shape(), dtype=self.gpu.dtype, device=dev)
-                pages_chunk_copy(buf, pool, ids, to_chunk=True)
-                host = torch.empty(self._chunk_shape(), dtype=self.gpu.dtype, pin_memory=True)
-                host.copy_(buf, non_blocking=True)
-                staged.append(host)
-            torch.cuda.current_stream(dev).synchronize()
-            self._host_cache[full_key] = (staged[0], staged[1])
+            shape = self._chunk_shape()
+            self._host_cache[full_key] = (
+                torch.empty(shape, dtype=self.gpu.dtype, pin_memory=True),
+                torch.empty(shape, dtype=self.gpu.dtype, pin_memory=True))
             self._prefix_index[full_key] = key
             self._touch_host(full_key)
+            new.append((chunk_idx, full_key))
             sunk += 1
+        # A chunk evicted again by a later one of the same call never needs its data.
+        live = [(idx, k) for idx, k in new if k in self._host_cache]
+        if live:
+            ids: list[int] = []
+            for idx, _ in live:
+                ids.extend(self._chunk_page_ids(cache, idx))
+            ids_t = _ids_tensor(ids, dev)
+            for side, pool in ((0, self.gpu.k_pages), (1, self.gpu.v_pages)):
+                pages_chunks_copy([self._host_cache[k][side] for _, k in live], pool, ids_t,
+                                  to_chunk=True)
+            torch.cuda.current_stream(dev).synchronize()
         return sunk
 
     # -- prefix loading (host -> HBM) ---------------------------------------------------------
@@ -219,7 +243,12 @@ class KVStore:
     def load_prefix(self, cache: KVRequestCache, tokens: list[int]
                     ) -> tuple[int, list[ChunkKey]]:
         """Load the longest cached prefix of `tokens` into freshly allocated pages.
-        Returns (matched_tokens, matched chunk keys)."""
+        Returns (matched_tokens, matched chunk keys).
+
+        All matched chunks move in ONE chunk->page launch per pool that reads their pinned
+        host tensors directly; the call returns with the copy in flight on the current stream
+        (kernels queued behind it see the pages), and the host tensors are kept from eviction
+        until it has finished."""
         cfg = self.config
         matches, _ = longest_prefix_hits(self._prefix_index, tokens,
                                          chunk_size=cfg.tokens_per_chunk)
@@ -229,18 +258,21 @@ class KVStore:
         if self.gpu.allocator.free_pages < need:
             self.evict_chunks(need - self.gpu.allocator.free_pages)
         dev = self.gpu.device
-        for chunk_key in matches:
-            k_host, v_host = self._host_cache[chunk_key.full_key]
-            ids: list[int] = []
+        # Page ids in the order the reference's per-page alloc() loop (chunk, layer, page)
+        # hands them out; alloc_many yields exactly that sequence.
+        ids = self.gpu.allocator.alloc_many(need)
+        ppc = cfg.pages_per_chunk
+        for m in range(len(matches)):
             for layer in range(cfg.n_layers):
-                for _ in range(cfg.pages_per_chunk):
-                    pid = self.gpu.allocator.alloc()
-                    cache.block_table.append_page(layer, pid)
-                    ids.append(pid)
-            ids_t = torch.tensor(ids, dtype=torch.int64).to(dev)
-            for host, pool in ((k_host, self.gpu.k_pages), (v_host, self.gpu.v_pages)):
-                staged = host.to(dev, non_blocking=True)
-                pages_chunk_copy(staged, pool, ids_t, to_chunk=False)
+                lo = (m * cfg.n_layers + layer) * ppc
+                cache.block_table.pages[layer].extend(ids[lo:lo + ppc])
+        ids_t = _ids_tensor(ids, dev)
+        for side, pool in ((0, self.gpu.k_pages), (1, self.gpu.v_pages)):
+            pages_chunks_copy([self._host_cache[k.full_key][side] for k in matches], pool, ids_t,
+                              to_chunk=False)
+        done = torch.cuda.Event()
+        done.record(torch.cuda.current_stream(dev))
+        self._host_reads = done
         cache._length = len(matches) * cfg.tokens_per_chunk
         cache.chunk_keys = list(matches)
         cache._final_hash = matches[-1].cumulative_key
@@ -276,6 +308,10 @@ class KVStore:
         if not self._host_lru:
             return
         oldest, _ = self._host_lru.popitem(last=False)
+        if self._host_reads is not None:
+            # A prefix load may still be reading this chunk's pinned memory.
+            self._host_reads.synchronize()
+            self._host_reads = None
         del self._host_cache[oldest]
         self._prefix_index.pop(oldest, None)
 

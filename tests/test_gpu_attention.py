@@ -318,3 +318,96 @@ def test_rejects_host_tensors():
         paged_decode_attention(torch.zeros(1, 2, 128), torch.zeros(2, 1, 128, 16),
                                torch.zeros(2, 1, 128, 16), torch.zeros(1, 1, dtype=torch.int32),
                                torch.ones(1, dtype=torch.int32))
+
+
+def _hs_split(total, host_len, chunk, Hkv, D, dtype, seed, where):
+    g = torch.Generator().manual_seed(seed)
+    kf = (torch.randn(1, total, Hkv, D, generator=g) * 0.5).to(dtype)
+    vf = torch.randn(1, total, Hkv, D, generator=g).to(dtype)
+    chunks = []
+    for s in range(0, host_len, chunk):
+        e = min(s + chunk, host_len)
+        k_c = kf[0, s:e].permute(1, 2, 0).contiguous()
+        v_c = vf[0, s:e].permute(1, 2, 0).contiguous()
+        if where == "pinned":
+            k_c, v_c = k_c.pin_memory(), v_c.pin_memory()
+        elif where == "device":
+            k_c, v_c = k_c.cuda(), v_c.cuda()
+        chunks.append((k_c, v_c))
+    return kf, vf, chunks
+
+
+@pytest.mark.parametrize("where", ["pinned", "device", "pageable"])
+@pytest.mark.parametrize("dtype,Hq,Hkv,D", [(torch.bfloat16, 32, 8, 128),
+                                            (torch.float16, 8, 2, 256),
+                                            (torch.float32, 16, 4, 64)])
+@pytest.mark.parametrize("q_len,causal", [(1, True), (4, True), (3, False), (20, True)])
+def test_host_stream_attention_shapes(dev, where, dtype, Hq, Hkv, D, q_len, causal):
+    """Chunks of 256 tokens with a ragged 100-token last chunk and a 37-token device tail;
+    q rows at the end of the KV (decode / a few appended tokens), in the middle (non-causal), and
+    enough rows (20 x G) that the chunks are staged to HBM instead of streamed."""
+    host_len, chunk, tail = 5 * 256 + 100, 256, 37
+    total = host_len + tail
+    kf, vf, chunks = _hs_split(total, host_len, chunk, Hkv, D, dtype, 31 + q_len, where)
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(1, q_len, Hq, D, generator=g).to(dtype)
+    q_start = total - q_len if causal else 500
+    rk, rv = kf[:, host_len:].to(dev), vf[:, host_len:].to(dev)
+    out = host_stream_attention_v1(q.to(dev), chunks, rk, rv, q_start_pos=q_start,
+                                   causal=causal)
+    f32 = [(k.float().cpu(), v.float().cpu()) for k, v in chunks]
+    ref = OP.host_stream_attention(q.float(), f32, kf[:, host_len:].float(),
+                                   vf[:, host_len:].float(), q_start_pos=q_start, causal=causal)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    err = (out.float().cpu() - ref).abs().max().item()
+    assert err <= tol, err
+
+
+def test_host_stream_attention_long_pinned_decode(dev):
+    """8192 host tokens (32 pinned chunks) + 300 resident: several tiles per split."""
+    Hq, Hkv, D = 32, 8, 128
+    host_len, tail = 8192, 300
+    kf, vf, chunks = _hs_split(host_len + tail, host_len, 256, Hkv, D, torch.bfloat16, 5,
+                               "pinned")
+    q = torch.randn(1, 1, Hq, D).to(torch.bfloat16)
+    rk, rv = kf[:, host_len:].to(dev), vf[:, host_len:].to(dev)
+    out = host_stream_attention_v1(q.to(dev), chunks, rk, rv, q_start_pos=host_len + tail)
+    f32 = [(k.float(), v.float()) for k, v in chunks]
+    ref = OP.host_stream_attention(q.float(), f32, kf[:, host_len:].float(),
+                                   vf[:, host_len:].float(), q_start_pos=host_len + tail)
+    assert (out.float().cpu() - ref).abs().max().item() <= 2e-2
+
+
+def test_host_stream_attention_edge_cases(dev):
+    Hq, Hkv, D = 4, 2, 16
+    kf, vf, chunks = _hs_split(30, 20, 8, Hkv, D, torch.float32, 9, "pinned")
+    q = torch.randn(1, 2, Hq, D)
+    # resident tail given as a strided view: rows of a wider [T, 2*Hkv, D] buffer
+    wide_k = torch.zeros(10, 2 * Hkv, D)
+    wide_v = torch.zeros(10, 2 * Hkv, D)
+    wide_k[:, :Hkv] = kf[0, 20:]
+    wide_v[:, :Hkv] = vf[0, 20:]
+    rk = wide_k.to(dev)[:, :Hkv].unsqueeze(0)
+    rv = wide_v.to(dev)[:, :Hkv].unsqueeze(0)
+    out = host_stream_attention_v1(q.to(dev), chunks, rk, rv, q_start_pos=28)
+    ref = OP.host_stream_attention(q, chunks, kf[:, 20:], vf[:, 20:], q_start_pos=28)
+    assert torch.allclose(out.cpu(), ref, atol=1e-4)
+    # chunks of unequal lengths (not C, ..., C, last <= C): laid out as a device tail
+    odd = [(kf[0, 0:5].permute(1, 2, 0).contiguous(), vf[0, 0:5].permute(1, 2, 0).contiguous()),
+           (kf[0, 5:20].permute(1, 2, 0).contiguous(), vf[0, 5:20].permute(1, 2, 0).contiguous())]
+    out = host_stream_attention_v1(q.to(dev), odd, kf[:, 20:].to(dev), vf[:, 20:].to(dev),
+                                   q_start_pos=28)
+    assert torch.allclose(out.cpu(), ref, atol=1e-4)
+    # causal rows that see only a prefix of the host chunks (keys past q_start + q_len dropped)
+    out = host_stream_attention_v1(q.to(dev), chunks, kf[:, 20:].to(dev), vf[:, 20:].to(dev),
+                                   q_start_pos=3)
+    ref = OP.host_stream_attention(q, chunks, kf[:, 20:], vf[:, 20:], q_start_pos=3)
+    assert torch.allclose(out.cpu(), ref, atol=1e-4)
+    # no keys at all: zeros (the reference's SDPA over an empty KV has no defined output)
+    empty = torch.zeros(1, 0, Hkv, D, device=dev)
+    out = host_stream_attention_v1(q.to(dev), [], empty, empty, q_start_pos=0)
+    assert out.shape == (1, 2, Hq, D) and not out.any()
+    # mismatched dtypes are rejected
+    with pytest.raises(ValueError):
+        host_stream_attention_v1(q.to(dev), [(c[0].half(), c[1].half()) for c in chunks],
+                                 kf[:, 20:].to(dev), vf[:, 20:].to(dev), q_start_pos=28)

@@ -9,7 +9,7 @@ import torch
 
 import oracle.paged_kv as OP
 import oracle.workloads as W
-from plastic_infer.kernel import kv_gather, kv_scatter, pages_chunk_copy
+from plastic_infer.kernel import kv_gather, kv_scatter, pages_chunk_copy, pages_chunks_copy
 from plastic_infer.kv.kv_store import KVConfig, KVStore
 
 pytestmark = pytest.mark.gpu
@@ -153,6 +153,52 @@ def test_pages_chunk_copy_both_ways(dev):
                 assert torch.equal(back[pid].cpu(), pages[pid])
 
 
+@pytest.mark.parametrize("where", ["device", "pinned"])
+@pytest.mark.parametrize("dtype,P", [(torch.float32, 4), (torch.bfloat16, 4),
+                                     (torch.bfloat16, 16), (torch.bfloat16, 3)])
+def test_pages_chunks_copy_many_chunks(dev, where, dtype, P):
+    """Several chunks in one launch, each at its own address (HBM or pinned host memory),
+    page rows of 16, 8 and 6 bytes (16-, 8- and 2-byte words), absent pages left alone."""
+    g = torch.Generator().manual_seed(15 + P)
+    L, H, D, ppc, n_pages, n_chunks = 3, 2, 8, 2, 40, 4
+    pages = torch.randn(n_pages, H, D, P, generator=g).to(dtype)
+    perm = torch.randperm(n_pages, generator=g).tolist()
+    ids = perm[:n_chunks * L * ppc]
+    ids[5] = -1
+    ids[17] = -1
+    if where == "pinned":
+        chunks = [torch.zeros(L, H, D, ppc * P, dtype=dtype, pin_memory=True)
+                  for _ in range(n_chunks)]
+    else:
+        chunks = [torch.zeros(L, H, D, ppc * P, dtype=dtype, device=dev) for _ in range(n_chunks)]
+    ids_t = torch.tensor(ids, dtype=torch.int64, device=dev)
+    pages_chunks_copy(chunks, pages.to(dev), ids_t, to_chunk=True)
+    torch.cuda.synchronize()
+    per = L * ppc
+    for c in range(n_chunks):
+        ref = OP.pages_to_chunk(pages, ids[c * per:(c + 1) * per], L, ppc)
+        assert torch.equal(chunks[c].cpu(), ref), c
+    back = torch.zeros(n_pages, H, D, P, dtype=dtype, device=dev)
+    pages_chunks_copy(chunks, back, ids_t, to_chunk=False)
+    back = back.cpu()
+    listed = {pid for pid in ids if pid >= 0}
+    for pid in range(n_pages):
+        want = pages[pid] if pid in listed else torch.zeros_like(pages[pid])
+        assert torch.equal(back[pid], want), pid
+
+
+def test_pages_chunks_copy_rejects_pageable_and_bad_ids(dev):
+    pages = torch.zeros(8, 2, 4, 4, device=dev)
+    ids = torch.zeros(2 * 1 * 2, dtype=torch.int64, device=dev)
+    with pytest.raises(ValueError):
+        pages_chunks_copy([torch.zeros(1, 2, 4, 8), torch.zeros(1, 2, 4, 8)], pages, ids, True)
+    good = [torch.zeros(1, 2, 4, 8, device=dev) for _ in range(2)]
+    with pytest.raises(ValueError):
+        pages_chunks_copy(good, pages, ids[:3], True)
+    with pytest.raises(ValueError):
+        pages_chunks_copy([good[0], torch.zeros(1, 2, 4, 4, device=dev)], pages, ids, True)
+
+
 # ---- KV store (the reference's tests/test_kv_store.py scenarios, pools in HBM) ----------------
 
 @pytest.fixture
@@ -242,3 +288,45 @@ def test_store_evict_chunks(store):
     used = store.gpu.allocator.used_pages
     freed = store.evict_chunks(need_pages=1, protected_request=cache)
     assert freed >= 1 and store.gpu.allocator.used_pages == used - freed
+
+
+def test_store_sink_and_load_many_bf16_chunks(dev):
+    """Five 64-token chunks of a 4-layer bf16 store sink in one launch per pool and load back
+    in one launch per pool; both directions bit-exact against the oracle's page<->chunk copy."""
+    cfg = KVConfig(n_layers=4, n_kv_heads=2, head_dim=64, page_size=16, pages_per_chunk=4,
+                   max_pages=256, max_host_chunks=16, dtype=torch.bfloat16, device=dev)
+    store = KVStore(cfg)
+    C = cfg.tokens_per_chunk
+    n = 5 * C + 7
+    cache = store.new_request()
+    cache._ensure_pages(n)
+    cache._length = n
+    g = torch.Generator().manual_seed(21)
+    kp = torch.randn(store.gpu.k_pages.shape, generator=g).to(torch.bfloat16)
+    vp = torch.randn(store.gpu.v_pages.shape, generator=g).to(torch.bfloat16)
+    store.gpu.k_pages.copy_(kp)
+    store.gpu.v_pages.copy_(vp)
+    toks = list(range(1000, 1000 + n))
+    cache.set_token_ids(toks)
+    assert store.sink_completed_chunks(cache) == 5
+    assert store.sink_completed_chunks(cache) == 0
+    for c, key in enumerate(cache.chunk_keys):
+        ids = store._chunk_page_ids(cache, c)
+        hk, hv = store._host_cache[key.full_key]
+        assert hk.is_pinned() and hv.is_pinned()
+        assert torch.equal(hk, OP.pages_to_chunk(kp, ids, cfg.n_layers, cfg.pages_per_chunk))
+        assert torch.equal(hv, OP.pages_to_chunk(vp, ids, cfg.n_layers, cfg.pages_per_chunk))
+    old_tables = [list(cache.block_table.pages[l]) for l in range(cfg.n_layers)]
+    store.free_request(cache)
+    store.gpu.k_pages.zero_()
+    store.gpu.v_pages.zero_()
+    c2 = store.new_request()
+    matched, keys = store.load_prefix(c2, toks)
+    assert matched == 5 * C and len(keys) == 5
+    k_now, v_now = store.gpu.k_pages.cpu(), store.gpu.v_pages.cpu()
+    for layer in range(cfg.n_layers):
+        for lp in range(5 * cfg.pages_per_chunk):
+            new_pid = c2.block_table.get_page(layer, lp)
+            old_pid = old_tables[layer][lp]
+            assert torch.equal(k_now[new_pid], kp[old_pid])
+            assert torch.equal(v_now[new_pid], vp[old_pid])
