@@ -1002,6 +1002,108 @@ def _cpu_kv_sink(torch, store, snap, old) -> dict:
             "cpu_model": model, "physical_cores": phys}
 
 
+HS_HQ, HS_HKV, HS_D, HS_C, HS_CHUNKS, HS_TAIL, HS_SEED = 32, 8, 128, 256, 512, 512, 11
+
+
+def bench_host_stream(torch, dev, args) -> dict:
+    """Long-context decode over host-resident KV (the reference's host_stream_attention_v1):
+    one Qwen3-8B attention layer (32 q / 8 kv heads, D 128, bf16), 131072 context tokens in 512
+    pinned host chunks of 256 tokens ([8, 128, 256] K and V each, 537 MB) plus a 512-token
+    device tail; one step = one decode query row over all of it. The kernel streams the chunks
+    over the host link in place (no device copy of the KV)."""
+    from plastic_infer.exec.attention import host_stream_attention_v1
+
+    Hq, Hkv, D, C, n, tail = HS_HQ, HS_HKV, HS_D, HS_C, HS_CHUNKS, HS_TAIL
+    host_len = n * C
+    g = torch.Generator().manual_seed(HS_SEED)
+    print(f"bench: pinning {2 * host_len * Hkv * D * 2 / 1e6:.0f} MB of host chunks",
+          file=sys.stderr, flush=True)
+    kh = torch.empty(n, Hkv, D, C, dtype=torch.bfloat16, pin_memory=True)
+    vh = torch.empty(n, Hkv, D, C, dtype=torch.bfloat16, pin_memory=True)
+    kh.copy_((torch.randn(n, Hkv, D, C, generator=g) * 0.5).to(torch.bfloat16))
+    vh.copy_(torch.randn(n, Hkv, D, C, generator=g).to(torch.bfloat16))
+    chunks = [(kh[i], vh[i]) for i in range(n)]
+    rk = (torch.randn(1, tail, Hkv, D, generator=g) * 0.5).to(torch.bfloat16)
+    rv = torch.randn(1, tail, Hkv, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(1, 1, Hq, D, generator=g).to(torch.bfloat16)
+    rk_d, rv_d, q_d = rk.to(dev), rv.to(dev), q.to(dev)
+    pos = host_len + tail
+    host_bytes = 2 * host_len * Hkv * D * 2
+    step_bytes = host_bytes + 2 * tail * Hkv * D * 2 + 2 * Hq * D * 2
+
+    def step():
+        return host_stream_attention_v1(q_d, chunks, rk_d, rv_d, q_start_pos=pos)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    stream = torch.cuda.current_stream(dev)
+    wall0 = time.perf_counter()
+    for a, b in ev:
+        a.record(stream)
+        out = step()
+        b.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - wall0
+    ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    gbps = host_bytes / (ms / 1e3) / 1e9
+
+    # the DMA engines moving the same host bytes to HBM: the transfer a materialising
+    # implementation pays before its attention even starts
+    kd = torch.empty(kh.shape, dtype=kh.dtype, device=dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    kd.copy_(kh, non_blocking=True)
+    e0.record()
+    kd.copy_(kh, non_blocking=True)
+    kd.copy_(vh, non_blocking=True)
+    e1.record()
+    torch.cuda.synchronize(dev)
+    dma_ms = e0.elapsed_time(e1)
+    del kd
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = _cpu_host_stream(torch, q, chunks, rk, rv, pos, out)
+    return _result(
+        "host-stream decode attention GB/s over the host link", gbps, "GB/s", args, ms, "bf16",
+        {"workload": "qwen3-8b attention layer, 1 decode row over 131072 host tokens (512 pinned "
+                     "chunks of 256) + 512 device tokens, 32 q / 8 kv heads, head_dim 128",
+         "heads": Hq, "kv_heads": Hkv, "head_dim": D, "chunk_tokens": C, "host_chunks": n,
+         "resident_tokens": tail},
+        {"host_bytes_per_step": host_bytes, "bytes_per_step": step_bytes,
+         "dma_same_bytes_ms": round(dma_ms, 3),
+         "dma_gbps": round(host_bytes / (dma_ms / 1e3) / 1e9, 2),
+         "wall_s_timed": round(wall, 3)},
+        {"kernel": "hs_attn_partial<bf16, 2> + hs_attn_merge (one call)", "bound": "host-link",
+         "achieved": round(gbps, 2), "peak": 64.0, "unit": "GB/s", "frac": round(gbps / 64.0, 4),
+         "traffic": None, "algorithmic_bytes_per_launch": host_bytes,
+         "avg_launch_ms": round(ms, 4)}, cpu)
+
+
+def _cpu_host_stream(torch, q, chunks, rk, rv, pos, out) -> dict:
+    """The oracle (concatenate + GQA expand + SDPA, fp32) on the host cores over the whole
+    workload; its result also checks the GPU output (2e-2, the bf16 attention bar)."""
+    import oracle.paged_kv as OP
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    f32 = [(k.float(), v.float()) for k, v in chunks]
+    rkf, rvf, qf = rk.float(), rv.float(), q.float()
+    t0 = time.perf_counter()
+    ref = OP.host_stream_attention(qf, f32, rkf, rvf, q_start_pos=pos)
+    t = time.perf_counter() - t0
+    err = (out.float().cpu() - ref).abs().max().item()
+    if err > 2e-2:
+        raise RuntimeError(f"host stream: GPU output differs from the oracle ({err})")
+    nbytes = sum(k.numel() + v.numel() for k, v in chunks) * 2
+    model, phys = cpu_info()
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the whole step (fp32 copies of the bf16 KV), {t * 1e3:.0f} ms; max "
+                      f"|GPU - oracle| {err:.2e}",
+            "cpu_model": model, "physical_cores": phys}
+
+
 def calibrate_copy(torch, dev) -> int:
     """A plain elementwise copy of known size (2^30 bytes read, 2^30 written per launch) for
     scaling FETCH_SIZE / WRITE_SIZE readings of the attention kernel to bytes."""
@@ -1026,7 +1128,8 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--workload", choices=("decode", "decode-gqa8", "prefill-write",
                                            "moe-permute", "expert-stream", "moe-experts",
-                                           "moe-experts-prefill", "prefill-stream", "kv-sink"),
+                                           "moe-experts-prefill", "prefill-stream", "kv-sink",
+                                           "host-stream"),
                     default="decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -1049,6 +1152,7 @@ def main() -> int:
                "moe-experts": lambda t, d, a: bench_moe_experts(t, d, a, 64),
                "moe-experts-prefill": lambda t, d, a: bench_moe_experts(t, d, a, 4096),
                "prefill-stream": bench_prefill_stream, "kv-sink": bench_kv_sink,
+               "host-stream": bench_host_stream,
                }[args.workload]
         print(f"bench: workload {args.workload}", file=sys.stderr, flush=True)
         print(json.dumps(run(torch, dev, args)), flush=True)

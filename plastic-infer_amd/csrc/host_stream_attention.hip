@@ -8,13 +8,13 @@
 // host memory through its device mapping, which the kernel then reads over the host link in
 // place. The tail is token-major: row t at resident + t * token_stride holds [Hkv, D].
 //
-// hs_attn_partial<DT, DPL>: grid (split, kv head, row tile). The KV of one kv head is cut into
-// 64-token tiles (a tile never crosses a chunk); split s takes a contiguous run of tiles. A
-// 256-thread workgroup stages each tile's K as [D][64] and V as [64][D] in LDS (16-byte loads
-// where the layout allows), then its 4 waves each carry 8 of the row tile's 32 query rows
-// (row r = query i * G + g, head hk * G + g): lane = token for QK^T, an fp32 base-2 online
-// softmax per row, lane = head-dim element for PV. It writes one (max, sum, unnormalised acc)
-// partial per (split, query, head).
+// hs_attn_partial<DT, DPL, RT>: grid (split, kv head, row tile). The KV of one kv head is cut
+// into 64-token tiles (a tile never crosses a chunk); split s takes a contiguous run of tiles. A
+// 256-thread workgroup stages each tile's K as [D][64] and V as [64][D] in LDS (16-byte loads,
+// fetched into registers one tile ahead, where the layout allows), then its 4 waves each carry
+// RT/4 of the row tile's RT query rows (row r = query i * G + g, head hk * G + g): lane = token
+// for QK^T, an fp32 base-2 online softmax per row, lane = head-dim element for PV. It writes one
+// (max, sum, unnormalised acc) partial per (split, query, head).
 // hs_attn_merge<DT>: one 64-lane wave per (query, head) folds the splits' partials.
 //
 // With one row tile (decode: q_len * G <= 32) every KV byte crosses the host link once; the
@@ -28,9 +28,14 @@ namespace {
 
 constexpr float kLog2eHs = 1.4426950408889634f;
 constexpr float kNegBigHs = -1.0e30f;
-constexpr int HS_TILE = 64;     // tokens per tile
-constexpr int HS_RT = 32;       // query rows per workgroup
-constexpr int HS_RPW = HS_RT / 4;
+constexpr int HS_SUB = 64;      // tokens per compute step (one per lane)
+
+// Tokens per staged tile: 256-byte stored rows (128 bf16 / fp16 tokens, 64 fp32) for
+// head_dim <= 128, half that above. Host reads in 128-byte pieces run at about 3/4 of the rate of
+// 256-byte and longer ones, so a chunk's [d][t] rows are fetched 256 bytes at a time.
+__host__ __device__ constexpr int hs_tile_tokens(int dm, int elem_bytes) {
+  return (dm <= 128 ? 256 : 128) / elem_bytes;
+}
 
 struct HsGeom {
   const void* const* chunk_k;
@@ -55,18 +60,85 @@ struct HsGeom {
   int res_vec;            // ... for the tail
 };
 
-template <int DT, int DPL>
-__global__ __launch_bounds__(256) void hs_attn_partial(
+template <typename T>
+struct HsTile {
+  const T* kb;
+  const T* vb;
+  int64_t pos0;     // global position of the tile's token 0
+  int64_t rowlen;   // layout 0: tokens per stored (h, d) row; layout 1: elements per token row
+  int tl;           // tokens in the tile
+  int layout;       // 0: chunk [Hkv, D, len] (token innermost); 1: tail rows [len][Hkv, D]
+  int vec;          // 16-byte loads are aligned and stay inside the stored rows
+};
+
+template <typename T, int TT>
+__device__ __forceinline__ HsTile<T> hs_locate(const HsGeom& g, int tile, int hk, int D) {
+  HsTile<T> f;
+  if (tile < g.host_tiles) {
+    int c, j;
+    if (tile < g.full_tiles) {
+      c = tile / g.tpc;
+      j = tile - c * g.tpc;
+    } else {
+      c = g.num_chunks - 1;
+      j = tile - g.full_tiles;
+    }
+    // visible tokens of chunk c vs the row length it is stored with
+    const int64_t vis = c == g.num_chunks - 1 ? g.host_len - int64_t(c) * g.chunk_tokens
+                                              : g.chunk_tokens;
+    const bool last = c == g.stored_chunks - 1;
+    const int64_t clen = last ? g.last_row : g.chunk_tokens;
+    const int64_t t0 = int64_t(j) * TT;
+    f.tl = int(min<int64_t>(TT, vis - t0));
+    f.kb = reinterpret_cast<const T*>(g.chunk_k[c]) + int64_t(hk) * D * clen + t0;
+    f.vb = reinterpret_cast<const T*>(g.chunk_v[c]) + int64_t(hk) * D * clen + t0;
+    f.pos0 = int64_t(c) * g.chunk_tokens + t0;
+    f.rowlen = clen;
+    f.layout = 0;
+    f.vec = last ? g.last_vec : g.chunk_vec;
+  } else {
+    const int64_t t0 = int64_t(tile - g.host_tiles) * TT;
+    f.tl = int(min<int64_t>(TT, g.res_len - t0));
+    f.kb = reinterpret_cast<const T*>(g.res_k) + t0 * g.res_stride + int64_t(hk) * D;
+    f.vb = reinterpret_cast<const T*>(g.res_v) + t0 * g.res_stride + int64_t(hk) * D;
+    f.pos0 = g.host_len + t0;
+    f.rowlen = g.res_stride;
+    f.layout = 1;
+    f.vec = g.res_vec;
+  }
+  return f;
+}
+
+// 16-byte group n of a thread: layout 0 -> (d, t..t+VW), layout 1 -> (t, d..d+VW).
+template <int VW, int TT>
+__device__ __forceinline__ bool hs_group(int layout, int e, int D, int tl, int& d, int& t) {
+  if (layout == 0) {
+    constexpr int GPR = TT / VW;
+    d = e / GPR;
+    t = (e - d * GPR) * VW;
+    return d < D && t < tl;
+  }
+  const int gpr = D / VW;
+  t = e / gpr;
+  d = (e - t * gpr) * VW;
+  return t < tl;
+}
+
+template <int DT, int DPL, int RT>
+__global__ __launch_bounds__(256, 2) void hs_attn_partial(
     HsGeom g, const void* __restrict__ q_, int64_t q_len, int Hq, int Hkv, int D, int causal,
     float scale_log2, float* __restrict__ part) {
   using E = Elem<DT>;
   using T = typename E::T;
   constexpr int DM = 64 * DPL;
   constexpr int VW = 16 / int(sizeof(T));
-  __shared__ __align__(16) T k_s[DM * HS_TILE];     // [d][t]
-  __shared__ __align__(16) T v_s[HS_TILE * DM];     // [t][d]
-  __shared__ float q_s[HS_RT * DM];
-  __shared__ float p_s[HS_RT * HS_TILE];
+  constexpr int TT = hs_tile_tokens(DM, int(sizeof(T)));
+  constexpr int NV = DM * TT / VW / 256;   // 16-byte groups per thread per tile (K or V)
+  constexpr int RPW = RT / 4;                   // query rows per wave
+  __shared__ __align__(16) T k_s[DM * TT];     // [d][t]
+  __shared__ __align__(16) T v_s[TT * DM];     // [t][d]
+  __shared__ float q_s[RT * DM];
+  __shared__ float p_s[RT * HS_SUB];
 
   const T* q = reinterpret_cast<const T*>(q_);
   const int split = blockIdx.x, hk = blockIdx.y, rt = blockIdx.z;
@@ -74,9 +146,9 @@ __global__ __launch_bounds__(256) void hs_attn_partial(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = Hq / Hkv;
   const int64_t R = q_len * G;
-  const int64_t r0 = int64_t(rt) * HS_RT;
+  const int64_t r0 = int64_t(rt) * RT;
 
-  for (int e = tid; e < HS_RT * DM; e += 256) {
+  for (int e = tid; e < RT * DM; e += 256) {
     const int r = e / DM, d = e - r * DM;
     const int64_t row = r0 + r;
     float v = 0.f;
@@ -89,11 +161,11 @@ __global__ __launch_bounds__(256) void hs_attn_partial(
   }
 
   // rows of this wave: r0 + wave + 4k
-  int64_t qpos[HS_RPW];
-  bool live[HS_RPW];
-  float m[HS_RPW], l[HS_RPW], acc[HS_RPW][DPL];
+  int64_t qpos[RPW];
+  bool live[RPW];
+  float m[RPW], l[RPW], acc[RPW][DPL];
 #pragma unroll
-  for (int k = 0; k < HS_RPW; ++k) {
+  for (int k = 0; k < RPW; ++k) {
     const int64_t row = r0 + wave + 4 * k;
     live[k] = row < R;
     qpos[k] = g.q_start + (live[k] ? row / G : 0);
@@ -105,140 +177,118 @@ __global__ __launch_bounds__(256) void hs_attn_partial(
 
   const int tile_lo = split * g.tiles_per_split;
   const int tile_hi = min(g.total_tiles, tile_lo + g.tiles_per_split);
+  // 16-byte tiles are fetched into registers one tile ahead, so the host-link (or HBM) reads
+  // of tile n+1 are in flight while tile n is computed from LDS.
+  uint4 kr[NV], vr[NV];
+  auto fetch = [&](const HsTile<T>& f) {
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      int d, t;
+      const bool ok = hs_group<VW, TT>(f.layout, tid + 256 * n, D, f.tl, d, t);
+      const int64_t off = f.layout == 0 ? int64_t(d) * f.rowlen + t : int64_t(t) * f.rowlen + d;
+      kr[n] = ok ? *reinterpret_cast<const uint4*>(f.kb + off) : uint4{0, 0, 0, 0};
+      vr[n] = ok ? *reinterpret_cast<const uint4*>(f.vb + off) : uint4{0, 0, 0, 0};
+    }
+  };
+  HsTile<T> cur{};
+  if (tile_lo < tile_hi) {
+    cur = hs_locate<T, TT>(g, tile_lo, hk, D);
+    if (cur.vec) fetch(cur);
+  }
   for (int tile = tile_lo; tile < tile_hi; ++tile) {
-    // locate the tile: chunk c tile j, or tail tile j
-    const T* kb;
-    const T* vb;
-    int64_t pos0, rowlen;   // global position of token 0 of the tile; row length / stride
-    int tl, layout, vec;
-    if (tile < g.host_tiles) {
-      int c, j;
-      if (tile < g.full_tiles) {
-        c = tile / g.tpc;
-        j = tile - c * g.tpc;
-      } else {
-        c = g.num_chunks - 1;
-        j = tile - g.full_tiles;
-      }
-      // visible tokens of chunk c vs the row length it is stored with
-      const int64_t vis = c == g.num_chunks - 1 ? g.host_len - int64_t(c) * g.chunk_tokens
-                                                : g.chunk_tokens;
-      const bool last = c == g.stored_chunks - 1;
-      const int64_t clen = last ? g.last_row : g.chunk_tokens;
-      const int64_t t0 = int64_t(j) * HS_TILE;
-      tl = int(min<int64_t>(HS_TILE, vis - t0));
-      kb = reinterpret_cast<const T*>(g.chunk_k[c]) + int64_t(hk) * D * clen + t0;
-      vb = reinterpret_cast<const T*>(g.chunk_v[c]) + int64_t(hk) * D * clen + t0;
-      pos0 = int64_t(c) * g.chunk_tokens + t0;
-      rowlen = clen;
-      layout = 0;
-      vec = last ? g.last_vec : g.chunk_vec;
-    } else {
-      const int64_t t0 = int64_t(tile - g.host_tiles) * HS_TILE;
-      tl = int(min<int64_t>(HS_TILE, g.res_len - t0));
-      kb = reinterpret_cast<const T*>(g.res_k) + t0 * g.res_stride + int64_t(hk) * D;
-      vb = reinterpret_cast<const T*>(g.res_v) + t0 * g.res_stride + int64_t(hk) * D;
-      pos0 = g.host_len + t0;
-      rowlen = g.res_stride;
-      layout = 1;
-      vec = g.res_vec;
-    }
-
     __syncthreads();   // the previous tile's LDS reads are done
-    if (layout == 0) {
-      // element (t, d) at kb[d * rowlen + t]
-      if (vec) {
-        constexpr int GPR = HS_TILE / VW;   // 16-byte groups per d row
-        for (int e = tid; e < D * GPR; e += 256) {
-          const int d = e / GPR, t = (e - d * GPR) * VW;
-          if (t < tl) {
-            const uint4 kw = *reinterpret_cast<const uint4*>(kb + int64_t(d) * rowlen + t);
-            const uint4 vw = *reinterpret_cast<const uint4*>(vb + int64_t(d) * rowlen + t);
-            *reinterpret_cast<uint4*>(&k_s[d * HS_TILE + t]) = kw;
-            const T* ve = reinterpret_cast<const T*>(&vw);
+    if (cur.vec) {
 #pragma unroll
-            for (int x = 0; x < VW; ++x) v_s[(t + x) * DM + d] = ve[x];
-          }
+      for (int n = 0; n < NV; ++n) {
+        int d, t;
+        if (!hs_group<VW, TT>(cur.layout, tid + 256 * n, D, cur.tl, d, t)) continue;
+        const T* ke = reinterpret_cast<const T*>(&kr[n]);
+        const T* ve = reinterpret_cast<const T*>(&vr[n]);
+        if (cur.layout == 0) {
+          *reinterpret_cast<uint4*>(&k_s[d * TT + t]) = kr[n];
+#pragma unroll
+          for (int x = 0; x < VW; ++x) v_s[(t + x) * DM + d] = ve[x];
+        } else {
+          *reinterpret_cast<uint4*>(&v_s[t * DM + d]) = vr[n];
+#pragma unroll
+          for (int x = 0; x < VW; ++x) k_s[(d + x) * TT + t] = ke[x];
         }
-      } else {
-        for (int e = tid; e < D * HS_TILE; e += 256) {
-          const int d = e / HS_TILE, t = e - d * HS_TILE;
-          if (t < tl) {
-            k_s[d * HS_TILE + t] = kb[int64_t(d) * rowlen + t];
-            v_s[t * DM + d] = vb[int64_t(d) * rowlen + t];
-          }
+      }
+    } else if (cur.layout == 0) {
+      for (int e = tid; e < D * TT; e += 256) {
+        const int d = e / TT, t = e - d * TT;
+        if (t < cur.tl) {
+          k_s[d * TT + t] = cur.kb[int64_t(d) * cur.rowlen + t];
+          v_s[t * DM + d] = cur.vb[int64_t(d) * cur.rowlen + t];
         }
       }
     } else {
-      // element (t, d) at kb[t * rowlen + d]
-      if (vec) {
-        const int gpr = D / VW;
-        for (int e = tid; e < HS_TILE * gpr; e += 256) {
-          const int t = e / gpr, d = (e - t * gpr) * VW;
-          if (t < tl) {
-            const uint4 kw = *reinterpret_cast<const uint4*>(kb + int64_t(t) * rowlen + d);
-            const uint4 vw = *reinterpret_cast<const uint4*>(vb + int64_t(t) * rowlen + d);
-            *reinterpret_cast<uint4*>(&v_s[t * DM + d]) = vw;
-            const T* ke = reinterpret_cast<const T*>(&kw);
-#pragma unroll
-            for (int x = 0; x < VW; ++x) k_s[(d + x) * HS_TILE + t] = ke[x];
-          }
-        }
-      } else {
-        for (int e = tid; e < HS_TILE * D; e += 256) {
-          const int t = e / D, d = e - t * D;
-          if (t < tl) {
-            k_s[d * HS_TILE + t] = kb[int64_t(t) * rowlen + d];
-            v_s[t * DM + d] = vb[int64_t(t) * rowlen + d];
-          }
+      for (int e = tid; e < TT * D; e += 256) {
+        const int t = e / D, d = e - t * D;
+        if (t < cur.tl) {
+          k_s[d * TT + t] = cur.kb[int64_t(t) * cur.rowlen + d];
+          v_s[t * DM + d] = cur.vb[int64_t(t) * cur.rowlen + d];
         }
       }
     }
     __syncthreads();
+    const int64_t pos0 = cur.pos0;
+    const int tl = cur.tl;
+    if (tile + 1 < tile_hi) {
+      cur = hs_locate<T, TT>(g, tile + 1, hk, D);
+      if (cur.vec) fetch(cur);
+    }
 
-    // QK^T: lane = token
-    float s[HS_RPW];
+    for (int sub = 0; sub * HS_SUB < tl; ++sub) {
+      const int tls = min(HS_SUB, tl - sub * HS_SUB);
+      // QK^T: lane = token
+      float s[RPW];
 #pragma unroll
-    for (int k = 0; k < HS_RPW; ++k) s[k] = 0.f;
-    for (int d = 0; d < D; ++d) {
-      const float kv = E::load(k_s, d * HS_TILE + lane);
+      for (int k = 0; k < RPW; ++k) s[k] = 0.f;
+#pragma unroll 4
+      for (int d = 0; d < D; ++d) {
+        const float kv = E::load(k_s, d * TT + sub * HS_SUB + lane);
 #pragma unroll
-      for (int k = 0; k < HS_RPW; ++k) s[k] = fmaf(q_s[(wave + 4 * k) * DM + d], kv, s[k]);
-    }
-    const int64_t pos = pos0 + lane;
-#pragma unroll
-    for (int k = 0; k < HS_RPW; ++k) {
-      const bool valid = live[k] && lane < tl && (!causal || pos <= qpos[k]);
-      const float x = valid ? s[k] * scale_log2 : -INFINITY;
-      const float mnew = fmaxf(m[k], wave_max(x));
-      const float alpha = __builtin_amdgcn_exp2f(m[k] - mnew);
-      const float p = __builtin_amdgcn_exp2f(x - mnew);
-      l[k] = l[k] * alpha + wave_sum(p);
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) acc[k][i] *= alpha;
-      m[k] = mnew;
-      p_s[(wave + 4 * k) * HS_TILE + lane] = p;
-    }
-    __syncthreads();
-    // PV: lane = head-dim element
-    for (int t = 0; t < tl; ++t) {
-      float vv[DPL];
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) {
-        const int d = lane + 64 * i;
-        vv[i] = d < D ? E::load(v_s, t * DM + d) : 0.f;
+        for (int k = 0; k < RPW; ++k) s[k] = fmaf(q_s[(wave + 4 * k) * DM + d], kv, s[k]);
       }
+      const int64_t pos = pos0 + sub * HS_SUB + lane;
 #pragma unroll
-      for (int k = 0; k < HS_RPW; ++k) {
-        const float pk = p_s[(wave + 4 * k) * HS_TILE + t];
+      for (int k = 0; k < RPW; ++k) {
+        const bool valid = live[k] && lane < tls && (!causal || pos <= qpos[k]);
+        const float x = valid ? s[k] * scale_log2 : -INFINITY;
+        const float mnew = fmaxf(m[k], wave_max(x));
+        const float alpha = __builtin_amdgcn_exp2f(m[k] - mnew);
+        const float p = __builtin_amdgcn_exp2f(x - mnew);
+        l[k] = l[k] * alpha + wave_sum(p);
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) acc[k][i] = fmaf(pk, vv[i], acc[k][i]);
+        for (int i = 0; i < DPL; ++i) acc[k][i] *= alpha;
+        m[k] = mnew;
+        p_s[(wave + 4 * k) * HS_SUB + lane] = p;
       }
+      // p_s rows belong to this wave alone: LDS operations of one wave complete in order
+      __builtin_amdgcn_wave_barrier();
+      // PV: lane = head-dim element
+#pragma unroll 4
+      for (int t = 0; t < tls; ++t) {
+        float vv[DPL];
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) {
+          const int d = lane + 64 * i;
+          vv[i] = d < D ? E::load(v_s, (sub * HS_SUB + t) * DM + d) : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+          const float pk = p_s[(wave + 4 * k) * HS_SUB + t];
+#pragma unroll
+          for (int i = 0; i < DPL; ++i) acc[k][i] = fmaf(pk, vv[i], acc[k][i]);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
     }
   }
 
 #pragma unroll
-  for (int k = 0; k < HS_RPW; ++k) {
+  for (int k = 0; k < RPW; ++k) {
     if (!live[k]) continue;
     const int64_t row = r0 + wave + 4 * k;
     const int64_t i = row / G;
@@ -292,21 +342,35 @@ __global__ __launch_bounds__(64) void hs_attn_merge(void* __restrict__ out_,
 
 struct HsPlan {
   int64_t kv_len, tiles, row_tiles, want;
-  int splits, tiles_per_split;
+  int tt, rt, splits, tiles_per_split;
 };
 
-// Splits: enough workgroups to keep about 4 per CU streaming, never more than one per tile.
-HsPlan hs_plan(int64_t q_len, int num_heads, int num_kv_heads, int num_chunks,
-               int64_t chunk_tokens, int64_t host_len, int64_t resident_len) {
+// Row tile: 8 rows (2 per wave) when the kv head's rows fit, else 32. Splits: as many
+// workgroups as fit on the chip at once, never more than one per tile, and balanced so every
+// split takes the same number of tiles. elem_bytes 0 gives an upper bound on the split count of
+// any dtype (the workspace size).
+HsPlan hs_plan(int64_t q_len, int num_heads, int num_kv_heads, int head_dim, int elem_bytes,
+               int num_chunks, int64_t chunk_tokens, int64_t host_len, int64_t resident_len) {
   HsPlan p{};
   p.kv_len = host_len + resident_len;
-  const int64_t tpc = ceil_div(chunk_tokens, HS_TILE);
+  const int dm = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
+  // the smallest tile of any dtype when sizing the workspace
+  p.tt = elem_bytes > 0 ? hs_tile_tokens(dm, elem_bytes) : HS_SUB;
+  const int64_t tpc = ceil_div(chunk_tokens, p.tt);
   const int64_t last = num_chunks > 0 ? host_len - int64_t(num_chunks - 1) * chunk_tokens : 0;
-  p.tiles = (num_chunks > 0 ? int64_t(num_chunks - 1) * tpc + ceil_div(last, HS_TILE) : 0) +
-            ceil_div(resident_len, HS_TILE);
+  p.tiles = (num_chunks > 0 ? int64_t(num_chunks - 1) * tpc + ceil_div(last, p.tt) : 0) +
+            ceil_div(resident_len, p.tt);
   const int G = num_heads / num_kv_heads;
-  p.row_tiles = ceil_div(q_len * G, HS_RT);
-  p.want = ceil_div(int64_t(device_cus()) * 4, int64_t(num_kv_heads) * p.row_tiles);
+  p.rt = q_len * G <= 8 ? 8 : 32;
+  p.row_tiles = ceil_div(q_len * G, p.rt);
+  // workgroups per CU: the launch bounds (2) or the LDS, whichever
+  // is smaller
+  int occ = 4;
+  if (elem_bytes > 0) {
+    const int lds = 2 * dm * p.tt * elem_bytes + p.rt * dm * 4 + p.rt * HS_SUB * 4;
+    occ = std::max(1, std::min(2, 160 * 1024 / lds));
+  }
+  p.want = ceil_div(int64_t(device_cus()) * occ, int64_t(num_kv_heads) * p.row_tiles);
   const int64_t splits = std::max<int64_t>(1, std::min<int64_t>(p.want, p.tiles));
   p.tiles_per_split = int(ceil_div(std::max<int64_t>(p.tiles, 1), splits));
   p.splits = int(ceil_div(std::max<int64_t>(p.tiles, 1), p.tiles_per_split));
@@ -331,7 +395,7 @@ int hs_check(int64_t q_len, int num_heads, int num_kv_heads, int head_dim, int n
   } else if (host_len != 0) {
     return fail(PIA_EINVAL, "host_stream_attention: host_len > 0 without chunks");
   }
-  if (ceil_div(host_len + resident_len, HS_TILE) + num_chunks > 0x7fffffff)
+  if (ceil_div(host_len + resident_len, HS_SUB) + num_chunks > 0x7fffffff)
     return fail(PIA_EINVAL, "host_stream_attention: KV too long");
   return 0;
 }
@@ -346,8 +410,12 @@ int hs_launch(const HsGeom& g, const HsPlan& p, void* out, const void* q, int64_
 #define PIA_HS(DPL)                                                                           \
   do {                                                                                        \
     if (splits > 0) {                                                                         \
-      hipLaunchKernelGGL((hs_attn_partial<DT, DPL>), grid, dim3(256), 0, s, g, q, q_len, Hq,  \
-                         Hkv, D, causal, scale_log2, part);                                   \
+      if (p.rt == 8)                                                                          \
+        hipLaunchKernelGGL((hs_attn_partial<DT, DPL, 8>), grid, dim3(256), 0, s, g, q, q_len, \
+                           Hq, Hkv, D, causal, scale_log2, part);                             \
+      else                                                                                    \
+        hipLaunchKernelGGL((hs_attn_partial<DT, DPL, 32>), grid, dim3(256), 0, s, g, q,       \
+                           q_len, Hq, Hkv, D, causal, scale_log2, part);                      \
       if (int rc = check_launch("hs_attn_partial")) return rc;                                \
     }                                                                                         \
     hipLaunchKernelGGL((hs_attn_merge<DT, DPL>), dim3(rows), dim3(64), 0, s, out, part,       \
@@ -375,8 +443,8 @@ extern "C" int64_t pia_host_stream_attention_workspace_bytes(int64_t q_len, int 
     return -1;
   // Causal clipping in the call only removes tiles; min(want, tiles) bounds the splits of any
   // clipped plan.
-  const HsPlan p = hs_plan(q_len, num_heads, num_kv_heads, num_chunks, chunk_tokens, host_len,
-                           resident_len);
+  const HsPlan p = hs_plan(q_len, num_heads, num_kv_heads, head_dim, 0, num_chunks,
+                           chunk_tokens, host_len, resident_len);
   const int64_t bound = std::max<int64_t>(1, std::min<int64_t>(p.want, p.tiles));
   return bound * q_len * num_heads * (head_dim + 2) * int64_t(sizeof(float));
 }
@@ -419,8 +487,9 @@ extern "C" int pia_host_stream_attention(
       resident_len = std::min(resident_len, visible - host_len);
     }
   }
-  const HsPlan p = hs_plan(q_len, num_heads, num_kv_heads, num_chunks, chunk_tokens, host_len,
-                           resident_len);
+  const int eb = dtype == PIA_DTYPE_F32 ? 4 : 2;
+  const HsPlan p = hs_plan(q_len, num_heads, num_kv_heads, head_dim, eb, num_chunks,
+                           chunk_tokens, host_len, resident_len);
   const int64_t need = int64_t(p.splits) * q_len * num_heads * (head_dim + 2) * 4;
   if (!workspace || workspace_bytes < need || !aligned(workspace, 4))
     return fail(PIA_EINVAL, "host_stream_attention: workspace too small or misaligned");
@@ -428,7 +497,6 @@ extern "C" int pia_host_stream_attention(
   if (q_len * num_heads > 0x7fffffff)
     return fail(PIA_EINVAL, "host_stream_attention: too many query rows");
 
-  const int eb = dtype == PIA_DTYPE_F32 ? 4 : 2;
   HsGeom g{};
   g.chunk_k = chunk_k;
   g.chunk_v = chunk_v;
@@ -442,11 +510,11 @@ extern "C" int pia_host_stream_attention(
   g.last_row = last_row;
   g.num_chunks = num_chunks;
   g.stored_chunks = stored_chunks;
-  g.tpc = num_chunks > 0 ? int(ceil_div(chunk_tokens, HS_TILE)) : 0;
+  g.tpc = num_chunks > 0 ? int(ceil_div(chunk_tokens, p.tt)) : 0;
   g.full_tiles = num_chunks > 0 ? (num_chunks - 1) * g.tpc : 0;
   g.host_tiles = num_chunks > 0
                      ? g.full_tiles + int(ceil_div(host_len - int64_t(num_chunks - 1) *
-                                                              chunk_tokens, HS_TILE))
+                                                              chunk_tokens, p.tt))
                      : 0;
   g.total_tiles = int(p.tiles);
   g.tiles_per_split = p.tiles_per_split;

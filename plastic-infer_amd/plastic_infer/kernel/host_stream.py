@@ -73,7 +73,7 @@ def host_stream_attention(q: torch.Tensor, chunks: list[tuple[torch.Tensor, torc
                     t = t.to(dev, non_blocking=t.is_pinned())
             elif t.device != dev:
                 t = t.to(dev)
-            ptr = device_ptr(t)
+            ptr = device_ptr(t) if t.device.type == "cpu" else t.data_ptr()
             if ptr % 16:
                 t = t.to(dev, copy=True)
                 ptr = t.data_ptr()
@@ -91,7 +91,8 @@ def host_stream_attention(q: torch.Tensor, chunks: list[tuple[torch.Tensor, torc
         why = N.load().pia_last_error().decode(errors="replace")
         raise ValueError(f"host_stream_attention: unsupported shape ({why})")
     ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=dev)
-    tables = torch.tensor([kp + vp], dtype=torch.int64).to(dev) if n else None
+    tables = torch.tensor([kp + vp], dtype=torch.int64).pin_memory().to(
+        dev, non_blocking=True) if n else None
     kt = tables[0, :n].data_ptr() if n else 0
     vt = tables[0, n:].data_ptr() if n else 0
     qc = q.contiguous()

@@ -22,11 +22,28 @@ import torch
 from .. import _native as N
 
 
+_DEV_BASE: dict[tuple[int, int], int] = {}
+
+
 def device_ptr(t: torch.Tensor) -> int:
     """Address at which kernels reach `t`: device tensors as is, pinned host tensors through
-    their device mapping (pageable host tensors are rejected)."""
+    their device mapping (pageable host tensors are rejected). The mapping of a pinned
+    allocation is looked up once per (base address, size) and reused for every view of it, so
+    a call over hundreds of chunk views of one pinned buffer costs one runtime lookup."""
     import ctypes
 
+    if t.device.type == "cpu":
+        st = t.untyped_storage()
+        key = (st.data_ptr(), st.nbytes())
+        base = _DEV_BASE.get(key)
+        if base is None:
+            out = ctypes.c_void_p()
+            N.call("pia_device_pointer", key[0], ctypes.byref(out))
+            base = int(out.value or 0)
+            if len(_DEV_BASE) >= 4096:
+                _DEV_BASE.clear()
+            _DEV_BASE[key] = base
+        return base + (t.data_ptr() - key[0])
     out = ctypes.c_void_p()
     N.call("pia_device_pointer", t.data_ptr(), ctypes.byref(out))
     return int(out.value or 0)
