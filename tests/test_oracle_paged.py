@@ -249,3 +249,82 @@ def test_planted_causal_offset_is_caught():
     wrong = OP.paged_attention(q, kp, vp, [8, 3], 16, 20, causal=True, q_start_pos=15)  # off by one
     ref = brute_attention(q[0].numpy(), kp.numpy(), vp.numpy(), [8, 3], 16, 20, 16)
     assert not np.allclose(wrong[0].numpy(), ref, atol=1e-6)
+
+
+# ---- page -> chunk copy ------------------------------------------------------------------------
+
+def _chunk_by_token_map(pages, ids, L, ppc):
+    """The relation the reference's sink round-trip test checks (tests/test_kv_store.py:133-161):
+    chunk[layer, :, :, t] == pages[page of token t in that layer, :, :, t % P]."""
+    _, H, D, P = pages.shape
+    out = torch.zeros(L, H, D, ppc * P, dtype=pages.dtype)
+    for layer in range(L):
+        for t in range(ppc * P):
+            pid = ids[layer * ppc + t // P]
+            if pid >= 0:
+                out[layer, :, :, t] = pages[pid, :, :, t % P]
+    return out
+
+
+def test_pages_to_chunk_matches_the_token_map():
+    g = torch.Generator().manual_seed(8)
+    pages = torch.randn(12, 2, 3, 4, generator=g)
+    ids = [5, 0, 7, 11, -1, 2]               # 2 layers x 3 pages, one absent
+    assert torch.equal(OP.pages_to_chunk(pages, ids, 2, 3), _chunk_by_token_map(pages, ids, 2, 3))
+    # planted: page-major instead of layer-major ids
+    wrong = [ids[(i % 2) * 3 + i // 2] for i in range(6)]
+    assert not torch.equal(OP.pages_to_chunk(pages, wrong, 2, 3),
+                           _chunk_by_token_map(pages, ids, 2, 3))
+
+
+# ---- host-stream attention ---------------------------------------------------------------------
+
+HS_CASES = [  # (seed, total, host_len, chunk, q_len, q_start, causal); the first four are the
+              # reference's tests/test_ops.py:488-545 scenarios
+    (1, 10, 6, 3, 2, 10, True), (2, 8, 5, 4, 1, 8, True), (3, 8, 4, 2, 2, 5, True),
+    (4, 6, 6, 3, 6, 0, True), (5, 9, 7, 3, 2, 4, False), (6, 12, 12, 5, 3, 9, True)]
+
+
+def _hs_inputs(seed, total, host_len, chunk, q_len, Hkv=2, G=2, D=16):
+    g = torch.Generator().manual_seed(seed)
+    kf = torch.randn(1, total, Hkv, D, generator=g, dtype=torch.float64)
+    vf = torch.randn(1, total, Hkv, D, generator=g, dtype=torch.float64)
+    q = torch.randn(1, q_len, Hkv * G, D, generator=g, dtype=torch.float64)
+    chunks = [(kf[0, s:min(s + chunk, host_len)].permute(1, 2, 0).contiguous(),
+               vf[0, s:min(s + chunk, host_len)].permute(1, 2, 0).contiguous())
+              for s in range(0, host_len, chunk)]
+    return q, kf, vf, chunks
+
+
+def _hs_brute(q, kf, vf, q_start, causal):
+    """fp64 loops over the contiguous KV as one-token pages."""
+    T = kf.shape[1]
+    return brute_attention(q[0].numpy(), kf[0].unsqueeze(-1).numpy(), vf[0].unsqueeze(-1).numpy(),
+                           list(range(T)), 1, T, q_start if causal else None)
+
+
+@pytest.mark.parametrize("case", HS_CASES)
+def test_host_stream_oracle_vs_brute_force(case):
+    seed, total, host_len, chunk, q_len, q_start, causal = case
+    q, kf, vf, chunks = _hs_inputs(seed, total, host_len, chunk, q_len)
+    out = OP.host_stream_attention(q, chunks, kf[:, host_len:], vf[:, host_len:],
+                                   q_start_pos=q_start, causal=causal)
+    np.testing.assert_allclose(out[0].numpy(), _hs_brute(q, kf, vf, q_start, causal), atol=1e-10)
+
+
+def test_planted_host_stream_mistakes_are_caught():
+    # the mask cuts inside the host chunks, so their order matters (a softmax over all keys
+    # would not see it)
+    seed, total, host_len, chunk, q_len, q_start, causal = 7, 10, 8, 3, 2, 2, True
+    q, kf, vf, chunks = _hs_inputs(seed, total, host_len, chunk, q_len)
+    ref = _hs_brute(q, kf, vf, q_start, causal)
+    rk, rv = kf[:, host_len:], vf[:, host_len:]
+    newest_first = OP.host_stream_attention(q, chunks[::-1], rk, rv, q_start_pos=q_start)
+    assert not np.allclose(newest_first[0].numpy(), ref, atol=1e-6)
+    off_by_one = OP.host_stream_attention(q, chunks, rk, rv, q_start_pos=q_start - 1)
+    assert not np.allclose(off_by_one[0].numpy(), ref, atol=1e-6)
+    # [H, D, C] chunks read as if token-major
+    flat = [(k.reshape(k.shape[2], k.shape[0], k.shape[1]).permute(1, 2, 0),
+             v.reshape(v.shape[2], v.shape[0], v.shape[1]).permute(1, 2, 0)) for k, v in chunks]
+    wrong_layout = OP.host_stream_attention(q, flat, rk, rv, q_start_pos=q_start)
+    assert not np.allclose(wrong_layout[0].numpy(), ref, atol=1e-6)
