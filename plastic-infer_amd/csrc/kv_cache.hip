@@ -209,6 +209,41 @@ __global__ __launch_bounds__(64) void kv_scatter16_kernel(
   }
 }
 
+// Scatter of few tokens (decode: one new token per sequence, each on its own page): one wave
+// per (token, kv head), lane l moving rows d = l + 64i of K and of V. Every store is a 2-byte
+// write into a 32-byte page row, so the cost is latency, and spreading it over n * H waves
+// (2048 for a 256-sequence batch with 8 kv heads) instead of one wave per 16 tokens and head
+// keeps that latency to about one load and one store round trip.
+template <int D>
+__global__ __launch_bounds__(64) void kv_scatter16_rows_kernel(
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, uint16_t* __restrict__ kp,
+    uint16_t* __restrict__ vp, const int64_t* __restrict__ slots, int64_t k_stride,
+    int64_t v_stride, int H, int64_t total_slots) {
+  constexpr int P = T16_P, R = (D + 63) / 64;
+  const int64_t t = blockIdx.x;
+  const int h = blockIdx.y, lane = threadIdx.x;
+  const int64_t s = slots[t];
+  if (s < 0 || s >= total_slots) return;
+  const int64_t base = ((s / P) * H + h) * int64_t(D) * P + (s % P);
+  uint16_t kr[R], vr[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int d = lane + 64 * i;
+    if (d < D) {
+      kr[i] = k[t * k_stride + int64_t(h) * D + d];
+      vr[i] = v[t * v_stride + int64_t(h) * D + d];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int d = lane + 64 * i;
+    if (d < D) {
+      kp[base + int64_t(d) * P] = kr[i];
+      vp[base + int64_t(d) * P] = vr[i];
+    }
+  }
+}
+
 // Gather: LDS tile [D][16 tokens] (row pitch 24: 16-byte aligned rows for the tile loads).
 // Lane (t = lane & 15, ci = lane >> 4) builds 16-byte chunks c = 4co + ci of token t's row, so
 // one store instruction writes 64 contiguous bytes of each of 16 token rows.
@@ -310,6 +345,10 @@ __global__ __launch_bounds__(256) void kv_chunks_copy_kernel(
   }
 }
 
+// Token counts up to this take the one-wave-per-(token, kv head) scatter (decode batches);
+// larger ones (prefill chunks) the page-segment kernel, whose dword and sector writes pay off.
+constexpr int64_t kScatterRowsMaxTokens = 1024;
+
 int check_common(int H, int D, int P, int64_t num_pages, int eb) {
   if (H <= 0 || D <= 0 || P <= 0 || P > 1024 || num_pages <= 0)
     return fail(PIA_EINVAL, "kv: num_kv_heads, head_dim, num_pages must be > 0 and page_size "
@@ -348,6 +387,18 @@ extern "C" int pia_kv_scatter(const void* k, const void* v, void* k_pages, void*
       (head_dim == 64 || head_dim == 128 || head_dim == 256) && aligned(k, 16) &&
       aligned(v, 16) && k_token_stride % 8 == 0 && v_token_stride % 8 == 0 &&
       aligned(k_pages, 4) && aligned(v_pages, 4) && num_kv_heads <= 65535) {
+    if (num_tokens <= kScatterRowsMaxTokens) {  // few tokens: one wave per (token, kv head)
+      dim3 grid = dim3(unsigned(num_tokens), unsigned(num_kv_heads));
+#define PIA_SCR(DD)                                                                            \
+  hipLaunchKernelGGL(kv_scatter16_rows_kernel<DD>, grid, dim3(64), 0, s, (const uint16_t*)k,   \
+                     (const uint16_t*)v, (uint16_t*)k_pages, (uint16_t*)v_pages, slot_mapping, \
+                     k_token_stride, v_token_stride, num_kv_heads, total_slots)
+      if (head_dim == 64) PIA_SCR(64);
+      else if (head_dim == 128) PIA_SCR(128);
+      else PIA_SCR(256);
+#undef PIA_SCR
+      return check_launch("kv_scatter");
+    }
     dim3 grid = dim3(unsigned(blocks), unsigned(num_kv_heads));
 #define PIA_SC16(DD)                                                                           \
   hipLaunchKernelGGL(kv_scatter16_kernel<DD>, grid, dim3(64), 0, s, (const uint16_t*)k,        \

@@ -1,9 +1,9 @@
 // Paged GQA attention over the KV pool layout [num_pages, Hkv, D, P] (token innermost).
 //
 // 1. paged_decode_stream<G> (G = Hq/Hkv in {1,2,4,8}): the decode hot path for bf16, D = 128,
-//    P = 16 (described where it is defined): the batch's 128-token steps spread evenly over
-//    persistent single waves, two per SIMD (one for G = 8, whose accumulators need the
-//    registers). paged_decode_bf16_d128p16<8> is the earlier split-context G = 8 kernel, kept
+//    P = 16 (described where it is defined): the batch's 128-token steps split over persistent
+//    single waves (a fixed, XCD-aware split), two per SIMD (one for G = 8, whose accumulators
+//    need the registers). paged_decode_bf16_d128p16<8> is the earlier split-context G = 8 kernel, kept
 //    behind PIA_G8_STREAM=0: one 256-thread workgroup per (512-token partition, kv head,
 //    sequence); each of its 4 waves owns 8 pages (128 tokens) of the partition. Both use:
 //      K tile loads: lane l reads page l/8, rows d = 4i + (l&3), token half (l>>2)&1, so load i
@@ -370,10 +370,18 @@ __global__ __launch_bounds__(256, 2) void paged_decode_bf16_d128p16(
 //
 // The work of a launch is the ordered list of 128-token steps of every (sequence, kv head)
 // segment, sequence-major then head then step: T = Hkv * sum_b ceil(L_b / 128) steps. Wave w of
-// the NW launched (every CU full at two single-wave workgroups per SIMD) walks the contiguous
-// steps [w*C, min((w+1)*C, T)), C = ceil(T / NW), so every wave streams the same number of KV
-// bytes whatever the mix of context lengths, and only the first step of a wave waits on a
-// prologue: the next step's block-table row (and its q, when it opens a segment) is fetched one
+// the NW launched (every CU full at two single-wave workgroups per SIMD) walks one contiguous
+// range of the list, so every wave streams about the same number of KV bytes whatever the mix
+// of context lengths. Two measured effects shape the split:
+//   - Waves are dispatched to XCD w % 8, and the odd XCDs finish the same work about 8 % later
+//     than the even ones (the last ~50 us of an even split ran on odd XCDs only, at ~4.8 TB/s).
+//     So waves pair up as (2p, 2p + 1), one on an even and one on an odd XCD: the pair takes
+//     Dp = ceil(2T / NW) steps, the even wave the first Ce = 51.5 % of them, the odd one the rest.
+//   - The older of the two waves of a SIMD wins issue arbitration. Each wave sets its priority
+//     from its progress (quartiles of its range: 3 down to 0), so a wave that has fallen behind
+//     gets the issue slots first.
+// Both only move the point where the waves finish; results do not depend on them beyond the
+// fixed split. Only the first step of a wave waits on a prologue: the next step's block-table row (and its q, when it opens a segment) is fetched one
 // step ahead and its K tiles are prefetched during the current step's PV, across segment
 // boundaries. Per step the tile work uses the lane mappings above in four 16 KiB load groups,
 // K rows 0..63 (ka), K rows 64..127 (kb), V of pages 0..3 (va), V of pages 4..7 (vb):
@@ -383,12 +391,29 @@ __global__ __launch_bounds__(256, 2) void paged_decode_bf16_d128p16(
 // segment cut by a range boundary leaves (max, sum, unnormalised acc) partials, at most two per
 // wave: slot 0 for the segment that began before the wave's range, slot 1 for the one that
 // began inside it and continues after. paged_decode_stream_reduce merges them.
+//
+// Range of wave w (steps): pair p = w / 2 covers [p*Dp, (p+1)*Dp); the even wave [p*Dp, p*Dp+Ce),
+// the odd wave [p*Dp+Ce, (p+1)*Dp); both clipped to T. stream_range_of() is the inverse.
 // ---------------------------------------------------------------------------------------------
 constexpr int SD_MAX_SEQS = 1024;   // sequences per launch (step-prefix table in LDS)
 constexpr int SD_MAX_WAVES = 4096;  // partial slots are sized for this many waves
 constexpr int SD_WAVES_PER_CU = 8;  // two single-wave workgroups per SIMD
 constexpr int SD_STEP_TOKENS = FD_PAGES_PER_WAVE * FD_P;  // 128 tokens per step
-constexpr int SD_META_INTS = SD_MAX_SEQS + 4;              // step prefix [B + 1], range size C
+constexpr int SD_META_INTS = SD_MAX_SEQS + 4;              // step prefix [B + 1], Dp, Ce
+constexpr int SD_EVEN_SHARE_PERMILLE = 515;                // even-XCD wave's share of a pair
+
+// Steps of a wave pair and the even wave's share of them, for T steps over NW waves.
+__device__ __forceinline__ int stream_pair_steps(int T, int NW) {
+  return int((2 * int64_t(T) + NW - 1) / NW);
+}
+__device__ __forceinline__ int stream_even_share(int Dp) {
+  return (Dp * SD_EVEN_SHARE_PERMILLE + 500) / 1000;
+}
+// The wave whose range holds step st.
+__device__ __forceinline__ int stream_range_of(int st, int Dp, int Ce) {
+  const int p = st / Dp;
+  return 2 * p + (st - p * Dp >= Ce ? 1 : 0);
+}
 
 struct StreamCursor {
   int b, h, ls, ns, L;  // sequence, kv head, step in the segment, steps in it, its tokens
@@ -423,7 +448,7 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
   __shared__ uint32_t p_lds[64][G];
 
   // Step prefix over the batch: every wave builds its own copy in LDS, wave 0 also publishes
-  // it (and C) for the merge kernel.
+  // it (and the pair split) for the merge kernel.
   int lv[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -444,18 +469,20 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     carry = uniform(carry + __shfl(incl, 63, 64));
   }
   const int T = Hkv * carry;
-  const int C = (T + NW - 1) / NW;
+  const int Dp = stream_pair_steps(T, NW), Ce = stream_even_share(Dp);
   if (lane == 0) {
     seq_q[0] = 0;
     if (w == 0) {
       ws_meta[0] = 0;
-      ws_meta[B + 1] = C;
+      ws_meta[B + 1] = Dp;
+      ws_meta[B + 2] = Ce;
     }
   }
   __syncthreads();
-  const int start = w * C;
-  if (start >= T) return;
-  const int end = min(start + C, T);
+  const int start = (w >> 1) * Dp + ((w & 1) ? Ce : 0);
+  const int end = min((w >> 1) * Dp + ((w & 1) ? Dp : Ce), T);
+  if (start >= end) return;
+  const int span = end - start;
 
   // cursor of global step gs: the last sequence b with Hkv * seq_q[b] <= gs (it has steps)
   auto seg_of = [&](int gs) {
@@ -636,6 +663,13 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
   };
 
   for (;;) {
+    {  // issue priority from progress: quartile 0 of the range -> 3, quartile 3 -> 0
+      const int quarter = (4 * (gs - start)) / span;
+      if (quarter <= 0) __builtin_amdgcn_s_setprio(3);
+      else if (quarter == 1) __builtin_amdgcn_s_setprio(2);
+      else if (quarter == 2) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
     const bool has_next = gs + 1 < end;
     // The next step's block-table row and (when it opens a segment) q go out first, ahead of
     // this step's V loads, so they have landed by the time they are consumed. At the end of
@@ -774,19 +808,21 @@ __global__ __launch_bounds__(FD_D) void paged_decode_stream_reduce(
     out[row * D + d] = 0;
     return;
   }
-  const int C = ws_meta[B + 1];
+  const int Dp = ws_meta[B + 1], Ce = ws_meta[B + 2];
   const int q0 = ws_meta[b], ns = ws_meta[b + 1] - q0;
   const int h = hq / G, g = hq - h * G;
   const int s0 = Hkv * q0 + h * ns;
-  const int c0 = s0 / C, c1 = (s0 + ns - 1) / C;
+  const int c0 = stream_range_of(s0, Dp, Ce), c1 = stream_range_of(s0 + ns - 1, Dp, Ce);
   if (c0 == c1) return;  // finished inside one wave's range
   auto part = [&](int c) {
     return ws_part + (int64_t(c) * 2 + (c == c0 ? 1 : 0)) * G * (D + 2) + g * (D + 2);
   };
+  // odd waves hold no steps when a pair has one step (Dp = 1): skip them
+  const int inc = Ce < Dp ? 1 : 2;
   float M = kNegBig;
-  for (int c = c0; c <= c1; ++c) M = fmaxf(M, part(c)[D]);
+  for (int c = c0; c <= c1; c += inc) M = fmaxf(M, part(c)[D]);
   float o = 0.f, lt = 0.f;
-  for (int c = c0; c <= c1; ++c) {
+  for (int c = c0; c <= c1; c += inc) {
     const float* pp = part(c);
     const float f = fast_exp2(pp[D] - M);
     lt += f * pp[D + 1];
@@ -970,7 +1006,9 @@ bool fast_path(int dtype, int Hq, int Hkv, int D, int P) {
 // per device), capped by the partial slots the workspace holds.
 // persistent waves of the stream kernel: two per SIMD, or one for G = 8 (its registers)
 int stream_waves(int G) {
-  return std::min(device_cus() * (G > 4 ? SD_WAVES_PER_CU / 2 : SD_WAVES_PER_CU), SD_MAX_WAVES);
+  const int n = std::min(device_cus() * (G > 4 ? SD_WAVES_PER_CU / 2 : SD_WAVES_PER_CU),
+                         SD_MAX_WAVES);
+  return std::max(2, n & ~1);  // whole (even, odd) pairs
 }
 
 #ifndef PIA_G8_STREAM

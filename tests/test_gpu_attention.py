@@ -138,6 +138,53 @@ def test_decode_stream_batch_over_one_launch(dev, Hq):
     assert err <= BF16_TOL, err
 
 
+def test_decode_stream_workspace_any_contents(dev):
+    """The workspace needs no initialisation: filled with 0xFF bytes or random bytes (so the
+    chunk counter holds a value of no launch), the result equals that of a fresh workspace,
+    bit for bit, and the oracle's."""
+    g = torch.Generator().manual_seed(47)
+    lens = torch.randint(1, 2000, (96,), generator=g)
+    q, kp, vp, bt, lens_t = _decode_case(48, lens.tolist(), 32, 8, 12000)
+    args = (q.to(dev), kp.to(dev), vp.to(dev), bt.to(dev), lens_t.to(dev))
+    need = decode_workspace_bytes(96, 32, 8, 128, 16, bt.shape[1])
+    base = paged_decode_attention(*args).cpu()
+    filled = torch.full((need,), 255, dtype=torch.uint8, device=dev)
+    rnd = torch.randint(0, 256, (need,), generator=g, dtype=torch.uint8).to(dev)
+    for ws in (filled, rnd, rnd):   # random bytes, then the same buffer again
+        assert torch.equal(paged_decode_attention(*args, workspace=ws).cpu(), base)
+    ref = OP.decode_batch(q, kp, vp, bt, lens_t, 16)
+    err = (base.float() - ref.float()).abs().max().item()
+    assert err <= BF16_TOL, err
+
+
+def test_decode_stream_graph_replays(dev):
+    """One decode call captured in a HIP graph (one epoch for every replay): each of several
+    replays, with eager calls on the same workspace in between, equals the eager result."""
+    g = torch.Generator().manual_seed(49)
+    lens = torch.randint(1, 2500, (64,), generator=g)
+    q, kp, vp, bt, lens_t = _decode_case(50, lens.tolist(), 32, 8, 12000)
+    qd, kd, vd, btd, ld = q.to(dev), kp.to(dev), vp.to(dev), bt.to(dev), lens_t.to(dev)
+    ws = torch.empty(decode_workspace_bytes(64, 32, 8, 128, 16, bt.shape[1]), dtype=torch.uint8,
+                     device=dev)
+    out = torch.empty(64, 32, 128, dtype=torch.bfloat16, device=dev)
+    eager = paged_decode_attention(qd, kd, vd, btd, ld, workspace=ws).cpu()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):   # warm-up off the capture
+        paged_decode_attention(qd, kd, vd, btd, ld, out=out, workspace=ws)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        paged_decode_attention(qd, kd, vd, btd, ld, out=out, workspace=ws)
+    for i in range(4):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(out.cpu(), eager), f"replay {i}"
+        assert torch.equal(paged_decode_attention(qd, kd, vd, btd, ld, workspace=ws).cpu(), eager)
+
+
 def test_decode_qwen3_8b_b256_full_shape(dev):
     """Qwen3-8B decode at full size (B = 256, L ~ U[512, 8192], 160k-page pool) generated on
     the device; five sequences (the longest, shortest and three seeded picks) are checked

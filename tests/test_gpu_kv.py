@@ -70,17 +70,24 @@ def test_scatter_strided_rows_and_tile_path(dev):
     assert torch.equal(gk.cpu(), ref_k) and torch.equal(gv.cpu(), ref_v)
 
 
+@pytest.mark.parametrize("reps", [1, 13])
 @pytest.mark.parametrize("D,dtype", [(128, torch.bfloat16), (64, torch.float16),
                                      (256, torch.bfloat16)])
-def test_scatter16_slot_patterns(dev, D, dtype):
+def test_scatter16_slot_patterns(dev, D, dtype, reps):
     """16-bit pools with 16-token pages: runs starting at odd offsets and crossing pages, a run
-    of whole pages, scattered decode slots, padding and out-of-range slots, a strided source."""
+    of whole pages, scattered decode slots, padding and out-of-range slots, a strided source.
+    One copy of the pattern (87 tokens) takes the per-(token, kv head) kernel; 13 copies on
+    disjoint pages (1131 tokens) take the page-segment kernel."""
     g = torch.Generator().manual_seed(15 + D)
-    H, P, N_ = 3, 16, 40
-    runs = (list(range(16 * 5 + 3, 16 * 5 + 3 + 37))      # offset 3, crosses three pages
-            + list(range(16 * 20, 16 * 22))               # two whole pages
-            + [16 * 30 + 7, -1, 16 * 31, N_ * P + 5, 16 * 33 + 15, 16 * 34 + 14, 16 * 34 + 15]
-            + list(range(16 * 36 + 1, 16 * 36 + 12)))     # odd start inside one page
+    H, P, N_ = 3, 16, 40 * reps
+    runs = []
+    for r in range(reps):
+        o = 16 * 40 * r
+        runs += (list(range(o + 16 * 5 + 3, o + 16 * 5 + 3 + 37))   # offset 3, crosses 3 pages
+                 + list(range(o + 16 * 20, o + 16 * 22))             # two whole pages
+                 + [o + 16 * 30 + 7, -1, o + 16 * 31, N_ * P + 5, o + 16 * 33 + 15,
+                    o + 16 * 34 + 14, o + 16 * 34 + 15]
+                 + list(range(o + 16 * 36 + 1, o + 16 * 36 + 12)))   # odd start in one page
     n = len(runs)
     src = torch.randn(n, 2, H, D, generator=g).to(dtype)
     k, v = src[:, 0], src[:, 1]                        # token stride 2*H*D
