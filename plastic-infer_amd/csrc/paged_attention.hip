@@ -399,7 +399,10 @@ constexpr int SD_MAX_SEQS = 1024;   // sequences per launch (step-prefix table i
 constexpr int SD_MAX_WAVES = 4096;  // partial slots are sized for this many waves
 constexpr int SD_WAVES_PER_CU = 8;  // two single-wave workgroups per SIMD
 constexpr int SD_STEP_TOKENS = FD_PAGES_PER_WAVE * FD_P;  // 128 tokens per step
-constexpr int SD_META_INTS = SD_MAX_SEQS + 4;              // step prefix [B + 1], Dp, Ce
+// meta ints: step prefix [B + 1], then Dp, Ce, T, then one cut record per wave (the segment
+// its range starts inside, as b * Hkv + h, or -1 when the range starts a segment)
+constexpr int SD_META_CUT = SD_MAX_SEQS + 4;
+constexpr int SD_META_INTS = SD_META_CUT + SD_MAX_WAVES;
 constexpr int SD_EVEN_SHARE_PERMILLE = 515;                // even-XCD wave's share of a pair
 
 // Steps of a wave pair and the even wave's share of them, for T steps over NW waves.
@@ -476,9 +479,17 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
       ws_meta[0] = 0;
       ws_meta[B + 1] = Dp;
       ws_meta[B + 2] = Ce;
+      ws_meta[B + 3] = T;
     }
   }
   __syncthreads();
+  // empty sequences (no steps) get zero rows here: wave w takes sequences w, w + NW, ...
+  for (int b = w; b < B; b += NW) {
+    if (uniform(seq_len[b]) == 0) {
+      uint16_t* o = out + int64_t(b) * Hq * D;
+      for (int i = lane; i < Hq * D; i += 64) o[i] = 0;
+    }
+  }
   const int start = (w >> 1) * Dp + ((w & 1) ? Ce : 0);
   const int end = min((w >> 1) * Dp + ((w & 1) ? Dp : Ce), T);
   if (start >= end) return;
@@ -571,6 +582,7 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
 
   int gs = start;
   StreamCursor cur = seg_of(gs);
+  if (lane == 0) ws_meta[SD_META_CUT + w] = cur.ls != 0 ? cur.b * Hkv + cur.h : -1;
   int bt_cur;
   // Two 16 KiB register buffers whose role rotates through a step:
   //   A: K rows 0..63 -> V pages 0..3 -> next step's K rows 0..63
@@ -795,40 +807,70 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
   }
 }
 
-// Merge the partials of segments that cross a wave-range boundary (and zero the output of
-// empty sequences). One 128-thread block per (q head, sequence).
+// Merge the partials of the segments that cross a wave-range boundary. One 128-thread block per
+// wave w: its range starts inside segment (b, h) when its cut record says so, and the block
+// merges that segment's G rows (thread d: element d of every row) when w is the first wave
+// after the one holding the segment's first step (every other boundary inside the segment
+// returns at once). One online pass over the pieces, all G rows of a piece loaded together.
+template <int G>
 __global__ __launch_bounds__(FD_D) void paged_decode_stream_reduce(
     uint16_t* __restrict__ out, const float* __restrict__ ws_part,
-    const int32_t* __restrict__ ws_meta, const int32_t* __restrict__ context_lens,
-    int64_t bt_stride, int B, int Hkv, int G) {
+    const int32_t* __restrict__ ws_meta, int B, int Hkv) {
   constexpr int D = FD_D;
-  const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int64_t row = int64_t(b) * Hkv * G + hq;
-  if (clamp_len(context_lens[b], bt_stride, FD_P) == 0) {
-    out[row * D + d] = 0;
-    return;
-  }
-  const int Dp = ws_meta[B + 1], Ce = ws_meta[B + 2];
+  const int w = blockIdx.x, d = threadIdx.x;
+  const int Dp = ws_meta[B + 1], Ce = ws_meta[B + 2], T = ws_meta[B + 3];
+  const int start = (w >> 1) * Dp + ((w & 1) ? Ce : 0);
+  const int end = min((w >> 1) * Dp + ((w & 1) ? Dp : Ce), T);
+  if (start >= end) return;  // no steps: no cut record
+  const int cut = ws_meta[SD_META_CUT + w];
+  if (cut < 0) return;
+  const int b = cut / Hkv, h = cut - b * Hkv;
   const int q0 = ws_meta[b], ns = ws_meta[b + 1] - q0;
-  const int h = hq / G, g = hq - h * G;
   const int s0 = Hkv * q0 + h * ns;
-  const int c0 = stream_range_of(s0, Dp, Ce), c1 = stream_range_of(s0 + ns - 1, Dp, Ce);
-  if (c0 == c1) return;  // finished inside one wave's range
-  auto part = [&](int c) {
-    return ws_part + (int64_t(c) * 2 + (c == c0 ? 1 : 0)) * G * (D + 2) + g * (D + 2);
-  };
   // odd waves hold no steps when a pair has one step (Dp = 1): skip them
   const int inc = Ce < Dp ? 1 : 2;
-  float M = kNegBig;
-  for (int c = c0; c <= c1; c += inc) M = fmaxf(M, part(c)[D]);
-  float o = 0.f, lt = 0.f;
-  for (int c = c0; c <= c1; c += inc) {
-    const float* pp = part(c);
-    const float f = fast_exp2(pp[D] - M);
-    lt += f * pp[D + 1];
-    o += f * pp[d];
+  const int c0 = stream_range_of(s0, Dp, Ce), c1 = stream_range_of(s0 + ns - 1, Dp, Ce);
+  if (w != c0 + inc) return;
+  float M[G], o[G], lt[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    M[g] = kNegBig;
+    o[g] = 0.f;
+    lt[g] = 0.f;
   }
-  out[row * D + d] = f32_to_bf16(o / lt);
+  // one piece ahead: the next piece's loads are in flight while the current one is folded in
+  float mc[G], lc[G], ac[G];
+  auto load_piece = [&](int c) {
+    const float* pp = ws_part + (int64_t(c) * 2 + (c == c0 ? 1 : 0)) * G * (D + 2);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      mc[g] = pp[g * (D + 2) + D];
+      lc[g] = pp[g * (D + 2) + D + 1];
+      ac[g] = pp[g * (D + 2) + d];
+    }
+  };
+  load_piece(c0);
+  for (int c = c0; c <= c1; c += inc) {
+    float mcur[G], lcur[G], acur[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      mcur[g] = mc[g];
+      lcur[g] = lc[g];
+      acur[g] = ac[g];
+    }
+    if (c + inc <= c1) load_piece(c + inc);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float mn = fmaxf(M[g], mcur[g]);
+      const float fo = fast_exp2(M[g] - mn), fc = fast_exp2(mcur[g] - mn);
+      lt[g] = lt[g] * fo + lcur[g] * fc;
+      o[g] = o[g] * fo + acur[g] * fc;
+      M[g] = mn;
+    }
+  }
+  uint16_t* orow = out + (int64_t(b) * Hkv + h) * G * D + d;
+#pragma unroll
+  for (int g = 0; g < G; ++g) orow[g * D] = f32_to_bf16(o[g] / lt[g]);
 }
 
 // Merge the partition partials of sequences with more than one partition.
@@ -1115,9 +1157,16 @@ extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_se
       }
 #undef PIA_SD
       if (int rc = check_launch("paged_decode_stream")) return rc;
-      hipLaunchKernelGGL(paged_decode_stream_reduce, dim3(unsigned(num_heads), unsigned(Bs)),
-                         dim3(FD_D), 0, s, o, ws_part, ws_meta, cl, bt_stride, Bs, num_kv_heads,
-                         G);
+#define PIA_SR(GG)                                                                             \
+  hipLaunchKernelGGL((paged_decode_stream_reduce<GG>), dim3(unsigned(NW)), dim3(FD_D), 0, s, o, \
+                     ws_part, ws_meta, Bs, num_kv_heads)
+      switch (G) {
+        case 1: PIA_SR(1); break;
+        case 2: PIA_SR(2); break;
+        case 4: PIA_SR(4); break;
+        default: PIA_SR(8); break;
+      }
+#undef PIA_SR
       if (int rc = check_launch("paged_decode_stream_reduce")) return rc;
     }
     return 0;
