@@ -122,7 +122,7 @@ int pia_kv_pages_chunks_copy(void* const* chunks, int num_chunks, void* pages,
  * bytes, 4-byte aligned (may be NULL when that query returns 0). Calls that share a workspace
  * must be ordered (same stream): the kernels keep partials in it between their two launches.
  * bf16 with head_dim 128 and page_size 16 and Hq/Hkv in {1, 2, 4, 8} takes the fast kernel
- * (an even split of the batch's KV steps over persistent waves); every other supported
+ * (the batch's KV steps split over persistent waves, XCD-aware); every other supported
  * combination (f32/f16/bf16, head_dim <= 512, any page_size) takes the general kernel.
  * ------------------------------------------------------------------------------------------- */
 int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_heads,
