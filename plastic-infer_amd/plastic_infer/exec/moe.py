@@ -8,8 +8,14 @@
                       within an expert in ascending (token, slot) order, the order nonzero()
                       gives the reference), one permute kernel, one GEMM group per resident
                       expert on its contiguous rows, one unpermute kernel (fp32 accumulation).
+  moe_forward_v1      reference src/plastic_infer/exec/moe.py:41-82 — the dense-bank variant
+                      (w1 [E, H, I], w2 [E, I, H], one up projection, SiLU): the same permute
+                      plan, permute and unpermute, with the two GEMMs per expert in between.
   swiglu_mlp          the expert MLP (plain library GEMMs; expert math is not part of the
                       data path this package accelerates).
+
+The reference's per-token loops (moe_forward_reference, moe_forward_reference_swiglu) are its
+tests' ground truth; the tests here restate them next to the cases that use them.
 """
 
 from __future__ import annotations
@@ -34,6 +40,44 @@ def swiglu_mlp(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
     return F.linear(F.silu(F.linear(x, w1)) * F.linear(x, w3), w2)
 
 
+def _route_rows(hidden: torch.Tensor, expert_ids: torch.Tensor, num_experts: int):
+    """Permute plan (block 1: each expert's rows exactly contiguous), the permuted rows and each
+    expert's row count (one host read of the routed ids; the plan itself stays on the device)."""
+    k = expert_ids.shape[1]
+    ids32 = expert_ids.to(torch.int32)
+    sorted_ids, _, npp, route_pos = moe_align_block_size(ids32, 1, num_experts,
+                                                        return_route_pos=True)
+    x_perm = moe_permute(hidden, sorted_ids, npp, k, route_pos=route_pos)
+    counts = torch.bincount(ids32.view(-1).clamp(min=-1).add(1), minlength=num_experts + 2)
+    return x_perm, route_pos, counts[1:num_experts + 2].cpu().tolist()
+
+
+def moe_forward_v1(hidden: torch.Tensor, expert_w1: torch.Tensor, expert_w2: torch.Tensor,
+                   expert_ids: torch.Tensor, weights: torch.Tensor) -> torch.Tensor:
+    """out[t] = sum_s weights[t, s] * silu(hidden[t] @ w1[e]) @ w2[e], e = expert_ids[t, s];
+    expert_w1 [E, H, I], expert_w2 [E, I, H] (reference src/plastic_infer/exec/moe.py:41-82)."""
+    N.require_device(hidden, expert_w1, expert_w2, expert_ids, weights,
+                     names=("hidden", "expert_w1", "expert_w2", "expert_ids", "weights"))
+    T, H = hidden.shape
+    k = expert_ids.shape[1]
+    E = expert_w1.shape[0]
+    if expert_w1.dim() != 3 or expert_w2.shape != (E, expert_w1.shape[2], H) or \
+            expert_w1.shape[1] != H:
+        raise ValueError(f"expert_w1 must be [E, {H}, I] and expert_w2 [E, I, {H}], got "
+                         f"{tuple(expert_w1.shape)} and {tuple(expert_w2.shape)}")
+    if T == 0:
+        return torch.zeros_like(hidden)
+    x_perm, route_pos, counts = _route_rows(hidden, expert_ids, E)
+    y = torch.zeros_like(x_perm)
+    start = 0
+    for e in range(E):
+        n = counts[e]
+        if n:
+            y[start:start + n] = F.silu(x_perm[start:start + n] @ expert_w1[e]) @ expert_w2[e]
+        start += n
+    return moe_unpermute(y, route_pos, weights.to(torch.float32).contiguous(), T, k)
+
+
 def moe_forward_sparse(hidden: torch.Tensor, experts: dict[int, ExpertWeights],
                        expert_ids: torch.Tensor, weights: torch.Tensor) -> torch.Tensor:
     """out[t] = sum_s weights[t, s] * expert_{ids[t,s]}(hidden[t]) over the routed experts
@@ -44,14 +88,7 @@ def moe_forward_sparse(hidden: torch.Tensor, experts: dict[int, ExpertWeights],
     if T == 0 or not experts:
         return torch.zeros_like(hidden)
     num_experts = max(experts) + 1
-    ids32 = expert_ids.to(torch.int32)
-    # block_size 1: every expert's rows are exactly contiguous (no padding rows).
-    sorted_ids, _, npp, route_pos = moe_align_block_size(ids32, 1, num_experts,
-                                                        return_route_pos=True)
-    x_perm = moe_permute(hidden, sorted_ids, npp, k, route_pos=route_pos)
-    # Per-expert row ranges: one host read of the routed ids (the plan itself stays on device).
-    counts = torch.bincount(ids32.view(-1).clamp(min=-1).add(1), minlength=num_experts + 2)
-    counts = counts[1:num_experts + 2].cpu().tolist()
+    x_perm, route_pos, counts = _route_rows(hidden, expert_ids, num_experts)
     y = torch.zeros_like(x_perm)
     start = 0
     for e in range(num_experts + 1):
@@ -63,4 +100,4 @@ def moe_forward_sparse(hidden: torch.Tensor, experts: dict[int, ExpertWeights],
     return moe_unpermute(y, route_pos, weights.to(torch.float32).contiguous(), T, k)
 
 
-__all__ = ["topk_route", "swiglu_mlp", "moe_forward_sparse"]
+__all__ = ["topk_route", "swiglu_mlp", "moe_forward_v1", "moe_forward_sparse"]
