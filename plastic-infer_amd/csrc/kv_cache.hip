@@ -149,7 +149,7 @@ template <int D>
 __global__ __launch_bounds__(64) void kv_scatter16_kernel(
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, uint16_t* __restrict__ kp,
     uint16_t* __restrict__ vp, const int64_t* __restrict__ slots, int64_t n, int64_t k_stride,
-    int64_t v_stride, int H, int64_t total_slots) {
+    int64_t v_stride, int H, int64_t total_slots, int wide) {
   constexpr int P = T16_P, PITCH = D + 8, CH = D / 8, MAXT = 32;
   __shared__ __align__(16) uint16_t tile[MAXT * PITCH];
   const int lane = threadIdx.x;
@@ -181,18 +181,58 @@ __global__ __launch_bounds__(64) void kv_scatter16_kernel(
   const int64_t head_off = int64_t(h) * D * P;
   const int64_t b0 = has0 ? (s0 / P) * H * D * P + head_off + (s0 % P) : 0;
   const int64_t b1 = has1 ? (s1 / P) * H * D * P + head_off + (s1 % P) : 0;
+  // a whole page (16 consecutive slots from a page start) on 16-byte aligned pools: every page
+  // row (32 bytes) goes out as two 16-byte stores, lane l writing row d = 32r + l/2, tokens
+  // 8(l&1) .. 8(l&1) + 7, so one store instruction covers 1 KiB of the tile
+  const long long sfirst = __shfl(s, a & 63, 64);
+  const bool full = wide && m == P && sfirst >= 0 && (sfirst % P) == 0;
+  const int64_t fbase = full ? (sfirst / P) * H * D * P + head_off : 0;
 
-  for (int pass = 0; pass < 2; ++pass) {
-    const uint16_t* src = pass == 0 ? k : v;
-    const int64_t stride = pass == 0 ? k_stride : v_stride;
-    uint16_t* dst = pass == 0 ? kp : vp;
-    for (int it = lane; it < m * CH; it += 64) {
+  // The first 256 16-byte items of K and of V (all of a 16-token segment for D <= 128) are
+  // loaded together up front, so both tensors' reads are in flight at once; the LDS tile then
+  // transposes K, then V.
+  constexpr int NPRE = 4;
+  const int items = m * CH;
+  uint4 kpre[NPRE], vpre[NPRE];
+#pragma unroll
+  for (int j = 0; j < NPRE; ++j) {
+    const int it = lane + 64 * j;
+    const int t = it / CH, c = it - t * CH;
+    kpre[j] = vpre[j] = make_uint4(0u, 0u, 0u, 0u);
+    if (it < items) {
+      kpre[j] = *reinterpret_cast<const uint4*>(k + (t0 + t) * k_stride + int64_t(h) * D + c * 8);
+      vpre[j] = *reinterpret_cast<const uint4*>(v + (t0 + t) * v_stride + int64_t(h) * D + c * 8);
+    }
+  }
+
+  // one tensor: preloaded items and the rest into the tile, then the tile out to the pages
+  auto pass_of = [&](const uint16_t* src, int64_t stride, uint16_t* dst, const uint4 (&pre)[NPRE]) {
+#pragma unroll
+    for (int j = 0; j < NPRE; ++j) {
+      const int it = lane + 64 * j;
+      const int t = it / CH, c = it - t * CH;
+      if (it < items) *reinterpret_cast<uint4*>(&tile[t * PITCH + c * 8]) = pre[j];
+    }
+    for (int it = lane + 64 * NPRE; it < items; it += 64) {
       const int t = it / CH, c = it - t * CH;
       *reinterpret_cast<uint4*>(&tile[t * PITCH + c * 8]) =
           *reinterpret_cast<const uint4*>(src + (t0 + t) * stride + int64_t(h) * D + c * 8);
     }
     __syncthreads();
-    if (has0 || has1) {
+    if (full) {
+      const int th = lane & 1;
+#pragma unroll
+      for (int r = 0; r < D / 32; ++r) {
+        const int d = 32 * r + (lane >> 1);
+        const uint16_t* col = &tile[(8 * th) * PITCH + d];
+        uint32_t wv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          wv[j] = uint32_t(col[(2 * j) * PITCH]) | (uint32_t(col[(2 * j + 1) * PITCH]) << 16);
+        *reinterpret_cast<uint4*>(dst + fbase + int64_t(d) * P + 8 * th) =
+            make_uint4(wv[0], wv[1], wv[2], wv[3]);
+      }
+    } else if (has0 || has1) {
 #pragma unroll 4
       for (int d = dq; d < D; d += 4) {
         const uint16_t x0 = tile[(2 * pi) * PITCH + d], x1 = tile[(2 * pi + 1) * PITCH + d];
@@ -206,7 +246,9 @@ __global__ __launch_bounds__(64) void kv_scatter16_kernel(
       }
     }
     __syncthreads();
-  }
+  };
+  pass_of(k, k_stride, kp, kpre);
+  pass_of(v, v_stride, vp, vpre);
 }
 
 // Scatter of few tokens (decode: one new token per sequence, each on its own page): one wave
@@ -403,7 +445,8 @@ extern "C" int pia_kv_scatter(const void* k, const void* v, void* k_pages, void*
 #define PIA_SC16(DD)                                                                           \
   hipLaunchKernelGGL(kv_scatter16_kernel<DD>, grid, dim3(64), 0, s, (const uint16_t*)k,        \
                      (const uint16_t*)v, (uint16_t*)k_pages, (uint16_t*)v_pages, slot_mapping, \
-                     num_tokens, k_token_stride, v_token_stride, num_kv_heads, total_slots)
+                     num_tokens, k_token_stride, v_token_stride, num_kv_heads, total_slots, wide)
+    const int wide = aligned(k_pages, 16) && aligned(v_pages, 16) ? 1 : 0;
     if (head_dim == 64) PIA_SC16(64);
     else if (head_dim == 128) PIA_SC16(128);
     else PIA_SC16(256);
