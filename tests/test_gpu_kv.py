@@ -100,6 +100,34 @@ def test_scatter16_slot_patterns(dev, D, dtype, reps):
     assert torch.equal(gk.cpu(), ref_k) and torch.equal(gv.cpu(), ref_v)
 
 
+@pytest.mark.parametrize("pool_off", [0, 2])
+def test_scatter16_whole_pages_pool_alignment(dev, pool_off):
+    """Whole-page segments (16 slots from a page start) go out as 16-byte stores when both pools
+    are 16-byte aligned; pools 4 bytes off (pool_off = 2 elements) take the dword path. 1157
+    tokens, so the page-segment kernel runs; a ragged run at offset 5 rides along. Both bit-exact
+    against the oracle."""
+    g = torch.Generator().manual_seed(77 + pool_off)
+    H, D, P, N_ = 2, 128, 16, 90
+    slots = list(range(16 * 3, 16 * 73)) + list(range(16 * 80 + 5, 16 * 80 + 5 + 37))
+    n = len(slots)
+    k = torch.randn(n, H, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, H, D, generator=g).to(torch.bfloat16)
+    kp = torch.randn(N_, H, D, P, generator=g).to(torch.bfloat16)
+    vp = torch.randn(N_, H, D, P, generator=g).to(torch.bfloat16)
+    ref_k, ref_v = kp.clone(), vp.clone()
+    OP.scatter_slots(k, v, ref_k, ref_v, slots)
+    numel = kp.numel()
+    bk = torch.zeros(numel + 8, dtype=torch.bfloat16, device=dev)
+    bv = torch.zeros(numel + 8, dtype=torch.bfloat16, device=dev)
+    gk = bk[pool_off:pool_off + numel].view(N_, H, D, P)
+    gv = bv[pool_off:pool_off + numel].view(N_, H, D, P)
+    gk.copy_(kp.to(dev))
+    gv.copy_(vp.to(dev))
+    assert (gk.data_ptr() % 16 == 0) == (pool_off == 0)
+    kv_scatter(k.to(dev), v.to(dev), gk, gv, torch.tensor(slots, device=dev))
+    assert torch.equal(gk.cpu(), ref_k) and torch.equal(gv.cpu(), ref_v)
+
+
 def test_gather16_tables_with_invalid_pages(dev):
     g = torch.Generator().manual_seed(16)
     H, D, P = 4, 128, 16
