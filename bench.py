@@ -117,10 +117,12 @@ def cpu_info():
     return model, len(phys) or None
 
 
-def cpu_baseline(torch, inp, n_seqs):
+def cpu_baseline(torch, inp, n_seqs, gpu_out):
     """The oracle (CPU restatement of the reference torch path: per-token index store, then per
     sequence index_select gather + repeat_interleave + SDPA) on the first n_seqs sequences of
-    the same inputs, copied from the device. 1 warm-up, median of 3."""
+    the same inputs, copied from the device. 1 warm-up, median of 3. The warm-up's output is
+    also the parity check of the timed GPU step: gpu_out [B, Hq, D] (the attention output after
+    the same scatter) must agree on the sampled sequences within 2e-2 (the bf16 bar)."""
     import oracle.paged_kv as OP
 
     threads = len(os.sched_getaffinity(0))
@@ -146,9 +148,13 @@ def cpu_baseline(torch, inp, n_seqs):
 
     def step():
         OP.scatter_slots(k_new, v_new, kp, vp, slots.tolist())
-        OP.decode_batch(q, kp, vp, bt, lens, P)
+        return OP.decode_batch(q, kp, vp, bt, lens, P)
 
-    step()
+    ref = step()
+    max_err = (gpu_out[seqs].float().cpu() - ref.float()).abs().max().item()
+    if not max_err <= 2e-2:
+        raise AssertionError(f"bench parity: GPU decode output differs from the oracle on the "
+                             f"sampled sequences, max |err| {max_err:.3e} > 2e-2")
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
@@ -163,6 +169,7 @@ def cpu_baseline(torch, inp, n_seqs):
         "sample": f"first {len(seqs)} of {B} sequences of the same step (same input bits), "
                   f"1 warm-up + median of 3, {t * 1e3:.1f} ms per sample step",
         "tokens_per_s": round(len(seqs) / t, 2), "cpu_model": model, "physical_cores": phys,
+        "parity_max_abs_err": max_err, "parity_seqs": len(seqs),
     }
 
 
@@ -1411,7 +1418,11 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         print(f"bench: cpu baseline on {args.cpu_sample_seqs} sequences", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(torch, inp, args.cpu_sample_seqs)
+        result["cpu_baseline"] = cpu_baseline(torch, inp, args.cpu_sample_seqs, out)
+        result["parity"] = {"max_abs_err": result["cpu_baseline"]["parity_max_abs_err"],
+                            "tol": 2e-2, "seqs_checked": result["cpu_baseline"]["parity_seqs"],
+                            "against": "oracle (reference torch path restated) on the same "
+                                       "input bits, after the same scatter"}
     print(json.dumps(result), flush=True)
     return 0
 

@@ -116,6 +116,10 @@ int pia_kv_pages_chunks_copy(void* const* chunks, int num_chunks, void* pages,
  * tokens of block_tables[b, :ceil(L_b / P)]. fp32 accumulation and online softmax.
  * q row stride between sequences is q_seq_stride elements; heads are contiguous [H, D].
  * out is contiguous [num_seqs, num_heads, head_dim]; L_b == 0 writes zeros.
+ * A block-table id outside [0, num_pages) inside the first ceil(L_b / P) entries is not
+ * dereferenced: the tokens of that page are not keys (the reference's index_select would raise
+ * instead; its drop-in wrappers, which see host lists, raise IndexError before launching).
+ * A row left with no key writes zeros.
  * workspace: caller-owned device scratch of at least
  *     pia_paged_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim, page_size,
  *                                      bt_stride)
@@ -143,7 +147,9 @@ int pia_paged_decode_attention(void* out, const void* q, int64_t q_seq_stride,
  * attends keys j < kv_lens[b]; when q_pos_offsets != NULL additionally j <= q_pos_offsets[b] + s
  * (offset 0 = torch SDPA is_causal=True top-left alignment, reference
  * src/plastic_infer/exec/attention.py:189; offset q_start_pos = the explicit mask of
- * src/plastic_infer/exec/runner_paged.py:61-95). A row with no admissible key writes zeros.
+ * src/plastic_infer/exec/runner_paged.py:61-95). Pages whose block-table id is outside
+ * [0, num_pages) hold no keys, as in pia_paged_decode_attention. A row with no admissible key
+ * writes zeros.
  * ------------------------------------------------------------------------------------------- */
 int pia_paged_attention(void* out, const void* q, const void* k_pages, const void* v_pages,
                         const int32_t* block_tables, int64_t bt_stride,

@@ -183,9 +183,13 @@ __global__ __launch_bounds__(64) void kv_scatter16_kernel(
   const int64_t b1 = has1 ? (s1 / P) * H * D * P + head_off + (s1 % P) : 0;
   // a whole page (16 consecutive slots from a page start) on 16-byte aligned pools: every page
   // row (32 bytes) goes out as two 16-byte stores, lane l writing row d = 32r + l/2, tokens
-  // 8(l&1) .. 8(l&1) + 7, so one store instruction covers 1 KiB of the tile
+  // 8(l&1) .. 8(l&1) + 7, so one store instruction covers 1 KiB of the tile. The owned tokens
+  // must form ONE segment: m counts every segment that starts in the group, so several short
+  // segments (or a run followed by padding) can also add up to 16; those have a segment start
+  // among lanes a + 1 .. a + 15 and take the per-token path below.
   const long long sfirst = __shfl(s, a & 63, 64);
-  const bool full = wide && m == P && sfirst >= 0 && (sfirst % P) == 0;
+  const bool one_segment = ((starts >> (a + 1)) & 0x7fffull) == 0;
+  const bool full = wide && m == P && one_segment && sfirst >= 0 && (sfirst % P) == 0;
   const int64_t fbase = full ? (sfirst / P) * H * D * P + head_off : 0;
 
   // The first 256 16-byte items of K and of V (all of a 16-token segment for D <= 128) are

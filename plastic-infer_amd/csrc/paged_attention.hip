@@ -3,9 +3,7 @@
 // 1. paged_decode_stream<G> (G = Hq/Hkv in {1,2,4,8}): the decode hot path for bf16, D = 128,
 //    P = 16 (described where it is defined): the batch's 128-token steps split over persistent
 //    single waves (a fixed, XCD-aware split), two per SIMD (one for G = 8, whose accumulators
-//    need the registers). paged_decode_bf16_d128p16<8> is the earlier split-context G = 8 kernel, kept
-//    behind PIA_G8_STREAM=0: one 256-thread workgroup per (512-token partition, kv head,
-//    sequence); each of its 4 waves owns 8 pages (128 tokens) of the partition. Both use:
+//    need the registers). Per 8-page (128-token) step:
 //      K tile loads: lane l reads page l/8, rows d = 4i + (l&3), token half (l>>2)&1, so load i
 //        of the wave covers one whole 128-byte line of each of the 8 pages (32 loads / 8 pages).
 //      QK^T: pairs of rows (d, d+4) are packed per token with v_perm, then v_dot2_f32_bf16
@@ -14,8 +12,10 @@
 //      Softmax: fp32, base-2 with the scale folded in; wave max by DPP/shuffles.
 //      PV: lane l reads V rows d = 32j + l/2, token half l&1 (1 KiB contiguous per load); the
 //        probabilities of its 8 tokens come from LDS as bf16 pairs, v_dot2 accumulates in fp32.
-//      The 4 waves merge through LDS; a sequence with one partition writes its output directly,
-//      longer ones write (max, sum, unnormalised acc) partials merged by paged_decode_reduce.
+//    Segments cut by a wave-range boundary leave (max, sum, unnormalised acc) partials that
+//    paged_decode_stream_reduce merges.
+//    Block-table ids outside [0, num_pages) inside a context are not dereferenced: their tokens
+//    are not keys (score -inf, V zeroed); a row with no key at all is written as zeros.
 // 2. paged_attention_generic<DT, DPL>: any dtype / head_dim <= 512 / page size, several query
 //    rows per sequence with optional causal offsets. One wave per (query row, head); keys are
 //    processed 64 at a time (lane = key for QK, lane = head-dim element for PV).
@@ -132,9 +132,7 @@ __device__ __forceinline__ uint32_t mask_pair(uint32_t x, int t, int nvalid) {
 
 constexpr int FD_D = 128;
 constexpr int FD_P = 16;
-constexpr int FD_WAVES = 4;
-constexpr int FD_PAGES_PER_WAVE = 8;
-constexpr int FD_PART_PAGES = FD_WAVES * FD_PAGES_PER_WAVE;  // 32 pages = 512 tokens
+constexpr int FD_PAGES_PER_WAVE = 8;  // pages of one 128-token step
 
 __device__ __forceinline__ int clamp_len(int L, int64_t bt_stride, int P) {
   const int64_t cap = bt_stride * P;
@@ -142,231 +140,8 @@ __device__ __forceinline__ int clamp_len(int L, int64_t bt_stride, int P) {
   return int64_t(L) > cap ? int(cap) : L;
 }
 
-template <int G>
-__global__ __launch_bounds__(256, 2) void paged_decode_bf16_d128p16(
-    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
-    const uint16_t* __restrict__ kpool, const uint16_t* __restrict__ vpool,
-    const int32_t* __restrict__ block_tables, int64_t bt_stride,
-    const int32_t* __restrict__ context_lens, float* __restrict__ ws_acc,
-    float* __restrict__ ws_ml, int Hkv, int64_t num_pages, int max_parts, float scale_log2) {
-  constexpr int D = FD_D, P = FD_P, TILE = D * P;
-  const int part = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int Hq = Hkv * G;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int L = clamp_len(context_lens[b], bt_stride, P);
-  const int n_pages = (L + P - 1) / P;
-  const int n_parts = (n_pages + FD_PART_PAGES - 1) / FD_PART_PAGES;
-  const int64_t row0 = int64_t(b) * Hq + int64_t(h) * G;  // first output row of this kv head
-
-  if (n_parts == 0) {
-    if (part == 0)
-      for (int i = tid; i < G * D; i += 256) out[row0 * D + i] = 0;
-    return;
-  }
-  if (part >= n_parts) return;
-
-  __shared__ uint32_t q_lds[4][16][G];          // [d&3 of row d=8p+(d&3)][p][g]: (q[d], q[d+4])
-  __shared__ uint32_t p_lds[FD_WAVES][64][G];   // probabilities of tokens (2l, 2l+1) as bf16x2
-  __shared__ float m_lds[FD_WAVES][G];
-  __shared__ float l_lds[FD_WAVES][G];
-  __shared__ float acc_lds[FD_WAVES][G][D];
-
-  const uint16_t* qb = q + int64_t(b) * q_seq_stride + int64_t(h) * G * D;
-  for (int i = tid; i < 4 * 16 * G; i += 256) {
-    const int g = i % G, pp = (i / G) % 16, dsub = i / (G * 16);
-    const int d0 = 8 * pp + dsub;
-    q_lds[dsub][pp][g] = uint32_t(qb[g * D + d0]) | (uint32_t(qb[g * D + d0 + 4]) << 16);
-  }
-  __syncthreads();
-
-  float m[G], lsum[G], acc[4][G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = kNegBig;
-    lsum[g] = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j][g] = 0.f;
-  }
-
-  const int page0 = part * FD_PART_PAGES + wave * FD_PAGES_PER_WAVE;
-  if (page0 < n_pages) {
-    const int32_t* bt = block_tables + int64_t(b) * bt_stride;
-    int lp = page0 + (lane & 7);
-    if (lp > n_pages - 1) lp = n_pages - 1;  // pages past the end re-read the last page (masked)
-    int phys = bt[lp];
-    if (phys < 0 || int64_t(phys) >= num_pages) phys = 0;
-
-    // ---- K: 32 loads of 16 B; load i = one full 128-byte line of each of the 8 pages ----
-    const int kphys = __shfl(phys, lane >> 3, 64);
-    const uint16_t* kb = kpool + (int64_t(kphys) * Hkv + h) * TILE + (lane & 3) * P +
-                         ((lane >> 2) & 1) * 8;
-    uint4 kr[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) kr[i] = load16_nt(kb + 64 * i);
-
-    float s[8][G];
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-#pragma unroll
-      for (int g = 0; g < G; ++g) s[t][g] = 0.f;
-
-    const uint32_t* qrow = &q_lds[lane & 3][0][0];
-#pragma unroll
-    for (int pp = 0; pp < 16; ++pp) {
-      // one row pair at a time: hoisting every pair's q reads would cost 16*G VGPRs
-      __builtin_amdgcn_sched_barrier(0);
-      const uint4 a = kr[2 * pp], c = kr[2 * pp + 1];  // rows d = 8pp + (l&3) and d + 4
-      uint32_t kk[8];
-      kk[0] = pack_lo(a.x, c.x); kk[1] = pack_hi(a.x, c.x);
-      kk[2] = pack_lo(a.y, c.y); kk[3] = pack_hi(a.y, c.y);
-      kk[4] = pack_lo(a.z, c.z); kk[5] = pack_hi(a.z, c.z);
-      kk[6] = pack_lo(a.w, c.w); kk[7] = pack_hi(a.w, c.w);
-      uint32_t qq[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) qq[g] = qrow[pp * G + g];
-#pragma unroll
-      for (int t = 0; t < 8; ++t)
-#pragma unroll
-        for (int g = 0; g < G; ++g) s[t][g] = dot2_bf16(kk[t], qq[g], s[t][g]);
-    }
-
-    // ---- quad reduce-scatter of the 4 row subsets; lane l keeps tokens 2l, 2l+1 ----
-    float sc[2][G];
-    quad_reduce_scatter<G>(s, sc, lane);
-
-    // Keep the V loads below the QK^T math: hoisting them would hold K and V tiles (256 VGPRs)
-    // live together.
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- V loads for all 8 pages (issued before the softmax so they overlap it) ----
-    uint4 vr[8][4];
-#pragma unroll
-    for (int pg = 0; pg < 8; ++pg) {
-      const int vphys = __builtin_amdgcn_readlane(phys, pg);
-      const uint16_t* vb = vpool + (int64_t(vphys) * Hkv + h) * TILE + lane * 8;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        vr[pg][j] = load16_nt(vb + 512 * j);
-    }
-
-    const int tok0 = page0 * P + 2 * lane;
-    uint32_t pw[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float s0 = sc[0][g], s1 = sc[1][g];
-      const float x0 = tok0 < L ? s0 * scale_log2 : -INFINITY;
-      const float x1 = tok0 + 1 < L ? s1 * scale_log2 : -INFINITY;
-      const float mnew = fmaxf(m[g], wave_max_dpp(fmaxf(x0, x1)));
-      const float alpha = fast_exp2(m[g] - mnew);
-      const float p0 = fast_exp2(x0 - mnew), p1 = fast_exp2(x1 - mnew);
-      lsum[g] = lsum[g] * alpha + (p0 + p1);
-      m[g] = mnew;
-      pw[g] = pack_bf16x2(p0, p1);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j][g] *= alpha;
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) p_lds[wave][lane][g] = pw[g];
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-
-    // ---- PV ----
-    const int vhalf = lane & 1;
-    // PV over the 8 pages as straight-line code. Tokens at or past L (the sequence's partial
-    // last page and the clamped re-reads after it) carry P = 0, but their stale V words may be
-    // non-finite, so a wave whose pages reach past L zeroes them first (branch-free selects).
-    // Waves of full pages (the common case) take the variant without any masking.
-    auto pv_pages = [&](auto masked) {
-#pragma unroll
-      for (int pg = 0; pg < 8; ++pg) {
-        // one page at a time: hoisting later pages' probability reads costs 4*G VGPRs each
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (decltype(masked)::value) {
-          const int nvalid = L - ((page0 + pg) * P + vhalf * 8);  // valid tokens of this half
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            vr[pg][j].x = mask_pair(vr[pg][j].x, 0, nvalid);
-            vr[pg][j].y = mask_pair(vr[pg][j].y, 2, nvalid);
-            vr[pg][j].z = mask_pair(vr[pg][j].z, 4, nvalid);
-            vr[pg][j].w = mask_pair(vr[pg][j].w, 6, nvalid);
-          }
-        }
-        const uint32_t* prow = &p_lds[wave][pg * 8 + vhalf * 4][0];
-        uint32_t pr[4][G];
-#pragma unroll
-        for (int mm = 0; mm < 4; ++mm)
-#pragma unroll
-          for (int g = 0; g < G; ++g) pr[mm][g] = prow[mm * G + g];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            float a = acc[j][g];
-            a = dot2_bf16(vr[pg][j].x, pr[0][g], a);
-            a = dot2_bf16(vr[pg][j].y, pr[1][g], a);
-            a = dot2_bf16(vr[pg][j].z, pr[2][g], a);
-            a = dot2_bf16(vr[pg][j].w, pr[3][g], a);
-            acc[j][g] = a;
-          }
-      }
-    };
-    if ((page0 + FD_PAGES_PER_WAVE) * P <= L)
-      pv_pages(std::false_type{});
-    else
-      pv_pages(std::true_type{});
-
-    // lanes l and l^1 hold the two token halves of the same rows d
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int g = 0; g < G; ++g) acc[j][g] += dpp_f32<kDppQuadXor1>(acc[j][g]);
-#pragma unroll
-    for (int g = 0; g < G; ++g) lsum[g] = wave_sum_dpp(lsum[g]);
-  }
-
-  if (lane == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      m_lds[wave][g] = m[g];
-      l_lds[wave][g] = lsum[g];
-    }
-  }
-  if ((lane & 1) == 0) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int g = 0; g < G; ++g) acc_lds[wave][g][32 * j + (lane >> 1)] = acc[j][g];
-  }
-  __syncthreads();
-
-  for (int i = tid; i < G * D; i += 256) {
-    const int g = i / D, d = i - g * D;
-    float M = m_lds[0][g];
-#pragma unroll
-    for (int w = 1; w < FD_WAVES; ++w) M = fmaxf(M, m_lds[w][g]);
-    float o = 0.f, lt = 0.f;
-#pragma unroll
-    for (int w = 0; w < FD_WAVES; ++w) {
-      const float f = fast_exp2(m_lds[w][g] - M);
-      o += f * acc_lds[w][g][d];
-      lt += f * l_lds[w][g];
-    }
-    const int64_t row = row0 + g;
-    if (n_parts == 1) {
-      out[row * D + d] = f32_to_bf16(o / lt);
-    } else {
-      const int64_t slot = row * max_parts + part;
-      ws_acc[slot * D + d] = o;
-      if (d == 0) {
-        ws_ml[slot * 2 + 0] = M;
-        ws_ml[slot * 2 + 1] = lt;
-      }
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------------------------
-// Stream decode kernel (G <= 4): persistent single waves over an even split of the batch.
+// Stream decode kernel: persistent single waves over an even split of the batch.
 //
 // The work of a launch is the ordered list of 128-token steps of every (sequence, kv head)
 // segment, sequence-major then head then step: T = Hkv * sum_b ceil(L_b / 128) steps. Wave w of
@@ -631,12 +406,15 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     }
   };
 
-  // Tokens at or past the step's valid count (partial last page, re-read pages after it) carry
-  // P = 0, but their stale V words may be non-finite: zero them before the PV products.
-  auto mask_tail = [&](uint4 (&vr)[16], int pg0, int valid) {
+  // Tokens at or past the step's valid count (partial last page, re-read pages after it) and
+  // tokens of pages whose block-table id is out of the pool carry P = 0, but their V words
+  // (stale or another page's) may be non-finite: zero them before the PV products.
+  // bad: bit 8 * pg set when page pg of the step has an invalid id.
+  auto mask_tail = [&](uint4 (&vr)[16], int pg0, int valid, uint64_t bad) {
 #pragma unroll
     for (int pgi = 0; pgi < 4; ++pgi) {
-      const int nvalid = valid - ((pg0 + pgi) * P + vhalf * 8);
+      const bool pg_bad = (bad >> (8 * (pg0 + pgi))) & 1ull;
+      const int nvalid = pg_bad ? 0 : valid - ((pg0 + pgi) * P + vhalf * 8);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         uint4& wv = vr[4 * pgi + j];
@@ -696,6 +474,12 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     const int valid = min(SD_STEP_TOKENS, cur.L - cur.ls * SD_STEP_TOKENS);
     const uint16_t* head_v = vbase + int64_t(cur.h) * TILE;
 
+    // pages of this step whose id is outside the pool: their tokens are not keys (lane l holds
+    // the id of page l / 8, the page of its scores' tokens 2l and 2l + 1)
+    const bool pg_ok = bt_cur >= 0 && int64_t(bt_cur) < num_pages;
+    const uint64_t bad = __ballot(!pg_ok);
+    const bool masked_step = valid < SD_STEP_TOKENS || bad != 0;
+
     float sacc[8][G];
 #pragma unroll
     for (int t = 0; t < 8; ++t)
@@ -715,8 +499,8 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     uint32_t pw[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float x0 = tok0 < valid ? sc[0][g] * scale_log2 : -INFINITY;
-      const float x1 = tok0 + 1 < valid ? sc[1][g] * scale_log2 : -INFINITY;
+      const float x0 = (tok0 < valid && pg_ok) ? sc[0][g] * scale_log2 : -INFINITY;
+      const float x1 = (tok0 + 1 < valid && pg_ok) ? sc[1][g] * scale_log2 : -INFINITY;
       const float mnew = fmaxf(m[g], wave_max_dpp(fmaxf(x0, x1)));
       const float alpha = fast_exp2(m[g] - mnew);
       const float p0 = fast_exp2(x0 - mnew), p1 = fast_exp2(x1 - mnew);
@@ -733,8 +517,8 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     __builtin_amdgcn_sched_barrier(0);
     load_v(bufB, head_v, bt_cur, 4);
     __builtin_amdgcn_sched_barrier(0);
-    if (valid < SD_STEP_TOKENS) {
-      mask_tail(bufA, 0, valid);
+    if (masked_step) {
+      mask_tail(bufA, 0, valid, bad);
       pv_pages(bufA, 0);
     } else {
       pv_pages(bufA, 0);
@@ -744,8 +528,8 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
 #pragma unroll
     for (int i = 0; i < 16; ++i) bufA[i] = load16_nt(kp + 64 * i);
     __builtin_amdgcn_sched_barrier(0);
-    if (valid < SD_STEP_TOKENS) {
-      mask_tail(bufB, 4, valid);
+    if (masked_step) {
+      mask_tail(bufB, 4, valid, bad);
       pv_pages(bufB, 4);
     } else {
       pv_pages(bufB, 4);
@@ -773,7 +557,8 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
           for (int g = 0; g < G; ++g)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-              out[(row0 + g) * D + 32 * j + (lane >> 1)] = f32_to_bf16(acc[j][g] / lsum[g]);
+              out[(row0 + g) * D + 32 * j + (lane >> 1)] =
+                  f32_to_bf16(lsum[g] > 0.f ? acc[j][g] / lsum[g] : 0.f);
         }
       } else {
         float* part = ws_part + (int64_t(w) * 2 + (seg_first < start ? 0 : 1)) * G * (D + 2);
@@ -870,30 +655,7 @@ __global__ __launch_bounds__(FD_D) void paged_decode_stream_reduce(
   }
   uint16_t* orow = out + (int64_t(b) * Hkv + h) * G * D + d;
 #pragma unroll
-  for (int g = 0; g < G; ++g) orow[g * D] = f32_to_bf16(o[g] / lt[g]);
-}
-
-// Merge the partition partials of sequences with more than one partition.
-__global__ __launch_bounds__(FD_D) void paged_decode_reduce(
-    uint16_t* __restrict__ out, const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
-    const int32_t* __restrict__ context_lens, int64_t bt_stride, int Hq, int max_parts,
-    int part_pages) {
-  constexpr int D = FD_D, P = FD_P;
-  const int hq = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int L = clamp_len(context_lens[b], bt_stride, P);
-  const int n_parts = ((L + P - 1) / P + part_pages - 1) / part_pages;
-  if (n_parts <= 1) return;
-  const int64_t row = int64_t(b) * Hq + hq;
-  const float* ml = ws_ml + row * max_parts * 2;
-  float M = kNegBig;
-  for (int p = 0; p < n_parts; ++p) M = fmaxf(M, ml[2 * p]);
-  float o = 0.f, lt = 0.f;
-  for (int p = 0; p < n_parts; ++p) {
-    const float f = fast_exp2(ml[2 * p] - M);
-    lt += f * ml[2 * p + 1];
-    o += f * ws_acc[(row * max_parts + p) * D + d];
-  }
-  out[row * D + d] = f32_to_bf16(o / lt);
+  for (int g = 0; g < G; ++g) orow[g * D] = f32_to_bf16(lt[g] > 0.f ? o[g] / lt[g] : 0.f);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -947,16 +709,17 @@ __global__ __launch_bounds__(64) void paged_attention_generic(
   for (int j0 = 0; j0 < limit; j0 += 64) {
     const int j = j0 + lane;
     const bool valid = j < limit;
-    int64_t base = 0;
+    int64_t base = -1;  // -1: not a key (past the limit, or its page id is out of the pool)
     float sc = 0.f;
     if (valid) {
       const int lp = j / P, off = j - lp * P;
-      int64_t phys = btb[lp];
-      if (phys < 0 || phys >= num_pages) phys = 0;
-      base = (phys * Hkv + hk) * DP + off;
-      for (int d = 0; d < D; ++d) sc = fmaf(q_s[d], E::load(kp, base + int64_t(d) * P), sc);
+      const int64_t phys = btb[lp];
+      if (phys >= 0 && phys < num_pages) {
+        base = (phys * Hkv + hk) * DP + off;
+        for (int d = 0; d < D; ++d) sc = fmaf(q_s[d], E::load(kp, base + int64_t(d) * P), sc);
+      }
     }
-    const float x = valid ? sc * scale_log2 : -INFINITY;
+    const float x = base >= 0 ? sc * scale_log2 : -INFINITY;
     const float mnew = fmaxf(m, wave_max(x));
     const float alpha = fast_exp2(m - mnew);
     const float p = fast_exp2(x - mnew);
@@ -970,6 +733,7 @@ __global__ __launch_bounds__(64) void paged_attention_generic(
     for (int jj = 0; jj < cnt; ++jj) {
       const float pj = p_s[jj];
       const int64_t bj = base_s[jj];
+      if (bj < 0) continue;  // wave-uniform: every lane reads the same LDS entry
 #pragma unroll
       for (int i = 0; i < DPL; ++i) {
         const int d = lane + 64 * i;
@@ -1053,10 +817,6 @@ int stream_waves(int G) {
   return std::max(2, n & ~1);  // whole (even, odd) pairs
 }
 
-#ifndef PIA_G8_STREAM
-#define PIA_G8_STREAM 1  // G = 8 on the stream kernel (else the split-context partitions)
-#endif
-
 }  // namespace
 }  // namespace pia
 
@@ -1069,9 +829,6 @@ extern "C" int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads,
       num_kv_heads <= 0 || num_heads % num_kv_heads || bt_stride <= 0)
     return 0;
   const int G = num_heads / num_kv_heads;
-  if (G == 8 && !PIA_G8_STREAM)  // partition partials: (acc[128], max, sum) per (seq, head, part)
-    return int64_t(num_seqs) * num_heads * ceil_div(bt_stride, FD_PART_PAGES) * (FD_D + 2) *
-           int64_t(sizeof(float));
   if (G == 1 || G == 2 || G == 4 || G == 8)  // two partial slots per wave + step-prefix table
     return int64_t(SD_MAX_WAVES) * 2 * G * (FD_D + 2) * int64_t(sizeof(float)) +
            int64_t(SD_META_INTS) * int64_t(sizeof(int32_t));
@@ -1111,24 +868,6 @@ extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_se
       return fail(PIA_EINVAL, "paged_decode: q and workspace must be 4-byte and pools "
                               "16-byte aligned");
     const int G = num_heads / num_kv_heads;
-    if (G == 8 && !PIA_G8_STREAM) {
-      const int max_parts = int(ceil_div(bt_stride, FD_PART_PAGES));
-      float* ws_acc = reinterpret_cast<float*>(workspace);
-      float* ws_ml = ws_acc + int64_t(num_seqs) * num_heads * max_parts * FD_D;
-      dim3 grid = dim3(unsigned(max_parts), unsigned(num_kv_heads), unsigned(num_seqs));
-      hipLaunchKernelGGL((paged_decode_bf16_d128p16<8>), grid, dim3(256), 0, s, (uint16_t*)out,
-                         (const uint16_t*)q, q_seq_stride, (const uint16_t*)k_pages,
-                         (const uint16_t*)v_pages, block_tables, bt_stride, context_lens, ws_acc,
-                         ws_ml, num_kv_heads, num_pages, max_parts, scale_log2);
-      if (int rc = check_launch("paged_decode")) return rc;
-      if (max_parts > 1) {
-        hipLaunchKernelGGL(paged_decode_reduce, dim3(unsigned(num_heads), unsigned(num_seqs)),
-                           dim3(FD_D), 0, s, (uint16_t*)out, ws_acc, ws_ml, context_lens,
-                           bt_stride, num_heads, max_parts, int(FD_PART_PAGES));
-        if (int rc = check_launch("paged_decode_reduce")) return rc;
-      }
-      return 0;
-    }
     // Stream kernel, in launches of up to SD_MAX_SEQS sequences. Its step arithmetic is int32:
     // Hkv * (sequences) * (steps per sequence) plus a wave count must stay below 2^31.
     const int NW = stream_waves(G);

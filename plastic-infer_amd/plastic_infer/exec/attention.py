@@ -29,8 +29,14 @@ from ..kernel.host_stream import host_stream_attention
 from ..kernel.paged_kv import kv_gather, paged_attention, paged_decode_attention
 
 
-def _table_tensor(block_table: list[int], device: torch.device) -> torch.Tensor:
-    return torch.tensor([list(block_table)], dtype=torch.int32).to(device, non_blocking=True)
+def _table_tensor(block_table: list[int], device: torch.device, num_pages: int) -> torch.Tensor:
+    """The table as an int32 [1, n] device row. Every listed id must name a pool page: the
+    reference index_selects the whole list (src/plastic_infer/exec/attention.py:134-136), which
+    raises IndexError for an id < 0 or >= num_pages."""
+    ids = [int(x) for x in block_table]
+    if ids and (min(ids) < 0 or max(ids) >= num_pages):
+        raise IndexError("index out of range in self")
+    return torch.tensor([ids], dtype=torch.int32).to(device, non_blocking=True)
 
 
 def gather_paged_kv(k_pages: torch.Tensor, v_pages: torch.Tensor, block_table: list[int],
@@ -44,11 +50,12 @@ def gather_paged_kv(k_pages: torch.Tensor, v_pages: torch.Tensor, block_table: l
     _, H, D, P = k_pages.shape
     cap = len(block_table) * P
     T = cap if num_tokens is None else max(0, min(int(num_tokens), cap))
+    bt = _table_tensor(block_table, dev, k_pages.shape[0])
     if T == 0:
         empty = torch.empty(1, 0, H, D, dtype=k_pages.dtype, device=dev)
         return empty, empty.clone()
     cu = torch.tensor([0, T], dtype=torch.int64).to(dev, non_blocking=True)
-    k, v = kv_gather(k_pages, v_pages, _table_tensor(block_table, dev), cu, T,
+    k, v = kv_gather(k_pages, v_pages, bt, cu, T,
                      out=(torch.empty(T, H, D, dtype=k_pages.dtype, device=dev),
                           torch.empty(T, H, D, dtype=k_pages.dtype, device=dev)))
     return k.unsqueeze(0), v.unsqueeze(0)
@@ -73,7 +80,7 @@ def paged_attention_v1(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Te
         return torch.empty_like(q)
     if not block_table:
         return torch.zeros_like(q)
-    bt = _table_tensor(block_table, dev)
+    bt = _table_tensor(block_table, dev, k_pages.shape[0])
     lens = torch.tensor([kv_len], dtype=torch.int32).to(dev, non_blocking=True)
     q3 = q[0]
     if Sq == 1 and not causal:

@@ -19,7 +19,7 @@ import torch
 
 from ..kernel.paged_kv import kv_scatter, paged_attention
 from ..kv.kv_store import KVRequestCache, KVStore
-from .attention import paged_attention_v1
+from .attention import _table_tensor, paged_attention_v1
 
 
 def _write_kv_layer(cache: KVRequestCache, store: KVStore, layer_idx: int, start_pos: int,
@@ -50,7 +50,7 @@ def _attn_paged(q: torch.Tensor, cache: KVRequestCache, layer_idx: int, store: K
     dev = store.gpu.device
     q_len = q.shape[1]
     kv_len = kv_num_tokens or len(block_table) * cfg.page_size
-    bt = torch.tensor([block_table], dtype=torch.int32).to(dev, non_blocking=True)
+    bt = _table_tensor(block_table, dev, store.gpu.k_pages.shape[0])
     lens = torch.tensor([kv_len], dtype=torch.int32).to(dev, non_blocking=True)
     cu = torch.tensor([0, q_len], dtype=torch.int32).to(dev, non_blocking=True)
     offs = torch.tensor([q_start_pos], dtype=torch.int32).to(dev, non_blocking=True)

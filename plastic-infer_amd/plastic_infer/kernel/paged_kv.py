@@ -38,7 +38,8 @@ def kv_scatter(k: torch.Tensor, v: torch.Tensor, k_pages: torch.Tensor, v_pages:
                slot_mapping: torch.Tensor) -> None:
     """k_pages[s // P, :, :, s % P] = k[i] for s = slot_mapping[i] (same for v).
 
-    k, v: [N, H, D] (token rows may be strided, [H, D] contiguous); slot_mapping: int64 [N].
+    k, v: [N, H, D] (token rows may be strided; a row whose [H, D] is not contiguous is copied
+    first); slot_mapping: int64 [N].
     Negative slots are padding and skipped. Bit-exact.
     """
     dev = N.require_device(k, v, k_pages, v_pages, slot_mapping,
@@ -49,15 +50,20 @@ def kv_scatter(k: torch.Tensor, v: torch.Tensor, k_pages: torch.Tensor, v_pages:
         raise ValueError(f"k/v must be [N, {H}, {D}], got {tuple(k.shape)} / {tuple(v.shape)}")
     if k.dtype != k_pages.dtype or v.dtype != k_pages.dtype:
         raise ValueError("k/v dtype must match the pool dtype")
-    for name, t in (("k", k), ("v", v)):
-        if t.shape[0] > 1 and not (t.stride(2) == 1 and t.stride(1) == D):
-            raise ValueError(f"{name}: each token row [H, D] must be contiguous")
+    # The kernels read token i's row at base + i * stride(0) with heads D apart and elements
+    # adjacent; any other layout (for any N, including a single strided token) is copied first.
+    if not (k.stride(2) == 1 and k.stride(1) == D):
+        k = k.contiguous()
+    if not (v.stride(2) == 1 and v.stride(1) == D):
+        v = v.contiguous()
     if slot_mapping.dtype != torch.int64 or slot_mapping.dim() != 1 or slot_mapping.numel() != k.shape[0]:
         raise ValueError("slot_mapping must be int64 [N]")
     slot_mapping = slot_mapping.contiguous()
     n = k.shape[0]
     if n == 0:
         return
+    # a single token's stride(0) is never used to step (and torch may report any value for a
+    # size-1 dimension): pass the packed row size
     N.call("pia_kv_scatter", k.data_ptr(), v.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(),
            slot_mapping.data_ptr(), n, k.stride(0) if n > 1 else H * D,
            v.stride(0) if n > 1 else H * D, H, D, P, num_pages, k.element_size(),

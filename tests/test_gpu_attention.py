@@ -250,6 +250,105 @@ def test_decode_nonfinite_stale_tokens_are_ignored(dev):
     assert (out[0].float() - ref[0, 0].float()).abs().max() <= BF16_TOL
 
 
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_decode_invalid_table_ids_inside_context(dev, G):
+    """Block-table ids outside [0, num_pages) inside a context (-1, num_pages, INT32_MAX, -7):
+    those pages' tokens are not keys. Page 0 holds NaN/Inf, so a kernel that read a substitute
+    page there would show it. Decode attention is invariant under key order, so the expected
+    rows are the oracle's over the table with the invalid pages removed (the partial last page
+    stays last, or every kept page is whole). A row with every page invalid is zeros."""
+    Hkv, num_pages = 4, 600
+    lens = [300, 21, 130, 1000, 16, 64, 257]
+    q, kp, vp, bt, lens_t = _decode_case(60 + G, lens, Hkv * G, Hkv, num_pages)
+    kp[0] = float("nan")
+    vp[0] = float("inf")
+    used = set(bt[bt >= 0].tolist())
+    bt[bt == 0] = next(p for p in range(1, num_pages) if p not in used)   # no table uses page 0
+    bad_vals = [-1, num_pages, 2**31 - 1, -7]
+    g = torch.Generator().manual_seed(70 + G)
+    n_pages = [(L + 15) // 16 for L in lens]
+    for b, n in enumerate(n_pages):
+        if b == 4:
+            bt[b, :n] = -1                       # every page invalid
+            continue
+        for i in torch.randperm(n, generator=g)[: max(1, n // 5)].tolist():
+            bt[b, i] = bad_vals[(b + i) % len(bad_vals)]
+    bt[6, n_pages[6] - 1] = num_pages            # the partial last page (1 token) invalid
+    out = paged_decode_attention(q.to(dev), kp.to(dev), vp.to(dev), bt.to(dev),
+                                 lens_t.to(dev)).cpu()
+    assert torch.isfinite(out.float()).all()
+    assert not out[4].any()
+    for b, L in enumerate(lens):
+        if b == 4:
+            continue
+        row = bt[b, :n_pages[b]].tolist()
+        keep = [(i, p) for i, p in enumerate(row) if 0 <= p < num_pages]
+        toks = sum(min(16, L - 16 * i) for i, _ in keep)
+        ref = OP.paged_attention(q[b][None, None], kp, vp, [p for _, p in keep], 16, toks,
+                                 causal=False)[0, 0]
+        err = (out[b].float() - ref.float()).abs().max().item()
+        assert err <= BF16_TOL, (b, err)
+
+
+def _brute_masked(q, kp, vp, table, P, kv_len, offset, num_pages):
+    """fp64: row i of q [Sq, H, D] over keys j < kv_len (and j <= offset + i) whose page id is
+    inside the pool; no key -> zeros."""
+    q, kp, vp = (np.asarray(x, dtype=np.float64) for x in (q, kp, vp))
+    Sq, H, D = q.shape
+    G = H // kp.shape[1]
+    out = np.zeros((Sq, H, D))
+    for i in range(Sq):
+        lim = kv_len if offset is None else min(kv_len, offset + i + 1)
+        js = [j for j in range(lim) if 0 <= table[j // P] < num_pages]
+        if not js:
+            continue
+        for h in range(H):
+            ks = np.stack([kp[table[j // P], h // G, :, j % P] for j in js])
+            vs = np.stack([vp[table[j // P], h // G, :, j % P] for j in js])
+            s = ks @ q[i, h] / np.sqrt(D)
+            w = np.exp(s - s.max())
+            out[i, h] = (w / w.sum()) @ vs
+    return out
+
+
+@pytest.mark.parametrize("offset", [None, 5])
+def test_general_kernel_invalid_table_ids(dev, offset):
+    """The general kernel (fp32, head_dim 64, 4-token pages) with ids -1 and num_pages inside
+    the context: those keys are skipped, never read through a substitute page (page 0 is
+    NaN). The first row under the causal offset sees only an invalid page: zeros."""
+    g = torch.Generator().manual_seed(81)
+    n, Hkv, G, D, P = 9, 2, 2, 64, 4
+    kp = torch.randn(n, Hkv, D, P, generator=g)
+    vp = torch.randn(n, Hkv, D, P, generator=g)
+    kp[0] = float("nan")
+    vp[0] = float("nan")
+    table = [-1, 3, 9, 5, -1, 7, 2]
+    kv_len, Sq = 26, 4
+    q = torch.randn(Sq, Hkv * G, D, generator=g)
+    offs = None if offset is None else torch.tensor([offset - 5], dtype=torch.int32, device=dev)
+    out = paged_attention(q.to(dev), kp.to(dev), vp.to(dev),
+                          torch.tensor([table], dtype=torch.int32, device=dev),
+                          torch.tensor([kv_len], dtype=torch.int32, device=dev),
+                          cu_q=torch.tensor([0, Sq], dtype=torch.int32, device=dev),
+                          q_pos_offsets=offs).cpu()
+    ref = _brute_masked(q.numpy(), kp.numpy(), vp.numpy(), table, P, kv_len,
+                        None if offset is None else offset - 5, n)
+    assert np.isfinite(out.numpy()).all()
+    np.testing.assert_allclose(out.double().numpy(), ref, atol=1e-5)
+
+
+def test_dropin_tables_with_out_of_range_ids_raise(dev):
+    """The drop-in wrappers take host lists and raise IndexError for an id outside the pool,
+    as the reference's index_select does."""
+    kp = torch.zeros(4, 2, 8, 4, device=dev)
+    q = torch.zeros(1, 1, 2, 8, device=dev)
+    for bad in ([0, 4], [-1], [1, 2, 7]):
+        with pytest.raises(IndexError):
+            gather_paged_kv(kp, kp, bad, 4)
+        with pytest.raises(IndexError):
+            paged_attention_v1(q, kp, kp, bad, 4, causal=False)
+
+
 # ---- general kernel ---------------------------------------------------------------------------
 
 GEN_CASES = [  # (seed, n_pages, Hkv, G, D, P, table, kv_len, Sq, mode)

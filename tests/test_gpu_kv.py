@@ -128,6 +128,73 @@ def test_scatter16_whole_pages_pool_alignment(dev, pool_off):
     assert torch.equal(gk.cpu(), ref_k) and torch.equal(gv.cpu(), ref_v)
 
 
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_scatter16_segment_ownership_layouts(dev, seed):
+    """More than 1024 tokens (the page-segment kernel) of mixed segments on distinct pages:
+    short segments that add up to 16 tokens after a page start, page-start runs followed by
+    padding, single decode slots at offset 0, whole pages, the 21 / 11 / 40 ragged batch.
+    Bit-exact against the oracle's per-token store."""
+    from scatter_layouts import random_layout
+
+    g = torch.Generator().manual_seed(300 + seed)
+    H, D, P, N_ = 2, 128, 16, 4096
+    slots = random_layout(seed, n_min=1100, n_pages=N_)
+    n = len(slots)
+    k = torch.randn(n, H, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, H, D, generator=g).to(torch.bfloat16)
+    kp = torch.randn(N_, H, D, P, generator=g).to(torch.bfloat16)
+    vp = torch.randn(N_, H, D, P, generator=g).to(torch.bfloat16)
+    ref_k, ref_v = kp.clone(), vp.clone()
+    OP.scatter_slots(k, v, ref_k, ref_v, slots)
+    gk, gv = kp.to(dev), vp.to(dev)
+    kv_scatter(k.to(dev), v.to(dev), gk, gv, torch.tensor(slots, device=dev))
+    assert torch.equal(gk.cpu(), ref_k) and torch.equal(gv.cpu(), ref_v)
+
+
+def test_scatter16_large_decode_batch_and_padded_runs(dev):
+    """2048 single-token decode slots on pages 0..2047 (half at page offset 0) and 20 copies of
+    the 21 / 11 / 40 ragged batch on pages from 2048, then a page-start run of 8 followed by 8
+    padding slots. No slot repeats, so the result does not depend on write order."""
+    from scatter_layouts import ragged_21_11_40
+
+    g = torch.Generator().manual_seed(310)
+    H, D, P, N_ = 2, 128, 16, 4096
+    perm = torch.randperm(2048, generator=g).tolist()    # pages 0..2047: no slot repeats
+    slots = [perm[i] * P + (0 if i % 2 else (i * 7) % P) for i in range(2048)]
+    for r in range(20):
+        slots += ragged_21_11_40(2048 + 8 * r)
+    slots += [3000 * P + i for i in range(8)] + [-1] * 8
+    n = len(slots)
+    k = torch.randn(n, H, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, H, D, generator=g).to(torch.bfloat16)
+    kp = torch.randn(N_, H, D, P, generator=g).to(torch.bfloat16)
+    vp = torch.randn(N_, H, D, P, generator=g).to(torch.bfloat16)
+    ref_k, ref_v = kp.clone(), vp.clone()
+    OP.scatter_slots(k, v, ref_k, ref_v, slots)
+    gk, gv = kp.to(dev), vp.to(dev)
+    kv_scatter(k.to(dev), v.to(dev), gk, gv, torch.tensor(slots, device=dev))
+    assert torch.equal(gk.cpu(), ref_k) and torch.equal(gv.cpu(), ref_v)
+
+
+def test_scatter_single_token_with_strided_heads(dev):
+    """One token whose [H, D] row is not contiguous (a head_dim slice of a wider buffer, and a
+    head-transposed view): the rows are copied before the kernel reads them."""
+    g = torch.Generator().manual_seed(320)
+    H, D, P, N_ = 4, 128, 16, 8
+    wide = torch.randn(1, H, 2 * D, generator=g).to(torch.bfloat16)
+    k = wide[:, :, :D]                               # stride(1) = 2D
+    vt = torch.randn(1, D, H, generator=g).to(torch.bfloat16)
+    v = vt.transpose(1, 2)                           # stride(2) = H
+    kp = torch.randn(N_, H, D, P, generator=g).to(torch.bfloat16)
+    vp = torch.randn(N_, H, D, P, generator=g).to(torch.bfloat16)
+    ref_k, ref_v = kp.clone(), vp.clone()
+    OP.scatter_slots(k, v, ref_k, ref_v, [5 * P + 3])
+    gk, gv = kp.to(dev), vp.to(dev)
+    kv_scatter(wide.to(dev)[:, :, :D], vt.to(dev).transpose(1, 2), gk, gv,
+               torch.tensor([5 * P + 3], device=dev))
+    assert torch.equal(gk.cpu(), ref_k) and torch.equal(gv.cpu(), ref_v)
+
+
 def test_gather16_tables_with_invalid_pages(dev):
     g = torch.Generator().manual_seed(16)
     H, D, P = 4, 128, 16
