@@ -141,6 +141,29 @@ int pia_paged_decode_attention(void* out, const void* q, int64_t q_seq_stride,
                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * Paged GQA decode attention that allocates nothing and takes no workspace.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and results as pia_paged_decode_attention without the workspace: the fast
+ * kernel keeps its partials in a static device array of the library (16 MiB per GPU, held
+ * until the process ends; its address on each device is resolved on the first call there).
+ * No hipMalloc / hipFree / allocating library routine is called. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (different streams, or unordered host
+ * threads) race and must not be issued; calls ordered on one stream are safe. The array needs
+ * no clearing (each launch writes what it reads). Returns PIA_EUNSUPPORTED when the partials
+ * of the launch would not fit (pia_paged_decode_noalloc_scratch_bytes > 16 MiB).
+ * ------------------------------------------------------------------------------------------- */
+int64_t pia_paged_decode_noalloc_scratch_bytes(int num_heads, int num_kv_heads);
+
+int pia_paged_decode_attention_noalloc(void* out, const void* q, int64_t q_seq_stride,
+                                       const void* k_pages, const void* v_pages,
+                                       const int32_t* block_tables, int64_t bt_stride,
+                                       const int32_t* context_lens, int num_seqs,
+                                       int num_heads, int num_kv_heads, int head_dim,
+                                       int page_size, int64_t num_pages, float scale, int dtype,
+                                       void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * General paged attention over several query rows per sequence (prefill / chunked
  * prefill / the drop-in paged_attention_v1 and _attn_paged paths).
  * Rows of sequence b are q[cu_q[b] .. cu_q[b+1]) (cu_q NULL: one row per sequence). Row s of b

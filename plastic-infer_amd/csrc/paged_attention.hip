@@ -20,6 +20,8 @@
 //    rows per sequence with optional causal offsets. One wave per (query row, head); keys are
 //    processed 64 at a time (lane = key for QK, lane = head-dim element for PV).
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "pia_internal.h"
 
@@ -822,6 +824,122 @@ int stream_waves(int G) {
 
 using namespace pia;
 
+namespace pia {
+namespace {
+
+// Argument checks shared by both decode entry points (nothing enqueued on failure).
+int check_decode_args(const void* out, const void* q, int64_t q_seq_stride, const void* k_pages,
+                      const void* v_pages, const int32_t* block_tables, int64_t bt_stride,
+                      const int32_t* context_lens, int num_seqs, int num_heads, int num_kv_heads,
+                      int head_dim, int page_size, int64_t num_pages, int dtype) {
+  if (int rc = check_heads(num_heads, num_kv_heads, head_dim, page_size, num_pages, dtype))
+    return rc;
+  if (num_seqs < 0 || bt_stride < 0) return fail(PIA_EINVAL, "paged_decode: negative size");
+  if (num_seqs == 0) return 0;
+  if (!out || !q || !k_pages || !v_pages || !block_tables || !context_lens)
+    return fail(PIA_EINVAL, "paged_decode: null pointer");
+  if (bt_stride == 0) return fail(PIA_EINVAL, "paged_decode: bt_stride == 0");
+  if (num_seqs > 65535) return fail(PIA_EINVAL, "paged_decode: num_seqs > 65535");
+  if (q_seq_stride < int64_t(num_heads) * head_dim)
+    return fail(PIA_EINVAL, "paged_decode: q_seq_stride < num_heads*head_dim");
+  if (fast_path(dtype, num_heads, num_kv_heads, head_dim, page_size)) {
+    if (!aligned(q, 4) || !aligned(k_pages, 16) || !aligned(v_pages, 16) || (q_seq_stride & 1))
+      return fail(PIA_EINVAL, "paged_decode: q must be 4-byte and pools 16-byte aligned");
+    // The stream kernel's step arithmetic is int32: Hkv * (sequences of a launch) * (steps per
+    // sequence) plus a wave count must stay below 2^31.
+    const int NW = stream_waves(num_heads / num_kv_heads);
+    if (int64_t(num_kv_heads) * std::min(num_seqs, SD_MAX_SEQS) * ceil_div(bt_stride, 8) +
+            2 * int64_t(NW) >= (int64_t(1) << 31))
+      return fail(PIA_EUNSUPPORTED, "paged_decode: batch too large for int32 step indices");
+  }
+  return 0;
+}
+
+// The fast path (checked arguments): stream kernel + merge, in launches of up to SD_MAX_SEQS
+// sequences that reuse the same partial slots (ws_part: >= NW * 2 * G * (D + 2) floats) and
+// meta ints (ws_meta: SD_META_INTS). Launches on one stream are ordered, so the reuse is safe.
+int launch_stream_decode(void* out, const void* q, int64_t q_seq_stride, const void* k_pages,
+                         const void* v_pages, const int32_t* block_tables, int64_t bt_stride,
+                         const int32_t* context_lens, int num_seqs, int num_heads,
+                         int num_kv_heads, int64_t num_pages, float scale_log2, float* ws_part,
+                         int32_t* ws_meta, hipStream_t s) {
+  const int G = num_heads / num_kv_heads;
+  const int NW = stream_waves(G);
+  for (int b0 = 0; b0 < num_seqs; b0 += SD_MAX_SEQS) {
+    const int Bs = std::min(SD_MAX_SEQS, num_seqs - b0);
+    uint16_t* o = reinterpret_cast<uint16_t*>(out) + int64_t(b0) * num_heads * FD_D;
+    const uint16_t* qq = reinterpret_cast<const uint16_t*>(q) + int64_t(b0) * q_seq_stride;
+    const int32_t* bt = block_tables + int64_t(b0) * bt_stride;
+    const int32_t* cl = context_lens + b0;
+    const size_t lds = size_t(2 * Bs + 1) * sizeof(int32_t);
+#define PIA_SD(GG)                                                                             \
+  hipLaunchKernelGGL((paged_decode_stream<GG>), dim3(unsigned(NW)), dim3(64), lds, s, o, qq,   \
+                     q_seq_stride, (const uint16_t*)k_pages, (const uint16_t*)v_pages, bt,     \
+                     bt_stride, cl, Bs, num_kv_heads, num_pages, ws_part, ws_meta, scale_log2)
+    switch (G) {
+      case 1: PIA_SD(1); break;
+      case 2: PIA_SD(2); break;
+      case 4: PIA_SD(4); break;
+      default: PIA_SD(8); break;
+    }
+#undef PIA_SD
+    if (int rc = check_launch("paged_decode_stream")) return rc;
+#define PIA_SR(GG)                                                                             \
+  hipLaunchKernelGGL((paged_decode_stream_reduce<GG>), dim3(unsigned(NW)), dim3(FD_D), 0, s, o, \
+                     ws_part, ws_meta, Bs, num_kv_heads)
+    switch (G) {
+      case 1: PIA_SR(1); break;
+      case 2: PIA_SR(2); break;
+      case 4: PIA_SR(4); break;
+      default: PIA_SR(8); break;
+    }
+#undef PIA_SR
+    if (int rc = check_launch("paged_decode_stream_reduce")) return rc;
+  }
+  return 0;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Library-owned scratch for pia_paged_decode_attention_noalloc: the meta ints, then the wave
+// partials, in one static device array per GPU (held until the process ends). The kernels keep
+// nothing in it across calls that needs initialising (each launch writes what it reads), so it
+// is never cleared. Every call on one GPU shares that GPU's array: calls that overlap (two
+// streams, or two host threads without ordering) race on it.
+// ---------------------------------------------------------------------------------------------
+constexpr int64_t kNoAllocScratchBytes = int64_t(16) << 20;                  // 16 MiB per GPU
+constexpr int64_t kNoAllocMetaBytes = (int64_t(SD_META_INTS) * 4 + 255) / 256 * 256;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<unsigned char*> g_scratch_of[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device, resolved once per device with
+// hipGetSymbolAddress (in host code the array's name is not a device address).
+int scratch_ptr(unsigned char** ptr) {
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "paged_decode_noalloc: hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices) return fail(PIA_EUNSUPPORTED, "paged_decode_noalloc: device id >= 64");
+  unsigned char* p = g_scratch_of[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_of[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void* addr = nullptr;
+      if (int rc = check_hip(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)),
+                             "paged_decode_noalloc: hipGetSymbolAddress(scratch)"))
+        return rc;
+      p = static_cast<unsigned char*>(addr);
+      g_scratch_of[dev].store(p, std::memory_order_release);
+    }
+  }
+  *ptr = p;
+  return 0;
+}
+
+}  // namespace
+}  // namespace pia
+
 extern "C" int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_heads,
                                                     int head_dim, int page_size,
                                                     int64_t bt_stride) {
@@ -843,16 +961,11 @@ extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_se
                                           int page_size, int64_t num_pages, float scale,
                                           int dtype, void* workspace, int64_t workspace_bytes,
                                           void* stream) {
-  if (int rc = check_heads(num_heads, num_kv_heads, head_dim, page_size, num_pages, dtype))
+  if (int rc = check_decode_args(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride,
+                                 context_lens, num_seqs, num_heads, num_kv_heads, head_dim,
+                                 page_size, num_pages, dtype))
     return rc;
-  if (num_seqs < 0 || bt_stride < 0) return fail(PIA_EINVAL, "paged_decode: negative size");
   if (num_seqs == 0) return 0;
-  if (!out || !q || !k_pages || !v_pages || !block_tables || !context_lens)
-    return fail(PIA_EINVAL, "paged_decode: null pointer");
-  if (bt_stride == 0) return fail(PIA_EINVAL, "paged_decode: bt_stride == 0");
-  if (num_seqs > 65535) return fail(PIA_EINVAL, "paged_decode: num_seqs > 65535");
-  if (q_seq_stride < int64_t(num_heads) * head_dim)
-    return fail(PIA_EINVAL, "paged_decode: q_seq_stride < num_heads*head_dim");
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = as_stream(stream);
   if (fast_path(dtype, num_heads, num_kv_heads, head_dim, page_size)) {
@@ -863,57 +976,61 @@ extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_se
                 (long long)workspace_bytes);
       return PIA_EINVAL;
     }
-    if (!aligned(q, 4) || !aligned(k_pages, 16) || !aligned(v_pages, 16) ||
-        !aligned(workspace, 4) || (q_seq_stride & 1))
-      return fail(PIA_EINVAL, "paged_decode: q and workspace must be 4-byte and pools "
-                              "16-byte aligned");
+    if (!aligned(workspace, 4)) return fail(PIA_EINVAL, "paged_decode: workspace not 4-byte aligned");
     const int G = num_heads / num_kv_heads;
-    // Stream kernel, in launches of up to SD_MAX_SEQS sequences. Its step arithmetic is int32:
-    // Hkv * (sequences) * (steps per sequence) plus a wave count must stay below 2^31.
-    const int NW = stream_waves(G);
-    if (int64_t(num_kv_heads) * std::min(num_seqs, SD_MAX_SEQS) * ceil_div(bt_stride, 8) +
-            2 * int64_t(NW) >= (int64_t(1) << 31))
-      return fail(PIA_EUNSUPPORTED, "paged_decode: batch too large for int32 step indices");
     float* ws_part = reinterpret_cast<float*>(workspace);
     int32_t* ws_meta =
         reinterpret_cast<int32_t*>(ws_part + int64_t(SD_MAX_WAVES) * 2 * G * (FD_D + 2));
-    for (int b0 = 0; b0 < num_seqs; b0 += SD_MAX_SEQS) {
-      const int Bs = std::min(SD_MAX_SEQS, num_seqs - b0);
-      uint16_t* o = reinterpret_cast<uint16_t*>(out) + int64_t(b0) * num_heads * FD_D;
-      const uint16_t* qq = reinterpret_cast<const uint16_t*>(q) + int64_t(b0) * q_seq_stride;
-      const int32_t* bt = block_tables + int64_t(b0) * bt_stride;
-      const int32_t* cl = context_lens + b0;
-      const size_t lds = size_t(2 * Bs + 1) * sizeof(int32_t);
-#define PIA_SD(GG)                                                                             \
-  hipLaunchKernelGGL((paged_decode_stream<GG>), dim3(unsigned(NW)), dim3(64), lds, s, o, qq,   \
-                     q_seq_stride, (const uint16_t*)k_pages, (const uint16_t*)v_pages, bt,     \
-                     bt_stride, cl, Bs, num_kv_heads, num_pages, ws_part, ws_meta, scale_log2)
-      switch (G) {
-        case 1: PIA_SD(1); break;
-        case 2: PIA_SD(2); break;
-        case 4: PIA_SD(4); break;
-        default: PIA_SD(8); break;
-      }
-#undef PIA_SD
-      if (int rc = check_launch("paged_decode_stream")) return rc;
-#define PIA_SR(GG)                                                                             \
-  hipLaunchKernelGGL((paged_decode_stream_reduce<GG>), dim3(unsigned(NW)), dim3(FD_D), 0, s, o, \
-                     ws_part, ws_meta, Bs, num_kv_heads)
-      switch (G) {
-        case 1: PIA_SR(1); break;
-        case 2: PIA_SR(2); break;
-        case 4: PIA_SR(4); break;
-        default: PIA_SR(8); break;
-      }
-#undef PIA_SR
-      if (int rc = check_launch("paged_decode_stream_reduce")) return rc;
-    }
-    return 0;
+    return launch_stream_decode(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride,
+                                context_lens, num_seqs, num_heads, num_kv_heads, num_pages,
+                                scale_log2, ws_part, ws_meta, s);
   }
   return launch_generic_any(dtype, out, q, q_seq_stride, k_pages, v_pages, block_tables,
                             bt_stride, context_lens, nullptr, nullptr, num_seqs, num_seqs,
                             num_heads, num_kv_heads, head_dim, page_size, num_pages, scale_log2,
                             s);
+}
+
+extern "C" int64_t pia_paged_decode_noalloc_scratch_bytes(int num_heads, int num_kv_heads) {
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
+  const int G = num_heads / num_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return 0;
+  return kNoAllocMetaBytes + int64_t(stream_waves(G)) * 2 * G * (FD_D + 2) * int64_t(sizeof(float));
+}
+
+extern "C" int pia_paged_decode_attention_noalloc(void* out, const void* q, int64_t q_seq_stride,
+                                                  const void* k_pages, const void* v_pages,
+                                                  const int32_t* block_tables, int64_t bt_stride,
+                                                  const int32_t* context_lens, int num_seqs,
+                                                  int num_heads, int num_kv_heads, int head_dim,
+                                                  int page_size, int64_t num_pages, float scale,
+                                                  int dtype, void* stream) {
+  if (int rc = check_decode_args(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride,
+                                 context_lens, num_seqs, num_heads, num_kv_heads, head_dim,
+                                 page_size, num_pages, dtype))
+    return rc;
+  if (num_seqs == 0) return 0;
+  const float scale_log2 = scale * kLog2e;
+  hipStream_t s = as_stream(stream);
+  if (!fast_path(dtype, num_heads, num_kv_heads, head_dim, page_size))  // no scratch needed
+    return launch_generic_any(dtype, out, q, q_seq_stride, k_pages, v_pages, block_tables,
+                              bt_stride, context_lens, nullptr, nullptr, num_seqs, num_seqs,
+                              num_heads, num_kv_heads, head_dim, page_size, num_pages,
+                              scale_log2, s);
+  const int64_t need = pia_paged_decode_noalloc_scratch_bytes(num_heads, num_kv_heads);
+  if (need > kNoAllocScratchBytes) {
+    set_error("paged_decode_noalloc: %lld bytes of scratch needed (%d waves), the library's "
+              "static scratch holds %lld", (long long)need,
+              stream_waves(num_heads / num_kv_heads), (long long)kNoAllocScratchBytes);
+    return PIA_EUNSUPPORTED;
+  }
+  unsigned char* base = nullptr;
+  if (int rc = scratch_ptr(&base)) return rc;
+  int32_t* ws_meta = reinterpret_cast<int32_t*>(base);
+  float* ws_part = reinterpret_cast<float*>(base + kNoAllocMetaBytes);
+  return launch_stream_decode(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride,
+                              context_lens, num_seqs, num_heads, num_kv_heads, num_pages,
+                              scale_log2, ws_part, ws_meta, s);
 }
 
 extern "C" int pia_paged_attention(void* out, const void* q, const void* k_pages,

@@ -157,6 +157,43 @@ def paged_decode_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torc
     return out
 
 
+def paged_decode_attention_noalloc(q: torch.Tensor, k_pages: torch.Tensor,
+                                   v_pages: torch.Tensor, block_tables: torch.Tensor,
+                                   context_lens: torch.Tensor, out: torch.Tensor,
+                                   scale: float | None = None) -> torch.Tensor:
+    """paged_decode_attention for callers that cannot allocate (graph capture, serving loops):
+    the caller passes every tensor, already in the layout the kernels read, and the library
+    keeps its partials in a static per-GPU scratch array instead of a workspace. Nothing here
+    allocates; a tensor in another layout raises instead of being copied. Calls that overlap
+    on one GPU (two streams) race on the shared scratch; calls on one stream are ordered."""
+    dev = N.require_device(q, k_pages, v_pages, block_tables, context_lens, out,
+                           names=("q", "k_pages", "v_pages", "block_tables", "context_lens",
+                                  "out"))
+    _check_pool(k_pages, v_pages)
+    num_pages, Hkv, D, P = k_pages.shape
+    if q.dim() != 3 or q.shape[2] != D or q.shape[1] % Hkv or q.dtype != k_pages.dtype:
+        raise ValueError(f"q must be [B, Hq, {D}] of the pool dtype with Hq a multiple of {Hkv}")
+    if not (q.stride(2) == 1 and q.stride(1) == D):
+        raise ValueError("q rows [Hq, D] must be contiguous")
+    B, Hq, _ = q.shape
+    if (block_tables.dtype != torch.int32 or block_tables.dim() != 2
+            or block_tables.shape[0] != B or not block_tables.is_contiguous()):
+        raise ValueError("block_tables must be a contiguous int32 [B, max_pages] tensor")
+    if (context_lens.dtype != torch.int32 or context_lens.shape != (B,)
+            or not context_lens.is_contiguous()):
+        raise ValueError("context_lens must be a contiguous int32 [B] tensor")
+    if out.shape != (B, Hq, D) or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [B, Hq, D] tensor of q's dtype")
+    if B == 0:
+        return out
+    scale = (1.0 / math.sqrt(D)) if scale is None else float(scale)
+    N.call("pia_paged_decode_attention_noalloc", out.data_ptr(), q.data_ptr(), q.stride(0),
+           k_pages.data_ptr(), v_pages.data_ptr(), block_tables.data_ptr(),
+           block_tables.shape[1], context_lens.data_ptr(), B, Hq, Hkv, D, P, num_pages, scale,
+           N.dtype_code(q.dtype), N.stream_of(dev))
+    return out
+
+
 def paged_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
                     block_tables: torch.Tensor, kv_lens: torch.Tensor,
                     cu_q: torch.Tensor | None = None, q_pos_offsets: torch.Tensor | None = None,
