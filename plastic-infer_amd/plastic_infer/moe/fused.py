@@ -70,30 +70,55 @@ def _check_ffn_args(hidden_states, w1, w2, topk_weights, topk_ids, activation):
                      names=("hidden_states", "w1", "w2", "topk_weights", "topk_ids"))
 
 
-def _routed_ffn(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
-                topk_weights: torch.Tensor, topk_ids: torch.Tensor, activation: str,
-                apply_router_weight_on_input: bool, out: torch.Tensor) -> torch.Tensor:
+def routed_ffn_routes(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+                      topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+                      route_out: torch.Tensor, activation: str = "silu",
+                      apply_router_weight_on_input: bool = False,
+                      act_buffer: torch.Tensor | None = None) -> torch.Tensor:
+    """The routed FFN of every route whose id is in [0, E), into route_out [T, k, H]: row
+    (t, s) = w2[id] . act(w1[id] . x_t) times the routing weight, rounded to the storage dtype
+    at the reference's points. Routes with id -1 are left untouched, so the routes of one
+    token can be computed in several calls (e.g. experts already in HBM first, copied ones
+    after their copies land) and summed once with moe_sum_reduce: the result is bit-identical
+    to one call over all routes. act_buffer [T * k, I] may be shared between such calls."""
     M, H = hidden_states.shape
     E, two_i, _ = w1.shape
     k = topk_ids.shape[1]
     numel = M * k
     if numel == 0:
-        return out
+        return route_out
+    if route_out.shape != (M, k, H) or not route_out.is_contiguous() \
+            or route_out.dtype != hidden_states.dtype:
+        raise ValueError(f"route_out must be a contiguous [{M}, {k}, {H}] tensor of the "
+                         "hidden dtype")
     ids = topk_ids if topk_ids.dtype == torch.int32 else topk_ids.to(torch.int32)
     weights = topk_weights.to(torch.float32).contiguous()
     sorted_ids, expert_ids, npp = _align(ids, EXPERT_BLOCK_M, E)
     dev = hidden_states.device
     ws = torch.empty(N.query("pia_moe_expert_gemm_workspace_bytes", sorted_ids.numel(),
                              EXPERT_BLOCK_M), dtype=torch.uint8, device=dev)
-    cache2 = torch.empty(numel, two_i // 2, dtype=hidden_states.dtype, device=dev)
+    if act_buffer is None:
+        act_buffer = torch.empty(numel, two_i // 2, dtype=hidden_states.dtype, device=dev)
     moe_expert_gemm(hidden_states, w1, weights, sorted_ids, expert_ids, npp, EXPERT_BLOCK_M,
                     numel, k, activation=activation,
-                    mul_routed_weight=apply_router_weight_on_input, out=cache2, workspace=ws)
-    cache3 = torch.empty(M, k, H, dtype=hidden_states.dtype, device=dev)
-    moe_expert_gemm(cache2, w2, weights, sorted_ids, expert_ids, npp, EXPERT_BLOCK_M, numel, 1,
-                    activation=None, mul_routed_weight=not apply_router_weight_on_input,
-                    out=cache3.view(numel, H), workspace=ws)
-    moe_sum_reduce(cache3, out)
+                    mul_routed_weight=apply_router_weight_on_input, out=act_buffer, workspace=ws)
+    moe_expert_gemm(act_buffer, w2, weights, sorted_ids, expert_ids, npp, EXPERT_BLOCK_M, numel,
+                    1, activation=None, mul_routed_weight=not apply_router_weight_on_input,
+                    out=route_out.view(numel, H), workspace=ws)
+    return route_out
+
+
+def _routed_ffn(hidden_states: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+                topk_weights: torch.Tensor, topk_ids: torch.Tensor, activation: str,
+                apply_router_weight_on_input: bool, out: torch.Tensor) -> torch.Tensor:
+    M, H = hidden_states.shape
+    k = topk_ids.shape[1]
+    if M * k == 0:
+        return out
+    route_out = torch.empty(M, k, H, dtype=hidden_states.dtype, device=hidden_states.device)
+    routed_ffn_routes(hidden_states, w1, w2, topk_weights, topk_ids, route_out, activation,
+                      apply_router_weight_on_input)
+    moe_sum_reduce(route_out, out)
     return out
 
 
@@ -135,4 +160,4 @@ class FusedMoe(BaseMoeBackend):
 
 
 __all__ = ["fused_topk", "moe_align_block_size", "fused_experts_impl",
-           "fused_experts_decode_impl", "FusedMoe", "EXPERT_BLOCK_M"]
+           "fused_experts_decode_impl", "routed_ffn_routes", "FusedMoe", "EXPERT_BLOCK_M"]

@@ -1,590 +1,739 @@
-"""Unified GPU slot cache of MoE expert weights streamed from pinned host banks
-(reference src/plastic_infer/moe/offload_cache.py: OffloadMoeCache).
+"""HBM slot cache of MoE expert weights over pinned host banks.
 
-Decode: ``ensure_experts`` runs the device LRU admission (HIP ``pia_lru_ensure``), rewriting
-the routed expert ids to slot ids and writing the copy plan; ``copy_missing`` moves the planned
-rows of every bank from the pinned host banks in one multi-bank index-copy launch (the kernel
-reads host memory through its device mapping). Neither synchronises with the host.
+Drop-in for the reference's OffloadMoeCache (src/plastic_infer/moe/offload_cache.py; decode
+admission :347-408 and copy_missing :973-1024, prefill double buffer :568-803) on this
+package's HIP kernels and the DMA engines. Every layer's experts live in pinned host banks
+(one [num_experts, ...] tensor per layer and bank: "gate_up" [E, 2I, H], "down" [E, H, I]);
+the cache holds `cache_size` expert rows per bank in HBM.
 
-Prefill overlap: two whole-layer buffers borrowed from the first 2E slots, filled on a side
-copy stream with the DMA engines (``copy_rows_async``) under ready / release events, so layer
-l+1's experts cross PCIe while layer l computes. With ``prefill_hit_d2d``, experts already
-resident above slot 2E are gathered device-side instead and only the misses cross PCIe.
+Residency policies
+------------------
+"lru"     One least-recently-used cache over all slots and every layer's experts: the
+          reference's policy. ensure_experts runs the HIP admission kernel, which rewrites the
+          routed ids to slot ids and leaves a device copy plan; copy_missing executes the plan
+          with one multi-bank index-copy launch whose CUs read the pinned banks through their
+          device mapping. No host synchronisation, so the chain can be graph-captured.
+"static"  `resident_per_layer` chosen experts of every layer stay in the first slots for
+          good (filled once by set_bank_sources); the remaining slots are a staging area under
+          a host LRU with the same victim rule as the device kernel. A decode layer's misses are
+          planned on the host (its routing is read back, 4 bytes per route) and copied by the
+          DMA engines (hipMemcpyAsync) on the cache's copy stream.
 
-Supported here: decode on the GPU (``decode_target="gpu"``) with every layer's banks pinned.
-The reference's CPU-executor modes ("cpu", "hybrid") and LOCKED / PAGEABLE host residency
-depend on its CPU expert executor, which is outside this build; they raise
-NotImplementedError.
+For overlap, stage_layer(layer, topk_ids) serves either policy: it returns the routes split
+into those whose expert is already in HBM and those being copied, plus the event that marks
+the copies done. The routed FFN runs the first group on the compute stream while the copies
+are in flight, waits on the event, then runs the second (exec.runner_moe_paged does this).
+Under "lru" the device plan of the admission kernel is read back and turned into DMA runs.
+
+Prefill
+-------
+Two whole-layer buffers (slots [b, b + 2E), b = 0 under "lru", the staging area's start under
+"static") filled on the copy stream under ready / release events, so layer l + 1's experts
+cross the host link while layer l computes. Experts already in HBM (prefill_hit_d2d under
+"lru"; the resident set under "static") are gathered device-side instead.
+
+Only bf16 / fp16 expert banks (the "bf16" schema) and decode on the GPU are built here.
 """
 
 from __future__ import annotations
 
 import math
-import os
 from dataclasses import dataclass
 
 import numpy as np
 import torch
 
-from ..kernel.index_copy import copy_rows_async
-from ..kernel.lru_ensure import N_STATS, Stat
+from .. import _native as N
+from ..kernel.index_copy import copy_rows_async, device_ptr, fast_index_copy_multi
+from ..kernel.lru_ensure import N_STATS, Stat, lru_ensure
 
-_FUSED_COPY = os.getenv("FREETOKEN_FUSED_COPY", "1").strip().lower() not in {"0", "false", "no", "off"}
-
-# Banks whose rows are smaller than this are prefetched as one whole-layer copy (and left out
-# of the prefill hit gather), as in the reference, so every per-run copy stays large.
-_SMALL_BANK_FEAT_BYTES = 256 * 1024
-
-# quant_format -> bank names in registration order (reference offload_cache.py:34-85); the
-# cache machinery is layout-agnostic and only moves rows.
-_BANK_SCHEMAS: dict[str, tuple[str, ...]] = {
-    "bf16": ("gate_up", "down"),
-    "fp8_block": ("gate_up", "gate_up_scale", "down", "down_scale"),
-    "q4_0": ("gate_up", "down"),
-    "nvfp4": ("gate_up_packed", "gate_up_scale", "gate_up_global",
-              "down_packed", "down_scale", "down_global"),
-    "nvfp4_marlin": ("gate_up_packed", "gate_up_scale", "down_packed", "down_scale"),
-    "nvfp4_b12x": ("gate_up_packed", "gate_up_scale", "down_packed", "down_scale"),
-    "mxfp4_triton": ("gate_up_blocks", "gate_up_scales", "gate_up_bias",
-                     "down_blocks", "down_scales", "down_bias"),
-    "ds_fp4": ("gate_up_packed", "gate_up_scale", "down_packed", "down_scale"),
-}
-
-MARLIN_MAX_CACHE_SIZE = 992
+BANK_NAMES = ("gate_up", "down")
 PINNED = "pinned"
+POLICIES = ("lru", "static")
+
+# Banks whose rows are smaller than this are copied as a whole layer during prefill (and
+# kept out of the device-side gather), so every DMA transfer stays large.
+_SMALL_ROW_BYTES = 256 * 1024
+
+
+# ---------------------------------------------------------------------------------------------
+# Device maps: what every HIP slot-cache kernel reads and writes
+# ---------------------------------------------------------------------------------------------
+
+class _DeviceSlotMaps:
+    """slot_of_id [L, E] (flat ids layer * E + expert), id_of_slot [S], usage [S] and the clock,
+    plus the copy plan of the last admission (dst slots, src rows, count) and per-layer stats."""
+
+    def __init__(self, num_layers: int, num_experts: int, num_slots: int, dev: torch.device):
+        self.L, self.E, self.S = num_layers, num_experts, num_slots
+        self.slot_of_id = torch.full((num_layers, num_experts), -1, dtype=torch.int32, device=dev)
+        self.id_of_slot = torch.full((num_slots,), -1, dtype=torch.int32, device=dev)
+        self.usage = torch.zeros(num_slots, dtype=torch.int64, device=dev)
+        self.clock = torch.zeros((), dtype=torch.int64, device=dev)
+        plan = max(num_experts, num_slots)
+        self.plan_dst = torch.zeros(plan, dtype=torch.int32, device=dev)
+        self.plan_src = torch.zeros(plan, dtype=torch.int32, device=dev)
+        self.plan_len = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.stats = torch.zeros((num_layers, N_STATS), dtype=torch.int64, device=dev)
+
+    def _stream(self) -> int:
+        return N.stream_of(self.slot_of_id.device)
+
+    def admit(self, layer: int, ids: torch.Tensor, with_stats: bool) -> None:
+        """LRU admission of `ids` (layer-local expert ids, int32, rewritten to slots in place)."""
+        lru_ensure(ids, self.slot_of_id.view(-1), self.id_of_slot, self.usage, self.clock, ids,
+                   self.plan_src, self.plan_dst, self.plan_len,
+                   stats=self.stats[layer] if with_stats else None, id_base=layer * self.E)
+
+    def materialize(self, layer: int) -> None:
+        """Slots [0, E) take the layer's experts in id order; the plan copies the whole layer."""
+        N.call("pia_slot_cache_materialize", self.slot_of_id.data_ptr(), self.L * self.E,
+               self.id_of_slot.data_ptr(), self.usage.data_ptr(), self.S, self.clock.data_ptr(),
+               self.plan_dst.data_ptr(), self.plan_src.data_ptr(), self.plan_len.data_ptr(),
+               int(layer), self.E, self._stream())
+
+    def reset(self) -> None:
+        N.call("pia_slot_cache_reset", self.slot_of_id.data_ptr(), self.L * self.E,
+               self.id_of_slot.data_ptr(), self.usage.data_ptr(), self.S, self.clock.data_ptr(),
+               None, 0, self.plan_len.data_ptr(), self._stream())
+
+    def invalidate(self, lo: int, hi: int) -> None:
+        """Slots [lo, hi) emptied: owners unmapped, usage 0 (first to be reused)."""
+        N.call("pia_slot_cache_invalidate", self.slot_of_id.data_ptr(), self.L * self.E,
+               self.id_of_slot.data_ptr(), self.usage.data_ptr(), self.S, int(lo), int(hi),
+               self._stream())
+
+
+# ---------------------------------------------------------------------------------------------
+# Banks: pinned host sources, HBM slot tensors, copy descriptors
+# ---------------------------------------------------------------------------------------------
+
+class _BankSet:
+    """One HBM tensor [num_slots, ...] per bank over per-layer pinned host banks [E, ...].
+
+    Rows move three ways: by the multi-bank index-copy kernel from a device plan (the CUs read
+    pinned memory through its device mapping), by DMA runs (hipMemcpyAsync) from a host plan,
+    or slot to slot inside HBM (prefill gathers). The multi-bank descriptor needs 16-byte rows
+    and bases; without it the kernel copies bank by bank."""
+
+    def __init__(self, sources: dict[str, list[torch.Tensor]], num_layers: int,
+                 num_experts: int, num_slots: int, dev: torch.device, multi_bank: bool):
+        self.names = tuple(n for n in BANK_NAMES if n in sources)
+        if set(self.names) != set(sources):
+            raise ValueError(f"expert banks must be {BANK_NAMES}, got {sorted(sources)}")
+        self.sources: dict[str, list[torch.Tensor]] = {}
+        self.caches: dict[str, torch.Tensor] = {}
+        for name in self.names:
+            per_layer = list(sources[name])
+            if len(per_layer) != num_layers:
+                raise ValueError(f"bank {name!r}: {len(per_layer)} layers, expected {num_layers}")
+            head = per_layer[0]
+            for l, t in enumerate(per_layer):
+                if t.device.type != "cpu" or not t.is_pinned():
+                    raise ValueError(f"bank {name!r} layer {l} must be pinned host memory")
+                if not t.is_contiguous() or t.shape != head.shape or t.dtype != head.dtype:
+                    raise ValueError(f"bank {name!r} layer {l}: every layer must be a contiguous "
+                                     f"{tuple(head.shape)} {head.dtype} tensor")
+                if t.shape[0] != num_experts:
+                    raise ValueError(f"bank {name!r} layer {l} has {t.shape[0]} experts, "
+                                     f"expected {num_experts}")
+            if head.dtype not in (torch.bfloat16, torch.float16):
+                raise NotImplementedError("expert banks are built for bf16 / fp16 storage")
+            self.sources[name] = per_layer
+            self.caches[name] = torch.empty((num_slots, *head.shape[1:]), dtype=head.dtype,
+                                            device=dev)
+        self.row_bytes = [math.prod(self.caches[n].shape[1:]) * self.caches[n].element_size()
+                          for n in self.names]
+        self.multi_ok = False
+        if multi_bank and all(b % 16 == 0 for b in self.row_bytes):
+            dst = [self.caches[n].data_ptr() for n in self.names]
+            src = [[device_ptr(self.sources[n][l]) for n in self.names] for l in range(num_layers)]
+            if all(p % 16 == 0 for p in dst) and all(p % 16 == 0 for row in src for p in row):
+                self.dst_table = torch.tensor(dst, dtype=torch.int64, device=dev)
+                self.src_tables = [torch.tensor(r, dtype=torch.int64, device=dev) for r in src]
+                self.row_table = torch.tensor(self.row_bytes, dtype=torch.int64, device=dev)
+                big = [i for i, b in enumerate(self.row_bytes) if b >= _SMALL_ROW_BYTES]
+                self.big_banks = big
+                self.gather_dst = self.dst_table[big].contiguous() if big else None
+                self.gather_rows = self.row_table[big].contiguous() if big else None
+                self.multi_ok = True
+
+    def views(self, n: int | None = None) -> tuple[torch.Tensor, ...]:
+        return tuple(self.caches[name] if n is None else self.caches[name][:n]
+                     for name in self.names)
+
+    def copy_planned(self, layer: int, dst: torch.Tensor, src: torch.Tensor,
+                     count: torch.Tensor) -> None:
+        """Rows src[i] of the layer's host banks -> slots dst[i], i < count (device plan)."""
+        if self.multi_ok:
+            fast_index_copy_multi(self.dst_table, self.src_tables[layer], self.row_table, dst, src,
+                                  count)
+            return
+        from ..kernel.index_copy import fast_index_copy
+
+        for name in self.names:
+            fast_index_copy(self.caches[name], dst, self.sources[name][layer], src, count)
+
+    def copy_dma(self, layer: int, slots: np.ndarray, rows: np.ndarray,
+                 stream: torch.cuda.Stream, only_large: bool = False) -> int:
+        """hipMemcpyAsync of host rows -> slots for every bank on `stream`; returns bytes."""
+        moved = 0
+        for i, name in enumerate(self.names):
+            if only_large and self.row_bytes[i] < _SMALL_ROW_BYTES:
+                continue
+            copy_rows_async(self.caches[name], slots, self.sources[name][layer], rows,
+                            stream=stream)
+            moved += self.row_bytes[i] * len(rows)
+        return moved
+
+    def expert_bytes(self) -> int:
+        return sum(self.row_bytes)
+
+
+# ---------------------------------------------------------------------------------------------
+# Host LRU of the staging slots ("static" policy)
+# ---------------------------------------------------------------------------------------------
+
+class _StagingLru:
+    """Least-recently-used map of flat expert ids onto `n` staging slots, decided on the host.
+
+    Same rule as the device admission kernel: each call advances a clock; ids already staged
+    are hits and take the current clock; the distinct missing ids, in ascending order, take the
+    untouched slots in ascending (last use, slot) order."""
+
+    def __init__(self, n: int):
+        self.n = n
+        self.owner = np.full(n, -1, np.int64)
+        self.last_use = np.zeros(n, np.int64)
+        self.slot_of: dict[int, int] = {}
+        self.clock = 0
+
+    def place(self, flat_ids: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+        """flat_ids: distinct ids. Returns (slot of each id, ids copied in, their slots)."""
+        self.clock += 1
+        slots = np.full(flat_ids.size, -1, np.int64)
+        miss = []
+        for i, f in enumerate(flat_ids.tolist()):
+            s = self.slot_of.get(f)
+            if s is None:
+                miss.append(i)
+            else:
+                slots[i] = s
+                self.last_use[s] = self.clock
+        if not miss:
+            return slots, np.empty(0, np.int64), np.empty(0, np.int64)
+        if len(miss) > self.n - (flat_ids.size - len(miss)):
+            raise RuntimeError(f"{len(miss)} experts to stage but only "
+                               f"{self.n - (flat_ids.size - len(miss))} free staging slots")
+        key = np.where(self.last_use == self.clock, np.iinfo(np.int64).max, self.last_use)
+        victims = np.lexsort((np.arange(self.n), key))[:len(miss)]
+        order = np.argsort(flat_ids[miss], kind="stable")
+        new_ids = flat_ids[miss][order]
+        for f, s in zip(new_ids.tolist(), victims.tolist()):
+            old = int(self.owner[s])
+            if old >= 0:
+                del self.slot_of[old]
+            self.owner[s] = f
+            self.slot_of[f] = s
+            self.last_use[s] = self.clock
+        slots[np.asarray(miss)[order]] = victims
+        return slots, new_ids, victims.astype(np.int64)
+
+    def forget_range(self, lo: int, hi: int) -> None:
+        """Staging slots [lo, hi) emptied (borrowed by the prefill buffers)."""
+        for s in range(lo, hi):
+            old = int(self.owner[s])
+            if old >= 0:
+                del self.slot_of[old]
+            self.owner[s] = -1
+            self.last_use[s] = 0
+
+    def reset(self) -> None:
+        self.__init__(self.n)
 
 
 @dataclass
-class OffloadMoeCache:
-    num_layers: int
-    num_experts: int
-    cache_size: int
-    device: torch.device
-    cache_policy: str = "lru"
-    prefill_overlap: bool = False
-    prefill_hit_d2d: bool = False
-    quant_format: str = "bf16"
-    decode_target: str = "gpu"
-    hybrid_max_fetch: int = 1
-    hybrid_fetch_fraction: float = 0.0
+class StagedRoutes:
+    """A decode layer's routes split for an overlapped FFN (ids are slots; -1 = not in group).
 
-    def __post_init__(self) -> None:
-        policy_ids = {"lru": 0}
-        assert self.cache_policy in policy_ids
-        assert self.decode_target in ("gpu", "cpu", "hybrid"), self.decode_target
-        assert self.quant_format in _BANK_SCHEMAS, f"unknown quant_format {self.quant_format!r}"
-        if self.decode_target != "gpu":
-            raise NotImplementedError(
-                f"decode_target={self.decode_target!r} needs the CPU expert executor, which "
-                "is not part of this build")
-        self.device = torch.device(self.device)
+    in_hbm:  routes whose expert was in HBM before this call (resident, or an LRU hit);
+    copied:  routes whose expert is being copied; run them after the compute stream waits on
+             `ready` (recorded on the copy stream after the copies)."""
+    layer: int
+    in_hbm: torch.Tensor
+    copied: torch.Tensor
+    ready: torch.cuda.Event
+    experts: int          # distinct experts routed to
+    copied_experts: int   # distinct experts copied by this call
+    copied_bytes: int
+    issued: torch.cuda.Event | None = None   # copy stream, before the copies (timing only)
+
+
+# ---------------------------------------------------------------------------------------------
+# Prefill double buffer
+# ---------------------------------------------------------------------------------------------
+
+class _PrefillBuffers:
+    """Two whole-layer buffers [E, ...] per bank at slots [base, base + 2E) of the caches."""
+
+    def __init__(self, banks: _BankSet, num_experts: int, base: int, dev: torch.device):
+        E = num_experts
+        self.base = base
+        self.views = [banks.caches[n][base:base + 2 * E].view(2, E, *banks.caches[n].shape[1:])
+                      for n in banks.names]
+        self.stream = torch.cuda.Stream(device=dev)
+        self.ready = [torch.cuda.Event() for _ in range(2)]
+        self.released = [torch.cuda.Event() for _ in range(2)]
+        self.begin = torch.cuda.Event()
+        self.layer: list[int | None] = [None, None]
+        self.free = [True, True]
+        self.ever_released = [False, False]
+
+
+# ---------------------------------------------------------------------------------------------
+# The cache
+# ---------------------------------------------------------------------------------------------
+
+class OffloadMoeCache:
+    """Expert slot cache in HBM (see the module docstring for the policies)."""
+
+    def __init__(self, num_layers: int, num_experts: int, cache_size: int,
+                 device: torch.device | str, cache_policy: str = "lru",
+                 prefill_overlap: bool = False, prefill_hit_d2d: bool = False,
+                 quant_format: str = "bf16", decode_target: str = "gpu",
+                 resident_per_layer: int | None = None, multi_bank_copy: bool = True) -> None:
+        if cache_policy not in POLICIES:
+            raise ValueError(f"cache_policy must be one of {POLICIES}, got {cache_policy!r}")
+        if quant_format != "bf16":
+            raise NotImplementedError(f"quant_format {quant_format!r}: only bf16 / fp16 expert "
+                                      "banks are built")
+        if decode_target != "gpu":
+            raise NotImplementedError(f"decode_target {decode_target!r} needs a CPU expert "
+                                      "executor, which is not part of this build")
+        self.device = torch.device(device)
         if self.device.type != "cuda":
             raise ValueError("OffloadMoeCache lives on the HIP device")
-        self.cpu_executor = None
-        self.cpu_layer_ids: frozenset = frozenset()
-        self.validate_rebuild(self.cache_size)
-        assert not self.prefill_overlap or self.cache_size >= 2 * self.num_experts, (
-            "Prefill overlap borrows two full expert-layer buffers from the unified MoE "
-            "cache, so cache_size must be at least 2 * num_experts")
-        self.cache_policy_id = policy_ids[self.cache_policy]
-        dev = self.device
-        self.slot_for_id = torch.full((self.num_layers, self.num_experts), -1, dtype=torch.int32,
-                                      device=dev)
-        self.id_of_slot = torch.full((self.cache_size,), -1, dtype=torch.int32, device=dev)
-        self.usage = torch.zeros((self.cache_size,), dtype=torch.int64, device=dev)
-        self.step = torch.zeros((), dtype=torch.int64, device=dev)
-        self.active_mask = torch.zeros((self.num_experts,), dtype=torch.int32, device=dev)
-        plan_slots = max(self.num_experts, self.cache_size)
-        self.evict_slots = torch.empty((plan_slots,), dtype=torch.int32, device=dev)
-        self.src_indices = torch.empty((plan_slots,), dtype=torch.int32, device=dev)
-        self.num_indices = torch.zeros((1,), dtype=torch.int64, device=dev)
-        self.num_missing_full = torch.zeros((1,), dtype=torch.int64, device=dev)
-        self.expert_recency = torch.full((self.num_layers, self.num_experts), -1,
-                                         dtype=torch.int64, device=dev)
-        self.bank_schema = _BANK_SCHEMAS[self.quant_format]
-        self.bank_sources: dict[str, list[torch.Tensor]] = {}
-        self.bank_caches: dict[str, torch.Tensor] = {}
-        self.layer_residency: list[str] = []
-        self._unpinned_layers: frozenset = frozenset()
-        self.gate_up_alpha: torch.Tensor | None = None
-        self.down_alpha: torch.Tensor | None = None
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.num_layers, self.num_experts = int(num_layers), int(num_experts)
+        self.cache_size = int(cache_size)
+        self.cache_policy = cache_policy
+        self.prefill_overlap = bool(prefill_overlap)
+        self.prefill_hit_d2d = bool(prefill_hit_d2d)
+        self.multi_bank_copy = bool(multi_bank_copy)
+        self.quant_format = quant_format
+        self.decode_target = decode_target
+        L, E, S = self.num_layers, self.num_experts, self.cache_size
+        if S < E:
+            raise ValueError(f"cache_size {S} < num_experts {E}")
+
+        if cache_policy == "static":
+            R = E // 2 if resident_per_layer is None else int(resident_per_layer)
+            if not 0 <= R <= E:
+                raise ValueError(f"resident_per_layer must be in [0, {E}]")
+            self.resident_per_layer = R
+            self.staging_base = L * R
+            staging = S - L * R
+            need = max(E - R, 2 * E if self.prefill_overlap else 0)
+            if staging < need:
+                raise ValueError(f"cache_size {S}: {L} x {R} resident slots leave {staging} "
+                                 f"staging slots, {need} needed")
+            self._staging = _StagingLru(staging)
+        else:
+            if self.prefill_overlap and S < 2 * E:
+                raise ValueError("prefill overlap borrows two whole-layer buffers from the cache: "
+                                 "cache_size must be at least 2 * num_experts")
+            self.resident_per_layer = 0
+            self.staging_base = 0
+            self._staging = None
+        self._maps = _DeviceSlotMaps(L, E, S, self.device)
+        self._banks: _BankSet | None = None
+        self._prefill: _PrefillBuffers | None = None
+        self._resident_slot = np.full((L, E), -1, np.int64)   # "static": fixed slot or -1
+        self._pending_layer: int | None = None
+        self._copy_stream = torch.cuda.Stream(device=self.device)
+        self._host_ids = torch.empty(0, dtype=torch.int32, pin_memory=True)
+        self._host_plan = torch.empty(3 * max(E, S) + 2, dtype=torch.int64, pin_memory=True)
         self.collect_stats = False
-        self.lru_stats = torch.zeros((self.num_layers, N_STATS), dtype=torch.int64, device=dev)
-        self.stat_missing = torch.zeros((), dtype=torch.int64, device=dev)
-        self.stat_active = torch.zeros((), dtype=torch.int64, device=dev)
-        self.stat_calls = torch.zeros((), dtype=torch.int64, device=dev)
-        self.stat_fetched = torch.zeros((), dtype=torch.int64, device=dev)
-        self.stat_missing_layer = torch.zeros(self.num_layers, dtype=torch.int64, device=dev)
-        self.stat_active_layer = torch.zeros(self.num_layers, dtype=torch.int64, device=dev)
-        self.stat_fetched_layer = torch.zeros(self.num_layers, dtype=torch.int64, device=dev)
-        self.stat_steps_layer = torch.zeros(self.num_layers, dtype=torch.int64, device=dev)
-        self.collect_decode_freq = False
-        self.decode_freq = torch.zeros((self.num_layers, self.num_experts), dtype=torch.int64,
-                                       device=dev)
-        self.banks: list[tuple[list[torch.Tensor], torch.Tensor]] = []
-        self._copy_fused_ok = False
-        self._copy_dst_ptrs: torch.Tensor | None = None
-        self._copy_src_ptrs: list[torch.Tensor] | None = None
-        self._copy_feat_bytes: torch.Tensor | None = None
-        self._copy_dst_ptrs_host: list[int] = []
-        self._copy_src_ptrs_host: list[list[int]] = []
-        self._copy_feat_bytes_host: list[int] = []
-        self._gather_bank_ids: list[int] = []
-        self._gather_dst_ptrs: torch.Tensor | None = None
-        self._gather_feat_bytes: torch.Tensor | None = None
-        self._pending_src_layer: int | None = None
-        self._pending_whole_layer = False
-        self.prefill_bank_buffers: list[torch.Tensor] = []
-        self.prefill_copy_stream: torch.cuda.Stream | None = None
-        self.prefill_begin_event: torch.cuda.Event | None = None
-        self.prefill_ready_events: list[torch.cuda.Event] = []
-        self.prefill_release_events: list[torch.cuda.Event] = []
-        self._prefill_buffer_layer: list[int | None] = [None, None]
-        self._prefill_buffer_released: list[bool] = [True, True]
-        self._prefill_buffer_has_release_event: list[bool] = [False, False]
-        self._prefill_slot_snapshot: torch.Tensor | None = None
-        self._prefill_snapshot_np = None
-        self._prefill_hit_d2d_active = False
-        self._hit_d2d_fallback_logged = False
+        self.record_copy_start = False      # StagedRoutes.issued (overlap measurement)
+        self._host_stats = np.zeros((L, N_STATS), np.int64)   # "static" and staged calls
+        self.copied_bytes = 0
         self.prefill_hit_rows = 0
         self.prefill_total_rows = 0
 
-    # ---- banks -------------------------------------------------------------------------------
+    # ---- state views (the reference's attribute names) ----------------------------------------
 
-    def set_bank_sources(self, sources: dict[str, list[torch.Tensor]],
-                         layer_residency: list[str] | None = None) -> None:
-        """Attach the pinned host banks (one ``[num_experts, ...]`` tensor per layer and bank,
-        in the format's schema) and allocate one GPU slot cache ``[cache_size, ...]`` per bank."""
-        assert set(sources) == set(self.bank_schema), (
-            f"banks {sorted(sources)} do not match the {self.quant_format!r} schema "
-            f"{self.bank_schema}")
-        residency = [str(getattr(r, "value", r)) for r in
-                     (layer_residency or [PINNED] * self.num_layers)]
-        assert len(residency) == self.num_layers, (len(residency), self.num_layers)
-        if any(r != PINNED for r in residency):
-            raise NotImplementedError(
-                "LOCKED / PAGEABLE host banks decode on the CPU executor, which is not part of "
-                "this build; every layer must be pinned")
-        self._unpinned_layers = frozenset()
-        self.layer_residency = residency
-        for name in self.bank_schema:
-            per_layer = sources[name]
-            assert len(per_layer) == self.num_layers, (name, len(per_layer))
-            head = per_layer[0]
-            for layer_id, source in enumerate(per_layer):
-                assert source.is_contiguous(), f"bank {name!r} layer {layer_id} must be contiguous"
-                assert source.size(0) == self.num_experts, (name, layer_id, source.shape)
-                assert source.shape == head.shape and source.dtype == head.dtype, (
-                    name, layer_id, source.shape, source.dtype)
-                if source.device.type != "cpu" or not source.is_pinned():
-                    raise ValueError(f"bank {name!r} layer {layer_id} must be pinned host memory")
-            self.bank_sources[name] = list(per_layer)
-            self.bank_caches[name] = torch.empty((self.cache_size, *head.shape[1:]),
-                                                 dtype=head.dtype, device=self.device)
-        self.banks = [(self.bank_sources[n], self.bank_caches[n]) for n in self.bank_schema]
-        self._build_copy_plan()
-        if self.prefill_overlap:
-            self._init_prefill_overlap_buffers()
+    @property
+    def slot_for_id(self) -> torch.Tensor:
+        return self._maps.slot_of_id
 
-    def _build_copy_plan(self) -> None:
-        """Fused multi-bank copy descriptor: per-bank slot-cache base, per-layer host-bank
-        device aliases and row bytes, as device int64 tensors (fixed for the cache's
-        lifetime). Left disabled when a row size or base is not 16-byte aligned, or with
-        FREETOKEN_FUSED_COPY=0; copy_missing then copies bank by bank."""
-        self._copy_fused_ok = False
-        self._copy_dst_ptrs = None
-        self._copy_src_ptrs = None
-        self._copy_feat_bytes = None
-        self._copy_dst_ptrs_host = []
-        self._copy_src_ptrs_host = []
-        self._copy_feat_bytes_host = []
-        self._gather_bank_ids = []
-        self._gather_dst_ptrs = None
-        self._gather_feat_bytes = None
-        if not _FUSED_COPY or not self.banks:
-            return
-        from ..kernel.pinned import device_ptr
+    @property
+    def id_of_slot(self) -> torch.Tensor:
+        return self._maps.id_of_slot
 
-        dst_ptrs, feats = [], []
-        layer_src_ptrs: list[list[int]] = [[] for _ in range(self.num_layers)]
-        for per_layer, cache in self.banks:
-            feat = math.prod(per_layer[0].shape[1:]) * per_layer[0].element_size()
-            if feat % 16 != 0 or cache.data_ptr() % 16 != 0:
-                return
-            for layer_id, source in enumerate(per_layer):
-                src_dev = device_ptr(source)
-                if src_dev % 16 != 0:
-                    return
-                layer_src_ptrs[layer_id].append(src_dev)
-            dst_ptrs.append(cache.data_ptr())
-            feats.append(feat)
-        dev = self.device
-        self._copy_dst_ptrs = torch.tensor(dst_ptrs, dtype=torch.int64, device=dev)
-        self._copy_src_ptrs = [torch.tensor(p, dtype=torch.int64, device=dev)
-                               for p in layer_src_ptrs]
-        self._copy_feat_bytes = torch.tensor(feats, dtype=torch.int64, device=dev)
-        self._copy_dst_ptrs_host = dst_ptrs
-        self._copy_src_ptrs_host = layer_src_ptrs
-        self._copy_feat_bytes_host = feats
-        self._gather_bank_ids = [i for i, f in enumerate(feats) if f >= _SMALL_BANK_FEAT_BYTES]
-        if len(self._gather_bank_ids) == len(feats):
-            self._gather_dst_ptrs = self._copy_dst_ptrs
-            self._gather_feat_bytes = self._copy_feat_bytes
-        elif self._gather_bank_ids:
-            self._gather_dst_ptrs = self._copy_dst_ptrs[self._gather_bank_ids].contiguous()
-            self._gather_feat_bytes = self._copy_feat_bytes[self._gather_bank_ids].contiguous()
-        self._copy_fused_ok = True
+    @property
+    def step(self) -> torch.Tensor:
+        return self._maps.clock
 
-    def validate_rebuild(self, cache_size: int) -> None:
-        if cache_size < self.num_experts:
-            raise ValueError(f"cache_size {cache_size} < num_experts {self.num_experts}")
-        if self.quant_format == "nvfp4_marlin" and cache_size > MARLIN_MAX_CACHE_SIZE:
-            raise ValueError(f"moe_cache_size={cache_size} exceeds the marlin slot limit of "
-                             f"{MARLIN_MAX_CACHE_SIZE}")
+    @property
+    def lru_stats(self) -> torch.Tensor:
+        """[L, 3] int64: distinct experts routed, experts copied in, calls (cumulative)."""
+        if self.cache_policy == "static":
+            return torch.from_numpy(self._host_stats.copy())
+        return self._maps.stats + torch.from_numpy(self._host_stats).to(self.device)
 
-    def rebuild(self, cache_size: int) -> None:
-        """Resize the slot cache in place (cold start); the host banks are kept."""
-        assert self.bank_sources, "set_bank_sources must run before rebuild"
-        self.validate_rebuild(cache_size)
-        self.prefill_bank_buffers = []
-        self.prefill_copy_stream = None
-        self.prefill_begin_event = None
-        self.prefill_ready_events = []
-        self.prefill_release_events = []
-        self._prefill_buffer_layer = [None, None]
-        self._prefill_buffer_released = [True, True]
-        self._prefill_buffer_has_release_event = [False, False]
-        self.banks = []
-        self.bank_caches = {}
-        self.cache_size = cache_size
-        torch.cuda.synchronize(self.device)
-        torch.cuda.empty_cache()
-        for name in self.bank_schema:
-            head = self.bank_sources[name][0]
-            self.bank_caches[name] = torch.empty((cache_size, *head.shape[1:]), dtype=head.dtype,
-                                                 device=self.device)
-        self.banks = [(self.bank_sources[n], self.bank_caches[n]) for n in self.bank_schema]
-        self._build_copy_plan()
-        dev = self.device
-        self.slot_for_id.fill_(-1)
-        self.id_of_slot = torch.full((cache_size,), -1, dtype=torch.int32, device=dev)
-        self.usage = torch.zeros((cache_size,), dtype=torch.int64, device=dev)
-        plan_slots = max(self.num_experts, cache_size)
-        self.evict_slots = torch.empty((plan_slots,), dtype=torch.int32, device=dev)
-        self.src_indices = torch.empty((plan_slots,), dtype=torch.int32, device=dev)
-        self.step.zero_()
-        self.active_mask.zero_()
-        self.num_indices.zero_()
-        self.num_missing_full.zero_()
-        self.expert_recency.fill_(-1)
-        self.lru_stats.zero_()
-        for t in (self.stat_missing, self.stat_active, self.stat_calls, self.stat_fetched,
-                  self.stat_missing_layer, self.stat_active_layer, self.stat_fetched_layer,
-                  self.stat_steps_layer, self.decode_freq):
-            t.zero_()
-        self.prefill_hit_rows = 0
-        self.prefill_total_rows = 0
-        self._hit_d2d_fallback_logged = False
-        if self.prefill_overlap and cache_size < 2 * self.num_experts:
-            self.prefill_overlap = False
-        if self.prefill_overlap:
-            self._init_prefill_overlap_buffers()
+    @property
+    def bank_caches(self) -> dict[str, torch.Tensor]:
+        assert self._banks is not None, "set_bank_sources first"
+        return self._banks.caches
 
-    def set_alphas(self, gate_up_alpha: torch.Tensor | None,
-                   down_alpha: torch.Tensor | None) -> None:
-        """Per-expert global scales ``[L*E]`` kept on the GPU, looked up per slot."""
-        if gate_up_alpha is None and down_alpha is None:
-            return
-        assert gate_up_alpha is not None and down_alpha is not None
-        total = self.num_layers * self.num_experts
-        assert gate_up_alpha.shape == down_alpha.shape == (total,)
-        self.gate_up_alpha = gate_up_alpha.to(self.device)
-        self.down_alpha = down_alpha.to(self.device)
-
-    def set_cpu_executor(self, executor) -> None:
-        raise NotImplementedError("the CPU expert executor is not part of this build")
-
-    def is_cpu_layer(self, layer_id: int) -> bool:
-        return layer_id in self.cpu_layer_ids
-
-    def is_unpinned_layer(self, layer_id: int) -> bool:
-        return layer_id in self._unpinned_layers
-
-    def alphas_for_slots(self, layer_id: int):
-        if self.gate_up_alpha is None:
-            return None
-        idx = layer_id * self.num_experts + (self.id_of_slot.clamp(min=0).long() % self.num_experts)
-        return self.gate_up_alpha[idx], self.down_alpha[idx]
-
-    def alphas_for_layer(self, layer_id: int):
-        if self.gate_up_alpha is None:
-            return None
-        lo = layer_id * self.num_experts
-        return self.gate_up_alpha[lo:lo + self.num_experts], self.down_alpha[lo:lo + self.num_experts]
+    @property
+    def copy_stream(self) -> torch.cuda.Stream:
+        return self._copy_stream
 
     def bank_views(self, n: int | None = None) -> tuple[torch.Tensor, ...]:
-        """Per-bank slot caches (decode) or their first ``n`` slots (a materialized layer)."""
-        assert self.banks, "set_bank_sources must register the banks first"
-        if n is None:
-            return tuple(cache for _, cache in self.banks)
-        return tuple(cache[:n] for _, cache in self.banks)
+        """The slot caches (decode ids are slots), or their first n slots."""
+        assert self._banks is not None, "set_bank_sources first"
+        return self._banks.views(n)
 
-    # ---- prefill double buffer ---------------------------------------------------------------
+    def resident_experts(self, layer: int) -> np.ndarray:
+        """Experts of `layer` that stay in HBM ("static"; empty under "lru")."""
+        return np.nonzero(self._resident_slot[layer] >= 0)[0]
 
-    def _init_prefill_overlap_buffers(self) -> None:
-        assert self.banks, "set_bank_sources must register the banks first"
-        E = self.num_experts
-        self._prefill_buffer_layer = [None, None]
-        self._prefill_buffer_released = [True, True]
-        self._prefill_buffer_has_release_event = [False, False]
-        self.prefill_bank_buffers = [cache[:2 * E].view(2, E, *cache.shape[1:])
-                                     for _, cache in self.banks]
-        self.prefill_copy_stream = torch.cuda.Stream(device=self.device)
-        self.prefill_ready_events = [torch.cuda.Event() for _ in range(2)]
-        self.prefill_release_events = [torch.cuda.Event() for _ in range(2)]
-        self.prefill_begin_event = torch.cuda.Event()
-        if self.prefill_hit_d2d:
-            self._prefill_slot_snapshot = torch.empty((self.num_layers, E), dtype=torch.int32,
-                                                      pin_memory=True)
-            self._prefill_snapshot_np = self._prefill_slot_snapshot.numpy()
-            self._prefill_hit_dst = torch.empty((E,), dtype=torch.int32, device=self.device)
-            self._prefill_hit_src = torch.empty((E,), dtype=torch.int32, device=self.device)
-            self._prefill_hit_num = torch.zeros((1,), dtype=torch.int64, device=self.device)
+    # ---- banks ---------------------------------------------------------------------------------
 
-    def _invalidate_prefill_buffer(self, buffer_id: int) -> None:
-        """The buffer's slots are about to be overwritten: their owners become non-resident
-        and the slots the oldest (reference :597-605)."""
-        from .offload_kernels import invalidate_slots
+    def set_bank_sources(self, sources: dict[str, list[torch.Tensor]],
+                         layer_residency: list[str] | None = None,
+                         resident_experts: list[list[int]] | None = None) -> None:
+        """Attach the pinned per-layer host banks and allocate the HBM slot caches.
 
-        invalidate_slots(self, buffer_id * self.num_experts, (buffer_id + 1) * self.num_experts)
+        "static": resident_experts[l] lists the experts of layer l to keep in HBM (default the
+        first resident_per_layer ids); they are copied in now, on the copy stream, and the
+        call returns when they have landed."""
+        if layer_residency is not None and any(str(getattr(r, "value", r)) != PINNED
+                                               for r in layer_residency):
+            raise NotImplementedError("every layer's banks must be pinned (LOCKED / PAGEABLE "
+                                      "layers decode on a CPU executor, not part of this build)")
+        self._banks = _BankSet(sources, self.num_layers, self.num_experts, self.cache_size,
+                               self.device, self.multi_bank_copy)
+        if self.cache_policy == "static":
+            self._place_resident(resident_experts)
+        if self.prefill_overlap:
+            self._prefill = _PrefillBuffers(self._banks, self.num_experts, self.staging_base,
+                                            self.device)
 
-    def begin_prefill(self) -> None:
-        if not self.prefill_overlap:
-            return
-        self._prefill_buffer_layer = [None, None]
-        self._prefill_buffer_released = [True, True]
-        # fence this prefill's copies behind everything already queued on the compute stream
-        # (a decode still running may read slots the buffers borrow)
-        self.prefill_begin_event.record(torch.cuda.current_stream(self.device))
-        self.prefill_copy_stream.wait_event(self.prefill_begin_event)
-        self._prefill_hit_d2d_active = self.prefill_hit_d2d and self._hit_d2d_usable()
-        if self._prefill_hit_d2d_active:
-            with torch.cuda.stream(self.prefill_copy_stream):
-                self._prefill_slot_snapshot.copy_(self.slot_for_id, non_blocking=True)
-            self.prefill_copy_stream.synchronize()
+    def _place_resident(self, resident_experts) -> None:
+        L, E, R = self.num_layers, self.num_experts, self.resident_per_layer
+        self._resident_slot.fill(-1)
+        for l in range(L):
+            chosen = np.arange(R) if resident_experts is None else \
+                np.unique(np.asarray(resident_experts[l], np.int64))
+            if chosen.size != R or (chosen.size and (chosen.min() < 0 or chosen.max() >= E)):
+                raise ValueError(f"layer {l}: resident_experts must list {R} distinct ids < {E}")
+            self._resident_slot[l, chosen] = l * R + np.arange(R)
+        # device maps mirror the resident set (slot_for_id is the public residency view)
+        flat = torch.from_numpy(self._resident_slot.astype(np.int32)).to(self.device)
+        self._maps.slot_of_id.copy_(flat)
+        owners = np.full(self.cache_size, -1, np.int32)
+        ls, es = np.nonzero(self._resident_slot >= 0)
+        owners[self._resident_slot[ls, es]] = (ls * E + es).astype(np.int32)
+        self._maps.id_of_slot.copy_(torch.from_numpy(owners).to(self.device))
+        with torch.cuda.stream(self._copy_stream):
+            self._copy_stream.wait_stream(torch.cuda.current_stream(self.device))
+            for l in range(L):
+                rows = np.nonzero(self._resident_slot[l] >= 0)[0]
+                if rows.size:
+                    self._banks.copy_dma(l, self._resident_slot[l, rows], rows,
+                                         self._copy_stream)
+        self._copy_stream.synchronize()
 
-    def _copy_whole_layer(self, layer_id: int, buffer_id: int) -> None:
-        E = self.num_experts
-        rows = np.arange(E, dtype=np.int64)
-        for (per_layer, _), buffer in zip(self.banks, self.prefill_bank_buffers):
-            copy_rows_async(buffer[buffer_id], rows, per_layer[layer_id], rows,
-                            stream=torch.cuda.current_stream(self.device))
-
-    def prefetch_prefill_layer(self, layer_id: int) -> None:
-        if not self.prefill_overlap or layer_id >= self.num_layers:
-            return
-        if layer_id < 0:
-            raise ValueError(f"Invalid prefill layer id: {layer_id}")
-        assert self.banks and self.prefill_bank_buffers
-        buffer_id = layer_id % 2
-        if self._prefill_buffer_layer[buffer_id] == layer_id:
-            return
-        if self._prefill_buffer_layer[buffer_id] is not None:
-            assert self._prefill_buffer_released[buffer_id], (
-                "Prefill overlap buffer is being reused before release")
-        if self._prefill_hit_d2d_active:
-            self._prefetch_split(layer_id, buffer_id)
-        else:
-            with torch.cuda.stream(self.prefill_copy_stream):
-                if self._prefill_buffer_has_release_event[buffer_id]:
-                    self.prefill_copy_stream.wait_event(self.prefill_release_events[buffer_id])
-                self._invalidate_prefill_buffer(buffer_id)
-                self._copy_whole_layer(layer_id, buffer_id)
-                self.prefill_ready_events[buffer_id].record(self.prefill_copy_stream)
-        self._prefill_buffer_layer[buffer_id] = layer_id
-        self._prefill_buffer_released[buffer_id] = False
-
-    def _hit_d2d_usable(self) -> bool:
-        from ..kernel.fast_index_copy import _skip_fast_index_copy_enabled
-
-        if self._prefill_slot_snapshot is None or self.prefill_copy_stream is None:
-            return False
-        if _skip_fast_index_copy_enabled() or not self._copy_fused_ok:
-            return False
-        return self.cache_size > 2 * self.num_experts
-
-    def _prefetch_split(self, layer_id: int, buffer_id: int) -> None:
-        """Resident experts (slots >= 2E) gathered cache -> buffer on the current stream, the
-        misses copied host -> buffer as coalesced runs on the copy stream (reference
-        :708-778, with per-run hipMemcpyAsync in place of its batched memcpy)."""
-        from ..kernel.fast_index_copy import fast_index_copy_multi_jit
-        from .offload_kernels import prefill_hit_compact
-
-        E = self.num_experts
-        snap = self._prefill_snapshot_np[layer_id]
-        hit_mask = snap >= 2 * E
-        self.prefill_hit_rows += int(hit_mask.sum())
-        self.prefill_total_rows += E
-        if self._gather_dst_ptrs is not None:
-            prefill_hit_compact(self, layer_id, buffer_id)
-            fast_index_copy_multi_jit(self._gather_dst_ptrs, self._gather_dst_ptrs,
-                                      self._gather_feat_bytes, self._prefill_hit_dst,
-                                      self._prefill_hit_src, self._prefill_hit_num)
-        miss = np.nonzero(~hit_mask)[0].astype(np.int64)
-        with torch.cuda.stream(self.prefill_copy_stream):
-            if self._prefill_buffer_has_release_event[buffer_id]:
-                self.prefill_copy_stream.wait_event(self.prefill_release_events[buffer_id])
-            self._invalidate_prefill_buffer(buffer_id)
-            stream = torch.cuda.current_stream(self.device)
-            all_rows = np.arange(E, dtype=np.int64)
-            for b, ((per_layer, _), buffer) in enumerate(zip(self.banks,
-                                                             self.prefill_bank_buffers)):
-                if self._copy_feat_bytes_host[b] < _SMALL_BANK_FEAT_BYTES:
-                    copy_rows_async(buffer[buffer_id], all_rows, per_layer[layer_id], all_rows,
-                                    stream=stream)
-                elif miss.size:
-                    copy_rows_async(buffer[buffer_id], miss, per_layer[layer_id], miss,
-                                    stream=stream)
-            self.prefill_ready_events[buffer_id].record(self.prefill_copy_stream)
-
-    def wait_prefill_layer(self, layer_id: int) -> tuple[torch.Tensor, ...]:
-        """Full-layer ``[num_experts, ...]`` views of every bank for ``layer_id``."""
-        assert self.prefill_overlap
-        assert self.prefill_bank_buffers
-        self.prefetch_prefill_layer(layer_id)
-        buffer_id = layer_id % 2
-        assert self._prefill_buffer_layer[buffer_id] == layer_id
-        torch.cuda.current_stream(self.device).wait_event(self.prefill_ready_events[buffer_id])
-        return tuple(buffer[buffer_id] for buffer in self.prefill_bank_buffers)
-
-    def release_prefill_layer(self, layer_id: int) -> None:
-        if not self.prefill_overlap:
-            return
-        buffer_id = layer_id % 2
-        if self._prefill_buffer_layer[buffer_id] != layer_id:
-            return
-        self.prefill_release_events[buffer_id].record(torch.cuda.current_stream(self.device))
-        self._prefill_buffer_has_release_event[buffer_id] = True
-        self._prefill_buffer_released[buffer_id] = True
-
-    # ---- decode -----------------------------------------------------------------------------
+    # ---- decode: the reference's in-place path --------------------------------------------------
 
     def ensure_experts(self, layer_id: int, expert_ids: torch.Tensor) -> None:
-        """Make ``expert_ids`` (int32, this layer's routed experts) resident; rewritten in
-        place to slot ids, with the copy plan in evict_slots / src_indices / num_indices."""
-        from .offload_kernels import ensure_experts
+        """Make this layer's routed experts (int32 ids) resident and rewrite them to slot ids
+        in place. "lru": device admission (no host sync); copy_missing() moves the rows.
+        "static": staged through stage_layer; the current stream waits for the copies, so
+        copy_missing() has nothing left to do."""
+        if expert_ids.dtype != torch.int32 or not expert_ids.is_contiguous():
+            raise ValueError("expert_ids must be a contiguous int32 tensor")
+        if self.cache_policy == "lru":
+            self._pending_layer = int(layer_id)
+            self._maps.admit(int(layer_id), expert_ids.view(-1), self.collect_stats)
+            return
+        routes = self.stage_layer(layer_id, expert_ids)
+        torch.cuda.current_stream(self.device).wait_event(routes.ready)
+        expert_ids.copy_(torch.maximum(routes.in_hbm, routes.copied).view(expert_ids.shape))
+        self._pending_layer = None
 
-        if self.collect_decode_freq:
-            ids = expert_ids.reshape(-1).long()
-            self.decode_freq[layer_id].scatter_add_(0, ids, torch.ones_like(ids))
-        self._pending_src_layer = layer_id
-        self._pending_whole_layer = False
-        ensure_experts(self, layer_id, expert_ids)
-
-    def ensure_experts_hybrid(self, layer_id: int, expert_ids: torch.Tensor) -> None:
-        raise NotImplementedError("hybrid CPU/GPU expert decode is not part of this build")
+    def copy_missing(self) -> None:
+        """Execute the copy plan of the last ensure_experts / materialize_layer ("lru")."""
+        assert self._banks is not None, "set_bank_sources first"
+        if self.cache_policy == "static":
+            return
+        layer = self._pending_layer
+        assert layer is not None, "no pending plan (ensure_experts / materialize_layer first)"
+        self._banks.copy_planned(layer, self._maps.plan_dst, self._maps.plan_src,
+                                 self._maps.plan_len)
 
     def materialize_layer(self, layer_id: int) -> None:
-        from .offload_kernels import materialize_layer
+        """Slots [0, E) take the layer's experts in id order ("lru"); copy_missing() copies."""
+        if self.cache_policy != "lru":
+            raise NotImplementedError("materialize_layer belongs to the lru policy")
+        self._pending_layer = int(layer_id)
+        self._maps.materialize(int(layer_id))
 
-        self._pending_src_layer = layer_id
-        self._pending_whole_layer = True
-        materialize_layer(self, layer_id)
+    # ---- decode: staged, overlapped path --------------------------------------------------------
+
+    def stage_layer(self, layer_id: int, topk_ids: torch.Tensor) -> StagedRoutes:
+        """Plan the layer's misses on the host and copy them with the DMA engines on the copy
+        stream. Reads the routing back, which blocks the host until everything enqueued on the
+        compute stream so far has run; so no earlier reader of a slot is still in flight when
+        its new rows are copied. Returns the routes split into in-HBM and being-copied groups
+        (see StagedRoutes)."""
+        assert self._banks is not None, "set_bank_sources first"
+        layer = int(layer_id)
+        dev, E = self.device, self.num_experts
+        ids = topk_ids.contiguous().view(-1)
+        if ids.dtype != torch.int32:
+            raise ValueError("topk_ids must be int32")
+        n = ids.numel()
+        compute = torch.cuda.current_stream(dev)
+        if self._host_ids.numel() < n:
+            self._host_ids = torch.empty(max(n, 2 * self._host_ids.numel()), dtype=torch.int32,
+                                         pin_memory=True)
+        if self.cache_policy == "lru":
+            return self._stage_lru(layer, ids, topk_ids.shape, compute)
+        hid = self._host_ids[:n]
+        hid.copy_(ids, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record(compute)
+        done.synchronize()
+        rid = hid.numpy().astype(np.int64)
+        valid = (rid >= 0) & (rid < E)
+        distinct = np.unique(rid[valid])
+        res = self._resident_slot[layer, distinct]
+        stage_ids = distinct[res < 0]
+        slot_of_expert = np.full(E, -1, np.int64)
+        slot_of_expert[distinct[res >= 0]] = res[res >= 0]
+        new_ids = np.empty(0, np.int64)
+        victims = np.empty(0, np.int64)
+        if stage_ids.size:
+            st_slots, new_flat, victims = self._staging.place(layer * E + stage_ids)
+            slot_of_expert[stage_ids] = self.staging_base + st_slots
+            new_ids = new_flat - layer * E
+        copied_mask = np.zeros(E, bool)
+        copied_mask[new_ids] = True
+        rslot = np.where(valid, slot_of_expert[np.clip(rid, 0, E - 1)], -1)
+        rcopied = valid & copied_mask[np.clip(rid, 0, E - 1)]
+        in_hbm = np.where(rcopied, -1, rslot).astype(np.int32)
+        copied = np.where(rcopied, rslot, -1).astype(np.int32)
+        moved = 0
+        issued = self._copy_start_event()
+        if new_ids.size:
+            with torch.cuda.stream(self._copy_stream):
+                order = np.argsort(victims)
+                moved = self._banks.copy_dma(layer, self.staging_base + victims[order],
+                                             new_ids[order], self._copy_stream)
+        ready = torch.cuda.Event(enable_timing=self.record_copy_start)
+        ready.record(self._copy_stream)
+        self._host_stats[layer] += (distinct.size, new_ids.size, 1)
+        self.copied_bytes += moved
+        return StagedRoutes(layer, self._to_device(in_hbm, topk_ids.shape),
+                            self._to_device(copied, topk_ids.shape), ready, int(distinct.size),
+                            int(new_ids.size), moved, issued)
+
+    def _stage_lru(self, layer: int, ids: torch.Tensor, shape, compute) -> StagedRoutes:
+        """"lru" policy: device admission, then its plan read back and copied by DMA."""
+        slots = ids.clone()
+        self._maps.admit(layer, slots, self.collect_stats)
+        n = ids.numel()
+        hp = self._host_plan
+        E, S = self.num_experts, self.cache_size
+        plan = min(n, S)
+        buf = torch.cat([self._maps.plan_len, self._maps.plan_dst[:plan].long(),
+                         self._maps.plan_src[:plan].long()])
+        hp[:buf.numel()].copy_(buf, non_blocking=True)
+        hid = self._host_ids[:n]
+        hid.copy_(slots, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record(compute)
+        done.synchronize()
+        cnt = int(hp[0])
+        dst = hp[1:1 + cnt].numpy().copy()
+        src = hp[1 + plan:1 + plan + cnt].numpy().copy()
+        new_slot = np.zeros(S, bool)
+        new_slot[dst] = True
+        hs = hid.numpy().astype(np.int64)
+        fresh = (hs >= 0) & new_slot[np.clip(hs, 0, S - 1)]
+        in_hbm = np.where(fresh, -1, hs).astype(np.int32)
+        copied = np.where(fresh, hs, -1).astype(np.int32)
+        moved = 0
+        issued = self._copy_start_event()
+        if cnt:
+            with torch.cuda.stream(self._copy_stream):
+                order = np.argsort(dst)
+                moved = self._banks.copy_dma(layer, dst[order], src[order], self._copy_stream)
+        ready = torch.cuda.Event(enable_timing=self.record_copy_start)
+        ready.record(self._copy_stream)
+        self.copied_bytes += moved
+        return StagedRoutes(layer, self._to_device(in_hbm, shape), self._to_device(copied, shape),
+                            ready, int(np.unique(hs[hs >= 0]).size), cnt, moved, issued)
+
+    def _copy_start_event(self) -> torch.cuda.Event | None:
+        if not self.record_copy_start:
+            return None
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record(self._copy_stream)
+        return ev
+
+    def _to_device(self, a: np.ndarray, shape) -> torch.Tensor:
+        return torch.from_numpy(a).to(self.device).view(shape)
+
+    # ---- prefill double buffer ------------------------------------------------------------------
+
+    def begin_prefill(self) -> None:
+        """Start a prefill: its buffer copies queue behind everything on the compute stream."""
+        pb = self._prefill
+        if pb is None:
+            return
+        pb.layer = [None, None]
+        pb.free = [True, True]
+        pb.begin.record(torch.cuda.current_stream(self.device))
+        pb.stream.wait_event(pb.begin)
+        self._snapshot = None
+        if self.cache_policy == "lru" and self.prefill_hit_d2d and self._banks.multi_ok \
+                and self.cache_size > 2 * self.num_experts:
+            snap = torch.empty((self.num_layers, self.num_experts), dtype=torch.int32,
+                               pin_memory=True)
+            with torch.cuda.stream(pb.stream):
+                snap.copy_(self._maps.slot_of_id, non_blocking=True)
+            pb.stream.synchronize()
+            self._snapshot = snap.numpy()
+
+    def _empty_buffer_slots(self, buf: int) -> None:
+        E = self.num_experts
+        lo = self._prefill.base + buf * E
+        if self.cache_policy == "lru":
+            self._maps.invalidate(lo, lo + E)
+        else:
+            self._staging.forget_range(lo - self.staging_base, lo - self.staging_base + E)
+
+    def prefetch_prefill_layer(self, layer_id: int) -> None:
+        """Queue the copy of a whole layer into buffer layer_id % 2 (no-op when queued)."""
+        pb = self._prefill
+        if pb is None or layer_id >= self.num_layers:
+            return
+        if layer_id < 0:
+            raise ValueError(f"invalid prefill layer {layer_id}")
+        buf, E = layer_id % 2, self.num_experts
+        if pb.layer[buf] == layer_id:
+            return
+        if pb.layer[buf] is not None and not pb.free[buf]:
+            raise RuntimeError("prefill buffer reused before release_prefill_layer")
+        # experts already in HBM are gathered slot -> buffer row on the compute stream
+        in_hbm = np.empty(0, np.int64)
+        hbm_slot = np.empty(0, np.int64)
+        if self.cache_policy == "static":
+            rs = self._resident_slot[layer_id]
+            in_hbm = np.nonzero(rs >= 0)[0]
+            hbm_slot = rs[in_hbm]
+        elif self._snapshot is not None:
+            row = self._snapshot[layer_id].astype(np.int64)
+            in_hbm = np.nonzero(row >= 2 * E)[0]
+            hbm_slot = row[in_hbm]
+        if self.prefill_hit_d2d or self.cache_policy == "static":
+            self.prefill_hit_rows += int(in_hbm.size)
+            self.prefill_total_rows += E
+        if in_hbm.size and self._banks.multi_ok and self._banks.gather_dst is not None:
+            dst = torch.from_numpy((pb.base + buf * E + in_hbm).astype(np.int32)).to(self.device)
+            src = torch.from_numpy(hbm_slot.astype(np.int32)).to(self.device)
+            fast_index_copy_multi(self._banks.gather_dst, self._banks.gather_dst,
+                                  self._banks.gather_rows, dst, src)
+            gathered = True
+        else:
+            gathered = False
+        if not gathered:
+            in_hbm = np.empty(0, np.int64)
+        rest = np.setdiff1d(np.arange(E), in_hbm)
+        with torch.cuda.stream(pb.stream):
+            if pb.ever_released[buf]:
+                pb.stream.wait_event(pb.released[buf])
+            self._empty_buffer_slots(buf)
+            base = pb.base + buf * E
+            if gathered:     # large banks: only the rest; small banks: the whole layer
+                all_rows = np.arange(E)
+                for i, name in enumerate(self._banks.names):
+                    rows = rest if self._banks.row_bytes[i] >= _SMALL_ROW_BYTES else all_rows
+                    if rows.size:
+                        copy_rows_async(self._banks.caches[name], base + rows,
+                                        self._banks.sources[name][layer_id], rows, stream=pb.stream)
+            else:
+                self._banks.copy_dma(layer_id, base + rest, rest, pb.stream)
+            pb.ready[buf].record(pb.stream)
+        pb.layer[buf] = layer_id
+        pb.free[buf] = False
+
+    def wait_prefill_layer(self, layer_id: int) -> tuple[torch.Tensor, ...]:
+        """[E, ...] views of every bank for layer_id, ordered after its copies."""
+        pb = self._prefill
+        assert pb is not None, "prefill_overlap is off"
+        self.prefetch_prefill_layer(layer_id)
+        buf = layer_id % 2
+        torch.cuda.current_stream(self.device).wait_event(pb.ready[buf])
+        return tuple(v[buf] for v in pb.views)
+
+    def release_prefill_layer(self, layer_id: int) -> None:
+        """The layer's consumers are enqueued: its buffer may be refilled after them."""
+        pb = self._prefill
+        if pb is None:
+            return
+        buf = layer_id % 2
+        if pb.layer[buf] != layer_id:
+            return
+        pb.released[buf].record(torch.cuda.current_stream(self.device))
+        pb.ever_released[buf] = True
+        pb.free[buf] = True
+
+    # ---- lifecycle and stats --------------------------------------------------------------------
 
     def reset(self) -> None:
-        from .offload_kernels import reset_cache
-
-        reset_cache(self)
-        self.expert_recency.fill_(-1)
+        """Forget every cached expert ("static": the resident set stays)."""
+        if self.cache_policy == "lru":
+            self._maps.reset()
+        else:
+            self._staging.reset()
+            self._maps.clock.zero_()
+        self._pending_layer = None
 
     def reset_stats(self) -> None:
+        self._maps.stats.zero_()
+        self._host_stats[:] = 0
+        self.copied_bytes = 0
         self.prefill_hit_rows = 0
         self.prefill_total_rows = 0
-        self.lru_stats.zero_()
-        for t in (self.stat_missing, self.stat_active, self.stat_calls, self.stat_fetched,
-                  self.stat_missing_layer, self.stat_active_layer, self.stat_fetched_layer,
-                  self.stat_steps_layer):
-            t.zero_()
-
-    def record_decode_stats(self, layer_id: int) -> None:
-        """No-op: ensure_experts accumulates lru_stats inside its own launch."""
-
-    def record_decode_stats_hybrid(self, layer_id: int) -> None:
-        raise NotImplementedError("hybrid CPU/GPU expert decode is not part of this build")
 
     def decode_miss_stats(self) -> dict:
         active, missing, calls = (int(x) for x in self.lru_stats.sum(0))
-        fetched = int(self.stat_fetched.item())
         return {
             "layer_calls": calls,
-            "active_per_layer": (active / calls) if calls else 0.0,
-            "missing_per_layer": (missing / calls) if calls else 0.0,
-            "miss_rate": (missing / active) if active else 0.0,
-            "fetched_per_layer": (fetched / calls) if calls else 0.0,
-            "cpu_per_layer": ((missing - fetched) / calls) if calls else 0.0,
-            "fetch_rate": (fetched / missing) if missing else 0.0,
+            "active_per_layer": active / calls if calls else 0.0,
+            "missing_per_layer": missing / calls if calls else 0.0,
+            "miss_rate": missing / active if active else 0.0,
+            "hit_rate": 1.0 - missing / active if active else 0.0,
+            "copied_bytes": self.copied_bytes,
             "prefill_hit_rows": self.prefill_hit_rows,
             "prefill_rows": self.prefill_total_rows,
         }
 
     def decode_miss_stats_per_layer(self) -> dict:
-        cols = self.lru_stats.t().tolist()
-        active, missing, steps = cols[Stat.ACTIVE], cols[Stat.MISS], cols[Stat.CALLS]
-        fetched = self.stat_fetched_layer.tolist()
-        per_layer = []
-        for L in range(self.num_layers):
-            s, m, a, f = steps[L], missing[L], active[L], fetched[L]
-            per_layer.append({
-                "layer": L, "steps": s,
-                "active_per_step": (a / s) if s else 0.0,
-                "missing_per_step": (m / s) if s else 0.0,
-                "miss_rate": (m / a) if a else 0.0,
-                "fetched_per_step": (f / s) if s else 0.0,
-            })
-        return {"per_layer": per_layer}
+        st = self.lru_stats.cpu().numpy()
+        rows = []
+        for l in range(self.num_layers):
+            a, m, c = (int(v) for v in st[l, [Stat.ACTIVE, Stat.MISS, Stat.CALLS]])
+            rows.append({"layer": l, "steps": c, "active_per_step": a / c if c else 0.0,
+                         "missing_per_step": m / c if c else 0.0,
+                         "miss_rate": m / a if a else 0.0})
+        return {"per_layer": rows}
 
-    def decode_routing_stats(self) -> dict:
-        """Per-layer routing concentration from the ``collect_decode_freq`` histogram
-        (reference :941-971)."""
-        freq = self.decode_freq.float()
-        total = freq.sum(dim=1)
-        valid = total > 0
-        if int(valid.sum()) == 0:
-            return {}
-        C = max(1, int(round(self.cache_size / self.num_layers)))
-        sorted_f, _ = torch.sort(freq, dim=1, descending=True)
-        oracle_hit = (sorted_f[:, :C].sum(dim=1)[valid] / total[valid]).mean().item()
-        ws = (freq > 0).sum(dim=1).float()
-        cdf = torch.cumsum(sorted_f, dim=1) / total.clamp(min=1).unsqueeze(1)
-        cover90 = ((cdf < 0.9).sum(dim=1).float() + 1)[valid]
-        p = freq / total.clamp(min=1).unsqueeze(1)
-        ent = -(p * p.clamp(min=1e-12).log()).sum(dim=1)[valid]
-        norm_ent = (ent / torch.log(torch.tensor(float(self.num_experts)))).mean().item()
-        return {
-            "slots_per_layer": self.cache_size / self.num_layers,
-            "working_set_mean": ws[valid].mean().item(),
-            "working_set_max": int(ws[valid].max().item()),
-            "experts_for_90pct": cover90.mean().item(),
-            "oracle_hit_at_slots": oracle_hit,
-            "norm_entropy": norm_ent,
-        }
 
-    def copy_missing(self) -> None:
-        """Copy the rows planned by the last ensure_experts / materialize_layer from that
-        layer's pinned banks into their slots: one multi-bank launch, or one launch per bank
-        when the fused descriptor is unavailable. The count stays on the device."""
-        assert self.banks, "set_bank_sources must register the banks first"
-        layer_id = self._pending_src_layer
-        assert layer_id is not None, "no staged misses (ensure_experts/materialize_layer first)"
-        if self._copy_fused_ok:
-            from ..kernel.fast_index_copy import fast_index_copy_multi_jit
-
-            fast_index_copy_multi_jit(self._copy_dst_ptrs, self._copy_src_ptrs[layer_id],
-                                      self._copy_feat_bytes, self.evict_slots, self.src_indices,
-                                      self.num_indices)
-            return
-        from ..kernel.fast_index_copy import fast_index_copy_jit
-
-        for per_layer, cache in self.banks:
-            fast_index_copy_jit(cache, self.evict_slots, per_layer[layer_id], self.src_indices,
-                                self.num_indices)
+__all__ = ["OffloadMoeCache", "StagedRoutes", "POLICIES", "BANK_NAMES"]

@@ -45,45 +45,53 @@ class ExpertWeights:
 
 
 class ExpertBank:
-    """Host-resident bank of every expert, keyed (layer, expert_id)."""
+    """Every expert's weights in host memory, looked up by (layer, expert_id).
+
+    The bank is the source side of expert streaming: the slot pool copies an entry into HBM
+    when it is routed to and not resident. Entries are immutable once added (a second add of
+    the same key is an error), and each remembers its byte size so budgets need no tensor
+    walks. pin_memory() moves every entry into page-locked memory, which the DMA copies need.
+    """
 
     def __init__(self) -> None:
-        self._experts: dict[tuple[int, int], ExpertWeights] = {}
-        self._bytes: dict[tuple[int, int], int] = {}
+        self._entries: dict[tuple[int, int], tuple[ExpertWeights, int]] = {}
+        self._total = 0
 
     def add(self, layer: int, expert_id: int, weights: ExpertWeights) -> None:
-        key = (layer, expert_id)
-        assert key not in self._experts, f"duplicate expert {key}"
-        self._experts[key] = weights
-        self._bytes[key] = weights.bytes()
+        key = (int(layer), int(expert_id))
+        assert key not in self._entries, f"expert {key} is already in the bank"
+        size = weights.bytes()
+        self._entries[key] = (weights, size)
+        self._total += size
 
     def __contains__(self, key: tuple[int, int]) -> bool:
-        return key in self._experts
+        return key in self._entries
 
     def __getitem__(self, key: tuple[int, int]) -> ExpertWeights:
-        return self._experts[key]
-
-    def bytes(self, key: tuple[int, int]) -> int:
-        return self._bytes[key]
+        return self._entries[key][0]
 
     def __len__(self) -> int:
-        return len(self._experts)
+        return len(self._entries)
+
+    def bytes(self, key: tuple[int, int]) -> int:
+        return self._entries[key][1]
 
     def keys(self):
-        return self._experts.keys()
+        return self._entries.keys()
 
     @property
     def total_bytes(self) -> int:
-        return sum(self._bytes.values())
+        return self._total
 
     def pin_memory(self) -> None:
-        """Move every expert to contiguous pinned host memory (the DMA copy source)."""
-        for key, w in self._experts.items():
+        """Re-home every entry in contiguous page-locked host memory (the DMA copy source)."""
+        for key, (w, size) in list(self._entries.items()):
             if all(t.device.type == "cpu" and t.is_pinned() and t.is_contiguous()
                    for t in w.tensors()):
                 continue
-            self._experts[key] = ExpertWeights(
-                *(t.detach().to("cpu").contiguous().pin_memory() for t in w.tensors()))
+            pinned = ExpertWeights(*(t.detach().to("cpu").contiguous().pin_memory()
+                                     for t in w.tensors()))
+            self._entries[key] = (pinned, size)
 
 
 class ExpertSlotPool:

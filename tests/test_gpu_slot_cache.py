@@ -183,16 +183,14 @@ def _check_resident(cache, banks, layer: int, experts, slots):
 
 
 @pytest.mark.parametrize("fused", [True, False])
-def test_offload_cache_decode_steps(dev, fused, monkeypatch):
-    import plastic_infer.moe.offload_cache as OC
-
-    monkeypatch.setattr(OC, "_FUSED_COPY", fused)
+def test_offload_cache_decode_steps(dev, fused):
     L, E, H, I, B, K = 4, 16, 128, 64, 6, 4
     banks = _banks(L, E, H, I, 3)
-    cache = OffloadMoeCache(num_layers=L, num_experts=E, cache_size=24, device=dev)
+    cache = OffloadMoeCache(num_layers=L, num_experts=E, cache_size=24, device=dev,
+                            multi_bank_copy=fused)
     cache.collect_stats = True
     cache.set_bank_sources(banks)
-    assert cache._copy_fused_ok == fused
+    assert cache._banks.multi_ok == fused
     st = SC.new_state(L * E, 24)
     rng = np.random.default_rng(5)
     stats = np.zeros((L, 3), np.int64)
@@ -280,3 +278,108 @@ def test_fast_index_copy_dropin_names(dev):
     fast_index_copy_multi_jit(dp, sp, fb, di, si)
     exp[2] = src[5]
     assert torch.equal(dst.cpu(), exp) and torch.equal(dst2.cpu(), exp)
+
+
+# ---- staged (DMA, overlapped) decode path -----------------------------------------------------
+
+def _check_routes(cache, banks, layer, ids, routes):
+    """Every route's slot holds its expert's rows; in-HBM and copied groups partition the
+    routes; returns (slot per route, copied mask) as numpy."""
+    a, c = routes.in_hbm.cpu().numpy().reshape(-1), routes.copied.cpu().numpy().reshape(-1)
+    assert ((a >= 0) != (c >= 0)).all()
+    slots = np.maximum(a, c)
+    _check_resident(cache, banks, layer, ids.reshape(-1), slots)
+    return slots, c >= 0
+
+
+def test_offload_cache_static_policy_staging(dev):
+    """"static": resident experts sit in fixed slots from the start; every other routed expert
+    goes through the host staging LRU (its decisions checked against the slot-cache oracle), is
+    copied by DMA on the copy stream and marked as copied; rows bit-exact against the banks."""
+    L, E, H, I, B, K, R = 3, 16, 128, 64, 5, 4, 6
+    staging = E - R + 4
+    banks = _banks(L, E, H, I, 21)
+    resident = [[(3 * l + j) % E for j in range(R)] for l in range(L)]
+    cache = OffloadMoeCache(num_layers=L, num_experts=E, cache_size=L * R + staging, device=dev,
+                            cache_policy="static", resident_per_layer=R)
+    cache.set_bank_sources(banks, resident_experts=resident)
+    for l in range(L):
+        rs = sorted(resident[l])
+        _check_resident(cache, banks, l, rs, [l * R + j for j in range(R)])
+        assert cache.resident_experts(l).tolist() == rs
+    st = SC.new_state(L * E, staging)
+    rng = np.random.default_rng(22)
+    compute = torch.cuda.current_stream(dev)
+    for step in range(10):
+        for layer in range(L):
+            ids = np.stack([rng.choice(E, size=K, replace=False) for _ in range(B)])
+            routes = cache.stage_layer(layer, torch.tensor(ids, dtype=torch.int32, device=dev))
+            compute.wait_event(routes.ready)
+            slots, copied = _check_routes(cache, banks, layer, ids, routes)
+            flat = ids.reshape(-1)
+            res = np.isin(flat, resident[layer])
+            assert not copied[res].any()
+            stage_ids = np.unique(flat[~res]) + layer * E
+            out, src, dst, n, _ = SC.lru_ensure(st, stage_ids)
+            exp = dict(zip(stage_ids.tolist(), (out + L * R).tolist()))
+            for f, s_, cp in zip(flat[~res] + layer * E, slots[~res], copied[~res]):
+                assert exp[int(f)] == s_
+                assert cp == (int(f) in src.tolist())
+            assert routes.copied_experts == n
+    m = cache.decode_miss_stats()
+    assert m["layer_calls"] == 10 * L and 0 < m["miss_rate"] < 1
+
+
+def test_offload_cache_lru_policy_staged_matches_oracle(dev):
+    """"lru" through stage_layer: the device admission's decisions equal the oracle's; the
+    planned rows are copied by DMA; copied routes are exactly those of this call's plan."""
+    L, E, H, I, B, K = 4, 16, 128, 64, 6, 4
+    banks = _banks(L, E, H, I, 23)
+    cache = OffloadMoeCache(num_layers=L, num_experts=E, cache_size=24, device=dev)
+    cache.collect_stats = True
+    cache.set_bank_sources(banks)
+    st = SC.new_state(L * E, 24)
+    rng = np.random.default_rng(24)
+    compute = torch.cuda.current_stream(dev)
+    for step in range(8):
+        for layer in range(L):
+            ids = np.stack([rng.choice(E, size=K, replace=False) for _ in range(B)])
+            out, src, dst, n, _ = SC.lru_ensure(st, ids.reshape(-1), id_base=layer * E)
+            routes = cache.stage_layer(layer, torch.tensor(ids, dtype=torch.int32, device=dev))
+            compute.wait_event(routes.ready)
+            slots, copied = _check_routes(cache, banks, layer, ids, routes)
+            assert np.array_equal(slots, out)
+            assert np.array_equal(copied, np.isin(out, dst))
+    assert np.array_equal(cache.slot_for_id.cpu().numpy().reshape(-1), st["slot_of_id"])
+
+
+@pytest.mark.parametrize("policy", ["lru", "static"])
+def test_two_pass_routed_ffn_is_bit_identical(dev, policy):
+    """The FFN over the in-HBM routes, then (after the copy event) the copied routes, summed
+    once, equals one FFN over all routes on the same slots, bit for bit."""
+    from plastic_infer.kernel import moe_sum_reduce
+    from plastic_infer.moe.fused import fused_experts_decode_impl, routed_ffn_routes
+
+    L, E, H, I, B, K = 2, 16, 256, 128, 9, 4
+    banks = _banks(L, E, H, I, 25)
+    size = 2 * 8 + (E - 8) if policy == "static" else 24
+    cache = OffloadMoeCache(num_layers=L, num_experts=E, cache_size=size, device=dev,
+                            cache_policy=policy)
+    cache.set_bank_sources(banks)
+    g = torch.Generator().manual_seed(26)
+    x = (torch.randn(B, H, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    logits = torch.randn(B, E, generator=g).to(dev)
+    from plastic_infer.moe.fused import fused_topk
+
+    for layer in (0, 1, 0):
+        w, ids = fused_topk(x, logits, K, True)
+        routes = cache.stage_layer(layer, ids)
+        gu, dn = cache.bank_views()
+        buf = torch.empty(B, K, H, dtype=x.dtype, device=dev)
+        routed_ffn_routes(x, gu, dn, w, routes.in_hbm, buf)
+        torch.cuda.current_stream(dev).wait_event(routes.ready)
+        routed_ffn_routes(x, gu, dn, w, routes.copied, buf)
+        two = torch.empty_like(x)
+        moe_sum_reduce(buf, two)
+        one = fused_experts_decode_impl(x, gu, dn, w, torch.maximum(routes.in_hbm, routes.copied))
+        assert torch.equal(two.cpu(), one.cpu()), layer

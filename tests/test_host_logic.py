@@ -8,6 +8,7 @@ from __future__ import annotations
 import hashlib
 import random
 
+import numpy as np
 import pytest
 
 import oracle.expert_copy as OC
@@ -149,6 +150,115 @@ class TestLruPool:
         assert p2.used_bytes == 100 and len(p2) == 2
 
 
+class _ListModel:
+    """Executable statement of the LruPool contract on a plain recency list (oldest first):
+    the model the tracker must agree with on every observable after every operation."""
+
+    def __init__(self, budget):
+        self.budget, self.order, self.pages = budget, [], {}
+
+    def _use(self, k):
+        if k in self.order:
+            self.order.remove(k)
+        self.order.append(k)
+
+    def used(self):
+        return sum(b for b, t, _ in self.pages.values() if t == Tier.GPU)
+
+    def add(self, k, b, t):
+        self.pages[k] = [b, t, 0]
+        self._use(k)
+
+    def pin(self, k):
+        self.pages[k][2] += 1
+        self._use(k)
+
+    def unpin(self, k):
+        self.pages[k][2] -= 1
+        self._use(k)
+
+    def set_tier(self, k, t):
+        self.pages[k][1] = t
+        self._use(k)
+
+    def remove(self, k):
+        del self.pages[k]
+        self.order.remove(k)
+
+    def evict(self, need):
+        out, freed = [], 0
+        for k in list(self.order):
+            if freed >= need:
+                break
+            b, t, pins = self.pages[k]
+            if pins or t != Tier.GPU:
+                continue
+            self.remove(k)
+            out.append(k)
+            freed += b
+        return out
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_lru_pool_matches_recency_list_model(seed):
+    """3000 random operations (adds, pins, unpins, tier moves, removes, evictions with zero,
+    small and huge requests) on the tracker and on the list model: same evicted keys in the
+    same order, same byte accounting, same recency order, same errors."""
+    import random
+
+    rng = random.Random(seed)
+    pool: LruPool = LruPool(5000)
+    model = _ListModel(5000)
+    tiers = [Tier.GPU, Tier.GPU, Tier.GPU, Tier.HOST, Tier.DISK]
+    next_key = 0
+    for _ in range(3000):
+        keys = list(model.pages)
+        op = rng.randrange(7)
+        if op == 0 or not keys:
+            k, b, t = next_key, rng.randrange(0, 400), rng.choice(tiers)
+            next_key += 1
+            pool.add(k, b, t)
+            model.add(k, b, t)
+        elif op == 1:
+            k = rng.choice(keys)
+            pool.pin(k)
+            model.pin(k)
+        elif op == 2:
+            k = rng.choice(keys)
+            if model.pages[k][2] == 0:
+                with pytest.raises(AssertionError):
+                    pool.unpin(k)
+            else:
+                pool.unpin(k)
+                model.unpin(k)
+        elif op == 3:
+            k, t = rng.choice(keys), rng.choice(tiers)
+            pool.set_tier(k, t)
+            model.set_tier(k, t)
+        elif op == 4:
+            k = rng.choice(keys)
+            if model.pages[k][2]:
+                with pytest.raises(AssertionError):
+                    pool.remove(k)
+            else:
+                assert pool.remove(k).key == k
+                model.remove(k)
+        elif op == 5:
+            need = rng.choice([0, 1, rng.randrange(0, 1500), 10 ** 9])
+            assert [p.key for p in pool.evict_lru(need)] == model.evict(need)
+        else:
+            want = rng.randrange(0, 6000)
+            fits = model.used() + want <= model.budget
+            got = [p.key for p in pool.evict_to_fit(want)]
+            assert got == ([] if fits else model.evict(want - (model.budget - model.used())))
+        assert pool.used_bytes == model.used() and len(pool) == len(model.pages)
+        assert pool.lru_keys() == model.order
+        assert pool.all_pinned() == (not any(p == 0 and t == Tier.GPU
+                                             for _, t, p in model.pages.values()))
+    with pytest.raises(AssertionError):
+        pool.add(next(iter(model.pages)), 1) if model.pages else pool.add(-1, 1) or pool.add(-1, 1)
+
+
 class TestSlotPoolPolicyOracle:
     """The oracle's residency decisions on the reference's ExpertSlotPool scenarios
     (reference tests/test_experts.py:71-131)."""
@@ -174,3 +284,27 @@ class TestSlotPoolPolicyOracle:
         for ids in ([0, 1], [0, 1], [2, 3]):
             p.ensure(0, ids); p.release(0, ids)
         assert (p.hits, p.misses) == (2, 4)
+
+
+@pytest.mark.parametrize("seed,n_slots,universe,calls", [(0, 16, 64, 200), (1, 64, 6144, 100),
+                                                          (2, 5, 12, 300)])
+def test_staging_lru_follows_the_admission_rule(seed, n_slots, universe, calls):
+    """The host staging LRU of the "static" expert policy makes the decisions of the device
+    admission kernel, as the slot-cache oracle restates it: same slot for every id, same ids
+    copied into the same slots, call after call."""
+    import oracle.slot_cache as SC
+    from plastic_infer.moe.offload_cache import _StagingLru
+
+    rng = np.random.default_rng(seed)
+    lru = _StagingLru(n_slots)
+    st = SC.new_state(universe, n_slots)
+    for _ in range(calls):
+        n = int(rng.integers(1, n_slots + 1))
+        ids = rng.choice(universe, size=n, replace=False).astype(np.int64)
+        slots, new_ids, victims = lru.place(ids)
+        out, src, dst, num, _ = SC.lru_ensure(st, ids)
+        assert np.array_equal(slots, out.astype(np.int64))
+        assert np.array_equal(new_ids, src.astype(np.int64))
+        assert np.array_equal(victims, dst.astype(np.int64))
+    lru.forget_range(0, n_slots)
+    assert (lru.owner == -1).all() and not lru.slot_of
