@@ -101,3 +101,22 @@ def sum_reduce(inp: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
     T, k, H = inp.shape
     pos = np.arange(T * k, dtype=np.int64)
     return unpermute(inp.reshape(T * k, H), pos, None, T, k, out_dtype)
+
+
+def moe_forward_sparse(hidden: torch.Tensor, experts: dict, expert_ids: torch.Tensor,
+                       weights: torch.Tensor) -> torch.Tensor:
+    """reference src/plastic_infer/exec/moe.py:127-160 in the inputs' dtype: for each expert in
+    the dict's order, the (token, slot) pairs routed to it in nonzero() order, the SwiGLU MLP
+    silu(x w1^T) * (x w3^T) w2^T of their rows, times the weights, index_add_ into the output
+    (so with bf16 storage every product and every running sum is rounded to bf16)."""
+    out = torch.zeros_like(hidden)
+    for eid, w in experts.items():
+        pairs = (expert_ids == eid).nonzero()
+        if pairs.shape[0] == 0:
+            continue
+        rows = pairs[:, 0]
+        wts = weights[rows, pairs[:, 1]].unsqueeze(1)
+        x = hidden[rows]
+        inter = F.silu(F.linear(x, w.w1)) * F.linear(x, w.w3)
+        out.index_add_(0, rows, F.linear(inter, w.w2) * wts)
+    return out

@@ -186,9 +186,11 @@ def test_decode_stream_graph_replays(dev):
 
 
 def test_decode_qwen3_8b_b256_full_shape(dev):
-    """Qwen3-8B decode at full size (B = 256, L ~ U[512, 8192], 160k-page pool) generated on
-    the device; five sequences (the longest, shortest and three seeded picks) are checked
-    against the oracle from their own pages."""
+    """The Qwen3-8B decode step at full size (B = 256, L ~ U[512, 8192] including the new
+    token, 160k-page pool, block tables from one seeded permutation), generated on the device:
+    the 256-row scatter is checked bit for bit over the whole pool (the new rows at their slots,
+    every other element unchanged), then the attention of all 256 sequences against the oracle
+    over their own pages (2e-2), 64 sequences at a time."""
     B, Hq, Hkv, D, P, N_ = 256, 32, 8, 128, 16, 160_000
     g = torch.Generator().manual_seed(2)
     lens = torch.randint(512, 8193, (B,), generator=g)
@@ -199,6 +201,9 @@ def test_decode_qwen3_8b_b256_full_shape(dev):
     for b in range(B):
         bt[b, :n_pages[b]] = perm[off:off + n_pages[b]].to(torch.int32)
         off += int(n_pages[b])
+    last = lens - 1
+    page = bt[torch.arange(B), last // P].long()
+    slots = page * P + last % P
     gd = torch.Generator(device=dev).manual_seed(2)
     kp = torch.empty(N_, Hkv, D, P, dtype=torch.bfloat16, device=dev)
     vp = torch.empty_like(kp)
@@ -206,18 +211,34 @@ def test_decode_qwen3_8b_b256_full_shape(dev):
         for s in range(0, N_, 20_000):
             pool[s:s + 20_000] = torch.randn(pool[s:s + 20_000].shape, generator=gd,
                                              device=dev).to(torch.bfloat16)
+    k_new = torch.randn(B, Hkv, D, generator=gd, device=dev).to(torch.bfloat16)
+    v_new = torch.randn(B, Hkv, D, generator=gd, device=dev).to(torch.bfloat16)
     q = torch.randn(B, Hq, D, generator=gd, device=dev).to(torch.bfloat16)
-    out = paged_decode_attention(q, kp, vp, bt.to(dev), lens.to(torch.int32).to(dev))
-    picks = [int(lens.argmax()), int(lens.argmin()), 3, 100, 255]
-    for b in picks:
-        table = bt[b, :n_pages[b]].tolist()
-        ids = torch.tensor(table, device=dev)
-        kl = kp.index_select(0, ids).cpu()
-        vl = vp.index_select(0, ids).cpu()
-        ref = OP.paged_attention(q[b].cpu()[None, None], kl, vl, list(range(len(table))), P,
-                                 kv_num_tokens=int(lens[b]), causal=False)[0, 0]
-        err = (out[b].cpu().float() - ref.float()).abs().max().item()
-        assert err <= BF16_TOL, (b, err)
+    kb, vb = kp.clone(), vp.clone()
+    kv_scatter(k_new, v_new, kp, vp, slots.to(dev))
+    pg, of = page.to(dev), (last % P).to(dev)
+    kb[pg, :, :, of] = k_new
+    vb[pg, :, :, of] = v_new
+    assert torch.equal(kp, kb) and torch.equal(vp, vb)
+    del kb, vb
+    out = paged_decode_attention(q, kp, vp, bt.to(dev), lens.to(torch.int32).to(dev)).cpu()
+    worst = 0.0
+    for b0 in range(0, B, 64):
+        seqs = list(range(b0, b0 + 64))
+        ids, tables = [], []
+        for b in seqs:
+            n = int(n_pages[b])
+            tables.append(list(range(len(ids), len(ids) + n)))
+            ids += bt[b, :n].tolist()
+        sel = torch.tensor(ids, device=dev)
+        kl, vl = kp.index_select(0, sel).cpu(), vp.index_select(0, sel).cpu()
+        btl = torch.zeros(64, 512, dtype=torch.int32)
+        for i, t in enumerate(tables):
+            btl[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+        ref = OP.decode_batch(q[b0:b0 + 64].cpu(), kl, vl, btl, lens[seqs], P)
+        err = (out[b0:b0 + 64].float() - ref.float()).abs().max().item()
+        worst = max(worst, err)
+    assert worst <= BF16_TOL, worst
 
 
 def test_decode_empty_and_clamped_lengths(dev):

@@ -151,3 +151,27 @@ def test_moe_forward_sparse_vs_loop(dev):
             w = experts[int(eids[t, s_])]
             ref[t] += swiglu_mlp(hidden[t], w.w1, w.w2, w.w3) * weights[t, s_].cpu()
     assert torch.allclose(out, ref, atol=1e-5)
+
+
+def test_moe_forward_sparse_bf16_vs_reference_composition(dev):
+    """bf16: the drop-in (permute, per-expert GEMMs, one fp32 weighted unpermute, one rounding)
+    against the reference's composition (per-expert bf16 products and bf16 index_add_ in the
+    dict's order, oracle moe_route.moe_forward_sparse). The two round the k weighted terms of a
+    token differently: each bf16 running sum is off by at most half a bf16 step of its
+    magnitude, and the expert MLPs are bf16 GEMMs on different devices, so the bar is 4 bf16
+    steps (4 * 2^-8) of the output's largest magnitude."""
+    g = torch.Generator().manual_seed(12)
+    T, H, I, E, k = 64, 256, 128, 8, 2
+    dt = torch.bfloat16
+    hidden = (torch.randn(T, H, generator=g) * 0.5).to(dt)
+    experts = {e: ExpertWeights(*((torch.randn(*s, generator=g) * 0.1).to(dt)
+                                  for s in ((I, H), (H, I), (I, H)))) for e in range(E)}
+    logits = torch.randn(T, E, generator=g).to(dt)
+    eids, weights = topk_route(logits.to(dev), k=k)
+    dev_experts = {e: ExpertWeights(*(t.to(dev) for t in (w.w1, w.w2, w.w3)))
+                   for e, w in experts.items()}
+    out = moe_forward_sparse(hidden.to(dev), dev_experts, eids, weights).cpu()
+    ref = OM.moe_forward_sparse(hidden, experts, eids.cpu(), weights.cpu())
+    assert out.dtype == dt and ref.dtype == dt
+    err = (out.float() - ref.float()).abs().max().item()
+    assert err <= 4 * 2 ** -8 * ref.float().abs().max().item(), err

@@ -143,3 +143,34 @@ class TestPermuteCombine:
         out = OM.sum_reduce(x, torch.bfloat16)
         ref = ((x[:, 0].float() + x[:, 1].float()) + x[:, 2].float()).to(torch.bfloat16)
         assert torch.equal(out, ref)
+
+
+def test_oracle_moe_forward_sparse_equals_per_token_loop():
+    """fp32: the oracle's per-expert composition equals the per-token definition
+    out[t] = sum_s w[t, s] * mlp_{ids[t, s]}(x[t]) (the reference tests' ground truth); an
+    expert missing from the dict contributes nothing; dropping the weights breaks it."""
+    import types
+
+    import torch.nn.functional as F
+
+    g = torch.Generator().manual_seed(3)
+    T, H, I, E, k = 12, 16, 24, 5, 2
+    x = torch.randn(T, H, generator=g)
+    ex = {e: types.SimpleNamespace(w1=torch.randn(I, H, generator=g) * 0.3,
+                                   w2=torch.randn(H, I, generator=g) * 0.3,
+                                   w3=torch.randn(I, H, generator=g) * 0.3) for e in range(E)}
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+    w = torch.rand(T, k, generator=g)
+
+    def mlp(e, v):
+        return F.linear(F.silu(F.linear(v, ex[e].w1)) * F.linear(v, ex[e].w3), ex[e].w2)
+
+    ref = torch.stack([sum(w[t, s] * mlp(int(ids[t, s]), x[t]) for s in range(k))
+                       for t in range(T)])
+    assert torch.allclose(OM.moe_forward_sparse(x, ex, ids, w), ref, atol=1e-5)
+    part = {e: v for e, v in ex.items() if e != 2}
+    ref2 = torch.stack([sum((w[t, s] * mlp(int(ids[t, s]), x[t]) if int(ids[t, s]) != 2
+                             else torch.zeros(H)) for s in range(k)) for t in range(T)])
+    assert torch.allclose(OM.moe_forward_sparse(x, part, ids, w), ref2, atol=1e-5)
+    assert not torch.allclose(OM.moe_forward_sparse(x, ex, ids, torch.ones_like(w)), ref,
+                              atol=1e-3)
