@@ -310,7 +310,7 @@ def bench_moe_permute(torch, dev, args) -> dict:
     """Qwen3-30B-A3B MoE routing and permutation: router logits [4096, 128] fp32 N(0,1) ->
     softmax top-8 renormalised -> align (block 64) -> permute hidden [4096, 2048] bf16 into
     expert-contiguous rows -> identity expert -> weighted unpermute."""
-    from plastic_infer.kernel import moe_align_block_size, moe_permute, moe_topk, moe_unpermute
+    from plastic_infer.kernel import moe_permute, moe_topk_align, moe_unpermute
 
     g = torch.Generator().manual_seed(MOE_SEED)
     hidden = torch.randn(MOE_T, MOE_H, generator=g).to(torch.bfloat16).to(dev)
@@ -320,8 +320,7 @@ def bench_moe_permute(torch, dev, args) -> dict:
     def step(ev):
         if ev:
             ev[0].record()
-        w, ids = moe_topk(logits, MOE_K, True)
-        s, e, npp, pos = moe_align_block_size(ids, MOE_BS, MOE_E, return_route_pos=True)
+        w, ids, s, e, npp, pos = moe_topk_align(logits, MOE_K, MOE_BS)
         if ev:
             ev[1].record()
         xp = moe_permute(hidden, s, npp, MOE_K, route_pos=pos)
@@ -342,7 +341,7 @@ def bench_moe_permute(torch, dev, args) -> dict:
     perm_bytes = T * H * 2 + T * K * H * 2 + T * K * 4
     comb_bytes = T * K * H * 2 + T * H * 2 + T * K * 4 + T * K * 4
     step_bytes = route_bytes + perm_bytes + comb_bytes
-    phases = [("moe_topk + moe_align", route_bytes, route_ms),
+    phases = [("moe_topk_hist + moe_align_place", route_bytes, route_ms),
               ("moe_permute_kernel", perm_bytes, perm_ms),
               ("moe_combine_kernel", comb_bytes, comb_ms)]
     dom, dom_bytes, dom_ms = max(phases, key=lambda x: x[2])

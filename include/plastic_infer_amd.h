@@ -247,6 +247,23 @@ int pia_moe_align_block_size(int32_t* sorted_token_ids, int32_t* expert_ids,
                              void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * Router top-k and the permute plan in one call: the results of pia_moe_topk followed by
+ * pia_moe_align_block_size on its ids (reference: fused_topk then moe_align_block_size,
+ * src/plastic_infer/moe/fused.py:11-94; the batched moe_route_permute of the port's entry
+ * points). Plans of more than 4096 routes with num_experts <= 510 take two launches: the top-k
+ * kernel also writes the plan's per-chunk expert histogram (chunk = its block of tokens), then
+ * one placement kernel builds the plan from it. Other shapes run the two calls above.
+ * Arguments are those of the two calls; route_pos may be NULL.
+ * ------------------------------------------------------------------------------------------- */
+int pia_moe_topk_align(float* topk_weights, int32_t* topk_ids, const void* logits,
+                       int logits_dtype, int64_t num_tokens, int num_experts, int topk,
+                       int renormalize, int mode, int64_t num_token_non_padded,
+                       int32_t* sorted_token_ids, int32_t* expert_ids,
+                       int32_t* num_tokens_post_pad, int32_t* route_pos, int block_size,
+                       int64_t max_num_tokens_padded, void* workspace, int64_t workspace_bytes,
+                       void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Permute: x_perm[r, :] = hidden[sorted_token_ids[r] / topk, :] for r < *num_tokens_post_pad
  * and sorted_token_ids[r] < numel; padding rows (sentinel) are zero-filled; rows at or beyond
  * *num_tokens_post_pad are left untouched. Bit-exact row copy (row_bytes multiple of 4).

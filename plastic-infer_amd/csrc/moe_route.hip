@@ -1,5 +1,6 @@
 // MoE routing and token permutation:
-//   moe_topk_kernel       softmax / top-k / renormalise (one wave per token)
+//   moe_topk_wave_kernel  softmax / top-k / renormalise (one wave per token, radix select)
+//   moe_topk_hist_kernel  the same, also counting the permute plan's per-chunk experts
 //   moe_align_*           deterministic stable permute plan (counting sort by expert)
 //   moe_permute_kernel    hidden rows -> expert-contiguous rows
 //   moe_combine_kernel    weighted unpermute (and the plain top-k sum) with fp32 accumulation
@@ -20,133 +21,185 @@ __device__ __forceinline__ float dpp_f32(float x) {
 }
 constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppRor4 = 0x124, kDppRor8 = 0x128;
 
-// ---------------------------------------------------------------------------------------------
-// Top-k router. A token is served by LPT lanes (16: four tokens per wave, when k <= 16 and
-// E <= 256; else 64); lane s of its group holds experts e = s + LPT*i. Selection is by
-// descending logit with the lowest expert index winning exact ties; softmax is monotone in
-// the logit, so this is the order of descending probability.
-// ---------------------------------------------------------------------------------------------
-template <int LPT>
-__device__ __forceinline__ float group_max(float v) {
-  if constexpr (LPT == 16) {
-    v = fmaxf(v, dpp_f32<kDppXor1>(v));
-    v = fmaxf(v, dpp_f32<kDppXor2>(v));
-    v = fmaxf(v, dpp_f32<kDppRor4>(v));
-    return fmaxf(v, dpp_f32<kDppRor8>(v));
-  } else {
-#pragma unroll
-    for (int o = LPT / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-  }
-}
-template <int LPT>
-__device__ __forceinline__ float group_sum(float v) {
-  if constexpr (LPT == 16) {
-    v += dpp_f32<kDppXor1>(v);
-    v += dpp_f32<kDppXor2>(v);
-    v += dpp_f32<kDppRor4>(v);
-    return v + dpp_f32<kDppRor8>(v);
-  } else {
-#pragma unroll
-    for (int o = LPT / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-  }
-}
-// (value, expert) argmax step: keep the other lane's pick when it is larger, or equal with a
-// lower expert index; be == INT_MAX marks "nothing left".
-__device__ __forceinline__ void argmax_take(float& bv, int& be, float ov, int oe) {
-  if (oe != 0x7fffffff && (be == 0x7fffffff || ov > bv || (ov == bv && oe < be))) {
-    bv = ov;
-    be = oe;
-  }
+// Plan chunks of the counting-sort permute plan (histogram table row length: one top-k block
+// of 16 tokens per chunk up to 4096 tokens).
+constexpr int ALIGN_MAX_CHUNKS = 256;
+
+__device__ __forceinline__ uint32_t order_key(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-template <int DT, int EPL, int LPT>
-__global__ __launch_bounds__(256) void moe_topk_kernel(
-    float* __restrict__ w_out, int32_t* __restrict__ id_out, const void* __restrict__ logits_,
-    int64_t T, int E, int k, int renorm, int mode, int64_t n_non_padded) {
+__device__ __forceinline__ float wave_max_f(float v) {
+  v = fmaxf(v, dpp_f32<kDppXor1>(v));
+  v = fmaxf(v, dpp_f32<kDppXor2>(v));
+  v = fmaxf(v, dpp_f32<kDppRor4>(v));
+  v = fmaxf(v, dpp_f32<kDppRor8>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+  v += dpp_f32<kDppXor1>(v);
+  v += dpp_f32<kDppXor2>(v);
+  v += dpp_f32<kDppRor4>(v);
+  v += dpp_f32<kDppRor8>(v);
+  v += __shfl_xor(v, 16, 64);
+  return v + __shfl_xor(v, 32, 64);
+}
+
+// One token's top-k on one wave: writes k (weight, id) pairs at tok * k + slot and returns,
+// per held expert, whether it was selected (for the caller's histogram).
+template <int DT, int EPL>
+__device__ __forceinline__ void topk_one_token(float* __restrict__ w_out,
+                                               int32_t* __restrict__ id_out,
+                                               const typename Elem<DT>::T* __restrict__ logits,
+                                               int64_t tok, int E, int k, int renorm, int mode,
+                                               bool padded_tok, int lane, bool (&sel)[EPL]) {
   using El = Elem<DT>;
-  const auto* logits = reinterpret_cast<const typename El::T*>(logits_);
-  const int lane = threadIdx.x & 63, sub = lane % LPT, gbase = lane - sub;
-  const int64_t tok = (int64_t(blockIdx.x) * 256 + threadIdx.x) / LPT;
-  if (tok >= T) return;  // whole groups leave together; shuffles stay inside a group
   float x[EPL];
-  bool taken[EPL];
+  uint32_t key[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
-    const int e = sub + LPT * i;
+    const int e = lane + 64 * i;
     x[i] = e < E ? El::load(logits, tok * E + e) : -INFINITY;
-    taken[i] = e >= E;
+    key[i] = e < E ? order_key(x[i]) : 0u;
   }
-  float mx = -INFINITY;
+  // k-th largest key
+  uint32_t t = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = t | (1u << bit);
+    int cnt = 0;
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) mx = fmaxf(mx, x[i]);
-  mx = group_max<LPT>(mx);
-  float ex[EPL], sum = 0.f;
+    for (int i = 0; i < EPL; ++i) cnt += __popcll(__ballot(key[i] >= cand));
+    if (cnt >= k) t = cand;
+  }
+  int gt = 0;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) gt += __popcll(__ballot(key[i] > t));
+  int need = k - gt;  // keys == t to take, lowest expert index first
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  uint64_t msk[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
-    ex[i] = (sub + LPT * i) < E ? expf(x[i] - mx) : 0.f;
-    sum += ex[i];
+    const int e = lane + 64 * i;
+    const uint64_t eq = __ballot(e < E && key[i] == t);
+    sel[i] = (e < E) && (key[i] > t || (key[i] == t && __popcll(eq & below) < need));
+    need -= min(need, __popcll(eq));
+    msk[i] = __ballot(sel[i]);
   }
-  sum = group_sum<LPT>(sum);
-
-  // k rounds of group argmax; lane kk of the group keeps the kk-th pick.
-  float my_x = 0.f, my_ex = 0.f;
-  int my_id = -1;
-  for (int kk = 0; kk < k; ++kk) {
-    float bv = -INFINITY;
-    int be = 0x7fffffff;
+  // output slots
+  int slot[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) slot[i] = 0;
+#pragma unroll
+  for (int i2 = 0; i2 < EPL; ++i2) {
+    uint64_t m = msk[i2];
+    while (m) {
+      const int j = __builtin_ctzll(m);
+      m &= m - 1;
+      const uint32_t kj = __builtin_amdgcn_readlane(key[i2], j);
+      const int ej = j + 64 * i2;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        const int e = lane + 64 * i;
+        slot[i] += (kj > key[i] || (kj == key[i] && ej < e)) ? 1 : 0;
+      }
+    }
+  }
+  // weights
+  float wv[EPL];
+  if (mode == 0) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) mx = fmaxf(mx, x[i]);
+    mx = wave_max_f(mx);
+    float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
-      const int e = sub + LPT * i;
-      if (!taken[i] && (x[i] > bv || (x[i] == bv && e < be) || be == 0x7fffffff)) {
-        bv = x[i];
-        be = e;
-      }
+      wv[i] = (lane + 64 * i) < E ? expf(x[i] - mx) : 0.f;
+      sum += wv[i];
     }
-    if constexpr (LPT == 16) {
-      argmax_take(bv, be, dpp_f32<kDppXor1>(bv), dpp_i32<kDppXor1>(be));
-      argmax_take(bv, be, dpp_f32<kDppXor2>(bv), dpp_i32<kDppXor2>(be));
-      argmax_take(bv, be, dpp_f32<kDppRor4>(bv), dpp_i32<kDppRor4>(be));
-      argmax_take(bv, be, dpp_f32<kDppRor8>(bv), dpp_i32<kDppRor8>(be));
-    } else {
+    sum = wave_sum_f(sum);
+    float ssel = 0.f;
 #pragma unroll
-      for (int o = LPT / 2; o > 0; o >>= 1)
-        argmax_take(bv, be, __shfl_xor(bv, o, 64), __shfl_xor(be, o, 64));
+    for (int i = 0; i < EPL; ++i) {
+      wv[i] = wv[i] / sum;
+      ssel += sel[i] ? wv[i] : 0.f;
     }
-    // owner of expert be marks it taken and publishes its exp value
-    const int owner = be % LPT, slot = be / LPT;
-    float ex_be = 0.f;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i)
-      if (i == slot) {
-        ex_be = ex[i];
-        if (sub == owner) taken[i] = true;
-      }
-    ex_be = __shfl(ex_be, gbase + owner, 64);
-    if (sub == kk) {
-      my_x = bv;
-      my_ex = ex_be;
-      my_id = be;
-    }
-  }
-
-  float w;
-  if (mode == 0) {
-    w = my_ex / sum;
     if (renorm) {
-      const float ws = group_sum<LPT>(sub < k ? w : 0.f);
-      w = w / ws;
+      ssel = wave_sum_f(ssel);
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) wv[i] = wv[i] / ssel;
     }
   } else {
-    const float top = __shfl(my_x, gbase, 64);
-    const float e = sub < k ? expf(my_x - top) : 0.f;
-    w = e / group_sum<LPT>(e);
+    float top = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) top = fmaxf(top, sel[i] ? x[i] : -INFINITY);
+    top = wave_max_f(top);
+    float ssum = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      wv[i] = sel[i] ? expf(x[i] - top) : 0.f;
+      ssum += wv[i];
+    }
+    ssum = wave_sum_f(ssum);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) wv[i] = wv[i] / ssum;
   }
-  if (sub < k) {
-    w_out[tok * k + sub] = w;
-    id_out[tok * k + sub] = (n_non_padded >= 0 && tok >= n_non_padded) ? -1 : my_id;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    if (sel[i]) {
+      w_out[tok * k + slot[i]] = wv[i];
+      id_out[tok * k + slot[i]] = padded_tok ? -1 : lane + 64 * i;
+    }
   }
+}
+
+template <int DT, int EPL>
+__global__ __launch_bounds__(256) void moe_topk_wave_kernel(
+    float* __restrict__ w_out, int32_t* __restrict__ id_out, const void* __restrict__ logits_,
+    int64_t T, int E, int k, int renorm, int mode, int64_t n_non_padded) {
+  const int lane = threadIdx.x & 63;
+  const int64_t tok = (int64_t(blockIdx.x) * 256 + threadIdx.x) >> 6;
+  if (tok >= T) return;  // whole waves leave together
+  bool sel[EPL];
+  topk_one_token<DT, EPL>(w_out, id_out,
+                          reinterpret_cast<const typename Elem<DT>::T*>(logits_), tok, E, k,
+                          renorm, mode, n_non_padded >= 0 && tok >= n_non_padded, lane, sel);
+}
+
+// Top-k with the permute plan's histogram: block c (16 waves) routes tokens
+// [c * tpb, (c + 1) * tpb), which are exactly plan chunk c (csz = tpb * k routes), and writes
+// chunk_off[e][c] = routes of expert e in the chunk; routes of padded tokens (id -1) get
+// route_pos = -1. moe_align_place then builds the plan from the table.
+template <int DT, int EPL>
+__global__ __launch_bounds__(1024) void moe_topk_hist_kernel(
+    float* __restrict__ w_out, int32_t* __restrict__ id_out, const void* __restrict__ logits_,
+    int64_t T, int E, int k, int renorm, int mode, int64_t n_non_padded, int tpb,
+    int32_t* __restrict__ chunk_off, int32_t* __restrict__ route_pos) {
+  extern __shared__ int32_t hist[];  // [E + 1]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = blockIdx.x;
+  for (int e = tid; e <= E; e += 1024) hist[e] = 0;
+  __syncthreads();
+  for (int j = wave; j < tpb; j += 16) {
+    const int64_t tok = int64_t(c) * tpb + j;
+    if (tok >= T) break;
+    const bool padded_tok = n_non_padded >= 0 && tok >= n_non_padded;
+    bool sel[EPL];
+    topk_one_token<DT, EPL>(w_out, id_out,
+                            reinterpret_cast<const typename Elem<DT>::T*>(logits_), tok, E, k,
+                            renorm, mode, padded_tok, lane, sel);
+    if (padded_tok) {
+      if (route_pos && lane < k) route_pos[tok * k + lane] = -1;
+    } else {
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (sel[i]) atomicAdd(&hist[lane + 64 * i], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e <= E; e += 1024) chunk_off[int64_t(e) * ALIGN_MAX_CHUNKS + c] = hist[e];
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -164,7 +217,6 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(
 //                      per-expert count in LDS gives sorted position
 //                      base[e] + chunk_off[e][c] + running[e] + rank (ascending route index).
 // ---------------------------------------------------------------------------------------------
-constexpr int ALIGN_MAX_CHUNKS = 128;
 constexpr int ALIGN_SCAN_THREADS = 1024;
 
 __global__ __launch_bounds__(256) void moe_align_hist(int32_t* __restrict__ chunk_off,
@@ -293,6 +345,188 @@ __global__ __launch_bounds__(256) void moe_align_scatter(
     __syncthreads();
     if (ok) atomicAdd(&running[e], 1);
     __syncthreads();
+  }
+}
+
+// Placement in one launch after moe_align_hist (replaces scan + scatter when E_eff <= 1024):
+// one 256-thread block per chunk c. Each block derives what it needs from the histogram table
+// itself: for every expert e (a thread per expert) its total over all chunks and its count in
+// the chunks before c; an exclusive scan of the padded totals gives the expert bases (every
+// block computes the same bases), so a route of chunk c goes to
+//     base[e] + (routes of e in chunks < c) + (routes of e earlier in chunk c).
+// The last term: in rounds of 256 routes, the rank among the earlier lanes of its wave
+// (readlane loop), plus the routes of e in the earlier waves of the round (per-wave counts in
+// LDS), plus the routes of e in the earlier rounds (a running count per expert).
+// Block c also does a stripe of the fills: expert_ids and padding sentinels of the experts
+// e = c, c + nch, ..., and of the tail past num_tokens_post_pad.
+constexpr int ALIGN_PLACE_MAX_E = 512;   // LDS: (4 + 16 waves) x E_eff ints
+
+// Sum over the wave (modulo 2^32), wave-uniform: DPP inside rows of 16, then the four row sums
+// by readlane.
+__device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
+  v += uint32_t(dpp_i32<kDppXor1>(int(v)));
+  v += uint32_t(dpp_i32<kDppXor2>(int(v)));
+  v += uint32_t(dpp_i32<kDppRor4>(int(v)));
+  v += uint32_t(dpp_i32<kDppRor8>(int(v)));
+  return uint32_t(__builtin_amdgcn_readlane(int(v), 0)) +
+         uint32_t(__builtin_amdgcn_readlane(int(v), 16)) +
+         uint32_t(__builtin_amdgcn_readlane(int(v), 32)) +
+         uint32_t(__builtin_amdgcn_readlane(int(v), 48));
+}
+
+// Inclusive prefix sum over the 64 lanes by DPP: row_shr 1/2/4/8 inside rows of 16 (lanes
+// without a source add 0), then row_bcast:15 into rows 1 and 3 and row_bcast:31 into rows 2, 3.
+__device__ __forceinline__ int wave_incl_scan_dpp(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);
+  return x;
+}
+
+constexpr int PLACE_THREADS = 1024, PLACE_WAVES = PLACE_THREADS / 64;
+
+__global__ __launch_bounds__(PLACE_THREADS) void moe_align_place(
+    int32_t* __restrict__ sorted, int32_t* __restrict__ expert_ids,
+    int32_t* __restrict__ npp_out, int32_t* __restrict__ route_pos,
+    const int32_t* __restrict__ chunk_off, const int32_t* __restrict__ ids, int64_t numel,
+    int64_t csz, int nch, int E_eff, int bs, int64_t max_padded) {
+  // start[E_eff] | total[E_eff] | running[E_eff] | count[E_eff] | wcnt[PLACE_WAVES][E_eff]
+  extern __shared__ int32_t pl[];
+  int32_t* start = pl;
+  int32_t* total = pl + E_eff;
+  int32_t* running = pl + 2 * E_eff;
+  int32_t* count = pl + 3 * E_eff;
+  int32_t* wcnt = pl + 4 * E_eff;
+  __shared__ int32_t npp_lds;
+  const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t lo = int64_t(c) * csz, hi = min(numel, lo + csz);
+  // the first round's expert ids, fetched before the histogram reads and parked in LDS right
+  // after those reads are issued, so both latencies overlap
+  __shared__ int32_t first_ids[PLACE_THREADS];
+  int e_first = -1;
+  if (lo + tid < hi) e_first = ids[lo + tid];
+
+  // 1. per expert: routes in the chunks before c, and in all chunks. A wave reads an expert's
+  //    row of chunk counts with one instruction (lane: chunks 2l, 2l + 1), EB rows in flight
+  //    at once, and folds each row with one wave sum (both counts packed in one word when the
+  //    plan has fewer than 2^16 routes).
+  constexpr int EB = 12, CPL = ALIGN_MAX_CHUNKS / 64;   // chunks per lane
+  static_assert(CPL == 4, "one int4 of chunk counts per lane");
+  const bool packed = numel < 65536;
+  const int cb = CPL * lane;
+  for (int eb = wave * EB; eb < E_eff; eb += PLACE_WAVES * EB) {
+    int4 v[EB];
+#pragma unroll
+    for (int j = 0; j < EB; ++j) {
+      const int e = eb + j;
+      v[j] = make_int4(0, 0, 0, 0);
+      if (e < E_eff && cb < nch)
+        v[j] = *reinterpret_cast<const int4*>(chunk_off + int64_t(e) * ALIGN_MAX_CHUNKS + cb);
+    }
+    if (eb == wave * EB) first_ids[tid] = e_first;
+#pragma unroll
+    for (int j = 0; j < EB; ++j) {
+      const int x[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+      int sum_l = 0, pre_s = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int xv = cb + q < nch ? x[q] : 0;   // chunks past nch were never written
+        sum_l += xv;
+        pre_s += cb + q < c ? xv : 0;
+      }
+      const uint32_t pre_l = uint32_t(pre_s);
+      int all, pre;
+      if (packed) {   // both sums < 2^16: no carry between the halves
+        const uint32_t both = wave_sum_u((uint32_t(sum_l) << 16) | pre_l);
+        all = int(both >> 16);
+        pre = int(both & 0xffffu);
+      } else {
+        all = int(wave_sum_u(uint32_t(sum_l)));
+        pre = int(wave_sum_u(pre_l));
+      }
+      const int e = eb + j;
+      if (lane == 0 && e < E_eff) {
+        start[e] = pre;
+        total[e] = all;
+        count[e] = all;
+        running[e] = 0;
+      }
+    }
+  }
+  if (wave * EB >= E_eff) first_ids[tid] = e_first;   // waves without expert rows
+  for (int i = tid; i < PLACE_WAVES * E_eff; i += PLACE_THREADS) wcnt[i] = 0;
+  __syncthreads();
+  // 2. exclusive scan of the padded totals, by wave 0 (consecutive experts per lane)
+  if (wave == 0) {
+    const int per = (E_eff + 63) / 64;
+    const int e0 = min(E_eff, lane * per), e1 = min(E_eff, e0 + per);
+    int32_t mine = 0;
+    for (int e = e0; e < e1; ++e) mine += ((total[e] + bs - 1) / bs) * bs;
+    const int32_t incl = wave_incl_scan_dpp(mine);
+    int32_t off = incl - mine;
+    if (lane == 63) npp_lds = incl;
+    for (int e = e0; e < e1; ++e) {
+      const int32_t padded = ((total[e] + bs - 1) / bs) * bs;
+      start[e] += off;                   // base[e] + routes of e in the chunks before c
+      total[e] = off;                    // from here on: base[e]
+      off += padded;
+    }
+  }
+  __syncthreads();
+  const int32_t npp = npp_lds;
+  // 3. fills of this block's stripe of experts and of the tail
+  for (int e = c; e < E_eff; e += nch) {
+    const int32_t base = total[e];
+    const int32_t cnt = (e + 1 < E_eff ? total[e + 1] : npp) - base;  // padded extent
+    const int32_t n_e = count[e];                                      // unpadded count
+    for (int b = tid; b < cnt / bs; b += PLACE_THREADS) expert_ids[base / bs + b] = e;
+    for (int i = n_e + tid; i < cnt; i += PLACE_THREADS) sorted[base + i] = int32_t(numel);
+  }
+  for (int64_t i = npp + int64_t(c) * PLACE_THREADS + tid; i < max_padded;
+       i += int64_t(nch) * PLACE_THREADS)
+    sorted[i] = int32_t(numel);
+  const int64_t max_blocks = (max_padded + bs - 1) / bs;
+  for (int64_t i = npp / bs + int64_t(c) * PLACE_THREADS + tid; i < max_blocks;
+       i += int64_t(nch) * PLACE_THREADS)
+    expert_ids[i] = -1;
+  if (c == 0 && tid == 0) npp_out[0] = npp;
+  // 4. placement of the chunk's routes, PLACE_THREADS at a time in route order
+  for (int64_t s0 = lo; s0 < hi; s0 += PLACE_THREADS) {
+    const int64_t i = s0 + tid;
+    int e = s0 == lo ? first_ids[tid] : (i < hi ? ids[i] : -1);
+    if (e < 0 || e >= E_eff) e = -1;
+    int rank = 0;
+    if (s0 + int64_t(wave) * 64 < hi) {   // wave-uniform: waves past the chunk's end skip
+#pragma unroll 16
+      for (int j = 0; j < 64; ++j) {
+        const int ej = __builtin_amdgcn_readlane(e, j);
+        rank += (j < lane && ej == e) ? 1 : 0;
+      }
+    }
+    if (e >= 0) atomicAdd(&wcnt[wave * E_eff + e], 1);
+    __syncthreads();
+    if (e >= 0) {
+      int32_t before = 0;
+      for (int w = 0; w < wave; ++w) before += wcnt[w * E_eff + e];
+      const int32_t pos = start[e] + running[e] + before + rank;
+      sorted[pos] = int32_t(i);
+      if (route_pos) route_pos[i] = pos;
+    }
+    __syncthreads();
+    if (s0 + PLACE_THREADS < hi) {
+      for (int x = tid; x < E_eff; x += PLACE_THREADS) {
+        int32_t sum = 0;
+        for (int w = 0; w < PLACE_WAVES; ++w) {
+          sum += wcnt[w * E_eff + x];
+          wcnt[w * E_eff + x] = 0;
+        }
+        running[x] += sum;
+      }
+      __syncthreads();
+    }
   }
 }
 
@@ -581,37 +815,27 @@ extern "C" int pia_moe_topk(float* topk_weights, int32_t* topk_ids, const void* 
   if (num_tokens == 0) return 0;
   if (!topk_weights || !topk_ids || !logits) return fail(PIA_EINVAL, "moe_topk: null pointer");
   hipStream_t s = as_stream(stream);
-  const bool narrow = topk <= 16 && num_experts <= 256;  // 16 lanes per token
-  const int lpt = narrow ? 16 : 64;
-  const int64_t blocks = ceil_div(num_tokens * lpt, 256);
-  if (blocks > 0x7fffffff) return fail(PIA_EINVAL, "moe_topk: too many tokens");
-  const int epl = int(ceil_div(num_experts, lpt));
-#define PIA_TK(DT, EPL, LPT)                                                                    \
-  hipLaunchKernelGGL((moe_topk_kernel<DT, EPL, LPT>), dim3(unsigned(blocks)), dim3(256), 0, s,  \
-                     topk_weights, topk_ids, logits, num_tokens, num_experts, topk, renormalize, \
-                     mode, num_token_non_padded)
-#define PIA_TK_DT(DT)                                \
-  if (narrow) {                                      \
-    if (epl <= 1) PIA_TK(DT, 1, 16);                 \
-    else if (epl <= 2) PIA_TK(DT, 2, 16);            \
-    else if (epl <= 4) PIA_TK(DT, 4, 16);            \
-    else if (epl <= 8) PIA_TK(DT, 8, 16);            \
-    else PIA_TK(DT, 16, 16);                         \
-  } else {                                           \
-    if (epl <= 1) PIA_TK(DT, 1, 64);                 \
-    else if (epl <= 2) PIA_TK(DT, 2, 64);            \
-    else if (epl <= 4) PIA_TK(DT, 4, 64);            \
-    else if (epl <= 8) PIA_TK(DT, 8, 64);            \
-    else PIA_TK(DT, 16, 64);                         \
-  }
+  const int64_t wblocks = ceil_div(num_tokens * 64, 256);
+  if (wblocks > 0x7fffffff) return fail(PIA_EINVAL, "moe_topk: too many tokens");
+  const int wepl = int(ceil_div(num_experts, 64));
+#define PIA_TW(DT, EPL)                                                                       \
+  hipLaunchKernelGGL((moe_topk_wave_kernel<DT, EPL>), dim3(unsigned(wblocks)), dim3(256), 0, \
+                     s, topk_weights, topk_ids, logits, num_tokens, num_experts, topk,       \
+                     renormalize, mode, num_token_non_padded)
+#define PIA_TW_DT(DT)              \
+  if (wepl <= 1) PIA_TW(DT, 1);    \
+  else if (wepl <= 2) PIA_TW(DT, 2); \
+  else if (wepl <= 4) PIA_TW(DT, 4); \
+  else if (wepl <= 8) PIA_TW(DT, 8); \
+  else PIA_TW(DT, 16);
   switch (logits_dtype) {
-    case PIA_DTYPE_F32: PIA_TK_DT(PIA_DTYPE_F32); break;
-    case PIA_DTYPE_BF16: PIA_TK_DT(PIA_DTYPE_BF16); break;
-    case PIA_DTYPE_F16: PIA_TK_DT(PIA_DTYPE_F16); break;
+    case PIA_DTYPE_F32: PIA_TW_DT(PIA_DTYPE_F32); break;
+    case PIA_DTYPE_BF16: PIA_TW_DT(PIA_DTYPE_BF16); break;
+    case PIA_DTYPE_F16: PIA_TW_DT(PIA_DTYPE_F16); break;
     default: return fail(PIA_EINVAL, "moe_topk: unknown logits dtype");
   }
-#undef PIA_TK_DT
-#undef PIA_TK
+#undef PIA_TW_DT
+#undef PIA_TW
   return check_launch("moe_topk");
 }
 
@@ -658,6 +882,13 @@ extern "C" int pia_moe_align_block_size(int32_t* sorted_token_ids, int32_t* expe
                        route_pos, topk_ids, numel, csz, E_eff);
     if (int rc = check_launch("moe_align_hist")) return rc;
   }
+  if (nch > 0 && E_eff <= ALIGN_PLACE_MAX_E) {
+    hipLaunchKernelGGL(moe_align_place, dim3(unsigned(nch)), dim3(PLACE_THREADS),
+                       size_t(4 + PLACE_WAVES) * E_eff * sizeof(int32_t), s, sorted_token_ids, expert_ids,
+                       num_tokens_post_pad, route_pos, chunk_off, topk_ids, numel, csz, nch,
+                       E_eff, block_size, max_num_tokens_padded);
+    return check_launch("moe_align_place");
+  }
   hipLaunchKernelGGL(moe_align_scan, dim3(1), dim3(ALIGN_SCAN_THREADS), lds, s, sorted_token_ids,
                      expert_ids, num_tokens_post_pad, chunk_off, base, nch, E_eff, block_size,
                      numel, max_num_tokens_padded);
@@ -668,6 +899,74 @@ extern "C" int pia_moe_align_block_size(int32_t* sorted_token_ids, int32_t* expe
     if (int rc = check_launch("moe_align_scatter")) return rc;
   }
   return 0;
+}
+
+extern "C" int pia_moe_topk_align(float* topk_weights, int32_t* topk_ids, const void* logits,
+                                  int logits_dtype, int64_t num_tokens, int num_experts, int topk,
+                                  int renormalize, int mode, int64_t num_token_non_padded,
+                                  int32_t* sorted_token_ids, int32_t* expert_ids,
+                                  int32_t* num_tokens_post_pad, int32_t* route_pos,
+                                  int block_size, int64_t max_num_tokens_padded, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  const int64_t numel = num_tokens * int64_t(topk);
+  const int E_eff = num_experts + 1;
+  // chunks of tpb tokens: one top-k block and one plan chunk each
+  int64_t tpb = std::max<int64_t>(16, ceil_div(num_tokens, ALIGN_MAX_CHUNKS));
+  tpb = ceil_div(tpb, 16) * 16;
+  const bool fused = num_tokens > 0 && topk > 0 && topk <= 64 && num_experts > 0 &&
+                     num_experts <= 1024 && numel > ALIGN_SMALL_MAX && E_eff <= ALIGN_PLACE_MAX_E &&
+                     tpb * topk < 0x7fffffff;
+  if (!fused) {
+    if (int rc = pia_moe_topk(topk_weights, topk_ids, logits, logits_dtype, num_tokens,
+                              num_experts, topk, renormalize, mode, num_token_non_padded, stream))
+      return rc;
+    return pia_moe_align_block_size(sorted_token_ids, expert_ids, num_tokens_post_pad, route_pos,
+                                    topk_ids, numel, num_experts, block_size,
+                                    max_num_tokens_padded, workspace, workspace_bytes, stream);
+  }
+  if (mode != 0 && mode != 1) return fail(PIA_EINVAL, "moe_topk_align: mode must be 0 or 1");
+  if (topk > num_experts) return fail(PIA_EINVAL, "moe_topk_align: topk > num_experts");
+  if (block_size <= 0) return fail(PIA_EINVAL, "moe_topk_align: block_size must be > 0");
+  if (numel >= 0x7fffffff || max_num_tokens_padded >= 0x7fffffff)
+    return fail(PIA_EINVAL, "moe_topk_align: sizes must fit int32");
+  if (!topk_weights || !topk_ids || !logits || !sorted_token_ids || !expert_ids ||
+      !num_tokens_post_pad || !workspace)
+    return fail(PIA_EINVAL, "moe_topk_align: null pointer");
+  if (workspace_bytes < pia_moe_align_workspace_bytes(num_experts))
+    return fail(PIA_EINVAL, "moe_topk_align: workspace too small");
+  if (!aligned(workspace, 16)) return fail(PIA_EINVAL, "moe_topk_align: workspace must be 16-byte aligned");
+  if (max_num_tokens_padded < std::min<int64_t>(numel + int64_t(E_eff) * (block_size - 1),
+                                                numel * block_size))
+    return fail(PIA_EINVAL, "moe_topk_align: max_num_tokens_padded below the padded worst case");
+  hipStream_t s = as_stream(stream);
+  const int nch = int(ceil_div(num_tokens, tpb));
+  int32_t* chunk_off = reinterpret_cast<int32_t*>(workspace);
+  const int epl = int(ceil_div(num_experts, 64));
+  const size_t lds = size_t(E_eff) * sizeof(int32_t);
+#define PIA_TH(DT, EPL)                                                                           \
+  hipLaunchKernelGGL((moe_topk_hist_kernel<DT, EPL>), dim3(unsigned(nch)), dim3(1024), lds, s,    \
+                     topk_weights, topk_ids, logits, num_tokens, num_experts, topk, renormalize,  \
+                     mode, num_token_non_padded, int(tpb), chunk_off, route_pos)
+#define PIA_TH_DT(DT)                      \
+  if (epl <= 1) PIA_TH(DT, 1);             \
+  else if (epl <= 2) PIA_TH(DT, 2);        \
+  else if (epl <= 4) PIA_TH(DT, 4);        \
+  else if (epl <= 8) PIA_TH(DT, 8);        \
+  else PIA_TH(DT, 16);
+  switch (logits_dtype) {
+    case PIA_DTYPE_F32: PIA_TH_DT(PIA_DTYPE_F32); break;
+    case PIA_DTYPE_BF16: PIA_TH_DT(PIA_DTYPE_BF16); break;
+    case PIA_DTYPE_F16: PIA_TH_DT(PIA_DTYPE_F16); break;
+    default: return fail(PIA_EINVAL, "moe_topk_align: unknown logits dtype");
+  }
+#undef PIA_TH_DT
+#undef PIA_TH
+  if (int rc = check_launch("moe_topk_hist")) return rc;
+  hipLaunchKernelGGL(moe_align_place, dim3(unsigned(nch)), dim3(PLACE_THREADS),
+                     size_t(4 + PLACE_WAVES) * E_eff * sizeof(int32_t), s, sorted_token_ids,
+                     expert_ids, num_tokens_post_pad, route_pos, chunk_off, topk_ids, numel,
+                     tpb * topk, nch, E_eff, block_size, max_num_tokens_padded);
+  return check_launch("moe_align_place");
 }
 
 extern "C" int pia_moe_permute(void* x_perm, const void* hidden, const int32_t* sorted_token_ids,

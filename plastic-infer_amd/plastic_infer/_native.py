@@ -46,6 +46,8 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_moe_topk": (_I, [_P, _P, _P, _I, _L, _I, _I, _I, _I, _L, _P]),
     "pia_moe_align_workspace_bytes": (_L, [_I]),
     "pia_moe_align_block_size": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _L, _P, _L, _P]),
+    "pia_moe_topk_align": (_I, [_P, _P, _P, _I, _L, _I, _I, _I, _I, _L, _P, _P, _P, _P, _I, _L,
+                                _P, _L, _P]),
     "pia_moe_permute": (_I, [_P, _P, _P, _P, _P, _L, _L, _I, _L, _L, _P]),
     "pia_moe_unpermute": (_I, [_P, _P, _L, _P, _P, _L, _I, _I, _I, _P]),
     "pia_moe_sum_reduce": (_I, [_P, _P, _L, _I, _I, _I, _P]),

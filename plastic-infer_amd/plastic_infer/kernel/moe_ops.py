@@ -50,6 +50,36 @@ def moe_topk(logits: torch.Tensor, topk: int, renormalize: bool = True, mode: in
     return w, ids
 
 
+def moe_topk_align(logits: torch.Tensor, topk: int, block_size: int, renormalize: bool = True,
+                   mode: int = 0, num_token_non_padded: int | None = None):
+    """moe_topk then moe_align_block_size on its ids, in one call (two launches for large
+    plans: the router kernel also counts the plan's per-chunk experts).
+    Returns (weights, ids, sorted_token_ids, expert_ids, num_tokens_post_pad, route_pos)."""
+    dev = N.require_device(logits, names=("logits",))
+    if logits.dim() != 2:
+        raise ValueError("logits must be [num_tokens, num_experts]")
+    logits = logits.contiguous()
+    T, E = logits.shape
+    if not 0 < topk <= min(E, 64):
+        raise ValueError(f"topk must be in [1, min(num_experts, 64)], got {topk}")
+    w = torch.empty(T, topk, dtype=torch.float32, device=dev)
+    ids = torch.empty(T, topk, dtype=torch.int32, device=dev)
+    numel = T * topk
+    mpad = max_num_tokens_padded(numel, E, block_size)
+    sorted_ids = torch.empty(mpad, dtype=torch.int32, device=dev)
+    expert_ids = torch.empty((mpad + block_size - 1) // block_size, dtype=torch.int32, device=dev)
+    npp = torch.empty(1, dtype=torch.int32, device=dev)
+    route_pos = torch.empty(numel, dtype=torch.int32, device=dev)
+    ws_bytes = N.query("pia_moe_align_workspace_bytes", E)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    N.call("pia_moe_topk_align", w.data_ptr(), ids.data_ptr(), logits.data_ptr(),
+           N.dtype_code(logits.dtype), T, E, topk, 1 if renormalize else 0, mode,
+           -1 if num_token_non_padded is None else int(num_token_non_padded),
+           sorted_ids.data_ptr(), expert_ids.data_ptr(), npp.data_ptr(), route_pos.data_ptr(),
+           block_size, mpad, ws.data_ptr(), ws_bytes, N.stream_of(dev))
+    return w, ids, sorted_ids, expert_ids, npp, route_pos
+
+
 def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: int,
                          return_route_pos: bool = False):
     """(sorted_token_ids, expert_ids, num_tokens_post_pad[, route_pos]).

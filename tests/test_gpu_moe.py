@@ -175,3 +175,33 @@ def test_moe_forward_sparse_bf16_vs_reference_composition(dev):
     assert out.dtype == dt and ref.dtype == dt
     err = (out.float() - ref.float()).abs().max().item()
     assert err <= 4 * 2 ** -8 * ref.float().abs().max().item(), err
+
+
+@pytest.mark.parametrize("T,k,E,bs,dtype,n_np", [
+    (4096, 8, 128, 64, torch.float32, None),   # Qwen3-30B-A3B routing (two-launch path)
+    (600, 8, 64, 16, torch.float32, None),     # just past the one-block plan
+    (5000, 6, 200, 1, torch.bfloat16, 4900),   # 48-token chunks, ties in bf16, padded tokens
+    (2048, 8, 509, 16, torch.float16, None),   # the largest expert count of the fused path
+    (100, 2, 16, 16, torch.float32, 90),       # small: top-k then the one-block plan
+])
+def test_topk_align_matches_topk_then_oracle_plan(dev, T, k, E, bs, dtype, n_np):
+    """moe_topk_align: weights and ids bit-identical to moe_topk on the same logits (lowest
+    index first on ties, the stable argsort of the logits), the plan bit-exact against the
+    oracle's stable plan of those ids, route_pos -1 for the padded tokens' routes."""
+    from plastic_infer.kernel import moe_topk, moe_topk_align
+
+    g = torch.Generator().manual_seed(T + E)
+    logits = torch.randn(T, E, generator=g).to(dtype).to(dev)
+    w, ids, s, e, npp, pos = moe_topk_align(logits, k, bs, num_token_non_padded=n_np)
+    w1, ids1 = moe_topk(logits, k, True, num_token_non_padded=n_np)
+    assert torch.equal(ids, ids1) and torch.equal(w, w1)
+    lim = T if n_np is None else n_np
+    ref_ids = np.argsort(-logits.float().cpu().numpy(), 1, kind="stable")[:, :k]
+    assert np.array_equal(ids.cpu().numpy()[:lim], ref_ids[:lim])
+    assert (ids.cpu()[lim:] == -1).all()
+    rs, re_, rnpp, rpos = OM.moe_align_block_size(ids.cpu().numpy(), bs, E)
+    assert int(npp.item()) == rnpp
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(e.cpu().numpy()[:rnpp // bs], re_[:rnpp // bs])
+    assert (e.cpu().numpy()[rnpp // bs:] == -1).all()
+    assert np.array_equal(pos.cpu().numpy(), rpos)
