@@ -396,7 +396,9 @@ int pia_copy_rows_async(void* dst, const int64_t* dst_rows, const void* src,
  * dst_indices[j] = slot for j < *num_copy (the copy plan); stats (NULL or i64[3]) +=
  * (distinct ids, admitted misses, 1). Ids outside [0, num_total) are inert (out = -1). Misses
  * beyond the evictable slots are not admitted (out = -1); the reference leaves that case
- * undefined. Limits: num_queries <= 2048, 1 <= num_cached <= 16384.
+ * undefined. Limits: num_queries <= 2048, 1 <= num_cached <= 2^24 (caches of more than 16384
+ * slots stream their usage from global memory instead of holding it in LDS, with the same
+ * decisions; reference streaming variant src/plastic_infer/kernel/lru_ensure.py:214-270).
  * ------------------------------------------------------------------------------------------- */
 int pia_lru_ensure(const int32_t* query, int64_t num_queries, int32_t* slot_of_id,
                    int64_t num_total, int32_t* id_of_slot, int64_t* lru_usage,

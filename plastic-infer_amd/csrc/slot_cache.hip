@@ -119,33 +119,28 @@ constexpr int LRU_SPT = LRU_MAX_CACHED / LRU_THREADS;  // slots per thread in th
 constexpr int LRU_MAX_ROUNDS = 8;
 constexpr long long kUsageNone = 0x7fffffffffffffffll;
 
-__global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
-    const int32_t* __restrict__ query, int K, int32_t* __restrict__ slot_of_id,
-    int64_t num_total, int32_t* __restrict__ id_of_slot, int64_t* __restrict__ usage,
-    int C, int c_pad, int slot_bits, int64_t* __restrict__ step_ptr,
-    int32_t* __restrict__ out, int32_t* __restrict__ src_plan, int32_t* __restrict__ dst_plan,
-    int64_t* __restrict__ num_copy, int64_t* __restrict__ stats, int64_t id_base) {
-  // keys: the fallback sort; its first 8 KiB hold the round victims otherwise
-  __shared__ __attribute__((aligned(16))) unsigned long long keys[LRU_MAX_CACHED];
-  __shared__ __attribute__((aligned(16))) int32_t q_lds[LRU_MAX_QUERY];
-  __shared__ __attribute__((aligned(16))) int32_t fm_ids[LRU_MAX_QUERY];  // first misses' ids
-  __shared__ int32_t miss_ids[LRU_MAX_QUERY];
-  __shared__ int red[LRU_THREADS / 64 + 1];
-  __shared__ long long red64[LRU_THREADS / 64];
-  __shared__ int64_t step_lds;
-  int32_t* victims = reinterpret_cast<int32_t*>(keys);
-  const int tid = threadIdx.x;
-  constexpr int QPT = LRU_MAX_QUERY / LRU_THREADS;  // queries per thread
-  constexpr int kIdNone = 0x7fffffff;
+constexpr int LRU_QPT = LRU_MAX_QUERY / LRU_THREADS;  // queries per thread
+constexpr int kIdNone = 0x7fffffff;
 
+// Phase 1 of an admission call, shared by both kernels: advance the clock; load the query
+// (out-of-range ids are inert: never resident, never admitted, out = -1); find the first
+// occurrences and the first misses among them; bump every hit slot to the new step; rank every
+// missing position by the number of distinct missing ids below it (a duplicate shares its first
+// occurrence's rank) and list the distinct missing ids in ascending order in miss_ids.
+// Ends with a barrier, which also orders the hit bumps before any later read of usage.
+__device__ __forceinline__ void lru_phase1(
+    const int32_t* __restrict__ query, int K, const int32_t* __restrict__ slot_of_id,
+    int64_t num_total, int64_t* __restrict__ usage, int C, int64_t* __restrict__ step_ptr,
+    int64_t id_base, int32_t* q_lds, int32_t* fm_ids, int32_t* miss_ids, int* red,
+    int64_t* step_lds, int32_t (&qi)[LRU_QPT], int32_t (&si)[LRU_QPT], int (&rank)[LRU_QPT],
+    int* distinct_out, int* M_out, int64_t* step_out) {
+  const int tid = threadIdx.x;
+  constexpr int QPT = LRU_QPT;
   if (tid == 0) {
     const int64_t s = *step_ptr + 1;
     *step_ptr = s;
-    step_lds = s;
+    *step_lds = s;
   }
-  // Phase 1a: load the query (global ids; out-of-range ids are inert: never resident,
-  // never admitted, out = -1).
-  int32_t qi[QPT], si[QPT];
 #pragma unroll
   for (int r = 0; r < QPT; ++r) {
     const int i = tid + r * LRU_THREADS;
@@ -162,9 +157,7 @@ __global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
     if (i < LRU_MAX_QUERY) q_lds[i] = i < K ? qi[r] : -1;
   }
   __syncthreads();
-  const int64_t step = step_lds;
-
-  // Phase 1b: first occurrences and the first misses among them; bump every hit slot.
+  const int64_t step = *step_lds;
   int nfirst = 0, nfm = 0;
 #pragma unroll
   for (int r = 0; r < QPT; ++r) {
@@ -177,12 +170,8 @@ __global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
     nfm += fm ? 1 : 0;
     if (si[r] >= 0) usage[si[r]] = step;  // duplicated hits store the same value
   }
-  const int distinct = block_sum(nfirst, red);
-  const int M = block_sum(nfm, red);  // barriers inside also publish fm_ids[]
-
-  // Phase 1c: rank of every missing position = number of distinct missing ids below it
-  // (a duplicate shares its first occurrence's rank); the distinct ones list their id.
-  int rank[QPT];
+  *distinct_out = block_sum(nfirst, red);
+  *M_out = block_sum(nfm, red);  // barriers inside also publish fm_ids[]
 #pragma unroll
   for (int r = 0; r < QPT; ++r) {
     const int i = tid + r * LRU_THREADS;
@@ -192,8 +181,33 @@ __global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
     rank[r] = rk;
     if (fm_ids[i] != kIdNone) miss_ids[rk] = qi[r];
   }
-  __syncthreads();  // also orders the hit bumps before the usage reload below
+  __syncthreads();
+  *step_out = step;
+}
 
+__global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
+    const int32_t* __restrict__ query, int K, int32_t* __restrict__ slot_of_id,
+    int64_t num_total, int32_t* __restrict__ id_of_slot, int64_t* __restrict__ usage,
+    int C, int c_pad, int slot_bits, int64_t* __restrict__ step_ptr,
+    int32_t* __restrict__ out, int32_t* __restrict__ src_plan, int32_t* __restrict__ dst_plan,
+    int64_t* __restrict__ num_copy, int64_t* __restrict__ stats, int64_t id_base) {
+  // keys: the fallback sort; its first 8 KiB hold the round victims otherwise
+  __shared__ __attribute__((aligned(16))) unsigned long long keys[LRU_MAX_CACHED];
+  __shared__ __attribute__((aligned(16))) int32_t q_lds[LRU_MAX_QUERY];
+  __shared__ __attribute__((aligned(16))) int32_t fm_ids[LRU_MAX_QUERY];  // first misses' ids
+  __shared__ int32_t miss_ids[LRU_MAX_QUERY];
+  __shared__ int red[LRU_THREADS / 64 + 1];
+  __shared__ long long red64[LRU_THREADS / 64];
+  __shared__ int64_t step_lds;
+  int32_t* victims = reinterpret_cast<int32_t*>(keys);
+  const int tid = threadIdx.x;
+
+  int32_t qi[LRU_QPT], si[LRU_QPT];
+  int rank[LRU_QPT];
+  int distinct, M;
+  int64_t step;
+  lru_phase1(query, K, slot_of_id, num_total, usage, C, step_ptr, id_base, q_lds, fm_ids,
+             miss_ids, red, &step_lds, qi, si, rank, &distinct, &M, &step);
   int admitted = 0;
   bool sorted_path = false;
   const unsigned long long slot_mask = (1ull << slot_bits) - 1;
@@ -288,7 +302,7 @@ __global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
   }
   // out may alias query: every query read happened before the barriers above.
 #pragma unroll
-  for (int r = 0; r < QPT; ++r) {
+  for (int r = 0; r < LRU_QPT; ++r) {
     const int i = tid + r * LRU_THREADS;
     if (i >= K) continue;
     int32_t o = si[r];
@@ -296,6 +310,241 @@ __global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
       o = rank[r] < admitted ? (sorted_path ? int32_t(keys[rank[r]] & slot_mask)
                                             : victims[rank[r]])
                              : -1;
+    out[i] = o;
+  }
+  if (tid == 0) {
+    *num_copy = admitted;
+    if (stats) {
+      stats[0] += distinct;
+      stats[1] += admitted;
+      stats[2] += 1;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Admission over caches larger than the LDS-resident kernel holds (16384 < C <= 2^24 slots):
+// the same decisions, with the slot state streamed from global memory. Phase 1 is shared.
+// Victims: the `take` = min(M, evictable) smallest (usage, slot) keys among the untouched
+// slots, found without sorting the cache:
+//   a. one pass: smallest and largest usage of an evictable slot, and their count;
+//   b. a byte-wise radix select of the take-th smallest usage U over rel = usage - min (only
+//      the bytes in which rel can differ: an LRU cache's usages span few of them); per-byte
+//      256-bin histograms in LDS, updated once per distinct bin of a wave (the usages of an
+//      LRU cache cluster, so lanes mostly share bins); afterwards `need` is how many slots of
+//      usage U are victims, the lowest slots first;
+//   c. one pass in slot order collecting every evictable slot with usage < U and the first
+//      `need` with usage == U (exactly `take` slots);
+//   d. a bitonic sort of those by (usage, slot) in LDS.
+// Phase 3 is the install of the LDS kernel.
+// ---------------------------------------------------------------------------------------------
+constexpr int LRU_STREAM_MAX_CACHED = 1 << 24;
+constexpr int LRU_SORT_MAX = LRU_MAX_QUERY;  // victims per call (<= distinct misses)
+
+__device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v,
+                                                            unsigned long long* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long t = __shfl_xor(v, o, 64);
+    v = t > v ? t : v;
+  }
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  unsigned long long t = red[0];
+#pragma unroll
+  for (int w = 1; w < LRU_THREADS / 64; ++w) t = red[w] > t ? red[w] : t;
+  return t;
+}
+
+// hist[bin] += number of lanes of this wave with that bin (lanes with bin < 0 add nothing):
+// one LDS atomic per distinct bin of the wave.
+__device__ __forceinline__ void wave_bin_add(int* hist, int bin) {
+  uint64_t pending = __ballot(bin >= 0);
+  while (pending) {
+    const int leader = __builtin_ctzll(pending);
+    const int b = __builtin_amdgcn_readlane(bin, leader);
+    const uint64_t same = __ballot(bin == b) & pending;
+    if ((threadIdx.x & 63) == leader) atomicAdd(&hist[b], int(__popcll(same)));
+    pending &= ~same;
+  }
+}
+
+__global__ __launch_bounds__(LRU_THREADS) void lru_ensure_stream_kernel(
+    const int32_t* __restrict__ query, int K, int32_t* __restrict__ slot_of_id,
+    int64_t num_total, int32_t* __restrict__ id_of_slot, int64_t* __restrict__ usage, int C,
+    int64_t* __restrict__ step_ptr, int32_t* __restrict__ out, int32_t* __restrict__ src_plan,
+    int32_t* __restrict__ dst_plan, int64_t* __restrict__ num_copy, int64_t* __restrict__ stats,
+    int64_t id_base) {
+  __shared__ __attribute__((aligned(16))) int32_t q_lds[LRU_MAX_QUERY];
+  __shared__ __attribute__((aligned(16))) int32_t fm_ids[LRU_MAX_QUERY];
+  __shared__ int32_t miss_ids[LRU_MAX_QUERY];
+  __shared__ unsigned long long cand_u[LRU_SORT_MAX];  // victims' rel usage, then sorted keys
+  __shared__ int32_t cand_s[LRU_SORT_MAX];
+  __shared__ int hist[256];
+  __shared__ int red[LRU_THREADS / 64 + 1];
+  __shared__ unsigned long long red64[LRU_THREADS / 64];
+  __shared__ int64_t step_lds;
+  __shared__ int sel_lds[2];
+  const int tid = threadIdx.x;
+
+  int32_t qi[LRU_QPT], si[LRU_QPT];
+  int rank[LRU_QPT];
+  int distinct, M;
+  int64_t step;
+  lru_phase1(query, K, slot_of_id, num_total, usage, C, step_ptr, id_base, q_lds, fm_ids,
+             miss_ids, red, &step_lds, qi, si, rank, &distinct, &M, &step);
+  int admitted = 0;
+  if (M > 0) {
+    // a. range and count of the evictable usages
+    unsigned long long lmin = ~0ull, lmax = 0ull;
+    int nev = 0;
+    for (int c = tid; c < C; c += LRU_THREADS) {
+      const int64_t v = usage[c];
+      if (v != step) {
+        const unsigned long long k = static_cast<unsigned long long>(v) ^ (1ull << 63);
+        lmin = k < lmin ? k : lmin;
+        lmax = k > lmax ? k : lmax;
+        ++nev;
+      }
+    }
+    const unsigned long long kmin = ~block_max_u64(~lmin, red64);
+    const unsigned long long kmax = block_max_u64(lmax, red64);
+    const int take = min(M, block_sum(nev, red));
+    if (take > 0) {
+      // b. radix select of the take-th smallest rel = key - kmin
+      const unsigned long long range = kmax - kmin;
+      int nbytes = 0;
+      while (nbytes < 8 && (range >> (8 * nbytes)) != 0) ++nbytes;
+      unsigned long long prefix = 0;  // selected bytes above the current one
+      int left = take;                // rank (1-based) still to find inside the prefix
+      for (int byte = nbytes - 1; byte >= 0; --byte) {
+        for (int i = tid; i < 256; i += LRU_THREADS) hist[i] = 0;
+        __syncthreads();
+        const int sh = 8 * byte;
+        for (int c0 = 0; c0 < C; c0 += LRU_THREADS) {
+          const int c = c0 + tid;
+          int bin = -1;
+          if (c < C) {
+            const int64_t v = usage[c];
+            if (v != step) {
+              const unsigned long long rel =
+                  (static_cast<unsigned long long>(v) ^ (1ull << 63)) - kmin;
+              const unsigned long long above = sh + 8 < 64 ? (rel >> (sh + 8)) : 0ull;
+              if (above == (sh + 8 < 64 ? (prefix >> (sh + 8)) : 0ull))
+                bin = int((rel >> sh) & 255u);
+            }
+          }
+          wave_bin_add(hist, bin);
+        }
+        __syncthreads();
+        if (tid < 64) {  // one wave picks the bin holding the left-th key
+          int cnt[4], run = 0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            cnt[j] = hist[4 * tid + j];
+            run += cnt[j];
+          }
+          int incl = run;
+#pragma unroll
+          for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o, 64);
+            if (tid >= o) incl += t;
+          }
+          int before = incl - run;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (before < left && left <= before + cnt[j]) {
+              sel_lds[0] = 4 * tid + j;
+              sel_lds[1] = left - before;
+            }
+            before += cnt[j];
+          }
+        }
+        __syncthreads();
+        prefix |= static_cast<unsigned long long>(sel_lds[0]) << sh;
+        left = sel_lds[1];
+        __syncthreads();
+      }
+      const unsigned long long ustar = prefix;  // rel usage of the take-th smallest key
+      const int need = left;                    // slots of usage ustar to take, lowest first
+      // c. collect in slot order: rel < ustar, and the first `need` with rel == ustar
+      int n_lt = 0, n_eq = 0;
+      for (int c0 = 0; c0 < C; c0 += LRU_THREADS) {
+        const int c = c0 + tid;
+        unsigned long long rel = ~0ull;
+        if (c < C) {
+          const int64_t v = usage[c];
+          if (v != step) rel = (static_cast<unsigned long long>(v) ^ (1ull << 63)) - kmin;
+        }
+        const int lt = rel < ustar ? 1 : 0, eq = rel == ustar ? 1 : 0;
+        int tot_lt, tot_eq;
+        const int p_lt = block_excl_scan(lt, red, &tot_lt);
+        const int p_eq = block_excl_scan(eq, red, &tot_eq);
+        if (lt) {
+          cand_u[n_lt + p_lt] = rel;
+          cand_s[n_lt + p_lt] = c;
+        }
+        if (eq && n_eq + p_eq < need) {
+          const int at = (take - need) + n_eq + p_eq;
+          cand_u[at] = rel;
+          cand_s[at] = c;
+        }
+        n_lt += tot_lt;
+        n_eq += tot_eq;
+      }
+      __syncthreads();
+      // d. sort the take victims by (rel usage, slot): packed keys when the slot fits 24 bits
+      //    under a rel usage of at most 40 bits, else pairs compared field by field
+      int n_pad = 1;
+      while (n_pad < take) n_pad <<= 1;
+      for (int i = take + tid; i < n_pad; i += LRU_THREADS) {
+        cand_u[i] = ~0ull;
+        cand_s[i] = 0x7fffffff;
+      }
+      __syncthreads();
+      for (int size = 2; size <= n_pad; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          for (int t = tid; t < n_pad / 2; t += LRU_THREADS) {
+            const int lo = 2 * t - (t & (stride - 1));
+            const int hi = lo + stride;
+            const bool up = (lo & size) == 0;
+            const unsigned long long ua = cand_u[lo], ub = cand_u[hi];
+            const int sa = cand_s[lo], sb = cand_s[hi];
+            const bool a_gt_b = ua > ub || (ua == ub && sa > sb);
+            if (a_gt_b == up) {
+              cand_u[lo] = ub;
+              cand_u[hi] = ua;
+              cand_s[lo] = sb;
+              cand_s[hi] = sa;
+            }
+          }
+          __syncthreads();
+        }
+      }
+      admitted = take;
+      // Phase 3: install (as in the LDS kernel)
+      for (int i = tid; i < admitted; i += LRU_THREADS) {
+        const int victim = cand_s[i];
+        const int32_t e = miss_ids[i];
+        const int32_t old = id_of_slot[victim];
+        if (old >= 0 && old < num_total) slot_of_id[old] = -1;
+        id_of_slot[victim] = e;
+        slot_of_id[e] = victim;
+        usage[victim] = step;
+        dst_plan[i] = victim;
+        src_plan[i] = int32_t(int64_t(e) - id_base);
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < LRU_QPT; ++r) {
+    const int i = tid + r * LRU_THREADS;
+    if (i >= K) continue;
+    int32_t o = si[r];
+    if (rank[r] >= 0) o = rank[r] < admitted ? cand_s[rank[r]] : -1;
     out[i] = o;
   }
   if (tid == 0) {
@@ -434,12 +683,19 @@ extern "C" int pia_lru_ensure(const int32_t* query, int64_t num_queries, int32_t
     return fail(PIA_EINVAL, "lru_ensure: negative size");
   if (num_queries > LRU_MAX_QUERY)
     return fail(PIA_EUNSUPPORTED, "lru_ensure: more than 2048 queries per call");
-  if (num_cached < 1 || num_cached > LRU_MAX_CACHED)
-    return fail(PIA_EUNSUPPORTED, "lru_ensure: cache of 1..16384 slots supported");
+  if (num_cached < 1 || num_cached > LRU_STREAM_MAX_CACHED)
+    return fail(PIA_EUNSUPPORTED, "lru_ensure: cache of 1..2^24 slots supported");
   if (num_total > 0x7fffffff) return fail(PIA_EINVAL, "lru_ensure: id space beyond int32");
   if (!slot_of_id || !id_of_slot || !lru_usage || !lru_step || !num_copy ||
       (num_queries > 0 && (!query || !out_indices)) || !src_indices || !dst_indices)
     return fail(PIA_EINVAL, "lru_ensure: null pointer");
+  if (num_cached > LRU_MAX_CACHED) {
+    hipLaunchKernelGGL(lru_ensure_stream_kernel, dim3(1), dim3(LRU_THREADS), 0, as_stream(stream),
+                       query, int(num_queries), slot_of_id, num_total, id_of_slot, lru_usage,
+                       int(num_cached), lru_step, out_indices, src_indices, dst_indices,
+                       num_copy, stats, id_base);
+    return check_launch("lru_ensure_stream");
+  }
   int c_pad = 2, slot_bits = 1;
   while (c_pad < num_cached) {
     c_pad <<= 1;

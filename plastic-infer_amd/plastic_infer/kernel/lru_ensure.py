@@ -3,8 +3,11 @@
 Same call as the reference's ``lru_ensure`` (src/plastic_infer/kernel/lru_ensure.py:371-438),
 run by the HIP kernel ``pia_lru_ensure``: one launch on the current stream, fixed shapes, no
 host synchronisation. The reference routes between two strategies that it documents as
-bit-identical; here one kernel (a bitonic sort of packed (usage, slot) keys in LDS) serves
-every shape, so ``strategy`` only selects among the same results.
+bit-identical (register-resident argmins; a streaming insert for caches of 40000+ slots).
+Here caches of up to 16384 slots keep their state in LDS (victims by rounds of smallest
+usage), larger ones (up to 2^24 slots) stream it from global memory (a radix select of the
+victims' usage); both make the same decisions, so ``strategy`` only selects among the same
+results.
 """
 
 from __future__ import annotations
@@ -27,7 +30,7 @@ class Stat(IntEnum):
 N_STATS = len(Stat)
 _STRATEGIES = ("seq", "insert")
 MAX_QUERY = 2048
-MAX_CACHED = 16384
+MAX_CACHED = 1 << 24     # caches above 16384 slots take the streaming kernel
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -57,7 +60,7 @@ def lru_ensure(
     out_indices (K,) int32 out (may alias query); src_indices / dst_indices (>= min(K,
     num_cached),) int32 out; num_copy int64 [1] or () out; stats (3,) int64 accumulator or None.
     The distinct missing ids, ascending, take the least-recently-used slots not touched by
-    this call, lowest slot first on equal usage. K <= 2048, num_cached <= 16384.
+    this call, lowest slot first on equal usage. K <= 2048, num_cached <= 2^24.
     """
     if strategy is not None and strategy not in _STRATEGIES:
         raise KeyError(strategy)

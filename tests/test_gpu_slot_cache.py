@@ -165,6 +165,39 @@ def test_materialize_reset_invalidate_compact_match_oracle(dev):
     assert int(num) == 0
 
 
+@pytest.mark.parametrize("seed,total,cached,k,calls,spread", [
+    (10, 60000, 40000, 2000, 26, False),    # warm-up, then evictions among clustered usages
+    (11, 50000, 40000, 64, 3, False),       # a fresh cache: every usage 0, ties by slot
+    (12, 70000, 48000, 1500, 6, True),      # usages spread over five bytes: multi-pass select
+    (13, 200000, 131075, 700, 4, False),    # an odd cache size past 2^17
+])
+def test_lru_ensure_streamed_large_cache_matches_oracle(dev, seed, total, cached, k, calls,
+                                                        spread):
+    """Caches beyond the LDS-resident 16384 slots take the streaming admission kernel: the same
+    maps, usage, clock, plan and stats as the oracle's sequential argmin rule, call by call."""
+    rng = np.random.default_rng(seed)
+    st, ds = SC.new_state(total, cached), DevState(dev, total, cached)
+    if spread:   # usages of a long-running cache: distinct values over ~2^40
+        u = rng.integers(0, 1 << 40, size=cached).astype(np.int64)
+        st["usage"][:] = u
+        ds.usage.copy_(torch.from_numpy(u))
+        st["step"] = 1 << 41
+        ds.step.fill_(1 << 41)
+    stats = np.zeros(3, np.int64)
+    for c in range(calls):
+        ids = rng.choice(total, size=k, replace=False)
+        query = np.concatenate([ids, ids[: k // 10]])[:k] if c % 2 else ids
+        out, src, dst, n, dstats = SC.lru_ensure(st, query)
+        stats += dstats
+        got = ds.ensure(query, 0)
+        assert np.array_equal(got, out), c
+        assert int(ds.num) == n
+        assert np.array_equal(ds.dst.cpu().numpy()[:n], dst)
+        assert np.array_equal(ds.src.cpu().numpy()[:n], src)
+    ds.assert_equal(st)
+    assert np.array_equal(ds.stats.cpu().numpy(), stats)
+
+
 # ---- OffloadMoeCache --------------------------------------------------------------------------
 
 def _banks(L: int, E: int, H: int, I: int, seed: int):
