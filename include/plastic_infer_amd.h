@@ -195,7 +195,7 @@ int pia_paged_attention(void* out, const void* q, const void* k_pages, const voi
  * holds [num_kv_heads, head_dim]. Query row i sits at position q_start_pos + i; causal != 0 lets it
  * see keys at positions <= q_start_pos + i (the reference's mask, and SDPA is_causal when
  * q_start_pos == 0 and q_len == kv_len), causal == 0 sees all keys. Softmax in fp32; a row that
- * sees no key writes zeros. head_dim <= 256 (fp32: <= 128). workspace: at least
+ * sees no key writes zeros. head_dim <= 256. workspace: at least
  * pia_host_stream_attention_workspace_bytes(...) bytes of device memory (4-byte aligned).
  * ------------------------------------------------------------------------------------------- */
 int64_t pia_host_stream_attention_workspace_bytes(int64_t q_len, int num_heads, int num_kv_heads,
@@ -309,11 +309,13 @@ int pia_moe_sum_reduce(void* out, const void* in, int64_t num_tokens, int topk, 
  *                               out[r * ldo + n] = round(X(g) * u)              n < n_rows / 2
  * w_r = topk_weights[r] when mul_routed_weight != 0, else 1; round() is the storage dtype.
  * Routes of a block whose expert is outside [0, num_experts) get zero rows. Storage: a, w, out
- * bf16 or fp16 (dtype), topk_weights fp32 [numel]. k_dim and lda multiples of 8; a and w
- * 16-byte aligned; block_m a multiple of 16; a holds ceil(numel / a_div) rows. Small calls
- * (decode: fewer than 4096 routes) run a split-K kernel over 16-row plan blocks that streams
- * each expert's W once per block; larger calls run an LDS-tiled kernel over the experts present
- * in the plan (128 x 128 tiles). The first GEMM of the FFN is a_div = top_k
+ * bf16, fp16 or fp32 (dtype; for fp32 round() is the identity and the products are fp32
+ * MFMA products), topk_weights fp32 [numel]. k_dim and lda multiples of 8 (bf16 / fp16) or 4
+ * (fp32); a and w 16-byte aligned; block_m a multiple of 16; a holds ceil(numel / a_div) rows.
+ * Small calls (decode: fewer than 2048 routes) and every fp32 call run a split-K kernel over
+ * 16-row plan blocks that streams each expert's W once per block; larger bf16 / fp16 calls run
+ * an LDS-tiled kernel over the experts present in the plan (128 x 256 tiles). The first GEMM
+ * of the FFN is a_div = top_k
  * (a = hidden [T, H]) with the activation; the second is a_div = 1 (a = the first GEMM's
  * output [T*k, I]) without it, ldo = H, writing [T, k, H] for pia_moe_sum_reduce.
  * ------------------------------------------------------------------------------------------- */
@@ -333,7 +335,7 @@ int pia_moe_expert_gemm(void* out, const void* a, const void* w, const float* to
  * the plan on every call): (2 * ceil(max_num_tokens_padded / block_m) + 10) * 4. */
 int64_t pia_moe_expert_gemm_workspace_bytes(int64_t max_num_tokens_padded, int block_m);
 
-/* y[r, j] = round(act(x[r, j]) * x[r, d + j]) for x [rows, 2d], y [rows, d], bf16 or fp16
+/* y[r, j] = round(act(x[r, j]) * x[r, d + j]) for x [rows, 2d], y [rows, d], bf16, fp16 or fp32
  * (silu_and_mul / gelu_and_mul / gelu_tanh_and_mul, reference
  * src/plastic_infer/kernel/triton/activation.py:63-150). activation: PIA_ACT_SILU, _GELU,
  * _GELU_TANH. */

@@ -135,6 +135,9 @@ __global__ __launch_bounds__(256, 2) void hs_attn_partial(
   constexpr int TT = hs_tile_tokens(DM, int(sizeof(T)));
   constexpr int NV = DM * TT / VW / 256;   // 16-byte groups per thread per tile (K or V)
   constexpr int RPW = RT / 4;                   // query rows per wave
+  // tokens per compute step: one per lane, or all of a narrower tile (fp32 at head_dim > 128
+  // stages 32-token tiles; lanes SUB..63 then hold no token)
+  constexpr int SUB = TT < HS_SUB ? TT : HS_SUB;
   __shared__ __align__(16) T k_s[DM * TT];     // [d][t]
   __shared__ __align__(16) T v_s[TT * DM];     // [t][d]
   __shared__ float q_s[RT * DM];
@@ -239,19 +242,21 @@ __global__ __launch_bounds__(256, 2) void hs_attn_partial(
       if (cur.vec) fetch(cur);
     }
 
-    for (int sub = 0; sub * HS_SUB < tl; ++sub) {
-      const int tls = min(HS_SUB, tl - sub * HS_SUB);
+    // lanes past SUB read token 0 of the step (in bounds) and are masked below
+    const int tok = lane < SUB ? lane : 0;
+    for (int sub = 0; sub * SUB < tl; ++sub) {
+      const int tls = min(SUB, tl - sub * SUB);
       // QK^T: lane = token
       float s[RPW];
 #pragma unroll
       for (int k = 0; k < RPW; ++k) s[k] = 0.f;
 #pragma unroll 4
       for (int d = 0; d < D; ++d) {
-        const float kv = E::load(k_s, d * TT + sub * HS_SUB + lane);
+        const float kv = E::load(k_s, d * TT + sub * SUB + tok);
 #pragma unroll
         for (int k = 0; k < RPW; ++k) s[k] = fmaf(q_s[(wave + 4 * k) * DM + d], kv, s[k]);
       }
-      const int64_t pos = pos0 + sub * HS_SUB + lane;
+      const int64_t pos = pos0 + sub * SUB + lane;
 #pragma unroll
       for (int k = 0; k < RPW; ++k) {
         const bool valid = live[k] && lane < tls && (!causal || pos <= qpos[k]);
@@ -274,7 +279,7 @@ __global__ __launch_bounds__(256, 2) void hs_attn_partial(
 #pragma unroll
         for (int i = 0; i < DPL; ++i) {
           const int d = lane + 64 * i;
-          vv[i] = d < D ? E::load(v_s, (sub * HS_SUB + t) * DM + d) : 0.f;
+          vv[i] = d < D ? E::load(v_s, (sub * SUB + t) * DM + d) : 0.f;
         }
 #pragma unroll
         for (int k = 0; k < RPW; ++k) {
@@ -354,8 +359,8 @@ HsPlan hs_plan(int64_t q_len, int num_heads, int num_kv_heads, int head_dim, int
   HsPlan p{};
   p.kv_len = host_len + resident_len;
   const int dm = head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
-  // the smallest tile of any dtype when sizing the workspace
-  p.tt = elem_bytes > 0 ? hs_tile_tokens(dm, elem_bytes) : HS_SUB;
+  // the smallest tile of any dtype (the widest element, fp32) when sizing the workspace
+  p.tt = hs_tile_tokens(dm, elem_bytes > 0 ? elem_bytes : 4);
   const int64_t tpc = ceil_div(chunk_tokens, p.tt);
   const int64_t last = num_chunks > 0 ? host_len - int64_t(num_chunks - 1) * chunk_tokens : 0;
   p.tiles = (num_chunks > 0 ? int64_t(num_chunks - 1) * tpc + ceil_div(last, p.tt) : 0) +
@@ -423,7 +428,7 @@ int hs_launch(const HsGeom& g, const HsPlan& p, void* out, const void* q, int64_
   } while (0)
   if (D <= 64) PIA_HS(1);
   else if (D <= 128) PIA_HS(2);
-  else if constexpr (DT != PIA_DTYPE_F32) PIA_HS(4);
+  else PIA_HS(4);
 #undef PIA_HS
   return check_launch("hs_attn_merge");
 }
@@ -460,8 +465,6 @@ extern "C" int pia_host_stream_attention(
     return rc;
   if (dtype != PIA_DTYPE_F32 && dtype != PIA_DTYPE_F16 && dtype != PIA_DTYPE_BF16)
     return fail(PIA_EINVAL, "host_stream_attention: unknown dtype");
-  if (dtype == PIA_DTYPE_F32 && head_dim > 128)
-    return fail(PIA_EUNSUPPORTED, "host_stream_attention: fp32 needs head_dim <= 128");
   if (q_len == 0) return 0;
   if (!out || !q) return fail(PIA_EINVAL, "host_stream_attention: null q / out");
   if (num_chunks > 0 && (!chunk_k || !chunk_v))

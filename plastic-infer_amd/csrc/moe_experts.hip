@@ -17,13 +17,19 @@
 //
 // Kernel: moe_gemm_splitk. A work item is (16 plan rows, one column tile): 64 W rows, which are
 // 64 output columns, or 32 gate rows plus the matching 32 up rows when the activation is fused.
-// The four waves of a workgroup split the K dimension in quarters; each wave runs
-// v_mfma_f32_16x16x32 (bf16 / f16) over its quarter with the operands loaded straight from
-// global memory into registers (lane l: plan row / W row l%16, K elements 8*(l/16) .. +7 of a
-// 32-wide chunk; A and B use the same K assignment, so every MFMA sums the same K set for both).
+// The four waves of a workgroup split the K dimension in quarters; each wave multiplies its
+// quarter with the operands loaded straight from global memory into registers, one 16-byte
+// vector per lane, plan row / W row l%16, at K offset V*(l/16) of a 4V-wide chunk (V = 8
+// elements for bf16 / f16, 4 for fp32). bf16 / f16 run one v_mfma_f32_16x16x32 per vector;
+// fp32 runs four v_mfma_f32_16x16x4_f32, the j-th taking component j of the A and the W
+// vector, so lane group g supplies K index 4g + j of the chunk to both operands and the four
+// products cover the chunk's 16 K values once (fp32 products, fp32 sums: no rounding to a
+// narrower type anywhere, the epilogue's round() is the identity).
 // The four partial tiles meet in LDS and are summed in wave order (deterministic). Workgroups
 // are persistent over the items; W rows are streamed once per plan block, which is the HBM
 // bound at decode sizes (every expert's weights are read once per 16 routes it serves).
+#include <type_traits>
+
 #include "pia_internal.h"
 
 namespace pia {
@@ -32,6 +38,12 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Storage element of a dtype code and the elements in one 16-byte vector.
+template <int DT>
+using eg_elem = std::conditional_t<DT == PIA_DTYPE_F32, float, uint16_t>;
+template <int DT>
+constexpr int eg_vec = 16 / int(sizeof(eg_elem<DT>));
 
 constexpr int EG_ROWS = 16;       // plan rows per work item (MFMA M)
 constexpr int EG_WAVES = 4;       // waves per workgroup, one K quarter each
@@ -51,14 +63,31 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32(const uint4& a, const uint4& b,
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
+// One 16-byte vector of A and of W per lane: c += the 16 x 16 product over the 4 * eg_vec<DT>
+// K values the wave's lanes hold.
 template <int DT>
-__device__ __forceinline__ uint16_t to_dt(float v) {
-  if constexpr (DT == PIA_DTYPE_BF16) return f32_to_bf16(v);
+__device__ __forceinline__ f32x4_t mfma_vec(const uint4& a, const uint4& b, f32x4_t c) {
+  if constexpr (DT == PIA_DTYPE_F32) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.x), __uint_as_float(b.x), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.y), __uint_as_float(b.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.z), __uint_as_float(b.z), c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.w), __uint_as_float(b.w), c, 0,
+                                                0, 0);
+  } else {
+    return mfma_16x16x32<DT>(a, b, c);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ eg_elem<DT> to_dt(float v) {
+  if constexpr (DT == PIA_DTYPE_F32) return v;
+  else if constexpr (DT == PIA_DTYPE_BF16) return f32_to_bf16(v);
   else return f32_to_half(v);
 }
 template <int DT>
-__device__ __forceinline__ float from_dt(uint16_t x) {
-  if constexpr (DT == PIA_DTYPE_BF16) return bf16_to_f32(x);
+__device__ __forceinline__ float from_dt(eg_elem<DT> x) {
+  if constexpr (DT == PIA_DTYPE_F32) return x;
+  else if constexpr (DT == PIA_DTYPE_BF16) return bf16_to_f32(x);
   else return half_to_f32(x);
 }
 
@@ -77,11 +106,14 @@ __device__ __forceinline__ float act_fn(float g) {
 
 template <int DT, int ACT>
 __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_splitk(
-    uint16_t* __restrict__ out, const uint16_t* __restrict__ a, const uint16_t* __restrict__ w,
+    eg_elem<DT>* __restrict__ out, const eg_elem<DT>* __restrict__ a,
+    const eg_elem<DT>* __restrict__ w,
     const float* __restrict__ topk_w, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ expert_ids, const int32_t* __restrict__ npp, int64_t max_rows,
     int64_t numel, int block_m, int a_div, int64_t lda, int num_experts, int n_rows, int K,
     int64_t ldo, int n_tiles, int mulw) {
+  using E = eg_elem<DT>;
+  constexpr int V = eg_vec<DT>, CH = 4 * V;  // elements per lane vector, K per chunk
   constexpr bool FUSED = ACT != PIA_ACT_NONE;
   __shared__ float red[EG_WAVES][4][4][64];  // [wave][column block][row in quad][lane]
   __shared__ int32_t blk_route[EG_ROWS];
@@ -90,11 +122,11 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_splitk(
   const int li = lane & 15, kg = lane >> 4;
   const int64_t rows = min(max_rows, int64_t(npp[0]));
   const int64_t items = ((rows + EG_ROWS - 1) / EG_ROWS) * n_tiles;
-  const int nch = (K + 31) >> 5;
+  const int nch = (K + CH - 1) / CH;
   const int cpw = (nch + EG_WAVES - 1) / EG_WAVES;
   const int c0 = min(nch, wv * cpw), c1 = min(nch, c0 + cpw);
   const int half = n_rows >> 1;
-  const uint16_t* zero = g_zero8;
+  const E* zero = reinterpret_cast<const E*>(g_zero8);
 
   for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
     const int64_t mb = item / n_tiles;
@@ -104,9 +136,9 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_splitk(
     const int64_t p = mb * EG_ROWS + li;
     const int64_t r = p < rows ? int64_t(sorted[p]) : numel;
     const bool a_ok = r >= 0 && r < numel;
-    const uint16_t* arow = a + (a_ok ? (r / a_div) * lda : 0);
-    const uint16_t* wbase = w + (e_ok ? int64_t(e) * n_rows * K : 0);
-    const uint16_t* wrow[4];
+    const E* arow = a + (a_ok ? (r / a_div) * lda : 0);
+    const E* wbase = w + (e_ok ? int64_t(e) * n_rows * K : 0);
+    const E* wrow[4];
     bool w_ok[4];
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
@@ -135,7 +167,7 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_splitk(
 #pragma unroll
         for (int u = 0; u < EG_U; ++u) {
           const int cc = c + u;
-          const int k = cc * 32 + kg * 8;
+          const int k = cc * CH + kg * V;
           const bool k_ok = cc < c1 && k < K;
           va[u] = *reinterpret_cast<const uint4*>((k_ok && a_ok) ? arow + k : zero);
 #pragma unroll
@@ -148,7 +180,7 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_splitk(
 #pragma unroll
         for (int u = 0; u < EG_U; ++u)
 #pragma unroll
-          for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma_16x16x32<DT>(va[u], vb[u][cb], acc[cb]);
+          for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma_vec<DT>(va[u], vb[u][cb], acc[cb]);
       };
       load(sa0, sb0, c0);
       for (int c = c0; c < c1; c += 2 * EG_U) {
@@ -501,28 +533,31 @@ __global__ __launch_bounds__(TG_THREADS, 1) void moe_gemm_tiled(
   }
 }
 
-// y[r, j] = round(act(x[r, j]) * x[r, d + j]) over [rows, 2d] -> [rows, d]; eight elements per
-// thread on 16-byte aligned rows, one otherwise.
-template <int DT, int ACT, int VEC>
-__global__ __launch_bounds__(256) void act_and_mul_kernel(uint16_t* __restrict__ y,
-                                                          const uint16_t* __restrict__ x,
+// y[r, j] = round(act(x[r, j]) * x[r, d + j]) over [rows, 2d] -> [rows, d]; one 16-byte vector
+// per thread (eight bf16 / f16 or four fp32 elements) on 16-byte aligned rows, one element
+// otherwise.
+template <int DT, int ACT, bool VEC>
+__global__ __launch_bounds__(256) void act_and_mul_kernel(eg_elem<DT>* __restrict__ y,
+                                                          const eg_elem<DT>* __restrict__ x,
                                                           int64_t rows, int64_t d) {
-  const int64_t per_row = d / VEC;
+  using E = eg_elem<DT>;
+  constexpr int W = VEC ? eg_vec<DT> : 1;
+  const int64_t per_row = d / W;
   const int64_t total = rows * per_row;
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total;
        i += int64_t(gridDim.x) * 256) {
-    const int64_t r = i / per_row, j = (i - r * per_row) * VEC;
-    const uint16_t* xr = x + r * 2 * d;
-    uint16_t* yr = y + r * d;
-    if constexpr (VEC == 8) {
+    const int64_t r = i / per_row, j = (i - r * per_row) * W;
+    const E* xr = x + r * 2 * d;
+    E* yr = y + r * d;
+    if constexpr (VEC) {
       const uint4 gv = *reinterpret_cast<const uint4*>(xr + j);
       const uint4 uv = *reinterpret_cast<const uint4*>(xr + d + j);
-      const uint16_t* g = reinterpret_cast<const uint16_t*>(&gv);
-      const uint16_t* u = reinterpret_cast<const uint16_t*>(&uv);
+      const E* g = reinterpret_cast<const E*>(&gv);
+      const E* u = reinterpret_cast<const E*>(&uv);
       uint4 ov;
-      uint16_t* o = reinterpret_cast<uint16_t*>(&ov);
+      E* o = reinterpret_cast<E*>(&ov);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) o[q] = to_dt<DT>(act_fn<ACT>(from_dt<DT>(g[q])) * from_dt<DT>(u[q]));
+      for (int q = 0; q < W; ++q) o[q] = to_dt<DT>(act_fn<ACT>(from_dt<DT>(g[q])) * from_dt<DT>(u[q]));
       *reinterpret_cast<uint4*>(yr + j) = ov;
     } else {
       yr[j] = to_dt<DT>(act_fn<ACT>(from_dt<DT>(xr[j])) * from_dt<DT>(xr[d + j]));
@@ -548,17 +583,22 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
                                    int a_div, int64_t lda, int num_experts, int n_rows, int k_dim,
                                    int64_t ldo, int activation, int mul_routed_weight, int dtype,
                                    void* workspace, int64_t workspace_bytes, void* stream) {
-  if (dtype != PIA_DTYPE_BF16 && dtype != PIA_DTYPE_F16)
-    return fail(PIA_EUNSUPPORTED, "moe_expert_gemm: dtype must be bf16 or fp16");
+  if (dtype != PIA_DTYPE_BF16 && dtype != PIA_DTYPE_F16 && dtype != PIA_DTYPE_F32)
+    return fail(PIA_EUNSUPPORTED, "moe_expert_gemm: dtype must be bf16, fp16 or fp32");
   if (activation < PIA_ACT_NONE || activation > PIA_ACT_GELU_TANH)
     return fail(PIA_EINVAL, "moe_expert_gemm: unknown activation");
+  const bool f32 = dtype == PIA_DTYPE_F32;
+  const int vec = f32 ? 4 : 8;  // elements per 16-byte vector
   if (max_num_tokens_padded < 0 || numel < 0 || a_div <= 0 || num_experts <= 0 || n_rows <= 0 ||
       k_dim <= 0 || lda < k_dim || block_m <= 0)
     return fail(PIA_EINVAL, "moe_expert_gemm: invalid size");
   if (block_m % EG_ROWS)
     return fail(PIA_EUNSUPPORTED, "moe_expert_gemm: block_m must be a multiple of 16");
-  if (k_dim % 8 || lda % 8)
-    return fail(PIA_EUNSUPPORTED, "moe_expert_gemm: K and the A row stride must be multiples of 8");
+  if (k_dim % vec || lda % vec)
+    return fail(PIA_EUNSUPPORTED, f32 ? "moe_expert_gemm: K and the A row stride must be "
+                                        "multiples of 4 (fp32)"
+                                      : "moe_expert_gemm: K and the A row stride must be "
+                                        "multiples of 8");
   const bool fused = activation != PIA_ACT_NONE;
   if (fused && n_rows % 2) return fail(PIA_EINVAL, "moe_expert_gemm: gate/up rows must be even");
   const int out_cols = fused ? n_rows / 2 : n_rows;
@@ -578,11 +618,13 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
   const uint16_t* aa = reinterpret_cast<const uint16_t*>(a);
   const uint16_t* ww = reinterpret_cast<const uint16_t*>(w);
   const int mulw = mul_routed_weight ? 1 : 0;
+  const int64_t elt = f32 ? 4 : 2;
   const int cus = device_cus();
   // bytes of A the plan can reach: rows ceil(numel / a_div), the last one k_dim long
-  const int64_t a_bytes = ((ceil_div(numel, a_div) - 1) * lda + k_dim) * 2;
-  const int64_t w_bytes = int64_t(n_rows) * k_dim * 2;
-  if (numel >= PIA_EG_TILED_MIN_ROUTES && a_bytes < (int64_t(1) << 31) &&
+  const int64_t a_bytes = ((ceil_div(numel, a_div) - 1) * lda + k_dim) * elt;
+  const int64_t w_bytes = int64_t(n_rows) * k_dim * elt;
+  // the LDS-tiled kernel is built for 16-bit storage; fp32 runs the split-K kernel at every size
+  if (!f32 && numel >= PIA_EG_TILED_MIN_ROUTES && a_bytes < (int64_t(1) << 31) &&
       w_bytes < (int64_t(1) << 31)) {
     const int64_t max_blocks = ceil_div(max_num_tokens_padded, block_m);
     int32_t* seg_block = reinterpret_cast<int32_t*>(workspace);  // [max_blocks + 1]
@@ -625,7 +667,9 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
   const int64_t ub = ceil_div(max_num_tokens_padded, EG_ROWS) * n_tiles;
   const unsigned grid = unsigned(std::min<int64_t>(ub, int64_t(cus) * EG_WGS_PER_CU));
 #define PIA_EG(DT, ACT)                                                                           \
-  hipLaunchKernelGGL((moe_gemm_splitk<DT, ACT>), dim3(grid), dim3(EG_WAVES * 64), 0, s, o, aa, ww, \
+  hipLaunchKernelGGL((moe_gemm_splitk<DT, ACT>), dim3(grid), dim3(EG_WAVES * 64), 0, s,            \
+                     reinterpret_cast<eg_elem<DT>*>(out), reinterpret_cast<const eg_elem<DT>*>(a), \
+                     reinterpret_cast<const eg_elem<DT>*>(w),                                     \
                      topk_weights, sorted_token_ids, expert_ids, num_tokens_post_pad,             \
                      max_num_tokens_padded, numel, block_m, a_div, lda, num_experts, n_rows,       \
                      k_dim, ldo, n_tiles, mulw)
@@ -638,8 +682,10 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
   }
   if (dtype == PIA_DTYPE_BF16) {
     PIA_EG_ACT(PIA_DTYPE_BF16)
-  } else {
+  } else if (dtype == PIA_DTYPE_F16) {
     PIA_EG_ACT(PIA_DTYPE_F16)
+  } else {
+    PIA_EG_ACT(PIA_DTYPE_F32)
   }
 #undef PIA_EG_ACT
 #undef PIA_EG
@@ -648,27 +694,28 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
 
 extern "C" int pia_act_and_mul(void* out, const void* x, int64_t rows, int64_t d, int activation,
                                int dtype, void* stream) {
-  if (dtype != PIA_DTYPE_BF16 && dtype != PIA_DTYPE_F16)
-    return fail(PIA_EUNSUPPORTED, "act_and_mul: dtype must be bf16 or fp16");
+  if (dtype != PIA_DTYPE_BF16 && dtype != PIA_DTYPE_F16 && dtype != PIA_DTYPE_F32)
+    return fail(PIA_EUNSUPPORTED, "act_and_mul: dtype must be bf16, fp16 or fp32");
   if (activation < PIA_ACT_SILU || activation > PIA_ACT_GELU_TANH)
     return fail(PIA_EINVAL, "act_and_mul: unknown activation");
   if (rows < 0 || d < 0) return fail(PIA_EINVAL, "act_and_mul: invalid size");
   if (rows == 0 || d == 0) return 0;
   if (!out || !x) return fail(PIA_EINVAL, "act_and_mul: null pointer");
-  const bool vec = d % 8 == 0 && aligned(out, 16) && aligned(x, 16);
-  const int64_t work = rows * (vec ? d / 8 : d);
+  const int per_vec = dtype == PIA_DTYPE_F32 ? 4 : 8;
+  const bool vec = d % per_vec == 0 && aligned(out, 16) && aligned(x, 16);
+  const int64_t work = rows * (vec ? d / per_vec : d);
   const unsigned grid =
       unsigned(std::min<int64_t>(ceil_div(work, 256), int64_t(device_cus()) * 16));
   hipStream_t s = as_stream(stream);
-  uint16_t* y = reinterpret_cast<uint16_t*>(out);
-  const uint16_t* xx = reinterpret_cast<const uint16_t*>(x);
-#define PIA_AM(DT, ACT)                                                                  \
-  if (vec)                                                                               \
-    hipLaunchKernelGGL((act_and_mul_kernel<DT, ACT, 8>), dim3(grid), dim3(256), 0, s, y, \
-                       xx, rows, d);                                                     \
-  else                                                                                   \
-    hipLaunchKernelGGL((act_and_mul_kernel<DT, ACT, 1>), dim3(grid), dim3(256), 0, s, y, \
-                       xx, rows, d)
+#define PIA_AM(DT, ACT)                                                                      \
+  if (vec)                                                                                   \
+    hipLaunchKernelGGL((act_and_mul_kernel<DT, ACT, true>), dim3(grid), dim3(256), 0, s,     \
+                       reinterpret_cast<eg_elem<DT>*>(out),                                  \
+                       reinterpret_cast<const eg_elem<DT>*>(x), rows, d);                    \
+  else                                                                                       \
+    hipLaunchKernelGGL((act_and_mul_kernel<DT, ACT, false>), dim3(grid), dim3(256), 0, s,    \
+                       reinterpret_cast<eg_elem<DT>*>(out),                                  \
+                       reinterpret_cast<const eg_elem<DT>*>(x), rows, d)
 #define PIA_AM_ACT(DT)                                   \
   switch (activation) {                                  \
     case PIA_ACT_SILU: PIA_AM(DT, PIA_ACT_SILU); break;  \
@@ -677,8 +724,10 @@ extern "C" int pia_act_and_mul(void* out, const void* x, int64_t rows, int64_t d
   }
   if (dtype == PIA_DTYPE_BF16) {
     PIA_AM_ACT(PIA_DTYPE_BF16)
-  } else {
+  } else if (dtype == PIA_DTYPE_F16) {
     PIA_AM_ACT(PIA_DTYPE_F16)
+  } else {
+    PIA_AM_ACT(PIA_DTYPE_F32)
   }
 #undef PIA_AM_ACT
 #undef PIA_AM

@@ -4,7 +4,7 @@ src/plastic_infer/kernel/triton/activation.py:116-150):
     y = round(act(x[..., :d]) * x[..., d:])        halves widened to fp32, result in x's dtype
 
 silu g/(1+e^-g), gelu 0.5g(1+erf(g/sqrt 2)), gelu_tanh 0.5g(1+tanh(sqrt(2/pi)(g+0.044715g^3))).
-One HIP kernel (pia_act_and_mul), bf16 and fp16.
+One HIP kernel (pia_act_and_mul), bf16, fp16 and fp32.
 """
 
 from __future__ import annotations

@@ -11,7 +11,7 @@ route index (deterministic; the reference's atomic-based order is not). Both FFN
 share one plan-driven path: moe_align_block_size, the first expert GEMM with the activation
 fused into its epilogue, the second expert GEMM with the routing weight, moe_sum_reduce; the
 rounding points are the reference's (first GEMM output, activation output, second GEMM output
-and the sum are each rounded to the storage dtype).
+and the sum are each rounded to the storage dtype; with fp32 storage there is no rounding).
 """
 
 from __future__ import annotations
@@ -63,8 +63,8 @@ def _check_ffn_args(hidden_states, w1, w2, topk_weights, topk_ids, activation):
     assert w2.is_contiguous(), "Expert weights2 must be contiguous"
     if activation not in {"silu", "gelu", "gelu_tanh"}:
         raise ValueError(f"Unsupported activation: {activation}")
-    if hidden_states.dtype not in (torch.bfloat16, torch.float16):
-        raise NotImplementedError("expert GEMMs are built for bf16 and fp16 storage")
+    if hidden_states.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise NotImplementedError("expert GEMMs are built for bf16, fp16 and fp32 storage")
     assert w1.dtype == hidden_states.dtype and w2.dtype == hidden_states.dtype
     N.require_device(hidden_states, w1, w2, topk_weights, topk_ids,
                      names=("hidden_states", "w1", "w2", "topk_weights", "topk_ids"))

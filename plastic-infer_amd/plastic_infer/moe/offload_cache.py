@@ -137,8 +137,9 @@ class _BankSet:
                 if t.shape[0] != num_experts:
                     raise ValueError(f"bank {name!r} layer {l} has {t.shape[0]} experts, "
                                      f"expected {num_experts}")
-            if head.dtype not in (torch.bfloat16, torch.float16):
-                raise NotImplementedError("expert banks are built for bf16 / fp16 storage")
+            if head.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+                raise NotImplementedError("expert banks are built for bf16, fp16 and fp32 "
+                                          "storage")
             self.sources[name] = per_layer
             self.caches[name] = torch.empty((num_slots, *head.shape[1:]), dtype=head.dtype,
                                             device=dev)

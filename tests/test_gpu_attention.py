@@ -507,7 +507,9 @@ def _hs_split(total, host_len, chunk, Hkv, D, dtype, seed, where):
 @pytest.mark.parametrize("where", ["pinned", "device", "pageable"])
 @pytest.mark.parametrize("dtype,Hq,Hkv,D", [(torch.bfloat16, 32, 8, 128),
                                             (torch.float16, 8, 2, 256),
-                                            (torch.float32, 16, 4, 64)])
+                                            (torch.float32, 16, 4, 64),
+                                            (torch.float32, 8, 2, 256),
+                                            (torch.float32, 4, 4, 160)])
 @pytest.mark.parametrize("q_len,causal", [(1, True), (4, True), (3, False), (20, True)])
 def test_host_stream_attention_shapes(dev, where, dtype, Hq, Hkv, D, q_len, causal):
     """Chunks of 256 tokens with a ragged 100-token last chunk and a 37-token device tail;

@@ -5,7 +5,9 @@ The GPU accumulates in fp32 in its own order (MFMA), so the bar is a tolerance: 
 intermediate agrees with the oracle's except for a small fraction of elements near a rounding
 boundary (< 1 %, each within a few storage-dtype steps), and the FFN output is within 1e-2 of the
 output's largest magnitude (the reference's own GPU-vs-CPU bar is 2e-2,
-tests/test_cpu_moe_executor.py:86-119).
+tests/test_cpu_moe_executor.py:86-119). With fp32 storage nothing is rounded, so every
+intermediate and the output are held to 2e-5 of their largest magnitude (fp32 sums of up to
+2048 products in two orders, and the activations' exp / erf / tanh to a few fp32 ulps).
 """
 
 from __future__ import annotations
@@ -60,13 +62,24 @@ def _problem(seed, T, H, I, E, k, dtype, scale=0.05):
     return x, w1, w2, tw, ids
 
 
+F32_TOL = 2e-5
+
+
+def _agree(got, ref, what, dtype, **kw):
+    """The bar of the storage dtype: a tolerance for fp32, mostly-equal for bf16 / fp16."""
+    if dtype == torch.float32:
+        _close(got, ref, what, tol=F32_TOL)
+    else:
+        _mostly_equal(got, ref, what, **kw)
+
+
 @pytest.mark.parametrize("activation", ["silu", "gelu", "gelu_tanh"])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("rows,d", [(64, 768), (7, 100)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("rows,d", [(64, 768), (7, 100), (3, 10)])
 def test_act_and_mul(dev, activation, dtype, rows, d):
     x = torch.randn(rows, 2 * d, generator=torch.Generator().manual_seed(rows)).to(dtype) * 3
     got = ACT[activation](x.to(dev))
-    _mostly_equal(got, OF.act_and_mul(x, activation), f"{activation} {dtype}", steps=1)
+    _agree(got, OF.act_and_mul(x, activation), f"{activation} {dtype}", dtype, steps=1)
 
 
 @pytest.mark.parametrize("seed,T,H,I,E,k,dtype,activation,on_input", [
@@ -77,6 +90,10 @@ def test_act_and_mul(dev, activation, dtype, rows, d):
     (10, 1024, 512, 256, 8, 4, torch.bfloat16, "silu", False),   # 512 routes per expert
     (11, 700, 200, 40, 7, 6, torch.float16, "gelu", True),       # K tail, column tail
     (12, 512, 2048, 768, 128, 8, torch.bfloat16, "silu", False), # Qwen3-30B-A3B prefill chunk
+    # fp32 storage (split-K kernel at every size; K a multiple of 4 suffices)
+    (20, 64, 2048, 768, 128, 8, torch.float32, "silu", False),
+    (21, 5, 100, 36, 7, 3, torch.float32, "gelu", True),         # K = 100 and 36: not / 8
+    (22, 700, 204, 44, 7, 6, torch.float32, "gelu_tanh", False), # 4200 routes, column tails
 ])
 def test_expert_gemms_match_oracle_intermediates(dev, seed, T, H, I, E, k, dtype, activation,
                                                  on_input):
@@ -88,17 +105,19 @@ def test_expert_gemms_match_oracle_intermediates(dev, seed, T, H, I, E, k, dtype
     xd, w1d, w2d, twd = x.to(dev), w1.to(dev), w2.to(dev), tw.to(dev)
     c2 = moe_expert_gemm(xd, w1d, twd, s, e, npp, 16, numel, k, activation=activation,
                          mul_routed_weight=on_input)
-    _mostly_equal(c2, torch.from_numpy(rc2), "first GEMM + activation")
+    _agree(c2, torch.from_numpy(rc2), "first GEMM + activation", dtype)
     # the second GEMM from the oracle's own activation output isolates its error
     c3 = moe_expert_gemm(torch.from_numpy(rc2).to(dtype).to(dev), w2d, twd, s, e, npp, 16,
                          numel, 1, mul_routed_weight=not on_input)
-    _mostly_equal(c3, torch.from_numpy(rc3).view(numel, H), "second GEMM")
+    _agree(c3, torch.from_numpy(rc3).view(numel, H), "second GEMM", dtype)
 
 
 @pytest.mark.parametrize("seed,T,H,I,E,k,dtype,activation,on_input", [
     (3, 64, 2048, 768, 128, 8, torch.bfloat16, "silu", False),
     (4, 1, 1024, 512, 16, 4, torch.bfloat16, "silu", False),     # one token
     (5, 37, 256, 96, 60, 6, torch.float16, "gelu", True),
+    (13, 64, 2048, 768, 128, 8, torch.float32, "silu", False),
+    (14, 1, 132, 20, 5, 2, torch.float32, "gelu_tanh", True),
 ])
 def test_fused_experts_decode_matches_oracle(dev, seed, T, H, I, E, k, dtype, activation,
                                              on_input):
@@ -106,6 +125,9 @@ def test_fused_experts_decode_matches_oracle(dev, seed, T, H, I, E, k, dtype, ac
     ref = OF.fused_experts(x, w1, w2, tw, ids, activation, on_input)
     got = fused_experts_decode_impl(x.to(dev), w1.to(dev), w2.to(dev), tw.to(dev),
                                     ids.to(dev), activation, on_input)
+    if dtype == torch.float32:
+        _close(got, ref, "decode FFN", tol=F32_TOL)
+        return
     _close(got, ref, "decode FFN")
     # a flipped last bit in one of the k summed rows can be large relative to a sum that cancels,
     # so the output is held to the fraction of differing elements (the rows themselves are held
@@ -113,14 +135,15 @@ def test_fused_experts_decode_matches_oracle(dev, seed, T, H, I, E, k, dtype, ac
     _mostly_equal(got, ref, "decode FFN", frac_max=0.02, steps=None)
 
 
-@pytest.mark.parametrize("T", [300, 1100])
-def test_fused_experts_impl_overwrites_hidden(dev, T):
-    x, w1, w2, tw, ids = _problem(6, T, 512, 128, 32, 4, torch.bfloat16)
+@pytest.mark.parametrize("T,dtype", [(300, torch.bfloat16), (1100, torch.bfloat16),
+                                     (1100, torch.float32)])
+def test_fused_experts_impl_overwrites_hidden(dev, T, dtype):
+    x, w1, w2, tw, ids = _problem(6, T, 512, 128, 32, 4, dtype)
     ref = OF.fused_experts(x, w1, w2, tw, ids)
     xd = x.to(dev)
     got = fused_experts_impl(xd, w1.to(dev), w2.to(dev), tw.to(dev), ids.to(dev))
     assert got.data_ptr() == xd.data_ptr()
-    _close(got, ref, "prefill FFN")
+    _close(got, ref, "prefill FFN", tol=F32_TOL if dtype == torch.float32 else 1e-2)
 
 
 def test_fused_experts_over_slot_ids(dev):
@@ -157,3 +180,9 @@ def test_expert_gemm_rejects_bad_shapes(dev):
         moe_expert_gemm(x, w, None, s, e, npp, 16, 4, 1)
     with pytest.raises(RuntimeError, match="multiple of 16"):
         moe_expert_gemm(x[:, :8].contiguous(), w[:, :, :8].contiguous(), None, s, e, npp, 8, 4, 1)
+    xf = torch.zeros(4, 6, dtype=torch.float32, device=dev)       # fp32 needs K % 4 == 0
+    wf = torch.zeros(2, 8, 6, dtype=torch.float32, device=dev)
+    with pytest.raises(RuntimeError, match="multiples of 4"):
+        moe_expert_gemm(xf, wf, None, s, e, npp, 16, 4, 1)
+    with pytest.raises(ValueError, match="dtype"):
+        moe_expert_gemm(xf.double(), wf.double(), None, s, e, npp, 16, 4, 1)
