@@ -4,8 +4,11 @@
 Workload (Qwen3-8B-shaped decode, one layer): 32 query heads, 8 KV heads, head_dim 128, bf16,
 page size 16; batch 256 with context lengths ~ U[512, 8192] (including the new token); block
 tables are consecutive slices of one seeded permutation of a 160,000-page pool; K, V, q and the
-new K/V rows ~ N(0,1). One step = slot scatter of the 256 new K/V rows + paged GQA decode
-attention over every sequence. Inputs are resident in HBM before timing starts.
+new K/V rows ~ N(0,1). One step = the write of the 256 new K/V rows into their slots + paged
+GQA decode attention over every sequence (new token included), as one call
+(paged_decode_append_attention: the attention kernel takes each new token from k_new / v_new
+and stores it into its slot). --separate-write runs the same step as two calls (kv_scatter,
+then paged_decode_attention). Inputs are resident in HBM before timing starts.
 
 Prints ONE JSON line with the whole-job throughput (algorithmic GB/s of a step), tokens/s,
 the roofline of the dominant kernel (attention: algorithmic bytes / average duration measured
@@ -13,6 +16,7 @@ with HIP events on the launch stream) and the CPU baseline (the oracle's restate
 reference torch path on this host's cores, on a bounded sample of the same inputs).
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-sample-seqs S] [--no-cpu-baseline]
+                  [--separate-write]
   python bench.py --calibrate-copy     # 1 GiB read + 1 GiB write elementwise copy, three times:
                                        # the known-size reference for HBM byte counters
   python bench.py --workload decode-gqa8     # Qwen3-30B-A3B attention layer: 64 x 4096 tokens,
@@ -1351,6 +1355,8 @@ def main() -> int:
     ap.add_argument("--cpu-sample-seqs", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--separate-write", action="store_true",
+                    help="decode: write the new rows with kv_scatter, then attend (two calls)")
     ap.add_argument("--workload", choices=("decode", "decode-gqa8", "prefill-write",
                                            "moe-permute", "expert-stream", "moe-experts",
                                            "moe-experts-prefill", "prefill-stream", "kv-sink",
@@ -1365,7 +1371,12 @@ def main() -> int:
 
     import torch
 
-    from plastic_infer.kernel import decode_workspace_bytes, kv_scatter, paged_decode_attention
+    from plastic_infer.kernel import (
+        decode_workspace_bytes,
+        kv_scatter,
+        paged_decode_append_attention,
+        paged_decode_attention,
+    )
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -1388,12 +1399,20 @@ def main() -> int:
     ws = torch.empty(decode_workspace_bytes(B, HQ, HKV, D, P, MAX_PAGES), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
 
+    separate = args.separate_write
+
     def step(ev_a=None, ev_b=None):
-        kv_scatter(inp["k_new"], inp["v_new"], inp["kp"], inp["vp"], inp["slots_d"])
+        if separate:
+            kv_scatter(inp["k_new"], inp["v_new"], inp["kp"], inp["vp"], inp["slots_d"])
         if ev_a is not None:
             ev_a.record(stream)
-        paged_decode_attention(inp["q"], inp["kp"], inp["vp"], inp["bt_d"], inp["lens_d"],
-                               out=out, workspace=ws)
+        if separate:
+            paged_decode_attention(inp["q"], inp["kp"], inp["vp"], inp["bt_d"], inp["lens_d"],
+                                   out=out, workspace=ws)
+        else:
+            paged_decode_append_attention(inp["q"], inp["kp"], inp["vp"], inp["bt_d"],
+                                          inp["lens_d"], inp["k_new"], inp["v_new"], out=out,
+                                          workspace=ws)
         if ev_b is not None:
             ev_b.record(stream)
 
@@ -1419,7 +1438,10 @@ def main() -> int:
     attn_bytes, scatter_bytes = algorithmic_bytes(inp["lens"], inp["n_pages"])
     step_bytes = attn_bytes + scatter_bytes
     gbps = step_bytes / (ms_step / 1e3) / 1e9
-    attn_gbps = attn_bytes / (attn_ms / 1e3) / 1e9
+    # the dominant launch: the attention call alone (separate write) or the one call that also
+    # writes the new rows
+    launch_bytes = attn_bytes if separate else step_bytes
+    attn_gbps = launch_bytes / (attn_ms / 1e3) / 1e9
     traffic = None
     if PMC_FILE.exists():
         try:
@@ -1446,11 +1468,15 @@ def main() -> int:
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "bytes_per_step": step_bytes,
         "wall_s_timed": round(wall, 4),
+        "step": "kv_scatter + paged_decode_attention" if separate
+                else "paged_decode_append_attention (write + attention, one call)",
         "roofline": {
-            "kernel": "paged_decode_stream<4> + paged_decode_stream_reduce (one attention call)",
+            "kernel": ("paged_decode_stream<4> + paged_decode_stream_reduce (one attention call)"
+                       if separate else "paged_decode_stream<4, append> + "
+                       "paged_decode_stream_reduce (one write + attention call)"),
             "bound": "hbm", "achieved": round(attn_gbps, 2), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
-            "algorithmic_bytes_per_launch": attn_bytes, "avg_launch_ms": round(attn_ms, 4),
+            "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_ms": round(attn_ms, 4),
         },
     }
     if not args.no_cpu_baseline:

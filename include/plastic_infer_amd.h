@@ -141,6 +141,33 @@ int pia_paged_decode_attention(void* out, const void* q, int64_t q_seq_stride,
                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * The decode step's KV write and attention in one call: the reference's _write_kv_layer of the
+ * new token at position pos (page block_table[pos / P], offset pos % P) followed by
+ * _attn_paged(..., kv_num_tokens=pos + 1, causal=False)
+ * (src/plastic_infer/exec/runner_paged.py:112-129 and :251-255,
+ * src/plastic_infer/exec/runner_moe_paged.py:144-147).
+ * Row b's new token is position L_b - 1 (L_b = context_lens[b], counting it): k_new / v_new hold
+ * its K and V, [num_kv_heads, head_dim] per row, new_seq_stride elements between rows (heads
+ * contiguous). Results: the pools hold k_new / v_new at that slot, and out is what
+ * pia_paged_decode_attention gives over the updated pools (same arguments, workspace and
+ * rules). A row whose L_b is 0 or exceeds bt_stride * page_size writes no slot; a slot whose
+ * page id is outside [0, num_pages) is not written and the new token is then no key.
+ * The fast kernel (the same shapes as pia_paged_decode_attention's) takes the new token's K / V
+ * from k_new / v_new and stores them into the slot itself, so the step has no separate write
+ * launch ahead of the attention; other shapes write the slots with a small kernel first.
+ * A slot must belong to one row only (a row's new-token page is not read by another row of the
+ * call), as with any slot that a decode step writes.
+ * ------------------------------------------------------------------------------------------- */
+int pia_paged_decode_append_attention(void* out, const void* q, int64_t q_seq_stride,
+                                      void* k_pages, void* v_pages,
+                                      const int32_t* block_tables, int64_t bt_stride,
+                                      const int32_t* context_lens, const void* k_new,
+                                      const void* v_new, int64_t new_seq_stride, int num_seqs,
+                                      int num_heads, int num_kv_heads, int head_dim,
+                                      int page_size, int64_t num_pages, float scale, int dtype,
+                                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Paged GQA decode attention that allocates nothing and takes no workspace.
  * No counterpart in the reference: it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).

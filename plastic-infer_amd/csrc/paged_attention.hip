@@ -22,6 +22,7 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "pia_internal.h"
 
@@ -197,7 +198,13 @@ __device__ __forceinline__ int stream_range_of(int st, int Dp, int Ce) {
 
 struct StreamCursor {
   int b, h, ls, ns, L;  // sequence, kv head, step in the segment, steps in it, its tokens
+  bool app;             // append mode: position L - 1 is the new token given in k_new / v_new
 };
+
+// seq_len LDS word: the clamped context length, bit 30 set when (append mode) the row's raw
+// length does not fit its block table, so it has no new token to take from k_new / v_new.
+constexpr int SD_NO_APPEND = 1 << 30;
+constexpr int SD_APP_REC = 32;  // new-token slots a wave defers to the end of its range
 
 __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
 #pragma unroll
@@ -210,13 +217,29 @@ __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-template <int G>
+// Pool pointers of the stream kernel: restrict-qualified when the launch only reads the pools,
+// plain when it also writes the new tokens into them (append mode).
+template <bool APPEND>
+using PoolIn = std::conditional_t<APPEND, const uint16_t*, const uint16_t* __restrict__>;
+
+// Append mode (APPEND): every row's position L - 1 is its new token, given in k_new / v_new
+// ([B, Hkv, D] rows new_seq_stride elements apart). The wave that runs a segment's last step
+// scores the new key against the staged q (one v_dot2 per lane over the (d, d + 4) pairs, a
+// wave sum), puts that score in place of the pool slot's, zeroes the slot's V words and adds
+// p * v_new itself; the slot's old contents are never used and no other segment reads it.
+// The stores of k_new / v_new into the slot wait until the wave has run its last step: vector
+// memory counters retire in issue order, so a store issued between a step's loads would hold
+// every later wait on a load behind its write acknowledgment (a measured 9 % of the launch).
+// The wave keeps up to SD_APP_REC pending slots in LDS and stores any further ones at once.
+template <int G, bool APPEND>
 __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
-    const uint16_t* __restrict__ kpool, const uint16_t* __restrict__ vpool,
+    PoolIn<APPEND> kpool, PoolIn<APPEND> vpool,
     const int32_t* __restrict__ block_tables, int64_t bt_stride,
     const int32_t* __restrict__ context_lens, int B, int Hkv, int64_t num_pages,
-    float* __restrict__ ws_part, int32_t* __restrict__ ws_meta, float scale_log2) {
+    float* __restrict__ ws_part, int32_t* __restrict__ ws_meta, float scale_log2,
+    uint16_t* kpool_w, uint16_t* vpool_w, const uint16_t* __restrict__ k_new,
+    const uint16_t* __restrict__ v_new, int64_t new_seq_stride) {
   constexpr int D = FD_D, P = FD_P, TILE = D * P, STEP = FD_PAGES_PER_WAVE;
   constexpr int NCH = SD_MAX_SEQS / 64;
   const int lane = threadIdx.x, w = blockIdx.x, NW = gridDim.x;
@@ -226,14 +249,19 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
   int* seq_len = sd_lds + B + 1;  // [B]: clamped context length
   __shared__ uint32_t q_lds[4][16][G];
   __shared__ uint32_t p_lds[64][G];
+  // append mode: deferred new-token stores, {pool element offset of the slot, k_new offset}
+  __shared__ int64_t app_rec[APPEND ? SD_APP_REC : 1][2];
+  int n_rec = 0;
 
   // Step prefix over the batch: every wave builds its own copy in LDS, wave 0 also publishes
   // it (and the pair split) for the merge kernel.
-  int lv[NCH];
+  int lv[NCH], lflag[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int i = c * 64 + lane;
-    lv[c] = (c * 64 < B && i < B) ? clamp_len(context_lens[i], bt_stride, P) : 0;
+    const int raw = (c * 64 < B && i < B) ? context_lens[i] : 0;
+    lv[c] = clamp_len(raw, bt_stride, P);
+    lflag[c] = (APPEND && raw != lv[c]) ? SD_NO_APPEND : 0;
   }
   int carry = 0;
 #pragma unroll
@@ -243,7 +271,7 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     const int i = c * 64 + lane;
     if (i < B) {
       seq_q[i + 1] = carry + incl;
-      seq_len[i] = lv[c];
+      seq_len[i] = lv[c] | lflag[c];
       if (w == 0) ws_meta[i + 1] = carry + incl;
     }
     carry = uniform(carry + __shfl(incl, 63, 64));
@@ -262,7 +290,7 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
   __syncthreads();
   // empty sequences (no steps) get zero rows here: wave w takes sequences w, w + NW, ...
   for (int b = w; b < B; b += NW) {
-    if (uniform(seq_len[b]) == 0) {
+    if ((uniform(seq_len[b]) & ~SD_NO_APPEND) == 0) {
       uint16_t* o = out + int64_t(b) * Hq * D;
       for (int i = lane; i < Hq * D; i += 64) o[i] = 0;
     }
@@ -286,7 +314,9 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     const int r = gs - Hkv * q0;
     c.h = r / c.ns;
     c.ls = r - c.h * c.ns;
-    c.L = uniform(seq_len[lo]);
+    const int sl = uniform(seq_len[lo]);
+    c.L = sl & ~SD_NO_APPEND;
+    c.app = APPEND && !(sl & SD_NO_APPEND);
     return c;
   };
   // the step after c (only asked for when one exists inside the range)
@@ -297,7 +327,9 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
         c.h = 0;
         do { ++c.b; } while (c.b < B - 1 && uniform(seq_q[c.b + 1]) == uniform(seq_q[c.b]));
         c.ns = uniform(seq_q[c.b + 1]) - uniform(seq_q[c.b]);
-        c.L = uniform(seq_len[c.b]);
+        const int sl = uniform(seq_len[c.b]);
+        c.L = sl & ~SD_NO_APPEND;
+        c.app = APPEND && !(sl & SD_NO_APPEND);
       }
     }
     return c;
@@ -476,11 +508,29 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     const int valid = min(SD_STEP_TOKENS, cur.L - cur.ls * SD_STEP_TOKENS);
     const uint16_t* head_v = vbase + int64_t(cur.h) * TILE;
 
+    // append mode, the segment's last step: token tn of the step is the new one. Lane l takes
+    // k_new[d], k_new[d + 4] with d = 8 (l / 4) + l % 4 (the q pair q_lds[l % 4][l / 4]) and
+    // v_new[32 j + l / 2], j < 4 (the V rows of its PV accumulators).
+    const bool app_step = APPEND && cur.app && cur.ls == cur.ns - 1;
+    const int tn = valid - 1;
+    uint32_t kn = 0;
+    uint32_t vn[4] = {0u, 0u, 0u, 0u};
+    if (app_step) {
+      const uint16_t* kr = k_new + int64_t(cur.b) * new_seq_stride + int64_t(cur.h) * D;
+      const uint16_t* vr = v_new + int64_t(cur.b) * new_seq_stride + int64_t(cur.h) * D;
+      const int d0 = 8 * (lane >> 2) + (lane & 3);
+      kn = uint32_t(kr[d0]) | (uint32_t(kr[d0 + 4]) << 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vn[j] = vr[32 * j + (lane >> 1)];
+    }
+
     // pages of this step whose id is outside the pool: their tokens are not keys (lane l holds
     // the id of page l / 8, the page of its scores' tokens 2l and 2l + 1)
     const bool pg_ok = bt_cur >= 0 && int64_t(bt_cur) < num_pages;
     const uint64_t bad = __ballot(!pg_ok);
-    const bool masked_step = valid < SD_STEP_TOKENS || bad != 0;
+    const bool masked_step = valid < SD_STEP_TOKENS || bad != 0 || app_step;
+    // V words of tokens at or past v_valid are zeroed (the new token's slot in append mode)
+    const int v_valid = app_step ? tn : valid;
 
     float sacc[8][G];
 #pragma unroll
@@ -498,6 +548,15 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     float sc[2][G];
     quad_reduce_scatter<G>(sacc, sc, lane);
     const int tok0 = 2 * lane;
+    if (app_step) {  // the new token's score from k_new, in place of its pool slot's
+      const bool own0 = tok0 == tn, own1 = tok0 + 1 == tn;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float sn = wave_sum_dpp(dot2_bf16(kn, q_lds[lane & 3][lane >> 2][g], 0.f));
+        sc[0][g] = own0 ? sn : sc[0][g];
+        sc[1][g] = own1 ? sn : sc[1][g];
+      }
+    }
     uint32_t pw[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -516,11 +575,46 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     for (int g = 0; g < G; ++g) p_lds[lane][g] = pw[g];
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
+    if (app_step) {
+      // p of the new token (the bf16 value the pool tokens' products use) times v_new, on the
+      // even lanes (the odd lane of a pair accumulates the other token half); then k_new /
+      // v_new go into the slot, unless its page id is outside the pool (then it is no key)
+      const uint32_t half_sh = (tn & 1) ? 16u : 0u;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pn = __uint_as_float(((p_lds[tn >> 1][g] >> half_sh) & 0xffffu) << 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float v = (lane & 1) ? 0.f : __uint_as_float(vn[j] << 16);
+          acc[j][g] = pn > 0.f ? fmaf(pn, v, acc[j][g]) : acc[j][g];
+        }
+      }
+      const int idn = __builtin_amdgcn_readlane(bt_cur, 8 * (tn >> 4));
+      if (idn >= 0 && int64_t(idn) < num_pages) {
+        const int64_t slot = int64_t(idn) * page_stride + int64_t(cur.h) * TILE + (tn & 15);
+        if (n_rec < SD_APP_REC) {
+          if (lane == 0) {
+            app_rec[n_rec][0] = slot;
+            app_rec[n_rec][1] = int64_t(cur.b) * new_seq_stride + int64_t(cur.h) * D;
+          }
+          ++n_rec;
+        } else {
+          const int d0 = 8 * (lane >> 2) + (lane & 3);
+          kpool_w[slot + d0 * P] = uint16_t(kn & 0xffffu);
+          kpool_w[slot + (d0 + 4) * P] = uint16_t(kn >> 16);
+          if ((lane & 1) == 0) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              vpool_w[slot + (32 * j + (lane >> 1)) * P] = uint16_t(vn[j]);
+          }
+        }
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
     load_v(bufB, head_v, bt_cur, 4);
     __builtin_amdgcn_sched_barrier(0);
     if (masked_step) {
-      mask_tail(bufA, 0, valid, bad);
+      mask_tail(bufA, 0, v_valid, bad);
       pv_pages(bufA, 0);
     } else {
       pv_pages(bufA, 0);
@@ -531,7 +625,7 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     for (int i = 0; i < 16; ++i) bufA[i] = load16_nt(kp + 64 * i);
     __builtin_amdgcn_sched_barrier(0);
     if (masked_step) {
-      mask_tail(bufB, 4, valid, bad);
+      mask_tail(bufB, 4, v_valid, bad);
       pv_pages(bufB, 4);
     } else {
       pv_pages(bufB, 4);
@@ -591,6 +685,22 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     cur = nxt;
     bt_cur = bt_nxt;
     ++gs;
+  }
+  if constexpr (APPEND) {
+    // the deferred new-token stores (k_new / v_new rows reread: they are small and cached)
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const int d0 = 8 * (lane >> 2) + (lane & 3);
+    for (int r = 0; r < n_rec; ++r) {
+      const int64_t slot = app_rec[r][0], src = app_rec[r][1];
+      kpool_w[slot + d0 * P] = k_new[src + d0];
+      kpool_w[slot + (d0 + 4) * P] = k_new[src + d0 + 4];
+      if ((lane & 1) == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          vpool_w[slot + (32 * j + (lane >> 1)) * P] = v_new[src + 32 * j + (lane >> 1)];
+      }
+    }
   }
 }
 
@@ -793,6 +903,47 @@ int launch_generic_any(int dtype, void* out, const void* q, int64_t q_row_stride
   return fail(PIA_EINVAL, "paged attention: unknown dtype");
 }
 
+// The new tokens of a decode step into their slots (any dtype, head_dim, page size): row b's
+// k_new / v_new [Hkv, D] go to position L_b - 1 of its block table, for 1 <= L_b <= the table's
+// width in tokens and a page id inside the pool (other rows write nothing). One workgroup per
+// row, thread i over the row's Hkv * D elements.
+template <typename T>
+__global__ __launch_bounds__(256) void kv_append_kernel(
+    T* __restrict__ kpool, T* __restrict__ vpool, const T* __restrict__ k_new,
+    const T* __restrict__ v_new, int64_t new_seq_stride, const int32_t* __restrict__ bt,
+    int64_t bt_stride, const int32_t* __restrict__ context_lens, int Hkv, int D, int P,
+    int64_t num_pages) {
+  const int b = blockIdx.x;
+  const int L = context_lens[b];
+  if (L < 1 || int64_t(L) > bt_stride * P) return;
+  const int64_t page = bt[int64_t(b) * bt_stride + (L - 1) / P];
+  if (page < 0 || page >= num_pages) return;
+  const int off = (L - 1) % P;
+  const int n = Hkv * D;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const int h = i / D, d = i - h * D;
+    const int64_t dst = ((page * Hkv + h) * D + d) * P + off;
+    const int64_t src = int64_t(b) * new_seq_stride + i;
+    kpool[dst] = k_new[src];
+    vpool[dst] = v_new[src];
+  }
+}
+
+int launch_kv_append(int dtype, void* kp, void* vp, const void* k_new, const void* v_new,
+                     int64_t new_seq_stride, const int32_t* bt, int64_t bt_stride,
+                     const int32_t* context_lens, int B, int Hkv, int D, int P,
+                     int64_t num_pages, hipStream_t s) {
+#define PIA_KA(T)                                                                            \
+  hipLaunchKernelGGL(kv_append_kernel<T>, dim3(unsigned(B)), dim3(256), 0, s,                \
+                     reinterpret_cast<T*>(kp), reinterpret_cast<T*>(vp),                     \
+                     reinterpret_cast<const T*>(k_new), reinterpret_cast<const T*>(v_new),   \
+                     new_seq_stride, bt, bt_stride, context_lens, Hkv, D, P, num_pages)
+  if (dtype == PIA_DTYPE_F32) PIA_KA(float);
+  else PIA_KA(uint16_t);
+#undef PIA_KA
+  return check_launch("kv_append_kernel");
+}
+
 int check_heads(int Hq, int Hkv, int D, int P, int64_t num_pages, int dtype) {
   if (Hq <= 0 || Hkv <= 0 || D <= 0 || P <= 0 || num_pages <= 0)
     return fail(PIA_EINVAL, "paged attention: heads, head_dim, page_size, num_pages must be > 0");
@@ -858,29 +1009,48 @@ int check_decode_args(const void* out, const void* q, int64_t q_seq_stride, cons
 // The fast path (checked arguments): stream kernel + merge, in launches of up to SD_MAX_SEQS
 // sequences that reuse the same partial slots (ws_part: >= NW * 2 * G * (D + 2) floats) and
 // meta ints (ws_meta: SD_META_INTS). Launches on one stream are ordered, so the reuse is safe.
+// k_new != nullptr: append mode (the new tokens of the step in k_new / v_new, written into the
+// pools by the kernel; k_pages / v_pages are then written too).
 int launch_stream_decode(void* out, const void* q, int64_t q_seq_stride, const void* k_pages,
                          const void* v_pages, const int32_t* block_tables, int64_t bt_stride,
                          const int32_t* context_lens, int num_seqs, int num_heads,
                          int num_kv_heads, int64_t num_pages, float scale_log2, float* ws_part,
-                         int32_t* ws_meta, hipStream_t s) {
+                         int32_t* ws_meta, hipStream_t s, const void* k_new = nullptr,
+                         const void* v_new = nullptr, int64_t new_seq_stride = 0) {
   const int G = num_heads / num_kv_heads;
   const int NW = stream_waves(G);
+  uint16_t* kw = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(k_pages));
+  uint16_t* vw = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(v_pages));
   for (int b0 = 0; b0 < num_seqs; b0 += SD_MAX_SEQS) {
     const int Bs = std::min(SD_MAX_SEQS, num_seqs - b0);
     uint16_t* o = reinterpret_cast<uint16_t*>(out) + int64_t(b0) * num_heads * FD_D;
     const uint16_t* qq = reinterpret_cast<const uint16_t*>(q) + int64_t(b0) * q_seq_stride;
     const int32_t* bt = block_tables + int64_t(b0) * bt_stride;
     const int32_t* cl = context_lens + b0;
+    const uint16_t* kn =
+        k_new ? reinterpret_cast<const uint16_t*>(k_new) + int64_t(b0) * new_seq_stride : nullptr;
+    const uint16_t* vn =
+        k_new ? reinterpret_cast<const uint16_t*>(v_new) + int64_t(b0) * new_seq_stride : nullptr;
     const size_t lds = size_t(2 * Bs + 1) * sizeof(int32_t);
-#define PIA_SD(GG)                                                                             \
-  hipLaunchKernelGGL((paged_decode_stream<GG>), dim3(unsigned(NW)), dim3(64), lds, s, o, qq,   \
-                     q_seq_stride, (const uint16_t*)k_pages, (const uint16_t*)v_pages, bt,     \
-                     bt_stride, cl, Bs, num_kv_heads, num_pages, ws_part, ws_meta, scale_log2)
-    switch (G) {
-      case 1: PIA_SD(1); break;
-      case 2: PIA_SD(2); break;
-      case 4: PIA_SD(4); break;
-      default: PIA_SD(8); break;
+#define PIA_SD(GG, AP)                                                                         \
+  hipLaunchKernelGGL((paged_decode_stream<GG, AP>), dim3(unsigned(NW)), dim3(64), lds, s, o,   \
+                     qq, q_seq_stride, (const uint16_t*)k_pages, (const uint16_t*)v_pages, bt, \
+                     bt_stride, cl, Bs, num_kv_heads, num_pages, ws_part, ws_meta, scale_log2, \
+                     kw, vw, kn, vn, new_seq_stride)
+    if (kn) {
+      switch (G) {
+        case 1: PIA_SD(1, true); break;
+        case 2: PIA_SD(2, true); break;
+        case 4: PIA_SD(4, true); break;
+        default: PIA_SD(8, true); break;
+      }
+    } else {
+      switch (G) {
+        case 1: PIA_SD(1, false); break;
+        case 2: PIA_SD(2, false); break;
+        case 4: PIA_SD(4, false); break;
+        default: PIA_SD(8, false); break;
+      }
     }
 #undef PIA_SD
     if (int rc = check_launch("paged_decode_stream")) return rc;
@@ -985,6 +1155,53 @@ extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_se
                                 context_lens, num_seqs, num_heads, num_kv_heads, num_pages,
                                 scale_log2, ws_part, ws_meta, s);
   }
+  return launch_generic_any(dtype, out, q, q_seq_stride, k_pages, v_pages, block_tables,
+                            bt_stride, context_lens, nullptr, nullptr, num_seqs, num_seqs,
+                            num_heads, num_kv_heads, head_dim, page_size, num_pages, scale_log2,
+                            s);
+}
+
+extern "C" int pia_paged_decode_append_attention(
+    void* out, const void* q, int64_t q_seq_stride, void* k_pages, void* v_pages,
+    const int32_t* block_tables, int64_t bt_stride, const int32_t* context_lens,
+    const void* k_new, const void* v_new, int64_t new_seq_stride, int num_seqs, int num_heads,
+    int num_kv_heads, int head_dim, int page_size, int64_t num_pages, float scale, int dtype,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+  if (int rc = check_decode_args(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride,
+                                 context_lens, num_seqs, num_heads, num_kv_heads, head_dim,
+                                 page_size, num_pages, dtype))
+    return rc;
+  if (num_seqs == 0) return 0;
+  if (!k_new || !v_new) return fail(PIA_EINVAL, "paged_decode_append: null k_new / v_new");
+  if (new_seq_stride < int64_t(num_kv_heads) * head_dim)
+    return fail(PIA_EINVAL, "paged_decode_append: new_seq_stride < num_kv_heads*head_dim");
+  const float scale_log2 = scale * kLog2e;
+  hipStream_t s = as_stream(stream);
+  if (fast_path(dtype, num_heads, num_kv_heads, head_dim, page_size)) {
+    if (!aligned(k_new, 2) || !aligned(v_new, 2))
+      return fail(PIA_EINVAL, "paged_decode_append: k_new / v_new must be 2-byte aligned");
+    const int64_t need = pia_paged_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads,
+                                                          head_dim, page_size, bt_stride);
+    if (!workspace || workspace_bytes < need) {
+      set_error("paged_decode_append: workspace of %lld bytes needed, %lld given",
+                (long long)need, (long long)workspace_bytes);
+      return PIA_EINVAL;
+    }
+    if (!aligned(workspace, 4))
+      return fail(PIA_EINVAL, "paged_decode_append: workspace not 4-byte aligned");
+    const int G = num_heads / num_kv_heads;
+    float* ws_part = reinterpret_cast<float*>(workspace);
+    int32_t* ws_meta =
+        reinterpret_cast<int32_t*>(ws_part + int64_t(SD_MAX_WAVES) * 2 * G * (FD_D + 2));
+    return launch_stream_decode(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride,
+                                context_lens, num_seqs, num_heads, num_kv_heads, num_pages,
+                                scale_log2, ws_part, ws_meta, s, k_new, v_new, new_seq_stride);
+  }
+  // any other shape: the new tokens into their slots, then the decode over the pool
+  if (int rc = launch_kv_append(dtype, k_pages, v_pages, k_new, v_new, new_seq_stride,
+                                block_tables, bt_stride, context_lens, num_seqs, num_kv_heads,
+                                head_dim, page_size, num_pages, s))
+    return rc;
   return launch_generic_any(dtype, out, q, q_seq_stride, k_pages, v_pages, block_tables,
                             bt_stride, context_lens, nullptr, nullptr, num_seqs, num_seqs,
                             num_heads, num_kv_heads, head_dim, page_size, num_pages, scale_log2,

@@ -34,6 +34,9 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_paged_decode_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _L]),
     "pia_paged_decode_attention": (
         _I, [_P, _P, _L, _P, _P, _P, _L, _P, _I, _I, _I, _I, _I, _L, _F, _I, _P, _L, _P]),
+    "pia_paged_decode_append_attention": (
+        _I, [_P, _P, _L, _P, _P, _P, _L, _P, _P, _P, _L, _I, _I, _I, _I, _I, _L, _F, _I, _P, _L,
+             _P]),
     "pia_paged_decode_noalloc_scratch_bytes": (_L, [_I, _I]),
     "pia_paged_decode_attention_noalloc": (
         _I, [_P, _P, _L, _P, _P, _P, _L, _P, _I, _I, _I, _I, _I, _L, _F, _I, _P]),
@@ -66,7 +69,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_prefill_hit_compact": (_I, [_P, _P, _P, _P, _L, _L, _I, _P]),
 }
 
-EXPECTED_ABI = 6
+EXPECTED_ABI = 7
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

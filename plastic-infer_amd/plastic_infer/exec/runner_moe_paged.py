@@ -37,7 +37,7 @@ import torch
 import torch.nn.functional as F
 
 from ..kernel.moe_ops import moe_sum_reduce
-from ..kernel.paged_kv import decode_workspace_bytes, kv_scatter, paged_decode_attention
+from ..kernel.paged_kv import decode_workspace_bytes, paged_decode_append_attention
 from ..moe.fused import fused_experts_decode_impl, fused_topk, routed_ffn_routes
 from ..moe.offload_cache import OffloadMoeCache
 from .attention import build_rope_cache, rms_norm
@@ -119,7 +119,8 @@ class DecodeBatch:
     """Where a decode step's new tokens go and what each row attends.
 
     block_tables int32 [L, B, max_pages]: layer l's pages of every row; context_lens int32 [B]:
-    tokens including the new one; slot_mapping int64 [L, B]: the new token's slot per layer;
+    tokens including the new one; slot_mapping int64 [L, B]: the new token's slot per layer
+    (the block table's slot of position context_lens - 1, which is where the step writes it);
     positions int64 [B]: its position (context_lens - 1). All on the device."""
     block_tables: torch.Tensor
     context_lens: torch.Tensor
@@ -238,9 +239,11 @@ class MoePagedDecoder:
         q = self._rope(q, batch.positions).contiguous()
         k = self._rope(k, batch.positions).contiguous()
         v = v.contiguous()
-        kv_scatter(k, v, self.k_pages, self.v_pages, batch.slot_mapping[l])
-        attn = paged_decode_attention(q, self.k_pages, self.v_pages, batch.block_tables[l],
-                                      batch.context_lens, workspace=self._ws)
+        # the reference's _write_kv_layer then _attn_paged, as one call: the new token goes to
+        # its slot and the attention takes it from k / v directly
+        attn = paged_decode_append_attention(q, self.k_pages, self.v_pages,
+                                             batch.block_tables[l], batch.context_lens, k, v,
+                                             workspace=self._ws)
         x = residual + F.linear(attn.view(B, Hq * D), w[p + "self_attn.o_proj.weight"])
         residual = x
         h = rms_norm(x, w[p + "post_attention_layernorm.weight"])

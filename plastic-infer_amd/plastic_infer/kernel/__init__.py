@@ -19,6 +19,7 @@ from .paged_kv import (
     kv_scatter,
     paged_attention,
     paged_decode_attention,
+    paged_decode_append_attention,
     paged_decode_attention_noalloc,
     pages_chunk_copy,
     pages_chunks_copy,
@@ -30,6 +31,6 @@ __all__ = [
     "max_num_tokens_padded", "moe_align_block_size", "moe_expert_gemm", "moe_permute", "moe_sum_reduce",
     "moe_topk", "moe_topk_align", "moe_unpermute",
     "decode_workspace_bytes", "kv_gather", "kv_scatter", "paged_attention",
-    "paged_decode_attention", "paged_decode_attention_noalloc", "pages_chunk_copy",
+    "paged_decode_attention", "paged_decode_append_attention", "paged_decode_attention_noalloc", "pages_chunk_copy",
     "pages_chunks_copy",
 ]

@@ -157,6 +157,59 @@ def paged_decode_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torc
     return out
 
 
+def paged_decode_append_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                                  block_tables: torch.Tensor, context_lens: torch.Tensor,
+                                  k_new: torch.Tensor, v_new: torch.Tensor,
+                                  scale: float | None = None, out: torch.Tensor | None = None,
+                                  workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """A decode step's KV write and attention in one call (the reference's _write_kv_layer then
+    _attn_paged, src/plastic_infer/exec/runner_paged.py:251-255): row b's new token is position
+    context_lens[b] - 1, whose K / V are k_new[b] / v_new[b] ([B, Hkv, D]); they are written to
+    that position's slot of block_tables[b], and the result is paged_decode_attention over the
+    updated pools. The fast kernel reads the new token from k_new / v_new and writes the slot
+    itself, so no write launch precedes the attention."""
+    dev = N.require_device(q, k_pages, v_pages, block_tables, context_lens, k_new, v_new,
+                           names=("q", "k_pages", "v_pages", "block_tables", "context_lens",
+                                  "k_new", "v_new"))
+    _check_pool(k_pages, v_pages)
+    num_pages, Hkv, D, P = k_pages.shape
+    if q.dim() != 3 or q.shape[2] != D or q.shape[1] % Hkv:
+        raise ValueError(f"q must be [B, Hq, {D}] with Hq a multiple of {Hkv}, got {tuple(q.shape)}")
+    if q.dtype != k_pages.dtype or k_new.dtype != k_pages.dtype or v_new.dtype != k_pages.dtype:
+        raise ValueError("q, k_new and v_new dtypes must match the KV pool dtype")
+    if not (q.stride(2) == 1 and q.stride(1) == D):
+        q = q.contiguous()
+    B, Hq, _ = q.shape
+    for name, t in (("k_new", k_new), ("v_new", v_new)):
+        if t.shape != (B, Hkv, D):
+            raise ValueError(f"{name} must be [{B}, {Hkv}, {D}], got {tuple(t.shape)}")
+    if k_new.stride() != v_new.stride() or k_new.stride(2) != 1 or k_new.stride(1) != D:
+        k_new, v_new = k_new.contiguous(), v_new.contiguous()
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.shape[0] != B:
+        raise ValueError("block_tables must be int32 [B, max_pages]")
+    if context_lens.dtype != torch.int32 or context_lens.shape != (B,):
+        raise ValueError("context_lens must be int32 [B]")
+    block_tables = block_tables.contiguous()
+    context_lens = context_lens.contiguous()
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=q.dtype, device=dev)
+    elif out.shape != (B, Hq, D) or out.dtype != q.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [B, Hq, D] tensor of q's dtype")
+    if B == 0:
+        return out
+    need = decode_workspace_bytes(B, Hq, Hkv, D, P, block_tables.shape[1])
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    scale = (1.0 / math.sqrt(D)) if scale is None else float(scale)
+    N.call("pia_paged_decode_append_attention", out.data_ptr(), q.data_ptr(), q.stride(0),
+           k_pages.data_ptr(), v_pages.data_ptr(), block_tables.data_ptr(), block_tables.shape[1],
+           context_lens.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), B, Hq,
+           Hkv, D, P, num_pages, scale, N.dtype_code(q.dtype),
+           N.ptr(workspace) if need else None,
+           (workspace.numel() * workspace.element_size()) if need else 0, N.stream_of(dev))
+    return out
+
+
 def paged_decode_attention_noalloc(q: torch.Tensor, k_pages: torch.Tensor,
                                    v_pages: torch.Tensor, block_tables: torch.Tensor,
                                    context_lens: torch.Tensor, out: torch.Tensor,
