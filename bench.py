@@ -34,6 +34,8 @@ reference torch path on this host's cores, on a bounded sample of the same input
   python bench.py --workload moe-experts-prefill   # the same FFN over 4096 prefill tokens
   python bench.py --workload prefill-stream  # Qwen3-30B-A3B prefill of 4096 tokens through the
                                              # expert double buffer, 48 layers of pinned banks
+  python bench.py --workload prefill-attn    # chunked-prefill paged attention (matrix cores):
+                                             # 8 x 1024-token chunks after 3072 context tokens
 The default workload (decode) is the headline; the others print their own JSON line.
 """
 
@@ -451,6 +453,96 @@ def bench_decode_gqa8(torch, dev, args) -> dict:
          "bound": "hbm", "achieved": round(a_gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
          "frac": round(a_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
          "algorithmic_bytes_per_launch": attn_bytes, "avg_launch_ms": round(at_ms, 4)})
+
+
+PA_B, PA_CTX, PA_CHUNK, PA_SEED = 8, 4096, 1024, 9
+
+
+def bench_prefill_attn(torch, dev, args) -> dict:
+    """Chunked-prefill attention over the paged pool with Qwen3-8B heads (32 q / 8 kv,
+    head_dim 128, bf16, page 16): 8 sequences, each a 1024-token chunk whose rows attend
+    causally to the 3072 earlier tokens of the context and to the chunk itself (kv 4096,
+    q_pos_offset 3072), block tables a seeded permutation of the pool. One step = one
+    paged_attention call (the matrix-core prefill kernel). FLOPs: 4 * head_dim per (row, q head,
+    visible key) - the QK dot and the PV accumulation."""
+    from plastic_infer.kernel import paged_attention
+
+    b, ctx, chunk = PA_B, PA_CTX, PA_CHUNK
+    g = torch.Generator().manual_seed(PA_SEED)
+    per = ctx // P
+    npool = b * per + 64
+    bt = torch.randperm(npool, generator=g)[: b * per].view(b, per).to(torch.int32)
+    gd = torch.Generator(device=dev).manual_seed(PA_SEED)
+    kp = torch.randn(npool, HKV, D, P, generator=gd, device=dev).to(torch.bfloat16)
+    vp = torch.randn(npool, HKV, D, P, generator=gd, device=dev).to(torch.bfloat16)
+    q = torch.randn(b * chunk, HQ, D, generator=gd, device=dev).to(torch.bfloat16)
+    cu = torch.arange(0, (b + 1) * chunk, chunk, dtype=torch.int32).to(dev)
+    lens = torch.full((b,), ctx, dtype=torch.int32, device=dev)
+    offs = torch.full((b,), ctx - chunk, dtype=torch.int32, device=dev)
+    bt_d = bt.to(dev)
+    res = {}
+
+    def step(ev):
+        if ev:
+            ev[0].record()
+        res["out"] = paged_attention(q, kp, vp, bt_d, lens, cu_q=cu, q_pos_offsets=offs)
+        if ev:
+            ev[1].record()
+
+    ms, (k_ms,), wall = _phase_timer(torch, dev, step, 1, args.steps, args.warmup)
+    keys = chunk * (ctx - chunk) + chunk * (chunk + 1) // 2      # visible keys per (seq, head)
+    flops = b * HQ * keys * 4 * D
+    hbm = b * ctx * HKV * D * 2 * 2 + 2 * b * chunk * HQ * D * 2 + b * per * 4
+    tflops = flops / (k_ms / 1e3) / 1e12
+    cpu = None if args.no_cpu_baseline else _cpu_prefill_attn(torch, q, kp, vp, bt, res["out"])
+    return _result(
+        "paged chunked-prefill attention TFLOP/s (bf16 matrix cores)", tflops, "TFLOP/s", args,
+        ms, "bf16",
+        {"workload": "qwen3-8b chunked prefill attention: 8 seqs x 1024-token chunks after 3072 "
+                     "context tokens, 32 q / 8 kv heads, head_dim 128, page 16, causal",
+         "batch": b, "chunk": chunk, "context_len": ctx},
+        {"flops_per_step": flops, "hbm_bytes_per_step": hbm,
+         "hbm_gbps": round(hbm / (k_ms / 1e3) / 1e9, 2), "wall_s_timed": round(wall, 4)},
+        {"kernel": "paged_prefill_mfma<4>", "bound": "mfma", "achieved": round(tflops, 2),
+         "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+         "algorithmic_flops_per_launch": flops, "avg_launch_ms": round(k_ms, 4)},
+        cpu)
+
+
+def _cpu_prefill_attn(torch, q, kp, vp, bt, gpu_out) -> dict:
+    """The oracle (gather + GQA repeat + SDPA with the offset mask, on this host's cores) on the
+    last 128 rows of sequence 0 (the rows with the most keys), 1 warm-up + median of 3; its output
+    is also the parity check of the GPU's rows (2e-2)."""
+    import oracle.paged_kv as OP
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    n = 128
+    pages = bt[0].tolist()
+    ids = torch.tensor(pages, device=kp.device)
+    kc, vc = kp.index_select(0, ids).cpu(), vp.index_select(0, ids).cpu()
+    table = list(range(len(pages)))
+    rows = q[PA_CHUNK - n:PA_CHUNK].cpu()[None]
+    start = PA_CTX - n
+
+    def run():
+        return OP.paged_attention(rows, kc, vc, table, P, PA_CTX, causal=True, q_start_pos=start)
+
+    ref = run()[0]
+    err = (gpu_out[PA_CHUNK - n:PA_CHUNK].float().cpu() - ref.float()).abs().max().item()
+    if not err <= 2e-2:
+        raise AssertionError(f"bench parity: prefill attention differs from the oracle, {err:.3e}")
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    keys = sum(start + i + 1 for i in range(n))
+    flops = HQ * keys * 4 * D
+    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port", "sample": f"last {n} rows of sequence 0 (kv up to {PA_CTX}), "
+            f"1 warm-up + median of 3, {t * 1e3:.1f} ms", "parity_max_abs_err": err}
 
 
 XS_L, XS_E, XS_H, XS_I, XS_B, XS_K, XS_SLOTS, XS_SEED = 48, 128, 2048, 768, 64, 8, 3072, 5
@@ -1360,7 +1452,7 @@ def main() -> int:
     ap.add_argument("--workload", choices=("decode", "decode-gqa8", "prefill-write",
                                            "moe-permute", "expert-stream", "moe-experts",
                                            "moe-experts-prefill", "prefill-stream", "kv-sink",
-                                           "host-stream", "decode-step"),
+                                           "host-stream", "decode-step", "prefill-attn"),
                     default="decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -1389,6 +1481,7 @@ def main() -> int:
                "moe-experts-prefill": lambda t, d, a: bench_moe_experts(t, d, a, 4096),
                "prefill-stream": bench_prefill_stream, "kv-sink": bench_kv_sink,
                "host-stream": bench_host_stream, "decode-step": bench_decode_step,
+               "prefill-attn": bench_prefill_attn,
                }[args.workload]
         print(f"bench: workload {args.workload}", file=sys.stderr, flush=True)
         print(json.dumps(run(torch, dev, args)), flush=True)
