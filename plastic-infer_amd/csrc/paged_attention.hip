@@ -1273,7 +1273,7 @@ extern "C" int pia_paged_attention(void* out, const void* q, const void* k_pages
     return fail(PIA_EINVAL, "paged_attention: without cu_q, total_q_rows must equal num_seqs");
   if (total_q_rows > 0x7fffffff) return fail(PIA_EINVAL, "paged_attention: too many rows");
   if (prefill_mfma_path(dtype, num_heads, num_kv_heads, head_dim, page_size, num_seqs,
-                        total_q_rows, cu_q) &&
+                        total_q_rows, cu_q, scale) &&
       aligned(q, 16) && aligned(out, 16) && aligned(k_pages, 16) && aligned(v_pages, 16))
     return launch_prefill_mfma(out, q, k_pages, v_pages, block_tables, bt_stride, kv_lens, cu_q,
                                q_pos_offsets, num_seqs, total_q_rows, num_heads, num_kv_heads,

@@ -5,13 +5,21 @@
 // one sequence, i.e. 64 (position, q head) rows that share the kv head's keys: row r is
 // position s0 + r / G, head h * G + r % G. Wave w owns rows 16 w .. 16 w + 15. The keys are
 // walked in 64-token tiles (four pages): K and V come from the pool into registers one tile
-// ahead, then into LDS (double buffered, one barrier per tile):
-//   K as [token][d] (the pool stores [d][token]; the transpose happens in the LDS writes),
-//   V as [d][token] (its pool layout).
+// ahead, then into LDS in their pool layout [d][token] (16-byte stores; double buffered, one
+// barrier per tile). A tile row (one d, 64 tokens, eight 16-byte chunks) is stored unpadded with
+// chunk c at c ^ ((d / 4) ^ 2 (d % 4)) % 8: with that swizzle the transposing K reads, the
+// 8-byte V reads and the 16-byte stores below ran without LDS bank conflicts when measured
+// (SQ_LDS_BANK_CONFLICT of each access pattern and offset replayed alone), where padded rows
+// left 2 to 24 conflict cycles per instruction on one pattern or another.
 // Per tile each wave runs
-//   S^T = K . Q^T   16 v_mfma_f32_16x16x32_bf16: A = K rows from LDS, B = the wave's q rows
-//                   (registers, loaded once). Lane l then holds the scores of row l % 16 for
-//                   tokens 16 m + 4 (l / 16) + j (m < 4, j < 4) of the tile.
+//   S^T = K . Q^T   v_mfma_f32_16x16x32_bf16: A = K^T operands built by ds_read_b64_tr_b16
+//                   (within each 16-lane group the eight-byte reads of the lanes form a 16 x 4
+//                   matrix, and lane i receives elements (4 k + i / 4, i % 4), k < 4; so lane r
+//                   of group g reads the four tokens 16 m + 4 (r % 4) .. of K row d0 + r / 4 and
+//                   lane i ends with K[token 16 m + i][d0 .. d0 + 3]; two reads, d0 and d0 + 4,
+//                   make an operand), B = the wave's q rows (registers, loaded once). Lane l then
+//                   holds the scores of row l % 16 for tokens 16 m + 4 (l / 16) + j (m < 4,
+//                   j < 4) of the tile.
 //   online softmax  per row in fp32, base 2 with the scale folded in; a row's 64 scores sit
 //                   in four lanes (l, l ^ 16, l ^ 32, l ^ 48), reduced by two shuffles.
 //   O += P . V      16 MFMAs: the probabilities are the A operand straight from the score
@@ -39,16 +47,30 @@ typedef __bf16 pf_bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float pf_f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int PF_D = 128, PF_P = 16;
-constexpr int PF_ROWS = 64;           // (position, head) rows per work item: 4 waves x 16
+constexpr int PF_RB = 2;              // 16-row MFMA blocks per wave
+constexpr int PF_ROWS = 64 * PF_RB;   // (position, head) rows per work item: 4 waves x 32
 constexpr int PF_KT = 64;             // keys per tile: four pages
-constexpr int PF_KS = PF_D + 8;       // K tile row stride in LDS (elements), [token][d]
-constexpr int PF_VS = PF_KT + 8;      // V tile row stride in LDS (elements), [d][token]
 constexpr int PF_MAX_SEQS = 1024;     // sequences per launch (tile prefix in LDS)
-constexpr float kNegBigPf = -1.0e30f;
+
+// element offset of (row d, token t) in a swizzled [d][64 tokens] LDS tile
+__device__ __forceinline__ int pf_swz(int d, int t) {
+  return d * PF_KT + ((((t >> 3) ^ (d >> 2) ^ ((d & 3) << 1)) & 7) << 3) + (t & 7);
+}
+// lazy rescaling threshold (log2 units): a row's exponentials are taken against a reference
+// that trails its true max by at most this much, so probabilities stay <= 2^8
+constexpr float PF_RESCALE = 8.0f;
 
 __device__ __forceinline__ pf_f32x4_t pf_mfma(const uint4& a, const uint4& b, pf_f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(pf_bf16x8_t, a),
                                                  __builtin_bit_cast(pf_bf16x8_t, b), c, 0, 0, 0);
+}
+
+// ds_read_b64_tr_b16 at an 8-byte aligned LDS address (see the kernel's description)
+__device__ __forceinline__ uint2 pf_read_tr(const uint16_t* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(const_cast<uint16_t*>(p)));
+  return __builtin_bit_cast(uint2, v);
 }
 
 __device__ __forceinline__ uint32_t pf_pack(float lo, float hi) {
@@ -66,9 +88,10 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
     int64_t num_pages, float scale_log2) {
   constexpr int D = PF_D, P = PF_P, TILE = D * P;
   constexpr int PPT = PF_ROWS / G;  // query positions per work item
+  constexpr int RB = PF_RB;
   constexpr int XCDS = 8;
-  __shared__ __align__(16) uint16_t ks[2][PF_KT * PF_KS];
-  __shared__ __align__(16) uint16_t vs[2][PF_D * PF_VS];
+  __shared__ __align__(16) uint16_t ks[2][PF_D * PF_KT];
+  __shared__ __align__(16) uint16_t vs[2][PF_D * PF_KT];
   __shared__ int tile_pref[PF_MAX_SEQS + 1];
   __shared__ int wsum[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -124,52 +147,73 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
   const int nkt = (kmax + PF_KT - 1) / PF_KT;
   const int32_t* btb = bt + int64_t(b) * bt_stride;
 
-  // this lane's score row (16 wave + l % 16) and its q operand: d = 32 kc + 8 (l / 16) .. + 7
+  // this lane's score rows: 32 wave + 16 rb + l % 16 (rb < RB) and their q operands,
+  // d = 32 kc + 8 (l / 16) .. + 7
   const int g4 = lane >> 4, n16 = lane & 15;
-  const int r_s = 16 * wave + n16;
-  const int s_r = s0 + r_s / G;
-  const bool row_ok = s_r < n_b;
-  const int lim_r = !row_ok ? 0 : (offsets ? min(kv_len, off + s_r + 1) : kv_len);
-  uint4 qreg[4];
-  {
-    const uint16_t* qp = q + (row0 + (row_ok ? s_r : 0)) * q_row + int64_t(h * G + r_s % G) * D;
+  int lim_r[RB];
+  uint4 qreg[RB][4];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int r = 32 * wave + 16 * rb + n16;
+    const int sr = s0 + r / G;
+    const bool ok = sr < n_b;
+    lim_r[rb] = !ok ? 0 : (offsets ? min(kv_len, off + sr + 1) : kv_len);
+    const uint16_t* qp = q + (row0 + (ok ? sr : 0)) * q_row + int64_t(h * G + r % G) * D;
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc)
-      qreg[kc] = row_ok ? *reinterpret_cast<const uint4*>(qp + 32 * kc + 8 * g4)
+      qreg[rb][kc] = ok ? *reinterpret_cast<const uint4*>(qp + 32 * kc + 8 * g4)
                         : make_uint4(0u, 0u, 0u, 0u);
   }
+  // every valid row of the item sees at least the keys below lim_min (the first row's limit)
+  const int lim_min = offsets ? max(0, min(kv_len, off + s0 + 1)) : kv_len;
 
   // tile loads: thread t moves piece t of each of the tile's four (page, head) K and V tiles:
   // row d = t / 2, tokens 8 (t % 2) .. + 7 of page i
   const int ld_d = tid >> 1, ld_half = tid & 1;
+  const int ld_off = ld_d * P + ld_half * 8;  // the thread's piece inside a (page, head) tile
   uint4 kr[4], vr[4];
   auto fetch = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int pi = 4 * kt + i;
-      const int id = pi < npages ? btb[pi] : -1;
-      const bool ok = id >= 0 && int64_t(id) < num_pages;
-      const int64_t base = (int64_t(ok ? id : 0) * Hkv + h) * TILE + ld_d * P + ld_half * 8;
-      kr[i] = ok ? *reinterpret_cast<const uint4*>(kpool + base) : make_uint4(0u, 0u, 0u, 0u);
-      vr[i] = ok ? *reinterpret_cast<const uint4*>(vpool + base) : make_uint4(0u, 0u, 0u, 0u);
+      const int id = __builtin_amdgcn_readfirstlane(pi < npages ? btb[pi] : -1);
+      if (id >= 0 && int64_t(id) < num_pages) {  // uniform: one scalar base per page
+        const int64_t tile_off = (int64_t(id) * Hkv + h) * TILE;
+        kr[i] = *reinterpret_cast<const uint4*>(kpool + tile_off + ld_off);
+        vr[i] = *reinterpret_cast<const uint4*>(vpool + tile_off + ld_off);
+      } else {
+        kr[i] = make_uint4(0u, 0u, 0u, 0u);
+        vr[i] = make_uint4(0u, 0u, 0u, 0u);
+      }
     }
   };
+  // Swizzled LDS offsets, as per-lane bases XORed with compile-time terms (pf_swz(d, t) with
+  // the chunk index split into its bits): a store of piece i lands at st_base ^ 16 i; the K
+  // operand read (kc, hi, mb) at (k_base[hi] ^ 16 mb) + 2048 kc; the V operand read
+  // (nb, c, s) at (v_base[nb % 2] ^ (32 c + 16 s)) + 1024 nb.
+  int st_base, k_base[2], v_base[2];
+  {
+    const int f = ((ld_d >> 2) ^ ((ld_d & 3) << 1)) & 7;
+    st_base = (ld_d * PF_KT + 8 * (ld_half ^ (f & 1))) | (16 * (f >> 1));
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi) {
+      const int fk = ((2 * g4 + hi) ^ ((n16 >> 2) << 1)) & 7;
+      const int row = 8 * g4 + 4 * hi + (n16 >> 2);
+      k_base[hi] = (row * PF_KT + 4 * (n16 & 1) + 8 * (((n16 >> 1) & 1) ^ (fk & 1))) |
+                   (16 * (fk >> 1));
+      const int fv = ((4 * hi + (n16 >> 2)) ^ ((n16 & 3) << 1)) & 7;  // hi: parity of nb
+      v_base[hi] = (n16 * PF_KT + 4 * (g4 & 1)) | (8 * ((g4 >> 1) ^ fv));
+    }
+  }
   auto stage = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int t0 = i * P + ld_half * 8;
-      const uint16_t* ke = reinterpret_cast<const uint16_t*>(&kr[i]);
-#pragma unroll
-      for (int x = 0; x < 8; ++x) ks[buf][(t0 + x) * PF_KS + ld_d] = ke[x];
-      *reinterpret_cast<uint4*>(&vs[buf][ld_d * PF_VS + t0]) = vr[i];
+      const int e = st_base ^ (16 * i);
+      *reinterpret_cast<uint4*>(&ks[buf][e]) = kr[i];
+      *reinterpret_cast<uint4*>(&vs[buf][e]) = vr[i];
     }
   };
-
-  float m = kNegBigPf, l = 0.f;
-  pf_f32x4_t acc[8];
-#pragma unroll
-  for (int nb = 0; nb < 8; ++nb) acc[nb] = pf_f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // page ids of the tile, for the score mask: bit i set when page i holds keys
+  // pages of a tile that hold keys: bit i for page i
   auto page_mask = [&](int kt) {
     int mk = 0;
 #pragma unroll
@@ -181,102 +225,150 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
     return mk;
   };
 
+  // m[rb]: the row's running max in raw score units, the reference point of its exponentials.
+  // It only moves when a tile's max exceeds it by more than PF_RESCALE / scale_log2 (lazy
+  // rescaling: probabilities up to 2^PF_RESCALE in between, exact after the final division).
+  // acc[rb][8] is the row's unnormalised output in the MFMA layout (rows 4 g4 + j, column
+  // l % 16); lsum[rb] is its softmax denominator, summed by the matrix cores against a column
+  // of ones, so it sits in the same layout and is rescaled with the accumulators.
+  float m[RB];
+  pf_f32x4_t acc[RB][8], lsum[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    m[rb] = -INFINITY;
+    lsum[rb] = pf_f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) acc[rb][nb] = pf_f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const uint4 ones = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+
   if (nkt > 0) fetch(0);
   for (int kt = 0; kt < nkt; ++kt) {
     const int buf = kt & 1;
     stage(buf);
     __syncthreads();
     const int pmask = page_mask(kt);
+    // a tile every valid row sees whole (interior of the causal triangle, all pages valid)
+    const bool full = pmask == 0xF && (kt + 1) * PF_KT <= lim_min;
     if (kt + 1 < nkt) fetch(kt + 1);
 
-    // S^T for the wave's 16 rows: 4 token blocks (one per page) x 4 d chunks
-    pf_f32x4_t sc[4];
+    // S^T for the wave's rows: 4 token blocks (one per page) x 4 d chunks, each K operand
+    // serving both row blocks
+    pf_f32x4_t sc[RB][4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
-      sc[mb] = pf_f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
-        const uint4 a =
-            *reinterpret_cast<const uint4*>(&ks[buf][(16 * mb + n16) * PF_KS + 32 * kc + 8 * g4]);
-        sc[mb] = pf_mfma(a, qreg[kc], sc[mb]);
+        const uint2 lo = pf_read_tr(&ks[buf][(k_base[0] ^ (16 * mb)) + 2048 * kc]);
+        const uint2 hi = pf_read_tr(&ks[buf][(k_base[1] ^ (16 * mb)) + 2048 * kc]);
+        const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          sc[rb][mb] = pf_mfma(a, qreg[rb][kc],
+                               kc == 0 ? pf_f32x4_t{0.f, 0.f, 0.f, 0.f} : sc[rb][mb]);
       }
     }
-    // mask, scale, online softmax of row r_s (tokens 64 kt + 16 mb + 4 g4 + j)
-    float x[4][4];
-    float mx = -INFINITY;
+    uint4 pk[RB][2];
+    bool moved = false;
+    float alpha[RB];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int rb = 0; rb < RB; ++rb) {
+      // on boundary tiles, keys the row may not see (tokens 64 kt + 16 mb + 4 g4 + j) -> -inf
+      if (!full) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int t = kt * PF_KT + 16 * mb + 4 * g4 + j;
-        const bool ok = t < lim_r && ((pmask >> mb) & 1);
-        x[mb][j] = ok ? sc[mb][j] * scale_log2 : -INFINITY;
-        mx = fmaxf(mx, x[mb][j]);
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int t = kt * PF_KT + 16 * mb + 4 * g4 + j;
+            if (!(t < lim_r[rb] && ((pmask >> mb) & 1))) sc[rb][mb][j] = -INFINITY;
+          }
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-    float ps = 0.f;
-    uint4 pk[2];
+      float mx = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      float p[2][4];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          p[hh][j] = __builtin_amdgcn_exp2f(x[2 * c + hh][j] - mnew);
-          ps += p[hh][j];
-        }
-      pk[c] = make_uint4(pf_pack(p[0][0], p[0][1]), pf_pack(p[0][2], p[0][3]),
-                         pf_pack(p[1][0], p[1][1]), pf_pack(p[1][2], p[1][3]));
-    }
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
-    l = l * alpha + ps;
-    m = mnew;
-    // rescale O: lane l's accumulator rows are 4 g4 + j; their alpha sits in lane 4 g4 + j
-    float aj[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) aj[j] = __shfl(alpha, 4 * g4 + j, 64);
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[nb][j] *= aj[j];
-    // O += P . V over the tile's two 32-token chunks
-#pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const uint16_t* vrow = &vs[buf][(16 * nb + n16) * PF_VS + 4 * g4];
+      for (int mb = 0; mb < 4; ++mb)
+        mx = fmaxf(mx, fmaxf(fmaxf(sc[rb][mb][0], sc[rb][mb][1]), fmaxf(sc[rb][mb][2], sc[rb][mb][3])));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // move the reference point only for a large enough rise (or the first keys of the row)
+      const float mref = (mx - m[rb]) * scale_log2 > PF_RESCALE ? mx : m[rb];
+      alpha[rb] = m[rb] == mref ? 1.f : __builtin_amdgcn_exp2f((m[rb] - mref) * scale_log2);
+      moved = moved || m[rb] != mref;
+      m[rb] = mref;
+      // p = 2^((s - m) * scale_log2); a row with no key yet keeps m = -inf and p = 0
+      const float nm = mref == -INFINITY ? 0.f : -mref * scale_log2;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const uint2 v0 = *reinterpret_cast<const uint2*>(vrow + 32 * c);
-        const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 32 * c + 16);
-        acc[nb] = pf_mfma(pk[c], make_uint4(v0.x, v0.y, v1.x, v1.y), acc[nb]);
+        float p[2][4];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            p[hh][j] = __builtin_amdgcn_exp2f(fmaf(sc[rb][2 * c + hh][j], scale_log2, nm));
+        pk[rb][c] = make_uint4(pf_pack(p[0][0], p[0][1]), pf_pack(p[0][2], p[0][3]),
+                               pf_pack(p[1][0], p[1][1]), pf_pack(p[1][2], p[1][3]));
       }
     }
+    // rescale O and the sums when some row's reference point moved: lane l's accumulator rows
+    // are 4 g4 + j of each block; their alpha sits in lane 4 g4 + j
+    if (__ballot(moved)) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        float aj[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) aj[j] = __shfl(alpha[rb], 4 * g4 + j, 64);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          lsum[rb][j] *= aj[j];
+#pragma unroll
+          for (int nb = 0; nb < 8; ++nb) acc[rb][nb][j] *= aj[j];
+        }
+      }
+    }
+    // O += P . V over the tile's two 32-token chunks, each V operand serving both row blocks;
+    // the sums against a column of ones
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      const int vb = v_base[nb & 1];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const uint2 v0 =
+            *reinterpret_cast<const uint2*>(&vs[buf][(vb ^ (32 * c)) + 1024 * nb]);
+        const uint2 v1 =
+            *reinterpret_cast<const uint2*>(&vs[buf][(vb ^ (32 * c + 16)) + 1024 * nb]);
+        const uint4 vop = make_uint4(v0.x, v0.y, v1.x, v1.y);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) acc[rb][nb] = pf_mfma(pk[rb][c], vop, acc[rb][nb]);
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) lsum[rb] = pf_mfma(pk[rb][c], ones, lsum[rb]);
   }
 
-  // out = O / l for rows 4 g4 + j of the wave (their l sits in lane 4 g4 + j)
+  // out = O / sum for rows 4 g4 + j of each block
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float lj = __shfl(l, 4 * g4 + j, 64);
-    const int r = 16 * wave + 4 * g4 + j;
-    const int s = s0 + r / G;
-    if (s >= n_b) continue;
-    uint16_t* o = out + (row0 + s) * q_row + int64_t(h * G + r % G) * D + n16;
-    const float inv = lj > 0.f ? 1.f / lj : 0.f;
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) o[16 * nb] = f32_to_bf16(acc[nb][j] * inv);
-  }
+    for (int j = 0; j < 4; ++j) {
+      const float lj = lsum[rb][j];
+      const int r = 32 * wave + 16 * rb + 4 * g4 + j;
+      const int s = s0 + r / G;
+      if (s >= n_b) continue;
+      uint16_t* o = out + (row0 + s) * q_row + int64_t(h * G + r % G) * D + n16;
+      const float inv = lj > 0.f ? 1.f / lj : 0.f;
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) o[16 * nb] = f32_to_bf16(acc[rb][nb][j] * inv);
+    }
 }
 
 }  // namespace
 
 bool prefill_mfma_path(int dtype, int Hq, int Hkv, int D, int P, int num_seqs,
-                       int64_t total_q_rows, const int32_t* cu_q) {
+                       int64_t total_q_rows, const int32_t* cu_q, float scale) {
   const int G = Hq / Hkv;
-  return dtype == PIA_DTYPE_BF16 && D == PF_D && P == PF_P &&
+  // scale > 0: the kernel keeps its running max in raw score units
+  return dtype == PIA_DTYPE_BF16 && D == PF_D && P == PF_P && scale > 0.f &&
          (G == 1 || G == 2 || G == 4 || G == 8) && cu_q != nullptr && num_seqs <= PF_MAX_SEQS &&
          total_q_rows >= 4 * int64_t(num_seqs);
 }
