@@ -250,21 +250,31 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_splitk(
 // other: the row tiles that share a W tile run side by side, the column tiles that share the
 // expert's A rows run together, and both are fetched from HBM about once and shared through
 // that XCD's L2 (a compact per-XCD work list from moe_plan_segments, so no item is empty).
-// Per K step (64): A [128 plan rows x 64] gathered through the plan and B [256 W rows x 64] go
-// global -> registers -> LDS (16-byte chunks, eight threads per 128-byte row; XOR-swizzled LDS
-// rows), double buffered with one barrier per step and the global loads two steps ahead; eight
-// waves in a 2 x 4 arrangement each multiply 64 x 64 with v_mfma_f32_16x16x32 from LDS.
-// 16-row fragments past the tile's last real route are skipped. With the activation fused, the
-// W tile holds 128 gate and the matching 128 up rows, arranged so that each wave owns gate and
-// up of the same 32 columns.
+// Workgroups of four waves, two per compute unit, so that one workgroup's barrier waits overlap
+// the other's matrix products. Per K step of 32 the operands go from global memory straight
+// into LDS (16-byte direct loads through buffer descriptors, no staging registers), three step
+// buffers deep: the loads of step s + 2 are in flight while step s is multiplied. LDS holds
+// each 16-row x 32 operand fragment as 1 KiB: row r's 64 bytes at 64 r, its 16-byte K chunk c
+// in slot c ^ ((r >> 1) & 3). A direct load's lane l lands at byte 16 l, so lanes 4r .. 4r + 3
+// fetch row r's 64 contiguous bytes (one coalesced access). An MFMA operand read (ds_read_b128,
+// lane: row l % 16, chunk l / 16) in this order has no LDS bank conflicts, as measured with the
+// SQ_LDS_BANK_CONFLICT counter over the candidate chunk orders (with c ^ ((r >> 2) & 3), for
+// one, every read costs 3.8 conflict cycles). Waves in a 2 x 2 arrangement each multiply 64
+// plan rows by 128 W rows (4 x 8 fragments) with v_mfma_f32_16x16x32; a wave whose 64 rows
+// are all past the tile's last route skips its products. With the activation fused, the W
+// tile holds 128 gate and the matching 128 up rows, arranged so that each wave owns gate and
+// up of the same 64 columns.
 // ---------------------------------------------------------------------------------------------
-constexpr int TG_BM = 128, TG_BN = 256, TG_BK = 64;
-constexpr int TG_WM = 2, TG_WN = 4, TG_THREADS = 64 * TG_WM * TG_WN;  // 8 waves, 64 x 64 each
+constexpr int TG_BM = 128, TG_BN = 256, TG_BK = 32;
+constexpr int TG_THREADS = 256;                            // 4 waves, 2 x 2, 64 x 128 each
+constexpr int TG_AF = TG_BM / 16, TG_WF = TG_BN / 16;      // fragments per step: 8 A, 16 W
+constexpr int TG_LOADS = (TG_AF + TG_WF) / 4;              // direct loads per wave per step
+constexpr int TG_STAGE = (TG_AF + TG_WF) * 64;             // uint4 per step buffer (24 KiB)
 constexpr int TG_XCDS = 8;
 // Buffer resources: word 3 of a raw (stride 0) buffer descriptor on gfx9 parts; a load whose
-// offset is at or past the descriptor's byte count returns zeros, which masks plan padding, the
-// K tail and the column tail without branches. TG_OOB is such an offset for every buffer here
-// (the host keeps A and each expert's W below 2 GiB).
+// offset is at or past the descriptor's byte count returns zeros (a direct load writes zeros
+// to LDS), which masks plan padding, the K tail and the column tail without branches. TG_OOB
+// is such an offset for every buffer here (the host keeps A and each expert's W below 2 GiB).
 constexpr int TG_RSRC_WORD3 = 0x00020000;
 constexpr uint32_t TG_OOB = 0x80000000u;
 #ifndef PIA_EG_TILED_MIN_ROUTES
@@ -335,13 +345,25 @@ __global__ __launch_bounds__(1024) void moe_plan_segments(
   }
 }
 
-// LDS tile rows are 64 elements (128 bytes, eight 16-byte chunks); chunk c of row r is stored
-// at chunk c ^ ((r >> 1) & 7), so that a 16-byte store of two rows by sixteen lanes and a
-// 16-byte MFMA operand read of sixteen rows each touch all 64 banks once.
-__device__ __forceinline__ int tg_swz(int r, int c) { return r * TG_BK + ((c ^ ((r >> 1) & 7)) << 3); }
+typedef __attribute__((address_space(3))) void tg_lds_t;
+
+// Wait until at most N of this wave's vector-memory operations are outstanding and all of its
+// LDS operations are done, then meet the workgroup at a barrier. No memory fence: a fence would
+// also wait for the direct loads of the steps still in flight. The waits make this wave's
+// direct loads of the step complete (their LDS writes done) and its reads of the buffer about
+// to be refilled returned; the barrier makes both hold for every wave. The empty asm
+// statements keep the compiler from moving LDS accesses across the barrier.
+template <int N>
+__device__ __forceinline__ void tg_sync() {
+  asm volatile("" ::: "memory");
+  // s_waitcnt fields: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait), lgkmcnt [11:8]
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 template <int DT, int ACT>
-__global__ __launch_bounds__(TG_THREADS, 1) void moe_gemm_tiled(
+__global__ __launch_bounds__(TG_THREADS, 2) void moe_gemm_tiled(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ a, const uint16_t* __restrict__ w,
     const float* __restrict__ topk_w, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ expert_ids, const int32_t* __restrict__ seg_block,
@@ -349,25 +371,27 @@ __global__ __launch_bounds__(TG_THREADS, 1) void moe_gemm_tiled(
     const int32_t* __restrict__ xcd_items, int64_t numel, int block_m, int a_div, int64_t lda,
     int num_experts, int n_rows, int K, int64_t ldo, int n_tiles, int mulw, uint32_t a_bytes) {
   constexpr bool FUSED = ACT != PIA_ACT_NONE;
-  constexpr int AQ = TG_BM * 8 / TG_THREADS, BQ = TG_BN * 8 / TG_THREADS;  // chunks per thread
-  constexpr int RSTEP = TG_THREADS / 8;                                     // rows per pass
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][TG_BM * TG_BK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][TG_BN * TG_BK];
+  // three step buffers as separate arrays: the compiler tracks the direct loads into each one
+  // apart, so a read of one buffer does not wait for the loads still landing in the others
+  __shared__ __attribute__((aligned(16))) uint4 st0[TG_STAGE];
+  __shared__ __attribute__((aligned(16))) uint4 st1[TG_STAGE];
+  __shared__ __attribute__((aligned(16))) uint4 st2[TG_STAGE];
   __shared__ int32_t tile_route[TG_BM];
   __shared__ float tile_w[TG_BM];
   const int tid = threadIdx.x, lane = tid & 63;
-  // wave index as a scalar, so that per-wave decisions compile to scalar branches
+  // wave index as a scalar, so that per-wave decisions compile to scalar branches and the LDS
+  // bases of the direct loads are wave-uniform
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wv / TG_WN, wn = wv % TG_WN;
+  const int wm = wv >> 1, wn = wv & 1;
   const int li = lane & 15, kg = lane >> 4;
+  // direct loads: lane -> row lr of a fragment, K chunk kc; operand reads: lane -> LDS slot
+  const int lr = lane >> 2, kc = (lane & 3) ^ ((lr >> 1) & 3);
+  const int rslot = 4 * li + (kg ^ ((li >> 1) & 3));
   const int n_seg = seg_count[0];
   const int half = n_rows >> 1;
-  // K steps, rounded up to even (a trailing step past K reads zeros)
-  const int nk = ((K + 2 * TG_BK - 1) / (2 * TG_BK)) * 2;
+  const int nks = (K + TG_BK - 1) / TG_BK;
   const __amdgpu_buffer_rsrc_t ares =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a), 0, int(a_bytes), TG_RSRC_WORD3);
-  // loader: 16-byte chunk (row lrow + RSTEP q, K chunk lc) of a tile
-  const int lrow = tid >> 3, lc = tid & 7, lk = lc * 8;
   // this workgroup's XCD lane (workgroups are dealt to XCDs round robin; the grid is a
   // multiple of 8) and its segments x, x + 8, ...
   const int x = blockIdx.x % TG_XCDS;
@@ -392,28 +416,28 @@ __global__ __launch_bounds__(TG_THREADS, 1) void moe_gemm_tiled(
     const bool e_ok = e >= 0 && e < num_experts;  // else zero rows, as in moe_gemm_splitk
     const int64_t m0 = seg0 + int64_t(mt) * TG_BM;
 
-    // this thread's W rows of the tile as byte offsets into the expert's W; rows past the
-    // tile's end read as zeros (offset beyond the buffer's range)
+    // W fragments 4 wv .. 4 wv + 3 of a step are this wave's to load; this lane's W row of
+    // each as a byte offset into the expert's W (rows past the tile's end: out of range)
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(w + (e_ok ? int64_t(e) * n_rows * K : 0)), 0,
         e_ok ? n_rows * K * 2 : 0, TG_RSRC_WORD3);
-    uint32_t boff[BQ];
+    uint32_t woff[4];
 #pragma unroll
-    for (int q = 0; q < BQ; ++q) {
-      const int r = lrow + RSTEP * q;
+    for (int q = 0; q < 4; ++q) {
+      const int g = 4 * wv + q;  // W fragment: wave column g / 8 owns it, as its fragment g % 8
       int n;
       bool ok;
       if constexpr (FUSED) {
-        // each wave column owns 64 W rows: 32 gate rows and the matching 32 up rows
-        const int rw = r & 63, jj = rw >> 4;
-        const int col = t * (TG_BN / 2) + (r >> 6) * 32 + (jj & 1) * 16 + (rw & 15);
+        // fragments 0..3 of a wave column are gate rows, 4..7 the matching up rows
+        const int jj = g & 7;
+        const int col = t * (TG_BN / 2) + (g >> 3) * 64 + (jj & 3) * 16 + lr;
         ok = col < half;
-        n = (jj < 2 ? 0 : half) + col;
+        n = (jj < 4 ? 0 : half) + col;
       } else {
-        n = t * TG_BN + r;
+        n = t * TG_BN + g * 16 + lr;
         ok = n < n_rows;
       }
-      boff[q] = ok ? uint32_t(n) * uint32_t(K) * 2u + uint32_t(lk) * 2u : TG_OOB;
+      woff[q] = ok ? uint32_t(n) * uint32_t(K) * 2u + uint32_t(kc) * 16u : TG_OOB;
     }
 
     __syncthreads();  // the previous tile's epilogue is done with tile_route / tile_w
@@ -427,83 +451,70 @@ __global__ __launch_bounds__(TG_THREADS, 1) void moe_gemm_tiled(
     }
     // real routes come first in an expert's plan rows, so the live rows are a prefix
     const int nlive = __builtin_amdgcn_readfirstlane(__syncthreads_count(live));
-    uint32_t aoff[AQ];
+    // A fragments 2 wv, 2 wv + 1 of a step are this wave's to load
+    uint32_t aoff[2];
 #pragma unroll
-    for (int q = 0; q < AQ; ++q) {
-      const int32_t rr = tile_route[lrow + RSTEP * q];
-      aoff[q] = rr >= 0 ? uint32_t(rr / a_div) * uint32_t(lda) * 2u + uint32_t(lk) * 2u : TG_OOB;
+    for (int q = 0; q < 2; ++q) {
+      const int32_t rr = tile_route[(2 * wv + q) * 16 + lr];
+      aoff[q] = rr >= 0 ? uint32_t(rr / a_div) * uint32_t(lda) * 2u + uint32_t(kc) * 16u : TG_OOB;
     }
-    // K steps of 64: two register sets in flight ahead of the LDS buffer being multiplied
-    // (loads for step kt + 2 are issued while step kt is multiplied and kt + 1 is stored).
-    // Loads past K read as zeros (offset beyond the buffer), so every load is unconditional.
-    auto gload = [&](uint4(&ra)[AQ], uint4(&rb)[BQ], int k0) __attribute__((always_inline)) {
-      const bool k_ok = k0 + lk < K;
-      const uint32_t kb = uint32_t(k0) * 2u;
+    // direct loads of step s into buffer buf: K offset in the scalar offset; on a last step
+    // shorter than 32 the lanes past K, and on the two steps past the last every lane, read
+    // out of range (zeros, no memory access), so every step issues the same six loads
+    auto issue = [&](uint4* buf, int s) __attribute__((always_inline)) {
+      const int k0 = min(s, nks) * TG_BK;
+      const bool kin = k0 + 8 * kc < K;
 #pragma unroll
-      for (int q = 0; q < AQ; ++q)
-        ra[q] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(ares, k_ok ? aoff[q] + kb : TG_OOB, 0, 0));
+      for (int q = 0; q < 2; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (tg_lds_t*)(buf + (2 * wv + q) * 64), 16,
+                                                 kin ? aoff[q] : TG_OOB, k0 * 2, 0, 0);
 #pragma unroll
-      for (int q = 0; q < BQ; ++q)
-        rb[q] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, k_ok ? boff[q] + kb : TG_OOB, 0, 0));
+      for (int q = 0; q < 4; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (tg_lds_t*)(buf + (TG_AF + 4 * wv + q) * 64),
+                                                 16, kin ? woff[q] : TG_OOB, k0 * 2, 0, 0);
     };
-    auto sstore = [&](const uint4(&ra)[AQ], const uint4(&rb)[BQ], int buf)
-                      __attribute__((always_inline)) {
-#pragma unroll
-      for (int q = 0; q < AQ; ++q)
-        *reinterpret_cast<uint4*>(&As[buf][tg_swz(lrow + RSTEP * q, lc)]) = ra[q];
-#pragma unroll
-      for (int q = 0; q < BQ; ++q)
-        *reinterpret_cast<uint4*>(&Bs[buf][tg_swz(lrow + RSTEP * q, lc)]) = rb[q];
-    };
-    f32x4_t acc[4][4];
+    f32x4_t acc[4][8];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) acc[i][jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    bool frag_live[4];
+      for (int jj = 0; jj < 8; ++jj) acc[i][jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const bool wave_live = wm * 64 < nlive;
+    auto comp = [&](const uint4* buf) __attribute__((always_inline)) {
+      uint4 fa[4], fb[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) frag_live[i] = wm * 64 + i * 16 < nlive;
-    auto mma = [&](int buf) __attribute__((always_inline)) {
+      for (int jj = 0; jj < 8; ++jj) fb[jj] = buf[(TG_AF + wn * 8 + jj) * 64 + rslot];
 #pragma unroll
-      for (int s = 0; s < TG_BK / 32; ++s) {
-        const int c = s * 4 + kg;  // this lane's 16-byte K chunk of the step
-        uint4 fb[4];
+      for (int i = 0; i < 4; ++i) fa[i] = buf[(wm * 4 + i) * 64 + rslot];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-          fb[jj] = *reinterpret_cast<const uint4*>(&Bs[buf][tg_swz(wn * 64 + jj * 16 + li, c)]);
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (!frag_live[i]) continue;
-          const uint4 fa =
-              *reinterpret_cast<const uint4*>(&As[buf][tg_swz(wm * 64 + i * 16 + li, c)]);
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) acc[i][jj] = mfma_16x16x32<DT>(fa, fb[jj], acc[i][jj]);
-        }
-      }
+        for (int jj = 0; jj < 8; ++jj) acc[i][jj] = mfma_16x16x32<DT>(fa[i], fb[jj], acc[i][jj]);
     };
 
-    uint4 ra0[AQ], rb0[BQ], ra1[AQ], rb1[BQ];
-    gload(ra0, rb0, 0);
-    gload(ra1, rb1, TG_BK);
-    sstore(ra0, rb0, 0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt += 2) {
-      gload(ra0, rb0, (kt + 2) * TG_BK);
-      mma(0);
-      sstore(ra1, rb1, 1);
-      __syncthreads();
-      gload(ra1, rb1, (kt + 3) * TG_BK);
-      mma(1);
-      sstore(ra0, rb0, 0);
-      __syncthreads();
+    // steps s, s + 1, s + 2 in buffers st0, st1, st2; at the wait before step s the loads of
+    // steps s and s + 1 are outstanding, so vmcnt(TG_LOADS) leaves only step s + 1's. The
+    // loads issued for the two steps past the last land zeros in buffers nothing reads; the
+    // next tile's first barrier (with its fence) waits for them.
+    issue(st0, 0);
+    issue(st1, 1);
+    for (int s = 0; s < nks; s += 3) {
+      tg_sync<TG_LOADS>();
+      issue(st2, s + 2);
+      if (wave_live) comp(st0);
+      if (s + 1 >= nks) break;
+      tg_sync<TG_LOADS>();
+      issue(st0, s + 3);
+      if (wave_live) comp(st1);
+      if (s + 2 >= nks) break;
+      tg_sync<TG_LOADS>();
+      issue(st1, s + 4);
+      if (wave_live) comp(st2);
     }
 
     // epilogue: lane holds column li of each 16-column fragment, rows 4 kg + q
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (!frag_live[i]) continue;
+      if (wm * 64 + i * 16 >= nlive) continue;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int row = wm * 64 + i * 16 + kg * 4 + q;
@@ -513,18 +524,18 @@ __global__ __launch_bounds__(TG_THREADS, 1) void moe_gemm_tiled(
         uint16_t* orow = out + int64_t(rr) * ldo;
         if constexpr (FUSED) {
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj) {
-            const int col = t * (TG_BN / 2) + wn * 32 + jj * 16 + li;
+          for (int jj = 0; jj < 4; ++jj) {
+            const int col = t * (TG_BN / 2) + wn * 64 + jj * 16 + li;
             if (col < half) {
               const float gr = from_dt<DT>(to_dt<DT>(acc[i][jj][q] * wr));
-              const float ur = from_dt<DT>(to_dt<DT>(acc[i][jj + 2][q] * wr));
+              const float ur = from_dt<DT>(to_dt<DT>(acc[i][jj + 4][q] * wr));
               orow[col] = to_dt<DT>(act_fn<ACT>(gr) * ur);
             }
           }
         } else {
 #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const int col = t * TG_BN + wn * 64 + jj * 16 + li;
+          for (int jj = 0; jj < 8; ++jj) {
+            const int col = t * TG_BN + wn * 128 + jj * 16 + li;
             if (col < n_rows) orow[col] = to_dt<DT>(acc[i][jj][q] * wr);
           }
         }
@@ -639,7 +650,7 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
     // items: at most (used blocks * block_m / 128 + experts present) row tiles per column tile
     const int64_t max_seg = std::min<int64_t>(max_blocks, int64_t(num_experts) + 1);
     const int64_t ub = (ceil_div(max_num_tokens_padded, TG_BM) + max_seg) * n_tiles;
-    const int64_t g = std::min<int64_t>(ub, int64_t(cus));
+    const int64_t g = std::min<int64_t>(ub, 2 * int64_t(cus));  // two workgroups per CU
     const unsigned grid = unsigned(std::max<int64_t>(TG_XCDS, g / TG_XCDS * TG_XCDS));
 #define PIA_TG(DT, ACT)                                                                        \
   hipLaunchKernelGGL((moe_gemm_tiled<DT, ACT>), dim3(grid), dim3(TG_THREADS), 0, s, o, aa, ww, \
