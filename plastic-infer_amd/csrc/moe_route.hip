@@ -30,21 +30,25 @@ __device__ __forceinline__ uint32_t order_key(float x) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Wave reductions: DPP inside each row of 16 lanes (every lane of a row then holds the row's
+// result), then the four row results read as scalars (no LDS round trip), summed as
+// (row0 + row1) + (row2 + row3) in every lane.
+__device__ __forceinline__ float row_lane(float v, int row) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * row));
+}
 __device__ __forceinline__ float wave_max_f(float v) {
   v = fmaxf(v, dpp_f32<kDppXor1>(v));
   v = fmaxf(v, dpp_f32<kDppXor2>(v));
   v = fmaxf(v, dpp_f32<kDppRor4>(v));
   v = fmaxf(v, dpp_f32<kDppRor8>(v));
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+  return fmaxf(fmaxf(row_lane(v, 0), row_lane(v, 1)), fmaxf(row_lane(v, 2), row_lane(v, 3)));
 }
 __device__ __forceinline__ float wave_sum_f(float v) {
   v += dpp_f32<kDppXor1>(v);
   v += dpp_f32<kDppXor2>(v);
   v += dpp_f32<kDppRor4>(v);
   v += dpp_f32<kDppRor8>(v);
-  v += __shfl_xor(v, 16, 64);
-  return v + __shfl_xor(v, 32, 64);
+  return (row_lane(v, 0) + row_lane(v, 1)) + (row_lane(v, 2) + row_lane(v, 3));
 }
 
 // One token's top-k on one wave: writes k (weight, id) pairs at tok * k + slot and returns,
@@ -170,13 +174,14 @@ __global__ __launch_bounds__(256) void moe_topk_wave_kernel(
 
 // Top-k with the permute plan's histogram: block c (16 waves) routes tokens
 // [c * tpb, (c + 1) * tpb), which are exactly plan chunk c (csz = tpb * k routes), and writes
-// chunk_off[e][c] = routes of expert e in the chunk; routes of padded tokens (id -1) get
-// route_pos = -1. moe_align_place then builds the plan from the table.
+// chunk_cnt[e][c] = routes of expert e in the chunk, one byte each (a token routes to an expert
+// at most once, so a count is at most tpb <= 240); routes of padded tokens (id -1) get
+// route_pos = -1. moe_align_place<uint8_t> then builds the plan from the table.
 template <int DT, int EPL>
 __global__ __launch_bounds__(1024) void moe_topk_hist_kernel(
     float* __restrict__ w_out, int32_t* __restrict__ id_out, const void* __restrict__ logits_,
     int64_t T, int E, int k, int renorm, int mode, int64_t n_non_padded, int tpb,
-    int32_t* __restrict__ chunk_off, int32_t* __restrict__ route_pos) {
+    uint8_t* __restrict__ chunk_cnt, int32_t* __restrict__ route_pos) {
   extern __shared__ int32_t hist[];  // [E + 1]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = blockIdx.x;
@@ -199,7 +204,8 @@ __global__ __launch_bounds__(1024) void moe_topk_hist_kernel(
     }
   }
   __syncthreads();
-  for (int e = tid; e <= E; e += 1024) chunk_off[int64_t(e) * ALIGN_MAX_CHUNKS + c] = hist[e];
+  for (int e = tid; e <= E; e += 1024)
+    chunk_cnt[int64_t(e) * ALIGN_MAX_CHUNKS + c] = uint8_t(hist[e]);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -388,10 +394,17 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int x) {
 
 constexpr int PLACE_THREADS = 1024, PLACE_WAVES = PLACE_THREADS / 64;
 
+// Bytes b..b+3 of a word that belong to chunks below lim (chunk of byte b: cb).
+__device__ __forceinline__ uint32_t bytes_below(uint32_t word, int cb, int lim) {
+  const int n = min(max(lim - cb, 0), 4);
+  return n >= 4 ? word : word & ((1u << (8 * n)) - 1u);
+}
+
+template <typename CT>
 __global__ __launch_bounds__(PLACE_THREADS) void moe_align_place(
     int32_t* __restrict__ sorted, int32_t* __restrict__ expert_ids,
     int32_t* __restrict__ npp_out, int32_t* __restrict__ route_pos,
-    const int32_t* __restrict__ chunk_off, const int32_t* __restrict__ ids, int64_t numel,
+    const CT* __restrict__ chunk_off, const int32_t* __restrict__ ids, int64_t numel,
     int64_t csz, int nch, int E_eff, int bs, int64_t max_padded) {
   // start[E_eff] | total[E_eff] | running[E_eff] | count[E_eff] | wcnt[PLACE_WAVES][E_eff]
   extern __shared__ int32_t pl[];
@@ -409,54 +422,101 @@ __global__ __launch_bounds__(PLACE_THREADS) void moe_align_place(
   int e_first = -1;
   if (lo + tid < hi) e_first = ids[lo + tid];
 
-  // 1. per expert: routes in the chunks before c, and in all chunks. A wave reads an expert's
-  //    row of chunk counts with one instruction (lane: chunks 2l, 2l + 1), EB rows in flight
-  //    at once, and folds each row with one wave sum (both counts packed in one word when the
-  //    plan has fewer than 2^16 routes).
-  constexpr int EB = 12, CPL = ALIGN_MAX_CHUNKS / 64;   // chunks per lane
-  static_assert(CPL == 4, "one int4 of chunk counts per lane");
-  const bool packed = numel < 65536;
-  const int cb = CPL * lane;
-  for (int eb = wave * EB; eb < E_eff; eb += PLACE_WAVES * EB) {
-    int4 v[EB];
+  // 1. per expert: routes in the chunks before c, and in all chunks.
+  if constexpr (sizeof(CT) == 1) {
+    // One byte per chunk: a row of 256 counts is 16 lanes' 16 bytes, so one load instruction
+    // reads four experts' rows (lanes 16 g .. 16 g + 15: expert row g of the four, chunks
+    // 16 j .. 16 j + 15 in lane j). Byte sums by v_sad_u8, both counts packed in one word
+    // (an expert's total is at most the token count, < 2^16) and summed inside each row of
+    // 16 lanes by DPP.
+    constexpr int EB8 = 3;   // groups of four rows in flight per wave
+    const int g = lane >> 4, j = lane & 15;
+    for (int eb = wave * 4 * EB8; eb < E_eff; eb += PLACE_WAVES * 4 * EB8) {
+      uint4 v[EB8];
 #pragma unroll
-    for (int j = 0; j < EB; ++j) {
-      const int e = eb + j;
-      v[j] = make_int4(0, 0, 0, 0);
-      if (e < E_eff && cb < nch)
-        v[j] = *reinterpret_cast<const int4*>(chunk_off + int64_t(e) * ALIGN_MAX_CHUNKS + cb);
+      for (int q = 0; q < EB8; ++q) {
+        const int e = eb + 4 * q + g;
+        v[q] = make_uint4(0, 0, 0, 0);
+        if (e < E_eff)
+          v[q] = *reinterpret_cast<const uint4*>(chunk_off + int64_t(e) * ALIGN_MAX_CHUNKS + 16 * j);
+      }
+      if (eb == wave * 4 * EB8) first_ids[tid] = e_first;
+#pragma unroll
+      for (int q = 0; q < EB8; ++q) {
+        const uint32_t w4[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+        uint32_t sum_l = 0, pre_l = 0;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const int cb = 16 * j + 4 * h;   // chunk of the word's first byte
+          const uint32_t valid = bytes_below(w4[h], cb, nch);   // chunks past nch: unwritten
+          sum_l = __builtin_amdgcn_sad_u8(valid, 0u, sum_l);
+          pre_l = __builtin_amdgcn_sad_u8(bytes_below(valid, cb, c), 0u, pre_l);
+        }
+        int both = int((sum_l << 16) | pre_l);
+        both += dpp_i32<kDppXor1>(both);
+        both += dpp_i32<kDppXor2>(both);
+        both += dpp_i32<kDppRor4>(both);
+        both += dpp_i32<kDppRor8>(both);
+        const int e = eb + 4 * q + g;
+        if (j == 0 && e < E_eff) {
+          const int all = int(uint32_t(both) >> 16), pre = both & 0xffff;
+          start[e] = pre;
+          total[e] = all;
+          count[e] = all;
+          running[e] = 0;
+        }
+      }
     }
-    if (eb == wave * EB) first_ids[tid] = e_first;
+    if (wave * 4 * EB8 >= E_eff) first_ids[tid] = e_first;   // waves without expert rows
+  } else {
+    // A wave reads an expert's row of chunk counts with one instruction (lane: chunks
+    // 4l .. 4l + 3), EB rows in flight at once, and folds each row with one wave sum (both
+    // counts packed in one word when the plan has fewer than 2^16 routes).
+    constexpr int EB = 12, CPL = ALIGN_MAX_CHUNKS / 64;   // chunks per lane
+    static_assert(CPL == 4, "one int4 of chunk counts per lane");
+    const bool packed = numel < 65536;
+    const int cb = CPL * lane;
+    for (int eb = wave * EB; eb < E_eff; eb += PLACE_WAVES * EB) {
+      int4 v[EB];
 #pragma unroll
-    for (int j = 0; j < EB; ++j) {
-      const int x[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-      int sum_l = 0, pre_s = 0;
+      for (int j = 0; j < EB; ++j) {
+        const int e = eb + j;
+        v[j] = make_int4(0, 0, 0, 0);
+        if (e < E_eff && cb < nch)
+          v[j] = *reinterpret_cast<const int4*>(chunk_off + int64_t(e) * ALIGN_MAX_CHUNKS + cb);
+      }
+      if (eb == wave * EB) first_ids[tid] = e_first;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int xv = cb + q < nch ? x[q] : 0;   // chunks past nch were never written
-        sum_l += xv;
-        pre_s += cb + q < c ? xv : 0;
-      }
-      const uint32_t pre_l = uint32_t(pre_s);
-      int all, pre;
-      if (packed) {   // both sums < 2^16: no carry between the halves
-        const uint32_t both = wave_sum_u((uint32_t(sum_l) << 16) | pre_l);
-        all = int(both >> 16);
-        pre = int(both & 0xffffu);
-      } else {
-        all = int(wave_sum_u(uint32_t(sum_l)));
-        pre = int(wave_sum_u(pre_l));
-      }
-      const int e = eb + j;
-      if (lane == 0 && e < E_eff) {
-        start[e] = pre;
-        total[e] = all;
-        count[e] = all;
-        running[e] = 0;
+      for (int j = 0; j < EB; ++j) {
+        const int x[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        int sum_l = 0, pre_s = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int xv = cb + q < nch ? x[q] : 0;   // chunks past nch were never written
+          sum_l += xv;
+          pre_s += cb + q < c ? xv : 0;
+        }
+        const uint32_t pre_l = uint32_t(pre_s);
+        int all, pre;
+        if (packed) {   // both sums < 2^16: no carry between the halves
+          const uint32_t both = wave_sum_u((uint32_t(sum_l) << 16) | pre_l);
+          all = int(both >> 16);
+          pre = int(both & 0xffffu);
+        } else {
+          all = int(wave_sum_u(uint32_t(sum_l)));
+          pre = int(wave_sum_u(pre_l));
+        }
+        const int e = eb + j;
+        if (lane == 0 && e < E_eff) {
+          start[e] = pre;
+          total[e] = all;
+          count[e] = all;
+          running[e] = 0;
+        }
       }
     }
+    if (wave * EB >= E_eff) first_ids[tid] = e_first;   // waves without expert rows
   }
-  if (wave * EB >= E_eff) first_ids[tid] = e_first;   // waves without expert rows
   for (int i = tid; i < PLACE_WAVES * E_eff; i += PLACE_THREADS) wcnt[i] = 0;
   __syncthreads();
   // 2. exclusive scan of the padded totals, by wave 0 (consecutive experts per lane)
@@ -883,7 +943,7 @@ extern "C" int pia_moe_align_block_size(int32_t* sorted_token_ids, int32_t* expe
     if (int rc = check_launch("moe_align_hist")) return rc;
   }
   if (nch > 0 && E_eff <= ALIGN_PLACE_MAX_E) {
-    hipLaunchKernelGGL(moe_align_place, dim3(unsigned(nch)), dim3(PLACE_THREADS),
+    hipLaunchKernelGGL(moe_align_place<int32_t>, dim3(unsigned(nch)), dim3(PLACE_THREADS),
                        size_t(4 + PLACE_WAVES) * E_eff * sizeof(int32_t), s, sorted_token_ids, expert_ids,
                        num_tokens_post_pad, route_pos, chunk_off, topk_ids, numel, csz, nch,
                        E_eff, block_size, max_num_tokens_padded);
@@ -915,7 +975,7 @@ extern "C" int pia_moe_topk_align(float* topk_weights, int32_t* topk_ids, const 
   tpb = ceil_div(tpb, 16) * 16;
   const bool fused = num_tokens > 0 && topk > 0 && topk <= 64 && num_experts > 0 &&
                      num_experts <= 1024 && numel > ALIGN_SMALL_MAX && E_eff <= ALIGN_PLACE_MAX_E &&
-                     tpb * topk < 0x7fffffff;
+                     tpb <= 240;  // per-chunk counts fit one byte
   if (!fused) {
     if (int rc = pia_moe_topk(topk_weights, topk_ids, logits, logits_dtype, num_tokens,
                               num_experts, topk, renormalize, mode, num_token_non_padded, stream))
@@ -940,13 +1000,13 @@ extern "C" int pia_moe_topk_align(float* topk_weights, int32_t* topk_ids, const 
     return fail(PIA_EINVAL, "moe_topk_align: max_num_tokens_padded below the padded worst case");
   hipStream_t s = as_stream(stream);
   const int nch = int(ceil_div(num_tokens, tpb));
-  int32_t* chunk_off = reinterpret_cast<int32_t*>(workspace);
+  uint8_t* chunk_cnt = reinterpret_cast<uint8_t*>(workspace);
   const int epl = int(ceil_div(num_experts, 64));
   const size_t lds = size_t(E_eff) * sizeof(int32_t);
 #define PIA_TH(DT, EPL)                                                                           \
   hipLaunchKernelGGL((moe_topk_hist_kernel<DT, EPL>), dim3(unsigned(nch)), dim3(1024), lds, s,    \
                      topk_weights, topk_ids, logits, num_tokens, num_experts, topk, renormalize,  \
-                     mode, num_token_non_padded, int(tpb), chunk_off, route_pos)
+                     mode, num_token_non_padded, int(tpb), chunk_cnt, route_pos)
 #define PIA_TH_DT(DT)                      \
   if (epl <= 1) PIA_TH(DT, 1);             \
   else if (epl <= 2) PIA_TH(DT, 2);        \
@@ -962,9 +1022,9 @@ extern "C" int pia_moe_topk_align(float* topk_weights, int32_t* topk_ids, const 
 #undef PIA_TH_DT
 #undef PIA_TH
   if (int rc = check_launch("moe_topk_hist")) return rc;
-  hipLaunchKernelGGL(moe_align_place, dim3(unsigned(nch)), dim3(PLACE_THREADS),
+  hipLaunchKernelGGL(moe_align_place<uint8_t>, dim3(unsigned(nch)), dim3(PLACE_THREADS),
                      size_t(4 + PLACE_WAVES) * E_eff * sizeof(int32_t), s, sorted_token_ids,
-                     expert_ids, num_tokens_post_pad, route_pos, chunk_off, topk_ids, numel,
+                     expert_ids, num_tokens_post_pad, route_pos, chunk_cnt, topk_ids, numel,
                      tpb * topk, nch, E_eff, block_size, max_num_tokens_padded);
   return check_launch("moe_align_place");
 }
