@@ -177,6 +177,34 @@ def test_moe_forward_sparse_bf16_vs_reference_composition(dev):
     assert err <= 4 * 2 ** -8 * ref.float().abs().max().item(), err
 
 
+def _check_plan(ids, s, e, npp, pos, bs, E):
+    rs, re_, rnpp, rpos = OM.moe_align_block_size(ids.cpu().numpy(), bs, E)
+    assert int(npp.item()) == rnpp
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(e.cpu().numpy()[:rnpp // bs], re_[:rnpp // bs])
+    assert (e.cpu().numpy()[rnpp // bs:] == -1).all()
+    assert np.array_equal(pos.cpu().numpy(), rpos)
+
+
+@pytest.mark.parametrize("T", [61440, 61441])
+def test_topk_align_byte_count_boundary(dev, T):
+    """61,440 tokens is the largest call of the fused plan (240-token chunks, so a chunk's count
+    of one expert fits the byte the plan stores it in); one token more takes the three-launch
+    path. Every token routes to experts 0..7 (a large bias on their logits), so each chunk
+    counts 240 routes of each: the byte table at its maximum. Ids against the stable argsort,
+    the plan bit-exact against the oracle."""
+    from plastic_infer.kernel import moe_topk_align
+
+    k, E, bs = 8, 128, 64
+    g = torch.Generator().manual_seed(T)
+    logits = torch.randn(T, E, generator=g)
+    logits[:, :k] += 100.0
+    w, ids, s, e, npp, pos = moe_topk_align(logits.to(dev), k, bs)
+    ref_ids = np.argsort(-logits.numpy(), 1, kind="stable")[:, :k]
+    assert np.array_equal(ids.cpu().numpy(), ref_ids)
+    _check_plan(ids, s, e, npp, pos, bs, E)
+
+
 @pytest.mark.parametrize("T,k,E,bs,dtype,n_np", [
     (4096, 8, 128, 64, torch.float32, None),   # Qwen3-30B-A3B routing (two-launch path)
     (600, 8, 64, 16, torch.float32, None),     # just past the one-block plan
