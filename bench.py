@@ -449,7 +449,7 @@ def bench_decode_gqa8(torch, dev, args) -> dict:
         {"tokens_per_s": round(b / (ms / 1e3), 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
          "bytes_per_step": attn_bytes + sc_bytes, "scatter_ms": round(sc_ms, 4),
          "attention_ms": round(at_ms, 4), "wall_s_timed": round(wall, 4)},
-        {"kernel": "paged_decode_stream<8> + paged_decode_stream_reduce (one attention call)",
+        {"kernel": "paged_decode_stream<8> (one attention call, merges in the same launch)",
          "bound": "hbm", "achieved": round(a_gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
          "frac": round(a_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
          "algorithmic_bytes_per_launch": attn_bytes, "avg_launch_ms": round(at_ms, 4)})
@@ -1564,9 +1564,9 @@ def main() -> int:
         "step": "kv_scatter + paged_decode_attention" if separate
                 else "paged_decode_append_attention (write + attention, one call)",
         "roofline": {
-            "kernel": ("paged_decode_stream<4> + paged_decode_stream_reduce (one attention call)"
-                       if separate else "paged_decode_stream<4, append> + "
-                       "paged_decode_stream_reduce (one write + attention call)"),
+            "kernel": ("paged_decode_stream<4> (one attention call)"
+                       if separate else "paged_decode_stream<4, append> "
+                       "(one write + attention launch)"),
             "bound": "hbm", "achieved": round(attn_gbps, 2), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
             "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_ms": round(attn_ms, 4),

@@ -12,8 +12,8 @@
 //      Softmax: fp32, base-2 with the scale folded in; wave max by DPP/shuffles.
 //      PV: lane l reads V rows d = 32j + l/2, token half l&1 (1 KiB contiguous per load); the
 //        probabilities of its 8 tokens come from LDS as bf16 pairs, v_dot2 accumulates in fp32.
-//    Segments cut by a wave-range boundary leave (max, sum, unnormalised acc) partials that
-//    paged_decode_stream_reduce merges.
+//    Segments cut by a wave-range boundary leave (max, sum, unnormalised acc) partials; the
+//    wave that writes a segment's last partial merges them in the same launch.
 //    Block-table ids outside [0, num_pages) inside a context are not dereferenced: their tokens
 //    are not keys (score -inf, V zeroed); a row with no key at all is written as zeros.
 // 2. paged_attention_generic<DT, DPL>: any dtype / head_dim <= 512 / page size, several query
@@ -22,6 +22,7 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <random>
 #include <type_traits>
 
 #include "pia_internal.h"
@@ -168,7 +169,8 @@ __device__ __forceinline__ int clamp_len(int L, int64_t bt_stride, int P) {
 // A segment that lies inside one wave's range is finished there (output written directly); a
 // segment cut by a range boundary leaves (max, sum, unnormalised acc) partials, at most two per
 // wave: slot 0 for the segment that began before the wave's range, slot 1 for the one that
-// began inside it and continues after. paged_decode_stream_reduce merges them.
+// began inside it and continues after. The wave that writes a segment's last partial merges
+// them (see sd_arrive), in the same launch: no second kernel, no launch gap.
 //
 // Range of wave w (steps): pair p = w / 2 covers [p*Dp, (p+1)*Dp); the even wave [p*Dp, p*Dp+Ce),
 // the odd wave [p*Dp+Ce, (p+1)*Dp); both clipped to T. stream_range_of() is the inverse.
@@ -177,10 +179,9 @@ constexpr int SD_MAX_SEQS = 1024;   // sequences per launch (step-prefix table i
 constexpr int SD_MAX_WAVES = 4096;  // partial slots are sized for this many waves
 constexpr int SD_WAVES_PER_CU = 8;  // two single-wave workgroups per SIMD
 constexpr int SD_STEP_TOKENS = FD_PAGES_PER_WAVE * FD_P;  // 128 tokens per step
-// meta ints: step prefix [B + 1], then Dp, Ce, T, then one cut record per wave (the segment
-// its range starts inside, as b * Hkv + h, or -1 when the range starts a segment)
-constexpr int SD_META_CUT = SD_MAX_SEQS + 4;
-constexpr int SD_META_INTS = SD_META_CUT + SD_MAX_WAVES;
+// meta: one 64-bit arrival counter per wave w (for the cut segment whose first step lies in
+// w's range), from the first 8-byte boundary of the meta ints
+constexpr int SD_META_INTS = 2 * SD_MAX_WAVES + 2;
 constexpr int SD_EVEN_SHARE_PERMILLE = 515;                // even-XCD wave's share of a pair
 
 // Steps of a wave pair and the even wave's share of them, for T steps over NW waves.
@@ -233,6 +234,34 @@ using PoolIn = std::conditional_t<APPEND, const uint16_t*, const uint16_t* __res
 // The wave keeps up to SD_APP_REC pending slots in LDS and stores any further ones at once.
 // The stores are non-temporal (streamed through the cache): the next step reads these lines
 // from another XCD, and that read was measured 0.4 % faster than after ordinary stores.
+// A wave's arrival on the counter of a cut segment with n partials: the counter holds
+// (token << 16 | count) where token identifies the launch (the upper 48 bits, from the host, a
+// fresh value per launch); a count under another token is stale (an earlier launch, or a
+// workspace never used before) and reads as 0. Returns true for the n-th arrival, which also
+// leaves the count at 0 under this token, so a replay of the same launch (a graph) starts from
+// zero again. Workspace contents collide with a token with probability 2^-48.
+// Device-coherent partial stores and loads (sc1: through the XCD's L2 to memory).
+__device__ __forceinline__ void sd_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float sd_load(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool sd_arrive(uint64_t* ctr, uint64_t token, int n) {
+  uint64_t old = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {  // retried only when another wave updated the counter in between
+    const uint64_t cnt = (old >> 16) == (token >> 16) ? (old & 0xffffu) : 0u;
+    const bool last = int(cnt) + 1 >= n;
+    const uint64_t nv = token | (last ? 0u : cnt + 1);
+    uint64_t expect = old;
+    if (__hip_atomic_compare_exchange_strong(ctr, &expect, nv, __ATOMIC_RELAXED,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      return last;
+    old = expect;
+  }
+}
+
 template <int G, bool APPEND>
 __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
@@ -241,7 +270,7 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     const int32_t* __restrict__ context_lens, int B, int Hkv, int64_t num_pages,
     float* __restrict__ ws_part, int32_t* __restrict__ ws_meta, float scale_log2,
     uint16_t* kpool_w, uint16_t* vpool_w, const uint16_t* __restrict__ k_new,
-    const uint16_t* __restrict__ v_new, int64_t new_seq_stride) {
+    const uint16_t* __restrict__ v_new, int64_t new_seq_stride, uint64_t token) {
   constexpr int D = FD_D, P = FD_P, TILE = D * P, STEP = FD_PAGES_PER_WAVE;
   constexpr int NCH = SD_MAX_SEQS / 64;
   const int lane = threadIdx.x, w = blockIdx.x, NW = gridDim.x;
@@ -255,8 +284,7 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
   __shared__ int64_t app_rec[APPEND ? SD_APP_REC : 1][2];
   int n_rec = 0;
 
-  // Step prefix over the batch: every wave builds its own copy in LDS, wave 0 also publishes
-  // it (and the pair split) for the merge kernel.
+  // Step prefix over the batch: every wave builds its own copy in LDS.
   int lv[NCH], lflag[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -274,21 +302,12 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     if (i < B) {
       seq_q[i + 1] = carry + incl;
       seq_len[i] = lv[c] | lflag[c];
-      if (w == 0) ws_meta[i + 1] = carry + incl;
     }
     carry = uniform(carry + __shfl(incl, 63, 64));
   }
   const int T = Hkv * carry;
   const int Dp = stream_pair_steps(T, NW), Ce = stream_even_share(Dp);
-  if (lane == 0) {
-    seq_q[0] = 0;
-    if (w == 0) {
-      ws_meta[0] = 0;
-      ws_meta[B + 1] = Dp;
-      ws_meta[B + 2] = Ce;
-      ws_meta[B + 3] = T;
-    }
-  }
+  if (lane == 0) seq_q[0] = 0;
   __syncthreads();
   // empty sequences (no steps) get zero rows here: wave w takes sequences w, w + NW, ...
   for (int b = w; b < B; b += NW) {
@@ -393,7 +412,9 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
 
   int gs = start;
   StreamCursor cur = seg_of(gs);
-  if (lane == 0) ws_meta[SD_META_CUT + w] = cur.ls != 0 ? cur.b * Hkv + cur.h : -1;
+  // partials this wave writes (slot 0, slot 1): the first global step, step count and row of
+  // their segments, for the arrivals after the range (arr_first -1: no partial in that slot)
+  int arr_first[2] = {-1, -1}, arr_ns[2] = {0, 0}, arr_row[2] = {0, 0};
   int bt_cur;
   // Two 16 KiB register buffers whose role rotates through a step:
   //   A: K rows 0..63 -> V pages 0..3 -> next step's K rows 0..63
@@ -499,7 +520,7 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     const bool has_next = gs + 1 < end;
     // The next step's block-table row and (when it opens a segment) q go out first, ahead of
     // this step's V loads, so they have landed by the time they are consumed. At the end of
-    // the range the "next" step repeats the current one (its K prefetch is never used).
+    // the range the "next" step repeats the current one (its K is not prefetched).
     const StreamCursor nxt = has_next ? next_of(cur) : cur;
     const bool nxt_opens = has_next && nxt.ls == 0;
     const int bt_nxt = load_bt(nxt);
@@ -623,9 +644,13 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
       pv_pages(bufA, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
+    // the next step's K (none after the range's last step: the wave's end waits for its
+    // outstanding loads before it counts its partials in)
     const uint16_t* kp = kbase + int64_t(nxt.h) * TILE + page_ok(bt_nxt) * page_stride;
+    if (has_next) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) bufA[i] = load16_nt(kp + 64 * i);
+      for (int i = 0; i < 16; ++i) bufA[i] = load16_nt(kp + 64 * i);
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (masked_step) {
       mask_tail(bufB, 4, v_valid, bad);
@@ -634,8 +659,10 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
       pv_pages(bufB, 4);
     }
     __builtin_amdgcn_sched_barrier(0);
+    if (has_next) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) bufB[i] = load16_nt(kp + 64 * (16 + i));
+      for (int i = 0; i < 16; ++i) bufB[i] = load16_nt(kp + 64 * (16 + i));
+    }
     // the next step overwrites p_lds (and maybe q_lds): keep this step's reads ahead of them
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -660,18 +687,26 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
                   f32_to_bf16(lsum[g] > 0.f ? acc[j][g] / lsum[g] : 0.f);
         }
       } else {
-        float* part = ws_part + (int64_t(w) * 2 + (seg_first < start ? 0 : 1)) * G * (D + 2);
+        const int slot = seg_first < start ? 0 : 1;
+        arr_first[slot] = seg_first;
+        arr_ns[slot] = cur.ns;
+        arr_row[slot] = cur.b * Hkv + cur.h;
+        // partials go out as device-coherent stores (through this XCD's L2 to memory): the
+        // merging wave may run on another XCD and reads them with device-coherent loads, so
+        // neither side needs a cache-wide write-back or invalidate
+        float* part = ws_part + (int64_t(w) * 2 + slot) * G * (D + 2);
         if ((lane & 1) == 0) {
 #pragma unroll
           for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) part[g * (D + 2) + 32 * j + (lane >> 1)] = acc[j][g];
+            for (int j = 0; j < 4; ++j)
+              sd_store(part + g * (D + 2) + 32 * j + (lane >> 1), acc[j][g]);
         }
         if (lane == 0) {
 #pragma unroll
           for (int g = 0; g < G; ++g) {
-            part[g * (D + 2) + D] = m[g];
-            part[g * (D + 2) + D + 1] = lsum[g];
+            sd_store(part + g * (D + 2) + D, m[g]);
+            sd_store(part + g * (D + 2) + D + 1, lsum[g]);
           }
         }
       }
@@ -706,72 +741,78 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
       }
     }
   }
-}
 
-// Merge the partials of the segments that cross a wave-range boundary. One 128-thread block per
-// wave w: its range starts inside segment (b, h) when its cut record says so, and the block
-// merges that segment's G rows (thread d: element d of every row) when w is the first wave
-// after the one holding the segment's first step (every other boundary inside the segment
-// returns at once). One online pass over the pieces, all G rows of a piece loaded together.
-template <int G>
-__global__ __launch_bounds__(FD_D) void paged_decode_stream_reduce(
-    uint16_t* __restrict__ out, const float* __restrict__ ws_part,
-    const int32_t* __restrict__ ws_meta, int B, int Hkv) {
-  constexpr int D = FD_D;
-  const int w = blockIdx.x, d = threadIdx.x;
-  const int Dp = ws_meta[B + 1], Ce = ws_meta[B + 2], T = ws_meta[B + 3];
-  const int start = (w >> 1) * Dp + ((w & 1) ? Ce : 0);
-  const int end = min((w >> 1) * Dp + ((w & 1) ? Dp : Ce), T);
-  if (start >= end) return;  // no steps: no cut record
-  const int cut = ws_meta[SD_META_CUT + w];
-  if (cut < 0) return;
-  const int b = cut / Hkv, h = cut - b * Hkv;
-  const int q0 = ws_meta[b], ns = ws_meta[b + 1] - q0;
-  const int s0 = Hkv * q0 + h * ns;
-  // odd waves hold no steps when a pair has one step (Dp = 1): skip them
-  const int inc = Ce < Dp ? 1 : 2;
-  const int c0 = stream_range_of(s0, Dp, Ce), c1 = stream_range_of(s0 + ns - 1, Dp, Ce);
-  if (w != c0 + inc) return;
-  float M[G], o[G], lt[G];
+  // Arrivals: this wave's partials are written; count them in on their segments' counters and
+  // merge every segment whose last partial this is. All at the end of the range, so no fence
+  // drains a step's prefetch.
+  if (arr_first[0] < 0 && arr_first[1] < 0) return;
+  uint64_t* ctr = reinterpret_cast<uint64_t*>(
+      (reinterpret_cast<uintptr_t>(ws_meta) + 7) & ~uintptr_t(7));
+  const int inc = Ce < Dp ? 1 : 2;  // odd waves hold no steps when pairs have one step
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed before its count
+  bool merge[2] = {false, false};
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    M[g] = kNegBig;
-    o[g] = 0.f;
-    lt[g] = 0.f;
+  for (int k = 0; k < 2; ++k) {
+    if (arr_first[k] < 0) continue;
+    const int c0 = stream_range_of(arr_first[k], Dp, Ce);
+    const int c1 = stream_range_of(arr_first[k] + arr_ns[k] - 1, Dp, Ce);
+    int last = 0;
+    if (lane == 0) last = sd_arrive(ctr + c0, token, (c1 - c0) / inc + 1) ? 1 : 0;
+    merge[k] = __builtin_amdgcn_readfirstlane(last) != 0;
   }
-  // one piece ahead: the next piece's loads are in flight while the current one is folded in
-  float mc[G], lc[G], ac[G];
-  auto load_piece = [&](int c) {
-    const float* pp = ws_part + (int64_t(c) * 2 + (c == c0 ? 1 : 0)) * G * (D + 2);
+  if (!merge[0] && !merge[1]) return;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if (!merge[k]) continue;
+    // one online pass over the pieces in wave order (slot 1 of the first wave, slot 0 of the
+    // rest); lane l: elements l and l + 64 of every row
+    const int c0 = stream_range_of(arr_first[k], Dp, Ce);
+    const int c1 = stream_range_of(arr_first[k] + arr_ns[k] - 1, Dp, Ce);
+    float M[G], o0[G], o1[G], lt[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      mc[g] = pp[g * (D + 2) + D];
-      lc[g] = pp[g * (D + 2) + D + 1];
-      ac[g] = pp[g * (D + 2) + d];
+      M[g] = kNegBig;
+      o0[g] = o1[g] = lt[g] = 0.f;
     }
-  };
-  load_piece(c0);
-  for (int c = c0; c <= c1; c += inc) {
-    float mcur[G], lcur[G], acur[G];
+    // pieces four at a time: all their loads in flight together, then folded in order
+    constexpr int PB = 4;
+    for (int cb = c0; cb <= c1; cb += PB * inc) {
+      float mc[PB][G], lc[PB][G], a0[PB][G], a1[PB][G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      mcur[g] = mc[g];
-      lcur[g] = lc[g];
-      acur[g] = ac[g];
+      for (int u = 0; u < PB; ++u) {
+        const int c = cb + u * inc;
+        if (c > c1) continue;
+        const float* pp = ws_part + (int64_t(c) * 2 + (c == c0 ? 1 : 0)) * G * (D + 2);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          mc[u][g] = sd_load(pp + g * (D + 2) + D);
+          lc[u][g] = sd_load(pp + g * (D + 2) + D + 1);
+          a0[u][g] = sd_load(pp + g * (D + 2) + lane);
+          a1[u][g] = sd_load(pp + g * (D + 2) + 64 + lane);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < PB; ++u) {
+        if (cb + u * inc > c1) continue;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float mn = fmaxf(M[g], mc[u][g]);
+          const float fo = fast_exp2(M[g] - mn), fc = fast_exp2(mc[u][g] - mn);
+          lt[g] = lt[g] * fo + lc[u][g] * fc;
+          o0[g] = o0[g] * fo + a0[u][g] * fc;
+          o1[g] = o1[g] * fo + a1[u][g] * fc;
+          M[g] = mn;
+        }
+      }
     }
-    if (c + inc <= c1) load_piece(c + inc);
+    const int b = arr_row[k] / Hkv, h = arr_row[k] - b * Hkv;
+    uint16_t* orow = out + (int64_t(b) * Hq + int64_t(h) * G) * D;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float mn = fmaxf(M[g], mcur[g]);
-      const float fo = fast_exp2(M[g] - mn), fc = fast_exp2(mcur[g] - mn);
-      lt[g] = lt[g] * fo + lcur[g] * fc;
-      o[g] = o[g] * fo + acur[g] * fc;
-      M[g] = mn;
+      orow[g * D + lane] = f32_to_bf16(lt[g] > 0.f ? o0[g] / lt[g] : 0.f);
+      orow[g * D + 64 + lane] = f32_to_bf16(lt[g] > 0.f ? o1[g] / lt[g] : 0.f);
     }
   }
-  uint16_t* orow = out + (int64_t(b) * Hkv + h) * G * D + d;
-#pragma unroll
-  for (int g = 0; g < G; ++g) orow[g * D] = f32_to_bf16(lt[g] > 0.f ? o[g] / lt[g] : 0.f);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1010,11 +1051,21 @@ int check_decode_args(const void* out, const void* q, int64_t q_seq_stride, cons
   return 0;
 }
 
-// The fast path (checked arguments): stream kernel + merge, in launches of up to SD_MAX_SEQS
+// The fast path (checked arguments): the stream kernel, in launches of up to SD_MAX_SEQS
 // sequences that reuse the same partial slots (ws_part: >= NW * 2 * G * (D + 2) floats) and
-// meta ints (ws_meta: SD_META_INTS). Launches on one stream are ordered, so the reuse is safe.
+// arrival counters (ws_meta: SD_META_INTS ints). Launches on one stream are ordered, so the
+// reuse is safe; each launch takes a fresh token for its counters.
 // k_new != nullptr: append mode (the new tokens of the step in k_new / v_new, written into the
 // pools by the kernel; k_pages / v_pages are then written too).
+// Launch tokens for the arrival counters: the upper 48 bits of a 64-bit word, a process-wide
+// sequence from a random start (a workspace never used before matches one with probability
+// 2^-48 per counter).
+uint64_t next_stream_token() {
+  static std::atomic<uint64_t> seq{(uint64_t(std::random_device{}()) << 32) ^
+                                   uint64_t(std::random_device{}())};
+  return (seq.fetch_add(1, std::memory_order_relaxed) & 0xffffffffffffull) << 16;
+}
+
 int launch_stream_decode(void* out, const void* q, int64_t q_seq_stride, const void* k_pages,
                          const void* v_pages, const int32_t* block_tables, int64_t bt_stride,
                          const int32_t* context_lens, int num_seqs, int num_heads,
@@ -1036,11 +1087,12 @@ int launch_stream_decode(void* out, const void* q, int64_t q_seq_stride, const v
     const uint16_t* vn =
         k_new ? reinterpret_cast<const uint16_t*>(v_new) + int64_t(b0) * new_seq_stride : nullptr;
     const size_t lds = size_t(2 * Bs + 1) * sizeof(int32_t);
+    const uint64_t token = next_stream_token();
 #define PIA_SD(GG, AP)                                                                         \
   hipLaunchKernelGGL((paged_decode_stream<GG, AP>), dim3(unsigned(NW)), dim3(64), lds, s, o,   \
                      qq, q_seq_stride, (const uint16_t*)k_pages, (const uint16_t*)v_pages, bt, \
                      bt_stride, cl, Bs, num_kv_heads, num_pages, ws_part, ws_meta, scale_log2, \
-                     kw, vw, kn, vn, new_seq_stride)
+                     kw, vw, kn, vn, new_seq_stride, token)
     if (kn) {
       switch (G) {
         case 1: PIA_SD(1, true); break;
@@ -1058,27 +1110,17 @@ int launch_stream_decode(void* out, const void* q, int64_t q_seq_stride, const v
     }
 #undef PIA_SD
     if (int rc = check_launch("paged_decode_stream")) return rc;
-#define PIA_SR(GG)                                                                             \
-  hipLaunchKernelGGL((paged_decode_stream_reduce<GG>), dim3(unsigned(NW)), dim3(FD_D), 0, s, o, \
-                     ws_part, ws_meta, Bs, num_kv_heads)
-    switch (G) {
-      case 1: PIA_SR(1); break;
-      case 2: PIA_SR(2); break;
-      case 4: PIA_SR(4); break;
-      default: PIA_SR(8); break;
-    }
-#undef PIA_SR
-    if (int rc = check_launch("paged_decode_stream_reduce")) return rc;
   }
   return 0;
 }
 
 // ---------------------------------------------------------------------------------------------
-// Library-owned scratch for pia_paged_decode_attention_noalloc: the meta ints, then the wave
-// partials, in one static device array per GPU (held until the process ends). The kernels keep
-// nothing in it across calls that needs initialising (each launch writes what it reads), so it
-// is never cleared. Every call on one GPU shares that GPU's array: calls that overlap (two
-// streams, or two host threads without ordering) race on it.
+// Library-owned scratch for pia_paged_decode_attention_noalloc: the meta ints (arrival
+// counters), then the wave partials, in one static device array per GPU (held until the process
+// ends). It is never cleared: each launch writes the partials it reads, and the counters carry
+// a launch token, so whatever an earlier call left in them reads as stale. Every call on one
+// GPU shares that GPU's array: calls that overlap (two streams, or two host threads without
+// ordering) race on it.
 // ---------------------------------------------------------------------------------------------
 constexpr int64_t kNoAllocScratchBytes = int64_t(16) << 20;                  // 16 MiB per GPU
 constexpr int64_t kNoAllocMetaBytes = (int64_t(SD_META_INTS) * 4 + 255) / 256 * 256;

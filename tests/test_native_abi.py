@@ -52,15 +52,15 @@ def test_invalid_arguments_are_rejected_without_device_work():
     rc = lib.pia_moe_topk(None, None, None, 0, 4, 8, 9, 1, 0, -1, None)
     assert rc == -1
     # G = 4: two partial slots (128 accumulators + max + sum, fp32) per wave for up to 4096
-    # waves, then the step-prefix table (1024 sequences + 1), the split (3 ints) and one cut
-    # record per wave (4096); independent of the batch
+    # waves, then one 64-bit arrival counter per wave (4096, plus two ints to reach an 8-byte
+    # boundary from a 4-byte aligned workspace); independent of the batch
     assert N.query("pia_paged_decode_workspace_bytes", 256, 32, 8, 128, 16, 512) == \
-        4096 * 2 * 4 * 130 * 4 + (1028 + 4096) * 4
+        4096 * 2 * 4 * 130 * 4 + (2 * 4096 + 2) * 4
     assert N.query("pia_paged_decode_workspace_bytes", 1, 32, 8, 128, 16, 4) == \
-        4096 * 2 * 4 * 130 * 4 + (1028 + 4096) * 4
+        4096 * 2 * 4 * 130 * 4 + (2 * 4096 + 2) * 4
     # G = 8: the same layout with eight q rows per partial slot
     assert N.query("pia_paged_decode_workspace_bytes", 256, 64, 8, 128, 16, 512) == \
-        4096 * 2 * 8 * 130 * 4 + (1028 + 4096) * 4
+        4096 * 2 * 8 * 130 * 4 + (2 * 4096 + 2) * 4
     # general kernel (head_dim 64, or G = 3): no workspace
     assert N.query("pia_paged_decode_workspace_bytes", 4, 4, 4, 64, 16, 8) == 0
     assert N.query("pia_paged_decode_workspace_bytes", 4, 24, 8, 128, 16, 8) == 0
