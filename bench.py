@@ -180,22 +180,28 @@ def cpu_baseline(torch, inp, n_seqs, gpu_out):
 
 
 def _phase_timer(torch, dev, step, n_phases, steps, warmup):
-    """Runs step(events) warmup + steps times; step records n_phases + 1 events on the launch
-    stream. Returns (ms per step over the timed region, mean ms of each phase, wall s)."""
+    """Runs step(events) warmup + steps + steps times. The first timed region records no event
+    inside it (event records are queue packets that cost a few microseconds each, as much as a
+    short kernel's gaps); the second records n_phases + 1 events per step on the launch stream
+    for the split. Returns (ms per step over the first region, mean ms of each phase over the
+    second, wall s of the first)."""
     stream = torch.cuda.current_stream(dev)
     for _ in range(warmup):
         step(None)
     torch.cuda.synchronize(dev)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(n_phases + 1)]
-           for _ in range(steps)]
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
     t0.record(stream)
-    for i in range(steps):
-        step(evs[i])
+    for _ in range(steps):
+        step(None)
     t1.record(stream)
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - wall0
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(n_phases + 1)]
+           for _ in range(steps)]
+    for i in range(steps):
+        step(evs[i])
+    torch.cuda.synchronize(dev)
     phases = [statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs) for j in range(n_phases)]
     return t0.elapsed_time(t1) / steps, phases, wall
 
@@ -403,9 +409,12 @@ def _cpu_moe(torch, hidden, logits, step_bytes) -> dict:
 def bench_decode_gqa8(torch, dev, args) -> dict:
     """Qwen3-30B-A3B attention layer at its decode shape: 32 q heads over 4 kv heads (GQA 8),
     head_dim 128, bf16, page 16; 64 sequences of 4096 tokens in a seeded random page
-    permutation of a 20,000-page pool. One step = kv_scatter of the 64 new rows + paged
-    decode attention."""
-    from plastic_infer.kernel import decode_workspace_bytes, kv_scatter, paged_decode_attention
+    permutation of a 20,000-page pool. One step = the decode step's write of the 64 new rows
+    and the paged decode attention, as one paged_decode_append_attention call (the call the
+    paged MoE decoder makes per layer; --separate-write: kv_scatter, then
+    paged_decode_attention)."""
+    from plastic_infer.kernel import (decode_workspace_bytes, kv_scatter,
+                                      paged_decode_append_attention, paged_decode_attention)
 
     b, hq, hkv, L, npool = 64, 32, 4, 4096, 20_000
     g = torch.Generator().manual_seed(6)
@@ -425,34 +434,46 @@ def bench_decode_gqa8(torch, dev, args) -> dict:
     ws = torch.empty(max(1, decode_workspace_bytes(b, hq, hkv, D, P, bt.shape[1])),
                      dtype=torch.uint8, device=dev)
     bt_d, lens_d, slots_d = bt.to(dev), lens.to(torch.int32).to(dev), slots.to(dev)
+    separate = args.separate_write
 
     def step(ev):
         if ev:
             ev[0].record()
-        kv_scatter(kn, vn, kp, vp, slots_d)
+        if separate:
+            kv_scatter(kn, vn, kp, vp, slots_d)
         if ev:
             ev[1].record()
-        paged_decode_attention(q, kp, vp, bt_d, lens_d, out=out, workspace=ws)
+        if separate:
+            paged_decode_attention(q, kp, vp, bt_d, lens_d, out=out, workspace=ws)
+        else:
+            paged_decode_append_attention(q, kp, vp, bt_d, lens_d, kn, vn, out=out, workspace=ws)
         if ev:
             ev[2].record()
 
     ms, (sc_ms, at_ms), wall = _phase_timer(torch, dev, step, 2, args.steps, args.warmup)
+    if not separate:
+        at_ms = ms  # the step is the one launch: its time over the region with no events inside
     kv_row = 2 * hkv * D * 2
     attn_bytes = b * L * kv_row + b * hq * D * 2 * 2 + int(n_pages.sum()) * 4 + b * 4
     sc_bytes = b * kv_row * 2 + b * 8
     gbps = (attn_bytes + sc_bytes) / (ms / 1e3) / 1e9
-    a_gbps = attn_bytes / (at_ms / 1e3) / 1e9
+    launch_bytes = attn_bytes if separate else attn_bytes + sc_bytes
+    a_gbps = launch_bytes / (at_ms / 1e3) / 1e9
+    kernel = ("paged_decode_mfma<8, false> (attention call after a kv_scatter launch)" if separate
+              else "paged_decode_mfma<8, true> (one write + attention launch)")
     return _result(
         "KV scatter + paged decode-attn GB/s (GQA 8)", gbps, "GB/s", args, ms, "bf16",
         {"workload": "qwen3-30b-a3b attention layer decode: 64 seqs x 4096 tokens, 32 q / 4 kv "
                      "heads, head_dim 128, page 16", "batch": b, "context_len": L},
         {"tokens_per_s": round(b / (ms / 1e3), 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-         "bytes_per_step": attn_bytes + sc_bytes, "scatter_ms": round(sc_ms, 4),
+         "bytes_per_step": attn_bytes + sc_bytes,
+         "step": "kv_scatter, then paged_decode_attention" if separate
+                 else "paged_decode_append_attention (write + attention, one call)",
+         "scatter_ms": round(sc_ms, 4) if separate else None,
          "attention_ms": round(at_ms, 4), "wall_s_timed": round(wall, 4)},
-        {"kernel": "paged_decode_stream<8> (one attention call, merges in the same launch)",
-         "bound": "hbm", "achieved": round(a_gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-         "frac": round(a_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-         "algorithmic_bytes_per_launch": attn_bytes, "avg_launch_ms": round(at_ms, 4)})
+        {"kernel": kernel, "bound": "hbm", "achieved": round(a_gbps, 2), "peak": HBM_PEAK_GBPS,
+         "unit": "GB/s", "frac": round(a_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+         "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_ms": round(at_ms, 4)})
 
 
 PA_B, PA_CTX, PA_CHUNK, PA_SEED = 8, 4096, 1024, 9
@@ -1514,19 +1535,24 @@ def main() -> int:
     torch.cuda.synchronize(dev)
     print(f"bench: warmup done, timing {args.steps} steps", file=sys.stderr, flush=True)
 
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps)]
+    # the timed region records no event inside it; a second pass brackets each attention call
     t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize(dev)
     wall0 = time.perf_counter()
     t_start.record(stream)
-    for i in range(args.steps):
-        step(*ev[i])
+    for _ in range(args.steps):
+        step()
     t_end.record(stream)
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - wall0
     ms_step = t_start.elapsed_time(t_end) / args.steps
-    attn_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(*ev[i])
+    torch.cuda.synchronize(dev)
+    # the step is one launch unless the write is separate: then the attention call's events
+    attn_ms = statistics.mean(a.elapsed_time(b) for a, b in ev) if separate else ms_step
 
     attn_bytes, scatter_bytes = algorithmic_bytes(inp["lens"], inp["n_pages"])
     step_bytes = attn_bytes + scatter_bytes

@@ -1,9 +1,8 @@
 // Paged GQA attention over the KV pool layout [num_pages, Hkv, D, P] (token innermost).
 //
-// 1. paged_decode_stream<G> (G = Hq/Hkv in {1,2,4,8}): the decode hot path for bf16, D = 128,
+// 1. paged_decode_stream<G> (G = Hq/Hkv in {1,2,4}): the decode hot path for bf16, D = 128,
 //    P = 16 (described where it is defined): the batch's 128-token steps split over persistent
-//    single waves (a fixed, XCD-aware split), two per SIMD (one for G = 8, whose accumulators
-//    need the registers). Per 8-page (128-token) step:
+//    single waves (a fixed, XCD-aware split), two per SIMD. Per 8-page (128-token) step:
 //      K tile loads: lane l reads page l/8, rows d = 4i + (l&3), token half (l>>2)&1, so load i
 //        of the wave covers one whole 128-byte line of each of the 8 pages (32 loads / 8 pages).
 //      QK^T: pairs of rows (d, d+4) are packed per token with v_perm, then v_dot2_f32_bf16
@@ -16,7 +15,10 @@
 //    wave that writes a segment's last partial merges them in the same launch.
 //    Block-table ids outside [0, num_pages) inside a context are not dereferenced: their tokens
 //    are not keys (score -inf, V zeroed); a row with no key at all is written as zeros.
-// 2. paged_attention_generic<DT, DPL>: any dtype / head_dim <= 512 / page size, several query
+// 2. paged_decode_mfma<8>: the same split, cursor, partials and merge for G = 8, with the tile
+//    work of a step on the matrix cores (QK^T and PV as bf16 16x16x32 MFMAs, K through a
+//    swizzled LDS tile and transposing reads, V straight into the MFMA operand registers).
+// 3. paged_attention_generic<DT, DPL>: any dtype / head_dim <= 512 / page size, several query
 //    rows per sequence with optional causal offsets. One wave per (query row, head); keys are
 //    processed 64 at a time (lane = key for QK, lane = head-dim element for PV).
 #include <algorithm>
@@ -25,6 +27,7 @@
 #include <random>
 #include <type_traits>
 
+#include "attn_tiles.h"
 #include "pia_internal.h"
 
 namespace pia {
@@ -262,35 +265,21 @@ __device__ __forceinline__ bool sd_arrive(uint64_t* ctr, uint64_t token, int n) 
   }
 }
 
-template <int G, bool APPEND>
-__global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
-    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
-    PoolIn<APPEND> kpool, PoolIn<APPEND> vpool,
-    const int32_t* __restrict__ block_tables, int64_t bt_stride,
-    const int32_t* __restrict__ context_lens, int B, int Hkv, int64_t num_pages,
-    float* __restrict__ ws_part, int32_t* __restrict__ ws_meta, float scale_log2,
-    uint16_t* kpool_w, uint16_t* vpool_w, const uint16_t* __restrict__ k_new,
-    const uint16_t* __restrict__ v_new, int64_t new_seq_stride, uint64_t token) {
-  constexpr int D = FD_D, P = FD_P, TILE = D * P, STEP = FD_PAGES_PER_WAVE;
+// Step prefix of the batch, built by every wave in its own LDS copy: seq_q[b] = steps of the
+// sequences before b (seq_q[B] = all of them), seq_len[b] = b's clamped context length (with
+// SD_NO_APPEND in append mode when its raw length does not fit its block table). Returns the
+// steps per kv head, sum_b ceil(L_b / 128).
+template <bool APPEND>
+__device__ __forceinline__ int sd_build_prefix(const int32_t* __restrict__ context_lens, int B,
+                                               int64_t bt_stride, int* seq_q, int* seq_len,
+                                               int lane) {
   constexpr int NCH = SD_MAX_SEQS / 64;
-  const int lane = threadIdx.x, w = blockIdx.x, NW = gridDim.x;
-  const int Hq = Hkv * G;
-  extern __shared__ int sd_lds[];
-  int* seq_q = sd_lds;            // [B + 1]: steps of the sequences before b
-  int* seq_len = sd_lds + B + 1;  // [B]: clamped context length
-  __shared__ uint32_t q_lds[4][16][G];
-  __shared__ uint32_t p_lds[64][G];
-  // append mode: deferred new-token stores, {pool element offset of the slot, k_new offset}
-  __shared__ int64_t app_rec[APPEND ? SD_APP_REC : 1][2];
-  int n_rec = 0;
-
-  // Step prefix over the batch: every wave builds its own copy in LDS.
   int lv[NCH], lflag[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int i = c * 64 + lane;
     const int raw = (c * 64 < B && i < B) ? context_lens[i] : 0;
-    lv[c] = clamp_len(raw, bt_stride, P);
+    lv[c] = clamp_len(raw, bt_stride, FD_P);
     lflag[c] = (APPEND && raw != lv[c]) ? SD_NO_APPEND : 0;
   }
   int carry = 0;
@@ -305,24 +294,36 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     }
     carry = uniform(carry + __shfl(incl, 63, 64));
   }
-  const int T = Hkv * carry;
-  const int Dp = stream_pair_steps(T, NW), Ce = stream_even_share(Dp);
   if (lane == 0) seq_q[0] = 0;
   __syncthreads();
-  // empty sequences (no steps) get zero rows here: wave w takes sequences w, w + NW, ...
+  return carry;
+}
+
+// Rows of sequences with no steps are written as zeros: wave w takes sequences w, w + NW, ...
+__device__ __forceinline__ void sd_zero_empty_rows(uint16_t* out, const int* seq_len, int B,
+                                                   int Hq, int w, int NW, int lane) {
   for (int b = w; b < B; b += NW) {
     if ((uniform(seq_len[b]) & ~SD_NO_APPEND) == 0) {
-      uint16_t* o = out + int64_t(b) * Hq * D;
-      for (int i = lane; i < Hq * D; i += 64) o[i] = 0;
+      uint16_t* o = out + int64_t(b) * Hq * FD_D;
+      for (int i = lane; i < Hq * FD_D; i += 64) o[i] = 0;
     }
   }
-  const int start = (w >> 1) * Dp + ((w & 1) ? Ce : 0);
-  const int end = min((w >> 1) * Dp + ((w & 1) ? Dp : Ce), T);
-  if (start >= end) return;
-  const int span = end - start;
+}
 
+// Walks the ordered step list (sequence-major, then kv head, then step) over the LDS prefix.
+struct StreamPlan {
+  const int* seq_q;
+  const int* seq_len;
+  int B, Hkv;
+  bool append;
+
+  __device__ __forceinline__ void set_len(StreamCursor& c) const {
+    const int sl = uniform(seq_len[c.b]);
+    c.L = sl & ~SD_NO_APPEND;
+    c.app = append && !(sl & SD_NO_APPEND);
+  }
   // cursor of global step gs: the last sequence b with Hkv * seq_q[b] <= gs (it has steps)
-  auto seg_of = [&](int gs) {
+  __device__ __forceinline__ StreamCursor seg_of(int gs) const {
     int lo = 0, hi = B - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -335,26 +336,166 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     const int r = gs - Hkv * q0;
     c.h = r / c.ns;
     c.ls = r - c.h * c.ns;
-    const int sl = uniform(seq_len[lo]);
-    c.L = sl & ~SD_NO_APPEND;
-    c.app = APPEND && !(sl & SD_NO_APPEND);
+    set_len(c);
     return c;
-  };
+  }
   // the step after c (only asked for when one exists inside the range)
-  auto next_of = [&](StreamCursor c) {
+  __device__ __forceinline__ StreamCursor next_of(StreamCursor c) const {
     if (++c.ls == c.ns) {
       c.ls = 0;
       if (++c.h == Hkv) {
         c.h = 0;
         do { ++c.b; } while (c.b < B - 1 && uniform(seq_q[c.b + 1]) == uniform(seq_q[c.b]));
         c.ns = uniform(seq_q[c.b + 1]) - uniform(seq_q[c.b]);
-        const int sl = uniform(seq_len[c.b]);
-        c.L = sl & ~SD_NO_APPEND;
-        c.app = APPEND && !(sl & SD_NO_APPEND);
+        set_len(c);
       }
     }
     return c;
-  };
+  }
+};
+
+// Append mode: k_new / v_new rows of one new token into its pool slot (element offset `slot` of
+// its (page, kv head) tile plus its token), non-temporally; src = the rows' element offset.
+__device__ __forceinline__ void sd_store_new_token(const uint16_t* __restrict__ k_new,
+                                                   const uint16_t* __restrict__ v_new,
+                                                   uint16_t* kpool_w, uint16_t* vpool_w,
+                                                   int64_t slot, int64_t src, int lane) {
+  const int d0 = 8 * (lane >> 2) + (lane & 3);
+  __builtin_nontemporal_store(k_new[src + d0], kpool_w + slot + d0 * FD_P);
+  __builtin_nontemporal_store(k_new[src + d0 + 4], kpool_w + slot + (d0 + 4) * FD_P);
+  if ((lane & 1) == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_nontemporal_store(v_new[src + 32 * j + (lane >> 1)],
+                                  vpool_w + slot + (32 * j + (lane >> 1)) * FD_P);
+  }
+}
+
+// Append mode: the deferred new-token stores of a wave's range (k_new / v_new rows reread: they
+// are small and cached). rec[r] = {pool element offset of the slot, k_new / v_new offset}.
+__device__ __forceinline__ void sd_flush_appends(const int64_t (*rec)[2], int n_rec,
+                                                 const uint16_t* __restrict__ k_new,
+                                                 const uint16_t* __restrict__ v_new,
+                                                 uint16_t* kpool_w, uint16_t* vpool_w, int lane) {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  for (int r = 0; r < n_rec; ++r)
+    sd_store_new_token(k_new, v_new, kpool_w, vpool_w, rec[r][0], rec[r][1], lane);
+}
+
+// Arrivals at the end of a wave's range: its partials (slot 0 / 1: arr_first = the segment's
+// first global step or -1, arr_ns its steps, arr_row = b * Hkv + h) are written; count them in
+// on their segments' counters and merge every segment whose last partial this is. Partial
+// layout per slot: G rows of [D unnormalised output, running max (log2 units), row sum].
+template <int G>
+__device__ __forceinline__ void sd_arrive_and_merge(const int (&arr_first)[2],
+                                                    const int (&arr_ns)[2],
+                                                    const int (&arr_row)[2], int Dp, int Ce,
+                                                    const float* ws_part, int32_t* ws_meta,
+                                                    uint64_t token, uint16_t* out, int Hkv,
+                                                    int lane) {
+  constexpr int D = FD_D;
+  if (arr_first[0] < 0 && arr_first[1] < 0) return;
+  uint64_t* ctr = reinterpret_cast<uint64_t*>(
+      (reinterpret_cast<uintptr_t>(ws_meta) + 7) & ~uintptr_t(7));
+  const int inc = Ce < Dp ? 1 : 2;  // odd waves hold no steps when pairs have one step
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed before its count
+  bool merge[2] = {false, false};
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if (arr_first[k] < 0) continue;
+    const int c0 = stream_range_of(arr_first[k], Dp, Ce);
+    const int c1 = stream_range_of(arr_first[k] + arr_ns[k] - 1, Dp, Ce);
+    int last = 0;
+    if (lane == 0) last = sd_arrive(ctr + c0, token, (c1 - c0) / inc + 1) ? 1 : 0;
+    merge[k] = __builtin_amdgcn_readfirstlane(last) != 0;
+  }
+  if (!merge[0] && !merge[1]) return;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    if (!merge[k]) continue;
+    // one online pass over the pieces in wave order (slot 1 of the first wave, slot 0 of the
+    // rest); lane l: elements l and l + 64 of every row
+    const int c0 = stream_range_of(arr_first[k], Dp, Ce);
+    const int c1 = stream_range_of(arr_first[k] + arr_ns[k] - 1, Dp, Ce);
+    float M[G], o0[G], o1[G], lt[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      M[g] = kNegBig;
+      o0[g] = o1[g] = lt[g] = 0.f;
+    }
+    // pieces four at a time: all their loads in flight together, then folded in order
+    constexpr int PB = 4;
+    for (int cb = c0; cb <= c1; cb += PB * inc) {
+      float mc[PB][G], lc[PB][G], a0[PB][G], a1[PB][G];
+#pragma unroll
+      for (int u = 0; u < PB; ++u) {
+        const int c = cb + u * inc;
+        if (c > c1) continue;
+        const float* pp = ws_part + (int64_t(c) * 2 + (c == c0 ? 1 : 0)) * G * (D + 2);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          mc[u][g] = sd_load(pp + g * (D + 2) + D);
+          lc[u][g] = sd_load(pp + g * (D + 2) + D + 1);
+          a0[u][g] = sd_load(pp + g * (D + 2) + lane);
+          a1[u][g] = sd_load(pp + g * (D + 2) + 64 + lane);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < PB; ++u) {
+        if (cb + u * inc > c1) continue;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float mn = fmaxf(M[g], mc[u][g]);
+          const float fo = fast_exp2(M[g] - mn), fc = fast_exp2(mc[u][g] - mn);
+          lt[g] = lt[g] * fo + lc[u][g] * fc;
+          o0[g] = o0[g] * fo + a0[u][g] * fc;
+          o1[g] = o1[g] * fo + a1[u][g] * fc;
+          M[g] = mn;
+        }
+      }
+    }
+    const int b = arr_row[k] / Hkv, h = arr_row[k] - b * Hkv;
+    uint16_t* orow = out + (int64_t(b) * Hkv * G + int64_t(h) * G) * D;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      orow[g * D + lane] = f32_to_bf16(lt[g] > 0.f ? o0[g] / lt[g] : 0.f);
+      orow[g * D + 64 + lane] = f32_to_bf16(lt[g] > 0.f ? o1[g] / lt[g] : 0.f);
+    }
+  }
+}
+
+template <int G, bool APPEND>
+__global__ __launch_bounds__(64, 2) void paged_decode_stream(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
+    PoolIn<APPEND> kpool, PoolIn<APPEND> vpool,
+    const int32_t* __restrict__ block_tables, int64_t bt_stride,
+    const int32_t* __restrict__ context_lens, int B, int Hkv, int64_t num_pages,
+    float* __restrict__ ws_part, int32_t* __restrict__ ws_meta, float scale_log2,
+    uint16_t* kpool_w, uint16_t* vpool_w, const uint16_t* __restrict__ k_new,
+    const uint16_t* __restrict__ v_new, int64_t new_seq_stride, uint64_t token) {
+  static_assert(G == 1 || G == 2 || G == 4, "G = 8 runs paged_decode_mfma");
+  constexpr int D = FD_D, P = FD_P, TILE = D * P, STEP = FD_PAGES_PER_WAVE;
+  const int lane = threadIdx.x, w = blockIdx.x, NW = gridDim.x;
+  const int Hq = Hkv * G;
+  extern __shared__ int sd_lds[];
+  int* seq_q = sd_lds;            // [B + 1]: steps of the sequences before b
+  int* seq_len = sd_lds + B + 1;  // [B]: clamped context length
+  __shared__ uint32_t q_lds[4][16][G];
+  __shared__ uint32_t p_lds[64][G];
+  // append mode: deferred new-token stores, {pool element offset of the slot, k_new offset}
+  __shared__ int64_t app_rec[APPEND ? SD_APP_REC : 1][2];
+  int n_rec = 0;
+
+  const int T = Hkv * sd_build_prefix<APPEND>(context_lens, B, bt_stride, seq_q, seq_len, lane);
+  const int Dp = stream_pair_steps(T, NW), Ce = stream_even_share(Dp);
+  sd_zero_empty_rows(out, seq_len, B, Hq, w, NW, lane);
+  const int start = (w >> 1) * Dp + ((w & 1) ? Ce : 0);
+  const int end = min((w >> 1) * Dp + ((w & 1) ? Dp : Ce), T);
+  if (start >= end) return;
+  const int span = end - start;
+
+  const StreamPlan plan{seq_q, seq_len, B, Hkv, APPEND};
   // lane l: block-table entry of page l/8 of the step (entries past the sequence repeat its
   // last page; ids are range-checked where they are used)
   auto load_bt = [&](const StreamCursor& c) -> int {
@@ -367,8 +508,7 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
   };
   // q rows of a segment: lane l < 16G holds q[g][8pp .. 8pp+7], g = l/16, pp = l%16 (four dword
   // loads: q is only 4-byte aligned); staged as the (d, d+4) pairs of row-pair pp.
-  // (G = 8: lane l also holds row g + 4 in the second word group)
-  constexpr int QW = (G + 3) / 4;
+  constexpr int QW = 1;
   using QRows = uint4[QW];
   auto load_q = [&](const StreamCursor& c, QRows& r) {
 #pragma unroll
@@ -411,7 +551,7 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
   }
 
   int gs = start;
-  StreamCursor cur = seg_of(gs);
+  StreamCursor cur = plan.seg_of(gs);
   // partials this wave writes (slot 0, slot 1): the first global step, step count and row of
   // their segments, for the arrivals after the range (arr_first -1: no partial in that slot)
   int arr_first[2] = {-1, -1}, arr_ns[2] = {0, 0}, arr_row[2] = {0, 0};
@@ -521,7 +661,7 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     // The next step's block-table row and (when it opens a segment) q go out first, ahead of
     // this step's V loads, so they have landed by the time they are consumed. At the end of
     // the range the "next" step repeats the current one (its K is not prefetched).
-    const StreamCursor nxt = has_next ? next_of(cur) : cur;
+    const StreamCursor nxt = has_next ? plan.next_of(cur) : cur;
     const bool nxt_opens = has_next && nxt.ls == 0;
     const int bt_nxt = load_bt(nxt);
     QRows q_nxt;
@@ -724,95 +864,456 @@ __global__ __launch_bounds__(64, G > 4 ? 1 : 2) void paged_decode_stream(
     bt_cur = bt_nxt;
     ++gs;
   }
-  if constexpr (APPEND) {
-    // the deferred new-token stores (k_new / v_new rows reread: they are small and cached)
+  if constexpr (APPEND) sd_flush_appends(app_rec, n_rec, k_new, v_new, kpool_w, vpool_w, lane);
+  // All arrivals at the end of the range, so no fence drains a step's prefetch.
+  sd_arrive_and_merge<G>(arr_first, arr_ns, arr_row, Dp, Ce, ws_part, ws_meta, token, out, Hkv,
+                         lane);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Stream decode kernel on the matrix cores (bf16, D = 128, P = 16), launched for G = 8.
+//
+// The same work split, cursor, partial slots, arrivals and merge as paged_decode_stream, one wave
+// per SIMD; only the tile work of a step differs. Eight q rows against 128 keys cost 2048
+// v_dot2 per lane and step on the vector ALU (a third of the step's share of HBM time, issued
+// by the one wave that must also keep its loads in flight); on the matrix cores they are 32 +
+// 32 MFMAs and the vector ALU keeps only the softmax. A 128-token step is two 64-token tiles
+// (pages 0..3 and 4..7 of the step), each:
+//   K: sixteen 16-byte loads per lane (load 4 p + r: page p of the tile, rows 32 r + l / 2,
+//      token half l % 2; 1 KiB contiguous per load), stored into the wave's swizzled
+//      [d][64 tokens] LDS tile (tile::swz64).
+//   S^T = K . Q^T: 16 MFMAs (4 token blocks x 4 d chunks); A = K^T built by transposing LDS
+//      reads, B = the segment's q rows in registers (operand rows G..15 are zero). Lane l then
+//      holds the scores of q row l % 16 for tokens 16 mb + 4 (l / 16) + j.
+//   V: thirty-two 8-byte loads per lane straight into the B operands of P . V: for 32-token
+//      chunk c and d block nb, lane l reads row d = 16 nb + l % 16 at tokens 4 (l / 16) .. + 3
+//      of pages 2c (k slots 8 (l / 16) .. + 3) and 2c + 1 (k slots + 4 .. + 7): the tokens
+//      whose probabilities lane l already holds, in the same k order.
+//   O += P . V: 16 MFMAs, and 2 more against a column of ones for the row sums.
+// Softmax per q row in fp32, base 2 with the scale folded in; the reference point of a row's
+// exponentials moves only when a step's max exceeds it by more than SD_RESCALE (probabilities
+// stay <= 2^8; the final division is exact either way). Pipeline per step, two rotating 16 KiB
+// register buffers (A: K tile 0 -> V tile 0 -> next K tile 0; B likewise for tile 1):
+//   stage K0 | issue V0 | QK0 | stage K1 | issue V1 | QK1 | softmax | PV0 | issue K0' | PV1 |
+//   issue K1'
+// Append mode: the new token's key goes into the LDS tile and its value into the V operand
+// registers in place of the slot's, so it is scored and summed like every other token; the
+// stores into the slot are deferred to the end of the range as in paged_decode_stream.
+// ---------------------------------------------------------------------------------------------
+constexpr float SD_RESCALE = 8.0f;
+
+template <int G, bool APPEND>
+__global__ __launch_bounds__(64, 1) void paged_decode_mfma(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
+    PoolIn<APPEND> kpool, PoolIn<APPEND> vpool,
+    const int32_t* __restrict__ block_tables, int64_t bt_stride,
+    const int32_t* __restrict__ context_lens, int B, int Hkv, int64_t num_pages,
+    float* __restrict__ ws_part, int32_t* __restrict__ ws_meta, float scale_log2,
+    uint16_t* kpool_w, uint16_t* vpool_w, const uint16_t* __restrict__ k_new,
+    const uint16_t* __restrict__ v_new, int64_t new_seq_stride, uint64_t token) {
+  using tile::f32x4_t;
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  constexpr int D = FD_D, P = FD_P, TILE = D * P, STEP = FD_PAGES_PER_WAVE;
+  constexpr int KT = tile::kTileTokens;
+  const int lane = threadIdx.x, w = blockIdx.x, NW = gridDim.x;
+  const int Hq = Hkv * G;
+  extern __shared__ int sd_lds[];
+  int* seq_q = sd_lds;            // [B + 1]: steps of the sequences before b
+  int* seq_len = sd_lds + B + 1;  // [B]: clamped context length
+  __shared__ __align__(16) uint16_t ks[D * KT];
+  // append mode: deferred new-token stores, {pool element offset of the slot, k_new offset}
+  __shared__ int64_t app_rec[APPEND ? SD_APP_REC : 1][2];
+  int n_rec = 0;
+
+  const int T = Hkv * sd_build_prefix<APPEND>(context_lens, B, bt_stride, seq_q, seq_len, lane);
+  const int Dp = stream_pair_steps(T, NW), Ce = stream_even_share(Dp);
+  sd_zero_empty_rows(out, seq_len, B, Hq, w, NW, lane);
+  const int start = (w >> 1) * Dp + ((w & 1) ? Ce : 0);
+  const int end = min((w >> 1) * Dp + ((w & 1) ? Dp : Ce), T);
+  if (start >= end) return;
+  const int span = end - start;
+  const StreamPlan plan{seq_q, seq_len, B, Hkv, APPEND};
+
+  const int g4 = lane >> 4, n16 = lane & 15;
+  // lane l: block-table entry of page l/8 of the step (entries past the sequence repeat its
+  // last page; ids are range-checked where they are used)
+  auto load_bt = [&](const StreamCursor& c) -> int {
+    const int npg = (c.L + P - 1) / P;
+    const int i = min(c.ls * STEP + (lane >> 3), npg - 1);
+    return block_tables[int64_t(c.b) * bt_stride + i];
+  };
+  auto page_ok = [&](int p) -> int64_t {
+    return (p < 0 || int64_t(p) >= num_pages) ? 0 : int64_t(p);
+  };
+  // B operand of S^T: lane l holds q row l % 16 (zero for rows >= G) at d = 32 kc + 8 (l / 16)
+  // .. + 7 (dword loads: q is only 4-byte aligned)
+  auto load_q = [&](const StreamCursor& c, uint4 (&r)[4]) {
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      r[kc] = make_uint4(0u, 0u, 0u, 0u);
+      if (n16 < G) {
+        const uint32_t* qw = reinterpret_cast<const uint32_t*>(
+            q + int64_t(c.b) * q_seq_stride + int64_t(c.h * G + n16) * D + 32 * kc + 8 * g4);
+        r[kc] = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+      }
+    }
+  };
+  // Swizzled LDS offsets as per-lane bases XORed with compile-time terms: the store of K load
+  // 4 p + r lands at (st_base ^ 16 p) + 2048 r; the transposing read (mb, kc, hi) at
+  // (k_base[hi] ^ 16 mb) + 2048 kc.
+  int st_base, k_base[2];
+  {
+    const int d = lane >> 1, f = tile::swz64_row_term(d);
+    st_base = (d * KT + 8 * ((lane & 1) ^ (f & 1))) | (16 * (f >> 1));
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi) {
+      const int fk = ((2 * g4 + hi) ^ ((n16 >> 2) << 1)) & 7;
+      const int row = 8 * g4 + 4 * hi + (n16 >> 2);
+      k_base[hi] = (row * KT + 4 * (n16 & 1) + 8 * (((n16 >> 1) & 1) ^ (fk & 1))) |
+                   (16 * (fk >> 1));
+    }
+  }
+  const int64_t page_stride = int64_t(Hkv) * TILE;
+  const uint16_t* klane = kpool + 8 * lane;
+  const uint16_t* vlane = vpool + n16 * P + 4 * g4;
+
+  // K of tile t of a step into registers
+  auto load_k = [&](uint4 (&kr)[16], int h, int bt, int t) {
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi) {
+      const int64_t id = page_ok(__builtin_amdgcn_readlane(bt, 8 * (4 * t + pi)));
+      const uint16_t* kp = klane + int64_t(h) * TILE + id * page_stride;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) kr[4 * pi + r] = load16_nt(kp + 512 * r);
+    }
+  };
+  auto stage_k = [&](const uint4 (&kr)[16]) {
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<uint4*>(&ks[(st_base ^ (16 * pi)) + 2048 * r]) = kr[4 * pi + r];
+  };
+  // V operands of tile t: vr[8 c + nb] holds row 16 nb + l % 16 at tokens 4 (l / 16) .. + 3 of
+  // pages 2c (.x, .y) and 2c + 1 (.z, .w) of the tile
+  auto load_v = [&](uint4 (&vr)[16], int h, int bt, int t) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int64_t id = page_ok(__builtin_amdgcn_readlane(bt, 8 * (4 * t + 2 * c + s)));
+        const uint16_t* vp = vlane + int64_t(h) * TILE + id * page_stride;
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+          const u32x2_t x =
+              __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(vp + 256 * nb));
+          if (s == 0) {
+            vr[8 * c + nb].x = x.x;
+            vr[8 * c + nb].y = x.y;
+          } else {
+            vr[8 * c + nb].z = x.x;
+            vr[8 * c + nb].w = x.y;
+          }
+        }
+      }
+  };
+
+  float m = kNegBig;  // running reference point of row l % 16 (log2 units)
+  f32x4_t acc[8], lsum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint4 ones = tile::bf16_ones();
+  uint4 qreg[4];
+
+  auto qk_tile = [&](f32x4_t (&sc)[4]) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        const uint2 lo = tile::read_tr16(&ks[(k_base[0] ^ (16 * mb)) + 2048 * kc]);
+        const uint2 hi = tile::read_tr16(&ks[(k_base[1] ^ (16 * mb)) + 2048 * kc]);
+        sc[mb] = tile::mfma_bf16(make_uint4(lo.x, lo.y, hi.x, hi.y), qreg[kc],
+                                 kc == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sc[mb]);
+      }
+  };
+  // scores of tile t -> log2 units; on masked steps tokens at or past `valid` and tokens of
+  // pages with an id outside the pool (bit 8 pg of `bad`) -> -inf. Returns the lane's max.
+  auto prep = [&](f32x4_t (&sc)[4], int t, bool masked, int valid, uint64_t bad) -> float {
+    float mx = -INFINITY;
+    if (masked) {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const int pg = 4 * t + mb;
+        const int lim = ((bad >> (8 * pg)) & 1ull) ? 0 : valid - (16 * pg + 4 * g4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x = j < lim ? sc[mb][j] * scale_log2 : -INFINITY;
+          sc[mb][j] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x = sc[mb][j] * scale_log2;
+          sc[mb][j] = x;
+          mx = fmaxf(mx, x);
+        }
+    }
+    return mx;
+  };
+  // probabilities of tile t as the A operands of its two 32-token chunks
+  auto probs = [&](const f32x4_t (&sc)[4], float mref, uint4 (&pk)[2]) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float p[2][4];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[hh][j] = fast_exp2(sc[2 * c + hh][j] - mref);
+      pk[c] = make_uint4(tile::pack_bf16x2(p[0][0], p[0][1]), tile::pack_bf16x2(p[0][2], p[0][3]),
+                         tile::pack_bf16x2(p[1][0], p[1][1]), tile::pack_bf16x2(p[1][2], p[1][3]));
+    }
+  };
+  // V words of tokens at or past `valid` or in pages outside the pool -> 0 (stale memory may
+  // hold non-finite values, and 0 * inf is not 0)
+  auto mask_v = [&](uint4 (&vr)[16], int t, int valid, uint64_t bad) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int pg = 4 * t + 2 * c + s;
+        const int nvalid = ((bad >> (8 * pg)) & 1ull) ? 0 : valid - (16 * pg + 4 * g4);
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+          uint4& x = vr[8 * c + nb];
+          if (s == 0) {
+            x.x = mask_pair(x.x, 0, nvalid);
+            x.y = mask_pair(x.y, 2, nvalid);
+          } else {
+            x.z = mask_pair(x.z, 0, nvalid);
+            x.w = mask_pair(x.w, 2, nvalid);
+          }
+        }
+      }
+  };
+  auto pv_tile = [&](const uint4 (&vr)[16], const uint4 (&pk)[2]) {
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+      acc[nb] = tile::mfma_bf16(pk[0], vr[nb], acc[nb]);
+      acc[nb] = tile::mfma_bf16(pk[1], vr[8 + nb], acc[nb]);
+    }
+  };
+
+  int gs = start;
+  StreamCursor cur = plan.seg_of(gs);
+  // partials this wave writes (slot 0, slot 1): the first global step, step count and row of
+  // their segments, for the arrivals after the range (arr_first -1: no partial in that slot)
+  int arr_first[2] = {-1, -1}, arr_ns[2] = {0, 0}, arr_row[2] = {0, 0};
+  load_q(cur, qreg);
+  int bt_cur = load_bt(cur);
+  uint4 bufA[16], bufB[16];
+  load_k(bufA, cur.h, bt_cur, 0);
+  load_k(bufB, cur.h, bt_cur, 1);
+
+  for (;;) {
+    {  // issue priority from progress: quartile 0 of the range -> 3, quartile 3 -> 0
+      const int quarter = (4 * (gs - start)) / span;
+      if (quarter <= 0) __builtin_amdgcn_s_setprio(3);
+      else if (quarter == 1) __builtin_amdgcn_s_setprio(2);
+      else if (quarter == 2) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
+    const bool has_next = gs + 1 < end;
+    const StreamCursor nxt = has_next ? plan.next_of(cur) : cur;
+    const bool nxt_opens = has_next && nxt.ls == 0;
+    const int bt_nxt = load_bt(nxt);
+    uint4 q_nxt[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) q_nxt[kc] = make_uint4(0u, 0u, 0u, 0u);
+    if (nxt_opens) load_q(nxt, q_nxt);
+    const int valid = min(SD_STEP_TOKENS, cur.L - cur.ls * SD_STEP_TOKENS);
+
+    // append mode, the segment's last step: token tn of the step is the new one; lane l takes
+    // k_new[l], k_new[l + 64] (its LDS column) and v_new[16 nb + l % 16] (its V operand rows)
+    const bool app_step = APPEND && cur.app && cur.ls == cur.ns - 1;
+    const int tn = valid - 1;
+    const int64_t app_src = int64_t(cur.b) * new_seq_stride + int64_t(cur.h) * D;
+    uint16_t kn0 = 0, kn1 = 0, vn[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) vn[nb] = 0;
+    if (app_step) {
+      kn0 = k_new[app_src + lane];
+      kn1 = k_new[app_src + 64 + lane];
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) vn[nb] = v_new[app_src + 16 * nb + n16];
+    }
+    auto put_knew = [&](int t) {
+      if (app_step && (tn >> 6) == t) {
+        ks[tile::swz64(lane, tn & (KT - 1))] = kn0;
+        ks[tile::swz64(lane + 64, tn & (KT - 1))] = kn1;
+      }
+    };
+    auto put_vnew = [&](uint4 (&vr)[16], int t) {
+      if (!(app_step && (tn >> 6) == t)) return;
+      const int cn = (tn >> 5) & 1, wsel = 2 * ((tn >> 4) & 1) + ((tn >> 1) & 1);
+      const uint32_t sh = (tn & 1) ? 16u : 0u, keep = ~(0xffffu << sh);
+      const bool mine = g4 == ((tn >> 2) & 3);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const bool sel = mine && c == cn;  // per-element selects: the indices stay static
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+          uint4& x = vr[8 * c + nb];
+          const uint32_t nv = uint32_t(vn[nb]) << sh;
+          x.x = (sel && wsel == 0) ? ((x.x & keep) | nv) : x.x;
+          x.y = (sel && wsel == 1) ? ((x.y & keep) | nv) : x.y;
+          x.z = (sel && wsel == 2) ? ((x.z & keep) | nv) : x.z;
+          x.w = (sel && wsel == 3) ? ((x.w & keep) | nv) : x.w;
+        }
+      }
+    };
+
+    // pages of this step whose id is outside the pool: their tokens are not keys
+    const bool pg_ok = bt_cur >= 0 && int64_t(bt_cur) < num_pages;
+    const uint64_t bad = __ballot(!pg_ok);
+    const bool masked = valid < SD_STEP_TOKENS || bad != 0;
+
+    __builtin_amdgcn_sched_barrier(0);
+    stage_k(bufA);
+    put_knew(0);
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    const int d0 = 8 * (lane >> 2) + (lane & 3);
-    for (int r = 0; r < n_rec; ++r) {
-      const int64_t slot = app_rec[r][0], src = app_rec[r][1];
-      __builtin_nontemporal_store(k_new[src + d0], kpool_w + slot + d0 * P);
-      __builtin_nontemporal_store(k_new[src + d0 + 4], kpool_w + slot + (d0 + 4) * P);
-      if ((lane & 1) == 0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          __builtin_nontemporal_store(v_new[src + 32 * j + (lane >> 1)],
-                                      vpool_w + slot + (32 * j + (lane >> 1)) * P);
-      }
-    }
-  }
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(bufA, cur.h, bt_cur, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4_t sA[4], sB[4];
+    qk_tile(sA);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    stage_k(bufB);
+    put_knew(1);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(bufB, cur.h, bt_cur, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    qk_tile(sB);
 
-  // Arrivals: this wave's partials are written; count them in on their segments' counters and
-  // merge every segment whose last partial this is. All at the end of the range, so no fence
-  // drains a step's prefetch.
-  if (arr_first[0] < 0 && arr_first[1] < 0) return;
-  uint64_t* ctr = reinterpret_cast<uint64_t*>(
-      (reinterpret_cast<uintptr_t>(ws_meta) + 7) & ~uintptr_t(7));
-  const int inc = Ce < Dp ? 1 : 2;  // odd waves hold no steps when pairs have one step
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed before its count
-  bool merge[2] = {false, false};
+    // softmax: row max over the step (lanes l, l ^ 16, l ^ 32, l ^ 48 hold one row)
+    float mx = fmaxf(prep(sA, 0, masked, valid, bad), prep(sB, 1, masked, valid, bad));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mref = (mx - m > SD_RESCALE) ? mx : m;
+    const float alpha = m == mref ? 1.f : fast_exp2(m - mref);
+    const bool moved = m != mref;
+    m = mref;
+    uint4 pkA[2], pkB[2];
+    probs(sA, mref, pkA);
+    probs(sB, mref, pkB);
+    // rescale O and the sums when some row's reference point moved: lane l's accumulator rows
+    // are 4 (l / 16) + j; their alpha sits in lane 4 (l / 16) + j
+    if (__ballot(moved)) {
+      float aj[4];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    if (arr_first[k] < 0) continue;
-    const int c0 = stream_range_of(arr_first[k], Dp, Ce);
-    const int c1 = stream_range_of(arr_first[k] + arr_ns[k] - 1, Dp, Ce);
-    int last = 0;
-    if (lane == 0) last = sd_arrive(ctr + c0, token, (c1 - c0) / inc + 1) ? 1 : 0;
-    merge[k] = __builtin_amdgcn_readfirstlane(last) != 0;
-  }
-  if (!merge[0] && !merge[1]) return;
+      for (int j = 0; j < 4; ++j) aj[j] = __shfl(alpha, 4 * g4 + j, 64);
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    if (!merge[k]) continue;
-    // one online pass over the pieces in wave order (slot 1 of the first wave, slot 0 of the
-    // rest); lane l: elements l and l + 64 of every row
-    const int c0 = stream_range_of(arr_first[k], Dp, Ce);
-    const int c1 = stream_range_of(arr_first[k] + arr_ns[k] - 1, Dp, Ce);
-    float M[G], o0[G], o1[G], lt[G];
+      for (int j = 0; j < 4; ++j) {
+        lsum[j] *= aj[j];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      M[g] = kNegBig;
-      o0[g] = o1[g] = lt[g] = 0.f;
-    }
-    // pieces four at a time: all their loads in flight together, then folded in order
-    constexpr int PB = 4;
-    for (int cb = c0; cb <= c1; cb += PB * inc) {
-      float mc[PB][G], lc[PB][G], a0[PB][G], a1[PB][G];
-#pragma unroll
-      for (int u = 0; u < PB; ++u) {
-        const int c = cb + u * inc;
-        if (c > c1) continue;
-        const float* pp = ws_part + (int64_t(c) * 2 + (c == c0 ? 1 : 0)) * G * (D + 2);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          mc[u][g] = sd_load(pp + g * (D + 2) + D);
-          lc[u][g] = sd_load(pp + g * (D + 2) + D + 1);
-          a0[u][g] = sd_load(pp + g * (D + 2) + lane);
-          a1[u][g] = sd_load(pp + g * (D + 2) + 64 + lane);
-        }
+        for (int nb = 0; nb < 8; ++nb) acc[nb][j] *= aj[j];
       }
+    }
 #pragma unroll
-      for (int u = 0; u < PB; ++u) {
-        if (cb + u * inc > c1) continue;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float mn = fmaxf(M[g], mc[u][g]);
-          const float fo = fast_exp2(M[g] - mn), fc = fast_exp2(mc[u][g] - mn);
-          lt[g] = lt[g] * fo + lc[u][g] * fc;
-          o0[g] = o0[g] * fo + a0[u][g] * fc;
-          o1[g] = o1[g] * fo + a1[u][g] * fc;
-          M[g] = mn;
+    for (int c = 0; c < 2; ++c) {
+      lsum = tile::mfma_bf16(pkA[c], ones, lsum);
+      lsum = tile::mfma_bf16(pkB[c], ones, lsum);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    put_vnew(bufA, 0);
+    if (masked) mask_v(bufA, 0, valid, bad);
+    pv_tile(bufA, pkA);
+    __builtin_amdgcn_sched_barrier(0);
+    // the next step's K (none after the range's last step: the wave's end waits for its
+    // outstanding loads before it counts its partials in)
+    if (has_next) load_k(bufA, nxt.h, bt_nxt, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    put_vnew(bufB, 1);
+    if (masked) mask_v(bufB, 1, valid, bad);
+    pv_tile(bufB, pkB);
+    __builtin_amdgcn_sched_barrier(0);
+    if (has_next) load_k(bufB, nxt.h, bt_nxt, 1);
+
+    if (app_step) {  // the new token goes into its slot after the range (page ids checked)
+      const int idn = __builtin_amdgcn_readlane(bt_cur, 8 * (tn >> 4));
+      if (idn >= 0 && int64_t(idn) < num_pages) {
+        const int64_t slot = int64_t(idn) * page_stride + int64_t(cur.h) * TILE + (tn & 15);
+        if (n_rec < SD_APP_REC) {
+          if (lane == 0) {
+            app_rec[n_rec][0] = slot;
+            app_rec[n_rec][1] = app_src;
+          }
+          ++n_rec;
+        } else {
+          sd_store_new_token(k_new, v_new, kpool_w, vpool_w, slot, app_src, lane);
         }
       }
     }
-    const int b = arr_row[k] / Hkv, h = arr_row[k] - b * Hkv;
-    uint16_t* orow = out + (int64_t(b) * Hq + int64_t(h) * G) * D;
+
+    const bool seg_last = cur.ls == cur.ns - 1;
+    if (seg_last || !has_next) {
+      const int seg_first = gs - cur.ls;  // global index of the segment's first step
+      const int64_t row0 = int64_t(cur.b) * Hq + int64_t(cur.h) * G;
+      if (seg_last && seg_first >= start) {
+        if (4 * g4 < G) {  // lane l holds rows 4 (l / 16) + j
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      orow[g * D + lane] = f32_to_bf16(lt[g] > 0.f ? o0[g] / lt[g] : 0.f);
-      orow[g * D + 64 + lane] = f32_to_bf16(lt[g] > 0.f ? o1[g] / lt[g] : 0.f);
+          for (int j = 0; j < 4; ++j) {
+            if (4 * g4 + j >= G) continue;
+            const float inv = lsum[j] > 0.f ? 1.f / lsum[j] : 0.f;
+            uint16_t* o = out + (row0 + 4 * g4 + j) * D + n16;
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb) o[16 * nb] = f32_to_bf16(acc[nb][j] * inv);
+          }
+        }
+      } else {
+        const int slot = seg_first < start ? 0 : 1;
+        arr_first[slot] = seg_first;
+        arr_ns[slot] = cur.ns;
+        arr_row[slot] = cur.b * Hkv + cur.h;
+        // device-coherent partial stores (see paged_decode_stream)
+        float* part = ws_part + (int64_t(w) * 2 + slot) * G * (D + 2);
+        if (4 * g4 < G) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (4 * g4 + j >= G) continue;
+#pragma unroll
+            for (int nb = 0; nb < 8; ++nb)
+              sd_store(part + (4 * g4 + j) * (D + 2) + 16 * nb + n16, acc[nb][j]);
+            if (n16 == 0) sd_store(part + (4 * g4 + j) * (D + 2) + D + 1, lsum[j]);
+          }
+        }
+        if (g4 == 0 && n16 < G) sd_store(part + n16 * (D + 2) + D, m);
+      }
+      m = kNegBig;
+      lsum = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
+    if (!has_next) break;
+    if (nxt_opens) {
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) qreg[kc] = q_nxt[kc];
+    }
+    cur = nxt;
+    bt_cur = bt_nxt;
+    ++gs;
   }
+  if constexpr (APPEND) sd_flush_appends(app_rec, n_rec, k_new, v_new, kpool_w, vpool_w, lane);
+  sd_arrive_and_merge<G>(arr_first, arr_ns, arr_row, Dp, Ce, ws_part, ws_meta, token, out, Hkv,
+                         lane);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1006,11 +1507,18 @@ bool fast_path(int dtype, int Hq, int Hkv, int D, int P) {
          (G == 1 || G == 2 || G == 4 || G == 8);
 }
 
-// Waves of a stream launch: every CU at two single-wave workgroups per SIMD (CU count cached
-// per device), capped by the partial slots the workspace holds.
-// persistent waves of the stream kernel: two per SIMD, or one for G = 8 (its registers)
+// Whether a decode launch with G q rows per kv head runs the matrix-core engine: G = 8 only.
+// At G = 4 (Qwen3-8B, batch 256) the vector-ALU engine at two waves per SIMD measured 0.718 ms
+// per step against 0.740 ms for the matrix-core engine at one (its registers), so G <= 4 stays
+// on paged_decode_stream.
+bool stream_uses_mfma(int G) { return G == 8; }
+
+// Waves of a stream launch (CU count cached per device), capped by the partial slots the
+// workspace holds: two single-wave workgroups per SIMD for the vector-ALU engine, one for the
+// matrix-core engine (its registers).
 int stream_waves(int G) {
-  const int n = std::min(device_cus() * (G > 4 ? SD_WAVES_PER_CU / 2 : SD_WAVES_PER_CU),
+  const int n = std::min(device_cus() * (stream_uses_mfma(G) ? SD_WAVES_PER_CU / 2
+                                                              : SD_WAVES_PER_CU),
                          SD_MAX_WAVES);
   return std::max(2, n & ~1);  // whole (even, odd) pairs
 }
@@ -1093,22 +1601,28 @@ int launch_stream_decode(void* out, const void* q, int64_t q_seq_stride, const v
                      qq, q_seq_stride, (const uint16_t*)k_pages, (const uint16_t*)v_pages, bt, \
                      bt_stride, cl, Bs, num_kv_heads, num_pages, ws_part, ws_meta, scale_log2, \
                      kw, vw, kn, vn, new_seq_stride, token)
+#define PIA_SDM(GG, AP)                                                                        \
+  hipLaunchKernelGGL((paged_decode_mfma<GG, AP>), dim3(unsigned(NW)), dim3(64), lds, s, o, qq, \
+                     q_seq_stride, (const uint16_t*)k_pages, (const uint16_t*)v_pages, bt,     \
+                     bt_stride, cl, Bs, num_kv_heads, num_pages, ws_part, ws_meta, scale_log2, \
+                     kw, vw, kn, vn, new_seq_stride, token)
     if (kn) {
       switch (G) {
         case 1: PIA_SD(1, true); break;
         case 2: PIA_SD(2, true); break;
         case 4: PIA_SD(4, true); break;
-        default: PIA_SD(8, true); break;
+        default: PIA_SDM(8, true); break;
       }
     } else {
       switch (G) {
         case 1: PIA_SD(1, false); break;
         case 2: PIA_SD(2, false); break;
         case 4: PIA_SD(4, false); break;
-        default: PIA_SD(8, false); break;
+        default: PIA_SDM(8, false); break;
       }
     }
 #undef PIA_SD
+#undef PIA_SDM
     if (int rc = check_launch("paged_decode_stream")) return rc;
   }
   return 0;

@@ -38,13 +38,13 @@
 // (sequence, kv head) and read its K / V through that XCD's L2 once between them.
 #include <algorithm>
 
+#include "attn_tiles.h"
 #include "pia_internal.h"
 
 namespace pia {
 namespace {
 
-typedef __bf16 pf_bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float pf_f32x4_t __attribute__((ext_vector_type(4)));
+using tile::f32x4_t;
 
 constexpr int PF_D = 128, PF_P = 16;
 constexpr int PF_RB = 2;              // 16-row MFMA blocks per wave
@@ -52,32 +52,9 @@ constexpr int PF_ROWS = 64 * PF_RB;   // (position, head) rows per work item: 4 
 constexpr int PF_KT = 64;             // keys per tile: four pages
 constexpr int PF_MAX_SEQS = 1024;     // sequences per launch (tile prefix in LDS)
 
-// element offset of (row d, token t) in a swizzled [d][64 tokens] LDS tile
-__device__ __forceinline__ int pf_swz(int d, int t) {
-  return d * PF_KT + ((((t >> 3) ^ (d >> 2) ^ ((d & 3) << 1)) & 7) << 3) + (t & 7);
-}
 // lazy rescaling threshold (log2 units): a row's exponentials are taken against a reference
 // that trails its true max by at most this much, so probabilities stay <= 2^8
 constexpr float PF_RESCALE = 8.0f;
-
-__device__ __forceinline__ pf_f32x4_t pf_mfma(const uint4& a, const uint4& b, pf_f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(pf_bf16x8_t, a),
-                                                 __builtin_bit_cast(pf_bf16x8_t, b), c, 0, 0, 0);
-}
-
-// ds_read_b64_tr_b16 at an 8-byte aligned LDS address (see the kernel's description)
-__device__ __forceinline__ uint2 pf_read_tr(const uint16_t* p) {
-  typedef short v4i16 __attribute__((ext_vector_type(4)));
-  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(const_cast<uint16_t*>(p)));
-  return __builtin_bit_cast(uint2, v);
-}
-
-__device__ __forceinline__ uint32_t pf_pack(float lo, float hi) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  const bf16x2_t p = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
-  return __builtin_bit_cast(uint32_t, p);
-}
 
 template <int G>
 __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
@@ -187,8 +164,8 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
       }
     }
   };
-  // Swizzled LDS offsets, as per-lane bases XORed with compile-time terms (pf_swz(d, t) with
-  // the chunk index split into its bits): a store of piece i lands at st_base ^ 16 i; the K
+  // Swizzled LDS offsets, as per-lane bases XORed with compile-time terms (tile::swz64(d, t)
+  // with the chunk index split into its bits): a store of piece i lands at st_base ^ 16 i; the K
   // operand read (kc, hi, mb) at (k_base[hi] ^ 16 mb) + 2048 kc; the V operand read
   // (nb, c, s) at (v_base[nb % 2] ^ (32 c + 16 s)) + 1024 nb.
   int st_base, k_base[2], v_base[2];
@@ -232,15 +209,15 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
   // l % 16); lsum[rb] is its softmax denominator, summed by the matrix cores against a column
   // of ones, so it sits in the same layout and is rescaled with the accumulators.
   float m[RB];
-  pf_f32x4_t acc[RB][8], lsum[RB];
+  f32x4_t acc[RB][8], lsum[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     m[rb] = -INFINITY;
-    lsum[rb] = pf_f32x4_t{0.f, 0.f, 0.f, 0.f};
+    lsum[rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) acc[rb][nb] = pf_f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < 8; ++nb) acc[rb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
-  const uint4 ones = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+  const uint4 ones = tile::bf16_ones();
 
   if (nkt > 0) fetch(0);
   for (int kt = 0; kt < nkt; ++kt) {
@@ -254,18 +231,18 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
 
     // S^T for the wave's rows: 4 token blocks (one per page) x 4 d chunks, each K operand
     // serving both row blocks
-    pf_f32x4_t sc[RB][4];
+    f32x4_t sc[RB][4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
-        const uint2 lo = pf_read_tr(&ks[buf][(k_base[0] ^ (16 * mb)) + 2048 * kc]);
-        const uint2 hi = pf_read_tr(&ks[buf][(k_base[1] ^ (16 * mb)) + 2048 * kc]);
+        const uint2 lo = tile::read_tr16(&ks[buf][(k_base[0] ^ (16 * mb)) + 2048 * kc]);
+        const uint2 hi = tile::read_tr16(&ks[buf][(k_base[1] ^ (16 * mb)) + 2048 * kc]);
         const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
-          sc[rb][mb] = pf_mfma(a, qreg[rb][kc],
-                               kc == 0 ? pf_f32x4_t{0.f, 0.f, 0.f, 0.f} : sc[rb][mb]);
+          sc[rb][mb] = tile::mfma_bf16(a, qreg[rb][kc],
+                               kc == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sc[rb][mb]);
       }
     }
     uint4 pk[RB][2];
@@ -304,8 +281,9 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             p[hh][j] = __builtin_amdgcn_exp2f(fmaf(sc[rb][2 * c + hh][j], scale_log2, nm));
-        pk[rb][c] = make_uint4(pf_pack(p[0][0], p[0][1]), pf_pack(p[0][2], p[0][3]),
-                               pf_pack(p[1][0], p[1][1]), pf_pack(p[1][2], p[1][3]));
+        pk[rb][c] = make_uint4(
+            tile::pack_bf16x2(p[0][0], p[0][1]), tile::pack_bf16x2(p[0][2], p[0][3]),
+            tile::pack_bf16x2(p[1][0], p[1][1]), tile::pack_bf16x2(p[1][2], p[1][3]));
       }
     }
     // rescale O and the sums when some row's reference point moved: lane l's accumulator rows
@@ -337,13 +315,13 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
             *reinterpret_cast<const uint2*>(&vs[buf][(vb ^ (32 * c + 16)) + 1024 * nb]);
         const uint4 vop = make_uint4(v0.x, v0.y, v1.x, v1.y);
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) acc[rb][nb] = pf_mfma(pk[rb][c], vop, acc[rb][nb]);
+        for (int rb = 0; rb < RB; ++rb) acc[rb][nb] = tile::mfma_bf16(pk[rb][c], vop, acc[rb][nb]);
       }
     }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) lsum[rb] = pf_mfma(pk[rb][c], ones, lsum[rb]);
+      for (int c = 0; c < 2; ++c) lsum[rb] = tile::mfma_bf16(pk[rb][c], ones, lsum[rb]);
   }
 
   // out = O / sum for rows 4 g4 + j of each block

@@ -126,11 +126,12 @@ def test_append_decode_many_segment_ends_per_wave(dev):
     _check(dev, q, kp, vp, bt, lens_t, kn, vn, 16, oracle_rows=[0, 100, 1023])
 
 
-def test_append_decode_edge_rows(dev):
+@pytest.mark.parametrize("G", [4, 8])
+def test_append_decode_edge_rows(dev, G):
     """Row 0: L = 0 (zeros, no write). Row 1: L = 40 > its table's 32 tokens (clamped to 32, no
     write). Row 2: the new token's page id is outside the pool (no write, that token is no key).
-    Row 3: an ordinary row."""
-    q, kp, vp, _, _, kn, vn = _case(9, [1, 1, 1, 1], 16, 4, 40)
+    Row 3: an ordinary row. G = 4 runs the vector-ALU engine, G = 8 the matrix-core one."""
+    q, kp, vp, _, _, kn, vn = _case(9, [1, 1, 1, 1], 4 * G, 4, 40)
     bt = torch.tensor([[1, 2, -1], [3, 4, -1], [5, 6, 40], [7, 8, 9]], dtype=torch.int32)
     bt_w = bt[:, :2].contiguous()                               # row 1's table holds 32 tokens
     lens = torch.tensor([0, 40, 33, 35], dtype=torch.int32)
