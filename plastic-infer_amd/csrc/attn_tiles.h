@@ -1,6 +1,6 @@
 // Matrix-core building blocks shared by the paged attention kernels (gfx950): the bf16
 // 16x16x32 MFMA, the transposing LDS read, the swizzled [d][64 tokens] K/V tile layout and the
-// bf16 pair pack.
+// bf16 pair pack and masking.
 //
 // Operand layouts of v_mfma_f32_16x16x32_bf16 (lane l, g4 = l / 16, n16 = l % 16):
 //   A (16 x 32): lane l holds A[n16][8 g4 .. 8 g4 + 7]
@@ -51,6 +51,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   const bf16x2_t p = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
   return __builtin_bit_cast(uint32_t, p);
+}
+
+// Zero the bf16 tokens of a dword pair (t, t+1) that lie at or beyond nvalid.
+__device__ __forceinline__ uint32_t mask_pair(uint32_t x, int t, int nvalid) {
+  const uint32_t lo = (t < nvalid) ? 0x0000ffffu : 0u;
+  const uint32_t hi = (t + 1 < nvalid) ? 0xffff0000u : 0u;
+  return x & (lo | hi);
 }
 
 // bf16 1.0 in every element: the B operand of a row sum by the matrix cores.

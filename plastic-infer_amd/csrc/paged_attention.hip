@@ -130,12 +130,7 @@ __device__ __forceinline__ void quad_reduce_scatter(const float (&s)[8][G], floa
   }
 }
 
-// Zero the bf16 tokens of a dword pair (t, t+1) that lie at or beyond nvalid.
-__device__ __forceinline__ uint32_t mask_pair(uint32_t x, int t, int nvalid) {
-  const uint32_t lo = (t < nvalid) ? 0x0000ffffu : 0u;
-  const uint32_t hi = (t + 1 < nvalid) ? 0xffff0000u : 0u;
-  return x & (lo | hi);
-}
+using tile::mask_pair;
 
 constexpr int FD_D = 128;
 constexpr int FD_P = 16;

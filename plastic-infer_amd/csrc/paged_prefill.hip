@@ -182,12 +182,23 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
       v_base[hi] = (n16 * PF_KT + 4 * (g4 & 1)) | (8 * ((g4 >> 1) ^ fv));
     }
   }
-  auto stage = [&](int buf) {
+  // tokens past kv_len on the sequence's last page: their V words are zeroed before they reach
+  // LDS (stale pool memory may hold non-finite values, and p = 0 times inf is not 0)
+  const int tail = kv_len - P * (npages - 1);  // keys on the last page, 1..16
+  auto stage = [&](int buf, int kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = st_base ^ (16 * i);
+      uint4 v = vr[i];
+      if (4 * kt + i == npages - 1 && tail < P) {  // uniform
+        const int nv = tail - 8 * ld_half;
+        v.x = tile::mask_pair(v.x, 0, nv);
+        v.y = tile::mask_pair(v.y, 2, nv);
+        v.z = tile::mask_pair(v.z, 4, nv);
+        v.w = tile::mask_pair(v.w, 6, nv);
+      }
       *reinterpret_cast<uint4*>(&ks[buf][e]) = kr[i];
-      *reinterpret_cast<uint4*>(&vs[buf][e]) = vr[i];
+      *reinterpret_cast<uint4*>(&vs[buf][e]) = v;
     }
   };
   // pages of a tile that hold keys: bit i for page i
@@ -222,7 +233,7 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
   if (nkt > 0) fetch(0);
   for (int kt = 0; kt < nkt; ++kt) {
     const int buf = kt & 1;
-    stage(buf);
+    stage(buf, kt);
     __syncthreads();
     const int pmask = page_mask(kt);
     // a tile every valid row sees whole (interior of the causal triangle, all pages valid)

@@ -255,14 +255,16 @@ def test_decode_empty_and_clamped_lengths(dev):
         assert (out[b].float() - ref[0, 0].float()).abs().max() <= BF16_TOL
 
 
-def test_decode_nonfinite_stale_tokens_are_ignored(dev):
-    """Tokens past L in the last page may hold NaN/Inf (stale memory): output stays finite."""
+@pytest.mark.parametrize("G", [2, 8])
+def test_decode_nonfinite_stale_tokens_are_ignored(dev, G):
+    """Tokens past L in the last page may hold NaN/Inf (stale memory): output stays finite.
+    G = 2 runs the vector-ALU engine, G = 8 the matrix-core one."""
     g = torch.Generator().manual_seed(32)
     kp = torch.randn(4, 1, 128, 16, generator=g).to(torch.bfloat16)
     vp = torch.randn(4, 1, 128, 16, generator=g).to(torch.bfloat16)
     kp[2, :, :, 5:] = float("nan")
     vp[2, :, :, 5:] = float("inf")
-    q = torch.randn(1, 2, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(1, G, 128, generator=g).to(torch.bfloat16)
     bt = torch.tensor([[0, 2]], dtype=torch.int32)
     out = paged_decode_attention(q.to(dev), kp.to(dev), vp.to(dev), bt.to(dev),
                                  torch.tensor([21], dtype=torch.int32, device=dev)).cpu()

@@ -75,6 +75,29 @@ def test_prefill_causal_chunks(dev, G):
         assert err <= BF16_TOL, (b, err)
 
 
+@pytest.mark.parametrize("G", [1, 8])
+def test_prefill_nonfinite_stale_tail_tokens(dev, G):
+    """Slots past kv_len on a sequence's last page hold NaN (K) and Inf (V), as stale pool memory
+    may: they are no keys, so the outputs stay finite and match the oracle, which never reads
+    them. Causal chunks end at kv_len, so the last tile of every row crosses the tail."""
+    Hkv = 2
+    q_rows, kv_lens = [40, 9, 70], [300, 9, 1000]
+    offsets = [kv - n for kv, n in zip(kv_lens, q_rows)]
+    kp, vp, g = _pools(40 + G, 100, Hkv)
+    bt, tables = _tables(kv_lens, 100, g)
+    for t, L in zip(tables, kv_lens):
+        kp[t[-1], :, :, L % P:] = float("nan")
+        vp[t[-1], :, :, L % P:] = float("inf")
+    q = torch.randn(sum(q_rows), Hkv * G, D, generator=g).to(torch.bfloat16)
+    out, cu = _run(dev, q, kp, vp, bt, kv_lens, q_rows, offsets)
+    assert torch.isfinite(out.float()).all()
+    for b in range(3):
+        rows = q[cu[b]:cu[b + 1]][None]
+        ref = OP.paged_attention(rows, kp, vp, tables[b], P, kv_lens[b], causal=True,
+                                 q_start_pos=offsets[b])[0]
+        assert (out[cu[b]:cu[b + 1]].float() - ref.float()).abs().max() <= BF16_TOL, b
+
+
 def test_prefill_no_causal_limit(dev):
     """q_pos_offsets absent: every row attends all kv_len keys (SDPA without a mask)."""
     G, Hkv = 4, 2
