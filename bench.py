@@ -60,6 +60,7 @@ LEN_LO, LEN_HI, SEED = 512, 8192, 2
 MAX_PAGES = LEN_HI // P
 WORKLOAD = "qwen3-8b paged decode: kv scatter + gqa paged attention, 1 layer"
 PMC_FILE = ROOT / "profiles" / "paged_decode_qwen3_8b_b256_pmc.json"
+GQA8_PMC_FILE = ROOT / "profiles" / "paged_decode_gqa8_qwen3_30b_b64_pmc.json"
 
 
 def build_inputs(torch, dev):
@@ -461,6 +462,12 @@ def bench_decode_gqa8(torch, dev, args) -> dict:
     a_gbps = launch_bytes / (at_ms / 1e3) / 1e9
     kernel = ("paged_decode_mfma<8, false> (attention call after a kv_scatter launch)" if separate
               else "paged_decode_mfma<8, true> (one write + attention launch)")
+    traffic = None
+    if not separate and GQA8_PMC_FILE.exists():
+        try:
+            traffic = json.loads(GQA8_PMC_FILE.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
     return _result(
         "KV scatter + paged decode-attn GB/s (GQA 8)", gbps, "GB/s", args, ms, "bf16",
         {"workload": "qwen3-30b-a3b attention layer decode: 64 seqs x 4096 tokens, 32 q / 4 kv "
@@ -472,7 +479,7 @@ def bench_decode_gqa8(torch, dev, args) -> dict:
          "scatter_ms": round(sc_ms, 4) if separate else None,
          "attention_ms": round(at_ms, 4), "wall_s_timed": round(wall, 4)},
         {"kernel": kernel, "bound": "hbm", "achieved": round(a_gbps, 2), "peak": HBM_PEAK_GBPS,
-         "unit": "GB/s", "frac": round(a_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+         "unit": "GB/s", "frac": round(a_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
          "algorithmic_bytes_per_launch": launch_bytes, "avg_launch_ms": round(at_ms, 4)})
 
 
