@@ -341,8 +341,9 @@ int pia_moe_sum_reduce(void* out, const void* in, int64_t num_tokens, int topk, 
  * (fp32); a and w 16-byte aligned; block_m a multiple of 16; a holds ceil(numel / a_div) rows.
  * Small calls (decode: fewer than 2048 routes) and every fp32 call run a split-K kernel over
  * 16-row plan blocks that streams each expert's W once per block; larger bf16 / fp16 calls run
- * an LDS-tiled kernel over the experts present in the plan (128 x 256 tiles). The first GEMM
- * of the FFN is a_div = top_k
+ * an LDS-tiled kernel over the experts present in the plan (tiles of up to 320 routes x 256 W
+ * rows, so that each expert's W is streamed once when it serves up to 320 routes). The first
+ * GEMM of the FFN is a_div = top_k
  * (a = hidden [T, H]) with the activation; the second is a_div = 1 (a = the first GEMM's
  * output [T*k, I]) without it, ldo = H, writing [T, k, H] for pia_moe_sum_reduce.
  * ------------------------------------------------------------------------------------------- */

@@ -242,34 +242,7 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_splitk(
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// moe_gemm_tiled: the many-routes-per-expert case (prefill). A work item is one 128-row tile of
-// an expert's plan rows against one column tile of 256 W rows. Every item of one expert lands
-// on the same XCD (workgroup g runs on XCD g % 8 and the grid is a multiple of 8) and the
-// expert's items are adjacent in that XCD's list, row tiles of one column tile next to each
-// other: the row tiles that share a W tile run side by side, the column tiles that share the
-// expert's A rows run together, and both are fetched from HBM about once and shared through
-// that XCD's L2 (a compact per-XCD work list from moe_plan_segments, so no item is empty).
-// Workgroups of four waves, two per compute unit, so that one workgroup's barrier waits overlap
-// the other's matrix products. Per K step of 32 the operands go from global memory straight
-// into LDS (16-byte direct loads through buffer descriptors, no staging registers), three step
-// buffers deep: the loads of step s + 2 are in flight while step s is multiplied. LDS holds
-// each 16-row x 32 operand fragment as 1 KiB: row r's 64 bytes at 64 r, its 16-byte K chunk c
-// in slot c ^ ((r >> 1) & 3). A direct load's lane l lands at byte 16 l, so lanes 4r .. 4r + 3
-// fetch row r's 64 contiguous bytes (one coalesced access). An MFMA operand read (ds_read_b128,
-// lane: row l % 16, chunk l / 16) in this order has no LDS bank conflicts, as measured with the
-// SQ_LDS_BANK_CONFLICT counter over the candidate chunk orders (with c ^ ((r >> 2) & 3), for
-// one, every read costs 3.8 conflict cycles). Waves in a 2 x 2 arrangement each multiply 64
-// plan rows by 128 W rows (4 x 8 fragments) with v_mfma_f32_16x16x32; a wave whose 64 rows
-// are all past the tile's last route skips its products. With the activation fused, the W
-// tile holds 128 gate and the matching 128 up rows, arranged so that each wave owns gate and
-// up of the same 64 columns.
-// ---------------------------------------------------------------------------------------------
-constexpr int TG_BM = 128, TG_BN = 256, TG_BK = 32;
-constexpr int TG_THREADS = 256;                            // 4 waves, 2 x 2, 64 x 128 each
-constexpr int TG_AF = TG_BM / 16, TG_WF = TG_BN / 16;      // fragments per step: 8 A, 16 W
-constexpr int TG_LOADS = (TG_AF + TG_WF) / 4;              // direct loads per wave per step
-constexpr int TG_STAGE = (TG_AF + TG_WF) * 64;             // uint4 per step buffer (24 KiB)
+// Shared by the prefill kernel below: buffer descriptors, the per-XCD work list, the stage wait.
 constexpr int TG_XCDS = 8;
 // Buffer resources: word 3 of a raw (stride 0) buffer descriptor on gfx9 parts; a load whose
 // offset is at or past the descriptor's byte count returns zeros (a direct load writes zeros
@@ -277,22 +250,22 @@ constexpr int TG_XCDS = 8;
 // is such an offset for every buffer here (the host keeps A and each expert's W below 2 GiB).
 constexpr int TG_RSRC_WORD3 = 0x00020000;
 constexpr uint32_t TG_OOB = 0x80000000u;
-#ifndef PIA_EG_TILED_MIN_ROUTES
-#define PIA_EG_TILED_MIN_ROUTES 2048  // routes per call from which the tiled kernel is used
+#ifndef PIA_EG_WIDE_MIN_ROUTES
+#define PIA_EG_WIDE_MIN_ROUTES 2048  // routes per call from which moe_gemm_wide is used
 #endif
 
-// Work list of moe_gemm_tiled from a plan (expert_ids of the used blocks ascend):
+// Work list of moe_gemm_wide from a plan (expert_ids of the used blocks ascend):
 //   seg_block[s]   first plan block of the s-th expert present, seg_block[n_seg] = used blocks
 //   seg_count[0]   n_seg
 //   seg_xstart[s]  items of the segments before s on s's XCD lane (segments s' = s mod 8)
 //   xcd_items[x]   items on XCD lane x
-// where a segment has ceil(rows / 128) row tiles times n_tiles column tiles of items.
+// where a segment has ceil(rows / bm) row tiles times n_tiles column tiles of items.
 // One 1024-thread block: a compaction over the plan blocks, then waves 0..7 scan lanes 0..7.
 __global__ __launch_bounds__(1024) void moe_plan_segments(
     int32_t* __restrict__ seg_block, int32_t* __restrict__ seg_count,
     int32_t* __restrict__ seg_xstart, int32_t* __restrict__ xcd_items,
     const int32_t* __restrict__ expert_ids, const int32_t* __restrict__ npp, int block_m,
-    int64_t max_rows, int n_tiles) {
+    int64_t max_rows, int n_tiles, int bm) {
   __shared__ int32_t wsum[16];
   __shared__ int32_t base_lds;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -330,7 +303,7 @@ __global__ __launch_bounds__(1024) void moe_plan_segments(
       int items = 0;
       if (sg < n_seg) {
         const int64_t rows = int64_t(seg_block[sg + 1] - seg_block[sg]) * block_m;
-        items = int((rows + TG_BM - 1) / TG_BM) * n_tiles;
+        items = int((rows + bm - 1) / bm) * n_tiles;
       }
       int incl = items;
 #pragma unroll
@@ -362,8 +335,34 @@ __device__ __forceinline__ void tg_sync() {
   asm volatile("" ::: "memory");
 }
 
+// ---------------------------------------------------------------------------------------------
+// moe_gemm_wide: the many-routes-per-expert case (prefill), one work item per (expert, column
+// tile of 256 W rows) that holds all of the expert's plan rows up to TW_BM (an expert with more
+// gets further row tiles). Every W byte is then streamed from HBM by exactly one workgroup,
+// whatever the timing of the others; the expert's A rows are shared by its column tiles, which
+// are adjacent in their XCD's work list and, having identical work, run side by side through
+// that XCD's L2. One 8-wave workgroup per compute unit, waves 4 (rows) x 2 (columns), each
+// multiplying 16 TW_RF plan rows by 128 W rows (TW_RF x 8 fragments of v_mfma_f32_16x16x32,
+// 16 TW_RF accumulators per fragment column) - two waves per SIMD, so one wave's LDS reads and
+// barrier overlap the other's products.
+// K advances in stages of 64: each operand row contributes one whole 128-byte line per stage,
+// fetched by a 16-byte direct load (global -> LDS through a buffer descriptor, no staging
+// registers) whose eight lanes 8 r .. 8 r + 7 cover row r's line. Two stage buffers: the loads
+// of stage s + 1 are in flight while stage s is multiplied. LDS holds each operand as 16-row x
+// 64 K fragments of 2 KiB: row r's 128 bytes at 128 r, its 16-byte K chunk c in slot c ^ (r % 8).
+// A direct load of 8 rows lands lane l at byte 16 l, so lane l fetches chunk (l % 8) ^ (l / 8)
+// of row l / 8. An MFMA operand read (ds_read_b128; lane: row l % 16, chunk 4 h + l / 16 of
+// sub-step h) then touches eight different 16-byte bank groups in every eight lanes.
+// ---------------------------------------------------------------------------------------------
+constexpr int TW_RF = 5;                               // 16-row A fragments per wave
+constexpr int TW_BM = 4 * 16 * TW_RF, TW_BN = 256, TW_BK = 64;
+constexpr int TW_THREADS = 512;                        // 8 waves: 4 (rows) x 2 (columns)
+constexpr int TW_AH = TW_BM / 8, TW_WH = TW_BN / 8;    // 8-row half fragments per stage: A, W
+constexpr int TW_AL = TW_AH / 8, TW_WL = TW_WH / 8;    // direct loads per wave per stage: A, W
+constexpr int TW_STAGE = (TW_AH + TW_WH) * 64;         // uint4 per stage buffer
+
 template <int DT, int ACT>
-__global__ __launch_bounds__(TG_THREADS, 2) void moe_gemm_tiled(
+__global__ __launch_bounds__(TW_THREADS, 1) void moe_gemm_wide(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ a, const uint16_t* __restrict__ w,
     const float* __restrict__ topk_w, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ expert_ids, const int32_t* __restrict__ seg_block,
@@ -371,36 +370,27 @@ __global__ __launch_bounds__(TG_THREADS, 2) void moe_gemm_tiled(
     const int32_t* __restrict__ xcd_items, int64_t numel, int block_m, int a_div, int64_t lda,
     int num_experts, int n_rows, int K, int64_t ldo, int n_tiles, int mulw, uint32_t a_bytes) {
   constexpr bool FUSED = ACT != PIA_ACT_NONE;
-  // three step buffers as separate arrays: the compiler tracks the direct loads into each one
-  // apart, so a read of one buffer does not wait for the loads still landing in the others
-  __shared__ __attribute__((aligned(16))) uint4 st0[TG_STAGE];
-  __shared__ __attribute__((aligned(16))) uint4 st1[TG_STAGE];
-  __shared__ __attribute__((aligned(16))) uint4 st2[TG_STAGE];
-  __shared__ int32_t tile_route[TG_BM];
-  __shared__ float tile_w[TG_BM];
+  // two stage buffers as separate arrays (the compiler tracks the direct loads into each apart)
+  __shared__ __attribute__((aligned(16))) uint4 sb0[TW_STAGE];
+  __shared__ __attribute__((aligned(16))) uint4 sb1[TW_STAGE];
+  __shared__ int32_t tile_route[TW_BM];
+  __shared__ float tile_w[TW_BM];
   const int tid = threadIdx.x, lane = tid & 63;
-  // wave index as a scalar, so that per-wave decisions compile to scalar branches and the LDS
-  // bases of the direct loads are wave-uniform
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: wave-uniform LDS bases
   const int wm = wv >> 1, wn = wv & 1;
   const int li = lane & 15, kg = lane >> 4;
-  // direct loads: lane -> row lr of a fragment, K chunk kc; operand reads: lane -> LDS slot
-  const int lr = lane >> 2, kc = (lane & 3) ^ ((lr >> 1) & 3);
-  const int rslot = 4 * li + (kg ^ ((li >> 1) & 3));
+  const int lr = lane >> 3, lc = (lane & 7) ^ (lane >> 3);  // direct loads: row, K chunk
   const int n_seg = seg_count[0];
   const int half = n_rows >> 1;
-  const int nks = (K + TG_BK - 1) / TG_BK;
+  const int nks = (K + TW_BK - 1) / TW_BK;
   const __amdgpu_buffer_rsrc_t ares =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a), 0, int(a_bytes), TG_RSRC_WORD3);
-  // this workgroup's XCD lane (workgroups are dealt to XCDs round robin; the grid is a
-  // multiple of 8) and its segments x, x + 8, ...
   const int x = blockIdx.x % TG_XCDS;
   const int nx = (n_seg - x + TG_XCDS - 1) / TG_XCDS;
   const int total = xcd_items[x];
 
   for (int p = blockIdx.x / TG_XCDS; p < total; p += gridDim.x / TG_XCDS) {
-    // segment of item p: the last of this lane's segments starting at or before p
-    int lo = 0, hi = nx - 1;
+    int lo = 0, hi = nx - 1;  // segment of item p: the last of this lane's starting at or before p
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (seg_xstart[x + TG_XCDS * mid] <= p) lo = mid;
@@ -409,40 +399,39 @@ __global__ __launch_bounds__(TG_THREADS, 2) void moe_gemm_tiled(
     const int sg = x + TG_XCDS * lo;
     const int b0 = seg_block[sg], b1 = seg_block[sg + 1];
     const int64_t seg0 = int64_t(b0) * block_m, seg1 = int64_t(b1) * block_m;
-    const int mts = int((seg1 - seg0 + TG_BM - 1) / TG_BM);
+    const int mts = int((seg1 - seg0 + TW_BM - 1) / TW_BM);
     const int local = p - seg_xstart[sg];
-    const int t = local / mts, mt = local - t * mts;  // row tiles of one column tile adjacent
+    const int t = local / mts, mt = local - t * mts;
     const int e = expert_ids[b0];
     const bool e_ok = e >= 0 && e < num_experts;  // else zero rows, as in moe_gemm_splitk
-    const int64_t m0 = seg0 + int64_t(mt) * TG_BM;
+    const int64_t m0 = seg0 + int64_t(mt) * TW_BM;
 
-    // W fragments 4 wv .. 4 wv + 3 of a step are this wave's to load; this lane's W row of
-    // each as a byte offset into the expert's W (rows past the tile's end: out of range)
+    // this wave's W half fragments TW_WL wv + q: tile W rows 8 (TW_WL wv + q) + lr
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(w + (e_ok ? int64_t(e) * n_rows * K : 0)), 0,
         e_ok ? n_rows * K * 2 : 0, TG_RSRC_WORD3);
-    uint32_t woff[4];
+    uint32_t woff[TW_WL];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int g = 4 * wv + q;  // W fragment: wave column g / 8 owns it, as its fragment g % 8
+    for (int q = 0; q < TW_WL; ++q) {
+      const int j = 8 * (TW_WL * wv + q) + lr;  // W row of the tile; wave column j / 128 owns it
       int n;
       bool ok;
       if constexpr (FUSED) {
         // fragments 0..3 of a wave column are gate rows, 4..7 the matching up rows
-        const int jj = g & 7;
-        const int col = t * (TG_BN / 2) + (g >> 3) * 64 + (jj & 3) * 16 + lr;
+        const int jj = (j & 127) >> 4;
+        const int col = t * (TW_BN / 2) + (j >> 7) * 64 + (jj & 3) * 16 + (j & 15);
         ok = col < half;
         n = (jj < 4 ? 0 : half) + col;
       } else {
-        n = t * TG_BN + g * 16 + lr;
+        n = t * TW_BN + j;
         ok = n < n_rows;
       }
-      woff[q] = ok ? uint32_t(n) * uint32_t(K) * 2u + uint32_t(kc) * 16u : TG_OOB;
+      woff[q] = ok ? uint32_t(n) * uint32_t(K) * 2u + uint32_t(lc) * 16u : TG_OOB;
     }
 
-    __syncthreads();  // the previous tile's epilogue is done with tile_route / tile_w
+    __syncthreads();  // the previous item's products and epilogue are done
     bool live = false;
-    if (tid < TG_BM) {
+    if (tid < TW_BM) {
       const int64_t pr = m0 + tid;
       const int64_t rr = pr < seg1 ? int64_t(sorted[pr]) : numel;
       live = rr >= 0 && rr < numel;
@@ -451,73 +440,73 @@ __global__ __launch_bounds__(TG_THREADS, 2) void moe_gemm_tiled(
     }
     // real routes come first in an expert's plan rows, so the live rows are a prefix
     const int nlive = __builtin_amdgcn_readfirstlane(__syncthreads_count(live));
-    // A fragments 2 wv, 2 wv + 1 of a step are this wave's to load
-    uint32_t aoff[2];
+    uint32_t aoff[TW_AL];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int32_t rr = tile_route[(2 * wv + q) * 16 + lr];
-      aoff[q] = rr >= 0 ? uint32_t(rr / a_div) * uint32_t(lda) * 2u + uint32_t(kc) * 16u : TG_OOB;
+    for (int q = 0; q < TW_AL; ++q) {
+      const int32_t rr = tile_route[8 * (TW_AL * wv + q) + lr];
+      aoff[q] = rr >= 0 ? uint32_t(rr / a_div) * uint32_t(lda) * 2u + uint32_t(lc) * 16u : TG_OOB;
     }
-    // direct loads of step s into buffer buf: K offset in the scalar offset; on a last step
-    // shorter than 32 the lanes past K, and on the two steps past the last every lane, read
-    // out of range (zeros, no memory access), so every step issues the same six loads
+    // direct loads of stage s into buf (stages past the last read out of range: zeros, no
+    // memory access), K offset in the scalar offset
     auto issue = [&](uint4* buf, int s) __attribute__((always_inline)) {
-      const int k0 = min(s, nks) * TG_BK;
-      const bool kin = k0 + 8 * kc < K;
+      const int k0 = min(s, nks) * TW_BK;
+      const bool kin = k0 + 8 * lc < K;
 #pragma unroll
-      for (int q = 0; q < 2; ++q)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (tg_lds_t*)(buf + (2 * wv + q) * 64), 16,
-                                                 kin ? aoff[q] : TG_OOB, k0 * 2, 0, 0);
+      for (int q = 0; q < TW_AL; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, (tg_lds_t*)(buf + (TW_AL * wv + q) * 64),
+                                                 16, kin ? aoff[q] : TG_OOB, k0 * 2, 0, 0);
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (tg_lds_t*)(buf + (TG_AF + 4 * wv + q) * 64),
-                                                 16, kin ? woff[q] : TG_OOB, k0 * 2, 0, 0);
+      for (int q = 0; q < TW_WL; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            wres, (tg_lds_t*)(buf + (TW_AH + TW_WL * wv + q) * 64), 16,
+            kin ? woff[q] : TG_OOB, k0 * 2, 0, 0);
     };
-    f32x4_t acc[4][8];
+    f32x4_t acc[TW_RF][8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TW_RF; ++i)
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) acc[i][jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const bool wave_live = wm * 64 < nlive;
+    const bool wave_live = wm * 16 * TW_RF < nlive;
+    // operand slots: row li of a fragment, chunk 4 h + kg of sub-step h
+    const int rs0 = 8 * li + ((0 + kg) ^ (li & 7)), rs1 = 8 * li + ((4 + kg) ^ (li & 7));
     auto comp = [&](const uint4* buf) __attribute__((always_inline)) {
-      uint4 fa[4], fb[8];
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) fb[jj] = buf[(TG_AF + wn * 8 + jj) * 64 + rslot];
+      for (int h = 0; h < 2; ++h) {
+        const int rs = h ? rs1 : rs0;
+        uint4 fa[TW_RF], fb[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fa[i] = buf[(wm * 4 + i) * 64 + rslot];
+        for (int jj = 0; jj < 8; ++jj) fb[jj] = buf[(TW_AH + 2 * (wn * 8 + jj)) * 64 + rs];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < TW_RF; ++i) fa[i] = buf[2 * (wm * TW_RF + i) * 64 + rs];
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) acc[i][jj] = mfma_16x16x32<DT>(fa[i], fb[jj], acc[i][jj]);
+        for (int i = 0; i < TW_RF; ++i)
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj)
+            acc[i][jj] = mfma_16x16x32<DT>(fa[i], fb[jj], acc[i][jj]);
+      }
     };
 
-    // steps s, s + 1, s + 2 in buffers st0, st1, st2; at the wait before step s the loads of
-    // steps s and s + 1 are outstanding, so vmcnt(TG_LOADS) leaves only step s + 1's. The
-    // loads issued for the two steps past the last land zeros in buffers nothing reads; the
-    // next tile's first barrier (with its fence) waits for them.
-    issue(st0, 0);
-    issue(st1, 1);
-    for (int s = 0; s < nks; s += 3) {
-      tg_sync<TG_LOADS>();
-      issue(st2, s + 2);
-      if (wave_live) comp(st0);
+    // stage s in buffer s % 2: before it is multiplied, this wave's loads of it have completed
+    // (the only ones outstanding) and every wave has finished reading the other buffer, which
+    // the loads of stage s + 1 then refill
+    issue(sb0, 0);
+    for (int s = 0; s < nks; s += 2) {
+      tg_sync<0>();
+      issue(sb1, s + 1);
+      if (wave_live) comp(sb0);
       if (s + 1 >= nks) break;
-      tg_sync<TG_LOADS>();
-      issue(st0, s + 3);
-      if (wave_live) comp(st1);
-      if (s + 2 >= nks) break;
-      tg_sync<TG_LOADS>();
-      issue(st1, s + 4);
-      if (wave_live) comp(st2);
+      tg_sync<0>();
+      issue(sb0, s + 2);
+      if (wave_live) comp(sb1);
     }
 
     // epilogue: lane holds column li of each 16-column fragment, rows 4 kg + q
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (wm * 64 + i * 16 >= nlive) continue;
+    for (int i = 0; i < TW_RF; ++i) {
+      if (wm * 16 * TW_RF + i * 16 >= nlive) continue;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int row = wm * 64 + i * 16 + kg * 4 + q;
+        const int row = wm * 16 * TW_RF + i * 16 + kg * 4 + q;
         const int32_t rr = tile_route[row];
         if (rr < 0) continue;
         const float wr = tile_w[row];
@@ -525,7 +514,7 @@ __global__ __launch_bounds__(TG_THREADS, 2) void moe_gemm_tiled(
         if constexpr (FUSED) {
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
-            const int col = t * (TG_BN / 2) + wn * 64 + jj * 16 + li;
+            const int col = t * (TW_BN / 2) + wn * 64 + jj * 16 + li;
             if (col < half) {
               const float gr = from_dt<DT>(to_dt<DT>(acc[i][jj][q] * wr));
               const float ur = from_dt<DT>(to_dt<DT>(acc[i][jj + 4][q] * wr));
@@ -535,7 +524,7 @@ __global__ __launch_bounds__(TG_THREADS, 2) void moe_gemm_tiled(
         } else {
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) {
-            const int col = t * TG_BN + wn * 128 + jj * 16 + li;
+            const int col = t * TW_BN + wn * 128 + jj * 16 + li;
             if (col < n_rows) orow[col] = to_dt<DT>(acc[i][jj][q] * wr);
           }
         }
@@ -634,45 +623,43 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
   // bytes of A the plan can reach: rows ceil(numel / a_div), the last one k_dim long
   const int64_t a_bytes = ((ceil_div(numel, a_div) - 1) * lda + k_dim) * elt;
   const int64_t w_bytes = int64_t(n_rows) * k_dim * elt;
-  // the LDS-tiled kernel is built for 16-bit storage; fp32 runs the split-K kernel at every size
-  if (!f32 && numel >= PIA_EG_TILED_MIN_ROUTES && a_bytes < (int64_t(1) << 31) &&
+  // the wide kernel is built for 16-bit storage; fp32 runs the split-K kernel at every size
+  if (!f32 && numel >= PIA_EG_WIDE_MIN_ROUTES && a_bytes < (int64_t(1) << 31) &&
       w_bytes < (int64_t(1) << 31)) {
     const int64_t max_blocks = ceil_div(max_num_tokens_padded, block_m);
     int32_t* seg_block = reinterpret_cast<int32_t*>(workspace);  // [max_blocks + 1]
     int32_t* seg_count = seg_block + max_blocks + 1;                // [1]
     int32_t* seg_xstart = seg_count + 1;                             // [max_blocks]
     int32_t* xcd_items = seg_xstart + max_blocks;                   // [8]
-    const int n_tiles = int(ceil_div(out_cols, fused ? TG_BN / 2 : TG_BN));
+    const int n_tiles = int(ceil_div(out_cols, fused ? TW_BN / 2 : TW_BN));
     hipLaunchKernelGGL(moe_plan_segments, dim3(1), dim3(1024), 0, s, seg_block, seg_count,
                        seg_xstart, xcd_items, expert_ids, num_tokens_post_pad, block_m,
-                       max_num_tokens_padded, n_tiles);
+                       max_num_tokens_padded, n_tiles, TW_BM);
     if (int rc = check_launch("moe_plan_segments")) return rc;
-    // items: at most (used blocks * block_m / 128 + experts present) row tiles per column tile
     const int64_t max_seg = std::min<int64_t>(max_blocks, int64_t(num_experts) + 1);
-    const int64_t ub = (ceil_div(max_num_tokens_padded, TG_BM) + max_seg) * n_tiles;
-    const int64_t g = std::min<int64_t>(ub, 2 * int64_t(cus));  // two workgroups per CU
+    const int64_t ub = (ceil_div(max_num_tokens_padded, TW_BM) + max_seg) * n_tiles;
+    const int64_t g = std::min<int64_t>(ub, int64_t(cus));  // one workgroup per CU
     const unsigned grid = unsigned(std::max<int64_t>(TG_XCDS, g / TG_XCDS * TG_XCDS));
-#define PIA_TG(DT, ACT)                                                                        \
-  hipLaunchKernelGGL((moe_gemm_tiled<DT, ACT>), dim3(grid), dim3(TG_THREADS), 0, s, o, aa, ww, \
+#define PIA_TW(DT, ACT)                                                                        \
+  hipLaunchKernelGGL((moe_gemm_wide<DT, ACT>), dim3(grid), dim3(TW_THREADS), 0, s, o, aa, ww,  \
                      topk_weights, sorted_token_ids, expert_ids, seg_block, seg_count,         \
-                     seg_xstart, xcd_items, numel,                                             \
-                     block_m, a_div, lda, num_experts, n_rows, k_dim, ldo, n_tiles, mulw,      \
-                     uint32_t(a_bytes))
-#define PIA_TG_ACT(DT)                                                                         \
+                     seg_xstart, xcd_items, numel, block_m, a_div, lda, num_experts, n_rows,   \
+                     k_dim, ldo, n_tiles, mulw, uint32_t(a_bytes))
+#define PIA_TW_ACT(DT)                                                                         \
   switch (activation) {                                                                        \
-    case PIA_ACT_NONE: PIA_TG(DT, PIA_ACT_NONE); break;                                        \
-    case PIA_ACT_SILU: PIA_TG(DT, PIA_ACT_SILU); break;                                        \
-    case PIA_ACT_GELU: PIA_TG(DT, PIA_ACT_GELU); break;                                        \
-    default: PIA_TG(DT, PIA_ACT_GELU_TANH); break;                                             \
+    case PIA_ACT_NONE: PIA_TW(DT, PIA_ACT_NONE); break;                                        \
+    case PIA_ACT_SILU: PIA_TW(DT, PIA_ACT_SILU); break;                                        \
+    case PIA_ACT_GELU: PIA_TW(DT, PIA_ACT_GELU); break;                                        \
+    default: PIA_TW(DT, PIA_ACT_GELU_TANH); break;                                             \
   }
     if (dtype == PIA_DTYPE_BF16) {
-      PIA_TG_ACT(PIA_DTYPE_BF16)
+      PIA_TW_ACT(PIA_DTYPE_BF16)
     } else {
-      PIA_TG_ACT(PIA_DTYPE_F16)
+      PIA_TW_ACT(PIA_DTYPE_F16)
     }
-#undef PIA_TG_ACT
-#undef PIA_TG
-    return check_launch("moe_gemm_tiled");
+#undef PIA_TW_ACT
+#undef PIA_TW
+    return check_launch("moe_gemm_wide");
   }
   const int n_tiles = int(ceil_div(out_cols, fused ? 32 : 64));
   const int64_t ub = ceil_div(max_num_tokens_padded, EG_ROWS) * n_tiles;

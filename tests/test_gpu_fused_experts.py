@@ -86,10 +86,12 @@ def test_act_and_mul(dev, activation, dtype, rows, d):
     (0, 64, 2048, 768, 128, 8, torch.bfloat16, "silu", False),   # Qwen3-30B-A3B decode layer
     (1, 5, 200, 40, 7, 3, torch.float16, "gelu", True),          # K, N tails; weight on input
     (2, 100, 128, 64, 4, 2, torch.bfloat16, "gelu_tanh", False), # ~50 routes per expert
-    # from 4096 routes per call the LDS-tiled kernel runs
+    # from 2048 routes per call the LDS-tiled kernel runs (up to 320 routes per expert in one tile)
     (10, 1024, 512, 256, 8, 4, torch.bfloat16, "silu", False),   # 512 routes per expert
     (11, 700, 200, 40, 7, 6, torch.float16, "gelu", True),       # K tail, column tail
     (12, 512, 2048, 768, 128, 8, torch.bfloat16, "silu", False), # Qwen3-30B-A3B prefill chunk
+    (13, 2400, 256, 128, 64, 8, torch.bfloat16, "silu", False),  # ~300 routes per expert
+    (14, 2100, 136, 72, 3, 2, torch.float16, "gelu", True),      # ~1400 per expert: 5 row tiles
     # fp32 storage (split-K kernel at every size; K a multiple of 4 suffices)
     (20, 64, 2048, 768, 128, 8, torch.float32, "silu", False),
     (21, 5, 100, 36, 7, 3, torch.float32, "gelu", True),         # K = 100 and 36: not / 8
