@@ -153,8 +153,10 @@ __global__ __launch_bounds__(64) void kv_scatter16_kernel(
   constexpr int P = T16_P, PITCH = D + 8, CH = D / 8, MAXT = 32;
   __shared__ __align__(16) uint16_t tile[MAXT * PITCH];
   const int lane = threadIdx.x;
-  const int64_t i0 = int64_t(blockIdx.x) * P;
-  const int h = blockIdx.y;
+  // workgroup w: kv head w % H of input group w / H, so the H waves of a group run together
+  // and read each token's contiguous [H][D] row at once
+  const int h = int(blockIdx.x % unsigned(H));
+  const int64_t i0 = int64_t(blockIdx.x / unsigned(H)) * P;
   // lane j < 33 looks at token i0 - 1 + j
   const int64_t tj = i0 - 1 + lane;
   long long s = -1;
@@ -301,7 +303,9 @@ __global__ __launch_bounds__(64) void kv_gather16_kernel(
   constexpr int P = T16_P, PITCH = 24, CH = D / 8;
   __shared__ __align__(16) uint16_t tile[D * PITCH];
   const int lane = threadIdx.x;
-  const int lp = blockIdx.x, b = blockIdx.y, h = blockIdx.z;
+  // x = kv head + H * sequence page: the H waves of one page run together
+  const int h = int(blockIdx.x % unsigned(H)), lp = int(blockIdx.x / unsigned(H));
+  const int b = blockIdx.y;
   const int64_t row0 = cu[b];
   const int64_t len = cu[b + 1] - row0;
   if (int64_t(lp) * P >= len || lp >= bt_stride) return;
@@ -445,7 +449,8 @@ extern "C" int pia_kv_scatter(const void* k, const void* v, void* k_pages, void*
 #undef PIA_SCR
       return check_launch("kv_scatter");
     }
-    dim3 grid = dim3(unsigned(blocks), unsigned(num_kv_heads));
+    if (blocks * num_kv_heads > 0x7fffffff) return fail(PIA_EINVAL, "kv_scatter: too many tokens");
+    dim3 grid = dim3(unsigned(blocks * num_kv_heads));
 #define PIA_SC16(DD)                                                                           \
   hipLaunchKernelGGL(kv_scatter16_kernel<DD>, grid, dim3(64), 0, s, (const uint16_t*)k,        \
                      (const uint16_t*)v, (uint16_t*)k_pages, (uint16_t*)v_pages, slot_mapping, \
@@ -493,7 +498,8 @@ extern "C" int pia_kv_gather(void* k_out, void* v_out, const void* k_pages, cons
       (head_dim == 64 || head_dim == 128 || head_dim == 256) && aligned(k_pages, 16) &&
       aligned(v_pages, 16) && aligned(k_out, 16) && aligned(v_out, 16) &&
       num_kv_heads <= 65535) {
-    dim3 grid16 = dim3(unsigned(pages), unsigned(num_seqs), unsigned(num_kv_heads));
+    if (pages * num_kv_heads > 0x7fffffff) return fail(PIA_EINVAL, "kv_gather: too many pages");
+    dim3 grid16 = dim3(unsigned(pages * num_kv_heads), unsigned(num_seqs));
 #define PIA_GA16(DD)                                                                           \
   hipLaunchKernelGGL(kv_gather16_kernel<DD>, grid16, dim3(64), 0, s, (uint16_t*)k_out,         \
                      (uint16_t*)v_out, (const uint16_t*)k_pages, (const uint16_t*)v_pages,     \
