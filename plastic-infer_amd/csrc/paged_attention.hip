@@ -1020,11 +1020,12 @@ __global__ __launch_bounds__(64, 1) void paged_decode_mfma(
   const uint4 ones = tile::bf16_ones();
   uint4 qreg[4];
 
+  // d chunk outermost: consecutive products of one accumulator are four MFMAs apart
   auto qk_tile = [&](f32x4_t (&sc)[4]) {
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
+      for (int mb = 0; mb < 4; ++mb) {
         const uint2 lo = tile::read_tr16(&ks[(k_base[0] ^ (16 * mb)) + 2048 * kc]);
         const uint2 hi = tile::read_tr16(&ks[(k_base[1] ^ (16 * mb)) + 2048 * kc]);
         sc[mb] = tile::mfma_bf16(make_uint4(lo.x, lo.y, hi.x, hi.y), qreg[kc],
@@ -1094,12 +1095,12 @@ __global__ __launch_bounds__(64, 1) void paged_decode_mfma(
         }
       }
   };
+  // chunk outermost: consecutive products of one accumulator are eight MFMAs apart
   auto pv_tile = [&](const uint4 (&vr)[16], const uint4 (&pk)[2]) {
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      acc[nb] = tile::mfma_bf16(pk[0], vr[nb], acc[nb]);
-      acc[nb] = tile::mfma_bf16(pk[1], vr[8 + nb], acc[nb]);
-    }
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int nb = 0; nb < 8; ++nb) acc[nb] = tile::mfma_bf16(pk[c], vr[8 * c + nb], acc[nb]);
   };
 
   int gs = start;

@@ -241,19 +241,21 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
     if (kt + 1 < nkt) fetch(kt + 1);
 
     // S^T for the wave's rows: 4 token blocks (one per page) x 4 d chunks, each K operand
-    // serving both row blocks
+    // serving both row blocks; d chunk outermost, so consecutive products of one accumulator
+    // are 4 RB MFMAs apart (a product that reads the result of the one just issued waits for
+    // it to drain)
     f32x4_t sc[RB][4];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int kc = 0; kc < 4; ++kc) {
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
+      for (int mb = 0; mb < 4; ++mb) {
         const uint2 lo = tile::read_tr16(&ks[buf][(k_base[0] ^ (16 * mb)) + 2048 * kc]);
         const uint2 hi = tile::read_tr16(&ks[buf][(k_base[1] ^ (16 * mb)) + 2048 * kc]);
         const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
           sc[rb][mb] = tile::mfma_bf16(a, qreg[rb][kc],
-                               kc == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sc[rb][mb]);
+                                       kc == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sc[rb][mb]);
       }
     }
     uint4 pk[RB][2];
@@ -314,12 +316,13 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
       }
     }
     // O += P . V over the tile's two 32-token chunks, each V operand serving both row blocks;
-    // the sums against a column of ones
+    // the sums against a column of ones. Chunk outermost: consecutive products of one
+    // accumulator are 8 RB + RB MFMAs apart.
 #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) {
-      const int vb = v_base[nb & 1];
+    for (int c = 0; c < 2; ++c) {
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
+      for (int nb = 0; nb < 8; ++nb) {
+        const int vb = v_base[nb & 1];
         const uint2 v0 =
             *reinterpret_cast<const uint2*>(&vs[buf][(vb ^ (32 * c)) + 1024 * nb]);
         const uint2 v1 =
@@ -328,11 +331,9 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) acc[rb][nb] = tile::mfma_bf16(pk[rb][c], vop, acc[rb][nb]);
       }
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) lsum[rb] = tile::mfma_bf16(pk[rb][c], ones, lsum[rb]);
     }
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) lsum[rb] = tile::mfma_bf16(pk[rb][c], ones, lsum[rb]);
   }
 
   // out = O / sum for rows 4 g4 + j of each block
