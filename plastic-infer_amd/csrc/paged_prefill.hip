@@ -149,11 +149,17 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
   const int ld_d = tid >> 1, ld_half = tid & 1;
   const int ld_off = ld_d * P + ld_half * 8;  // the thread's piece inside a (page, head) tile
   uint4 kr[4], vr[4];
-  auto fetch = [&](int kt) {
+  // block-table ids of a tile: lane i < 4 holds page 4 kt + i's id (-1 past the table). They
+  // are loaded a tile ahead of the fetch that uses them, with one vector load, so no tile
+  // waits on a chain of dependent block-table reads.
+  auto bt_of = [&](int kt) -> int {
+    const int pi = 4 * kt + lane;
+    return (lane < 4 && pi < npages) ? btb[pi] : -1;
+  };
+  auto fetch = [&](int bt4) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int pi = 4 * kt + i;
-      const int id = __builtin_amdgcn_readfirstlane(pi < npages ? btb[pi] : -1);
+      const int id = __builtin_amdgcn_readlane(bt4, i);
       if (id >= 0 && int64_t(id) < num_pages) {  // uniform: one scalar base per page
         const int64_t tile_off = (int64_t(id) * Hkv + h) * TILE;
         kr[i] = *reinterpret_cast<const uint4*>(kpool + tile_off + ld_off);
@@ -202,12 +208,11 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
     }
   };
   // pages of a tile that hold keys: bit i for page i
-  auto page_mask = [&](int kt) {
+  auto page_mask = [&](int bt4) {
     int mk = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int pi = 4 * kt + i;
-      const int id = pi < npages ? btb[pi] : -1;
+      const int id = __builtin_amdgcn_readlane(bt4, i);
       mk |= (id >= 0 && int64_t(id) < num_pages) ? (1 << i) : 0;
     }
     return mk;
@@ -230,15 +235,17 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
   }
   const uint4 ones = tile::bf16_ones();
 
-  if (nkt > 0) fetch(0);
+  int bt_cur = bt_of(0), bt_nxt = bt_of(1);
+  if (nkt > 0) fetch(bt_cur);
   for (int kt = 0; kt < nkt; ++kt) {
     const int buf = kt & 1;
     stage(buf, kt);
     __syncthreads();
-    const int pmask = page_mask(kt);
+    const int pmask = page_mask(bt_cur);
     // a tile every valid row sees whole (interior of the causal triangle, all pages valid)
     const bool full = pmask == 0xF && (kt + 1) * PF_KT <= lim_min;
-    if (kt + 1 < nkt) fetch(kt + 1);
+    const int bt_far = bt_of(kt + 2);
+    if (kt + 1 < nkt) fetch(bt_nxt);
 
     // S^T for the wave's rows: 4 token blocks (one per page) x 4 d chunks, each K operand
     // serving both row blocks; d chunk outermost, so consecutive products of one accumulator
@@ -334,6 +341,8 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) lsum[rb] = tile::mfma_bf16(pk[rb][c], ones, lsum[rb]);
     }
+    bt_cur = bt_nxt;
+    bt_nxt = bt_far;
   }
 
   // out = O / sum for rows 4 g4 + j of each block
