@@ -60,6 +60,19 @@ __device__ __forceinline__ uint32_t mask_pair(uint32_t x, int t, int nvalid) {
   return x & (lo | hi);
 }
 
+// Max over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lanes that hold one column of an MFMA
+// output) by two lane swaps on the vector ALU, without the LDS crossbar of a shuffle. Called
+// with both operands equal, v_permlane16_swap returns (x[l & ~16], x[l | 16]) and
+// v_permlane32_swap (x[l & 31], x[l | 32]) (measured on gfx950).
+__device__ __forceinline__ float max_col4(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned w = __float_as_uint(m);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // bf16 1.0 in every element: the B operand of a row sum by the matrix cores.
 __device__ __forceinline__ uint4 bf16_ones() {
   return make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);

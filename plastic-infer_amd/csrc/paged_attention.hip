@@ -1200,9 +1200,8 @@ __global__ __launch_bounds__(64, 1) void paged_decode_mfma(
     qk_tile(sB);
 
     // softmax: row max over the step (lanes l, l ^ 16, l ^ 32, l ^ 48 hold one row)
-    float mx = fmaxf(prep(sA, 0, masked, valid, bad), prep(sB, 1, masked, valid, bad));
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float mx = tile::max_col4(
+        fmaxf(prep(sA, 0, masked, valid, bad), prep(sB, 1, masked, valid, bad)));
     const float mref = (mx - m > SD_RESCALE) ? mx : m;
     const float alpha = m == mref ? 1.f : fast_exp2(m - mref);
     const bool moved = m != mref;

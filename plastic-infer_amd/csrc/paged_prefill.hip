@@ -284,8 +284,7 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
         mx = fmaxf(mx, fmaxf(fmaxf(sc[rb][mb][0], sc[rb][mb][1]), fmaxf(sc[rb][mb][2], sc[rb][mb][3])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = tile::max_col4(mx);
       // move the reference point only for a large enough rise (or the first keys of the row)
       const float mref = (mx - m[rb]) * scale_log2 > PF_RESCALE ? mx : m[rb];
       alpha[rb] = m[rb] == mref ? 1.f : __builtin_amdgcn_exp2f((m[rb] - mref) * scale_log2);
