@@ -521,11 +521,13 @@ def bench_prefill_attn(torch, dev, args) -> dict:
     keys = chunk * (ctx - chunk) + chunk * (chunk + 1) // 2      # visible keys per (seq, head)
     flops = b * HQ * keys * 4 * D
     hbm = b * ctx * HKV * D * 2 * 2 + 2 * b * chunk * HQ * D * 2 + b * per * 4
-    tflops = flops / (k_ms / 1e3) / 1e12
+    tflops = flops / (k_ms / 1e3) / 1e12           # the launch, by its events
+    step_tflops = flops / (ms / 1e3) / 1e12        # the timed region (the chip's clocks ramp
+    #                                                up over the first ~50 calls: --warmup 50)
     cpu = None if args.no_cpu_baseline else _cpu_prefill_attn(torch, q, kp, vp, bt, res["out"])
     return _result(
-        "paged chunked-prefill attention TFLOP/s (bf16 matrix cores)", tflops, "TFLOP/s", args,
-        ms, "bf16",
+        "paged chunked-prefill attention TFLOP/s (bf16 matrix cores)", step_tflops, "TFLOP/s",
+        args, ms, "bf16",
         {"workload": "qwen3-8b chunked prefill attention: 8 seqs x 1024-token chunks after 3072 "
                      "context tokens, 32 q / 8 kv heads, head_dim 128, page 16, causal",
          "batch": b, "chunk": chunk, "context_len": ctx},

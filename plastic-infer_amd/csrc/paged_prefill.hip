@@ -1,16 +1,23 @@
 // Paged attention of many query rows per sequence (prefill, chunked prefill) on the matrix
 // cores, gfx950: bf16, head_dim 128, page size 16, Hq / Hkv = G in {1, 2, 4, 8}.
 //
-// Work item (one 256-thread workgroup): one kv head and 64 / G consecutive query positions of
-// one sequence, i.e. 64 (position, q head) rows that share the kv head's keys: row r is
-// position s0 + r / G, head h * G + r % G. Wave w owns rows 16 w .. 16 w + 15. The keys are
-// walked in 64-token tiles (four pages): K and V come from the pool into registers one tile
-// ahead, then into LDS in their pool layout [d][token] (16-byte stores; double buffered, one
-// barrier per tile). A tile row (one d, 64 tokens, eight 16-byte chunks) is stored unpadded with
-// chunk c at c ^ ((d / 4) ^ 2 (d % 4)) % 8: with that swizzle the transposing K reads, the
-// 8-byte V reads and the 16-byte stores below ran without LDS bank conflicts when measured
-// (SQ_LDS_BANK_CONFLICT of each access pattern and offset replayed alone), where padded rows
-// left 2 to 24 conflict cycles per instruction on one pattern or another.
+// Work item (one 256-thread workgroup): one kv head and 128 / G consecutive query positions of
+// one sequence, i.e. 128 (position, q head) rows that share the kv head's keys: row r is
+// position s0 + r / G, head h * G + r % G. Wave w owns rows 32 w .. 32 w + 31 (two 16-row MFMA
+// blocks). The keys are walked in 64-token tiles (four pages): K and V come from the pool into
+// registers one tile ahead, then into LDS (16-byte stores; double buffered, one barrier per
+// tile). Both tiles are [d][64 tokens], eight 16-byte units per row, unpadded and swizzled:
+//   K: unit u (tokens 8 u .. 8 u + 7) at u ^ ((d / 4) ^ 2 (d % 4)) % 8;
+//   V: unit 4 c + j holds tokens 32 c + 4 j .. + 3 then 32 c + 16 + 4 j .. + 3 (the order of the
+//      P operand's k slots below, so one 16-byte read is a whole B operand), at unit
+//      (4 c + j) ^ sv(d), sv(d) = (d & 1) | 4 ((d / 2) & 1) | 2 ((d / 8) & 1).
+// The swizzles follow the bank rules measured on gfx950 (SQ_LDS_BANK_CONFLICT of access
+// patterns replayed alone): ds_write_b128 serves lanes 8 k .. 8 k + 7 together over 32
+// four-byte banks; ds_read_b128 serves 16 lanes together over 64 banks, in the lane groups
+// {0-3, 12-15, 20-23, 24-27} and {4-11, 16-19, 28-31} and the same plus 32. Under them the K and
+// V stores, the transposing K reads and the 16-byte V reads are conflict-free. (Eight-byte V
+// reads in the K layout were conflict-free one by one, but the compiler pairs those of blocks nb
+// and nb + 2 into ds_read2st64_b64, whose two halves per lane share a bank: 8 conflict cycles.)
 // Per tile each wave runs
 //   S^T = K . Q^T   v_mfma_f32_16x16x32_bf16: A = K^T operands built by ds_read_b64_tr_b16
 //                   (within each 16-lane group the eight-byte reads of the lanes form a 16 x 4
@@ -21,13 +28,14 @@
 //                   holds the scores of row l % 16 for tokens 16 m + 4 (l / 16) + j (m < 4,
 //                   j < 4) of the tile.
 //   online softmax  per row in fp32, base 2 with the scale folded in; a row's 64 scores sit
-//                   in four lanes (l, l ^ 16, l ^ 32, l ^ 48), reduced by two shuffles.
-//   O += P . V      16 MFMAs: the probabilities are the A operand straight from the score
-//                   registers (bf16): k slot 8 (l / 16) + j of 32-token chunk c is token
+//                   in four lanes (l, l ^ 16, l ^ 32, l ^ 48), reduced by two lane swaps.
+//   O += P . V      the probabilities are the A operand straight from the score registers
+//                   (bf16): k slot 8 (l / 16) + j of 32-token chunk c is token
 //                   32 c + 4 (l / 16) + j for j < 4 and 32 c + 16 + 4 (l / 16) + j - 4 after,
-//                   and the B operand reads V at the same tokens (two 8-byte LDS reads), so
-//                   both sides of every MFMA sum the same 32 tokens. O (16 rows x 128) stays in
-//                   8 accumulator blocks; lane l holds rows 4 (l / 16) + j, column l % 16.
+//                   and the B operand is V unit 4 c + l / 16 of row 16 nb + l % 16 (one 16-byte
+//                   LDS read), so both sides of every MFMA sum the same 32 tokens. O (16 rows x
+//                   128 per block) stays in 8 accumulator blocks; lane l holds rows 4 (l / 16) + j,
+//                   column l % 16.
 // Keys a row may not see (past its causal limit or the sequence's length, on a page whose
 // block-table id is outside the pool) score -inf; their V words are zeros from the loads.
 //
@@ -51,6 +59,7 @@ constexpr int PF_RB = 2;              // 16-row MFMA blocks per wave
 constexpr int PF_ROWS = 64 * PF_RB;   // (position, head) rows per work item: 4 waves x 32
 constexpr int PF_KT = 64;             // keys per tile: four pages
 constexpr int PF_MAX_SEQS = 1024;     // sequences per launch (tile prefix in LDS)
+constexpr int PF_V_AHEAD = 4;         // V operand reads in flight ahead of the P . V products
 
 // lazy rescaling threshold (log2 units): a row's exponentials are taken against a reference
 // that trails its true max by at most this much, so probabilities stay <= 2^8
@@ -148,7 +157,11 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
   // row d = t / 2, tokens 8 (t % 2) .. + 7 of page i
   const int ld_d = tid >> 1, ld_half = tid & 1;
   const int ld_off = ld_d * P + ld_half * 8;  // the thread's piece inside a (page, head) tile
-  uint4 kr[4], vr[4];
+  // kr[i]: the thread's K piece of page i; vu[2 c + e]: its V unit 4 c + 2 h + e (h = ld_half),
+  // tokens 8 h + 4 e .. + 3 of page 2 c in .x/.y and of page 2 c + 1 in .z/.w, loaded by
+  // eight-byte loads straight into place (a unit assembled from two 16-byte loads would need
+  // register copies that wait on the loads)
+  uint4 kr[4], vu[4];
   // block-table ids of a tile: lane i < 4 holds page 4 kt + i's id (-1 past the table). They
   // are loaded a tile ahead of the fetch that uses them, with one vector load, so no tile
   // waits on a chain of dependent block-table reads.
@@ -156,25 +169,36 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
     const int pi = 4 * kt + lane;
     return (lane < 4 && pi < npages) ? btb[pi] : -1;
   };
+  // ld_off + 4, hidden from the compiler so it does not fuse the two V loads into one
+  int ld_off4 = ld_off + 4;
+  asm volatile("" : "+v"(ld_off4));
   auto fetch = [&](int bt4) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int id = __builtin_amdgcn_readlane(bt4, i);
+      uint2 v0 = make_uint2(0u, 0u), v1 = make_uint2(0u, 0u);
       if (id >= 0 && int64_t(id) < num_pages) {  // uniform: one scalar base per page
         const int64_t tile_off = (int64_t(id) * Hkv + h) * TILE;
         kr[i] = *reinterpret_cast<const uint4*>(kpool + tile_off + ld_off);
-        vr[i] = *reinterpret_cast<const uint4*>(vpool + tile_off + ld_off);
+        v0 = *reinterpret_cast<const uint2*>(vpool + tile_off + ld_off);
+        v1 = *reinterpret_cast<const uint2*>(vpool + tile_off + ld_off4);
       } else {
         kr[i] = make_uint4(0u, 0u, 0u, 0u);
-        vr[i] = make_uint4(0u, 0u, 0u, 0u);
+      }
+      uint4& u0 = vu[2 * (i >> 1)];
+      uint4& u1 = vu[2 * (i >> 1) + 1];
+      if (i & 1) {
+        u0.z = v0.x; u0.w = v0.y; u1.z = v1.x; u1.w = v1.y;
+      } else {
+        u0.x = v0.x; u0.y = v0.y; u1.x = v1.x; u1.y = v1.y;
       }
     }
   };
-  // Swizzled LDS offsets, as per-lane bases XORed with compile-time terms (tile::swz64(d, t)
-  // with the chunk index split into its bits): a store of piece i lands at st_base ^ 16 i; the K
-  // operand read (kc, hi, mb) at (k_base[hi] ^ 16 mb) + 2048 kc; the V operand read
-  // (nb, c, s) at (v_base[nb % 2] ^ (32 c + 16 s)) + 1024 nb.
-  int st_base, k_base[2], v_base[2];
+  // Swizzled LDS offsets, as per-lane bases XORed with compile-time terms (the unit index split
+  // into its bits): the K store of piece i lands at st_base ^ 16 i; the K operand read
+  // (kc, hi, mb) at (k_base[hi] ^ 16 mb) + 2048 kc; the V stores (c, e) at v_st ^ (32 c + 8 e);
+  // the V operand read (c, nb) at (v_rd ^ 32 c) + 1024 nb.
+  int st_base, k_base[2], v_st, v_rd;
   {
     const int f = ((ld_d >> 2) ^ ((ld_d & 3) << 1)) & 7;
     st_base = (ld_d * PF_KT + 8 * (ld_half ^ (f & 1))) | (16 * (f >> 1));
@@ -184,9 +208,10 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
       const int row = 8 * g4 + 4 * hi + (n16 >> 2);
       k_base[hi] = (row * PF_KT + 4 * (n16 & 1) + 8 * (((n16 >> 1) & 1) ^ (fk & 1))) |
                    (16 * (fk >> 1));
-      const int fv = ((4 * hi + (n16 >> 2)) ^ ((n16 & 3) << 1)) & 7;  // hi: parity of nb
-      v_base[hi] = (n16 * PF_KT + 4 * (g4 & 1)) | (8 * ((g4 >> 1) ^ fv));
     }
+    auto sv = [](int d) { return (d & 1) | ((d << 1) & 4) | ((d >> 2) & 2); };
+    v_st = ld_d * PF_KT + 8 * ((2 * ld_half) ^ sv(ld_d));
+    v_rd = n16 * PF_KT + 8 * (g4 ^ sv(n16));  // sv(16 nb + n16) = sv(n16)
   }
   // tokens past kv_len on the sequence's last page: their V words are zeroed before they reach
   // LDS (stale pool memory may hold non-finite values, and p = 0 times inf is not 0)
@@ -194,18 +219,29 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
   auto stage = [&](int buf, int kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int e = st_base ^ (16 * i);
-      uint4 v = vr[i];
+      *reinterpret_cast<uint4*>(&ks[buf][st_base ^ (16 * i)]) = kr[i];
       if (4 * kt + i == npages - 1 && tail < P) {  // uniform
         const int nv = tail - 8 * ld_half;
-        v.x = tile::mask_pair(v.x, 0, nv);
-        v.y = tile::mask_pair(v.y, 2, nv);
-        v.z = tile::mask_pair(v.z, 4, nv);
-        v.w = tile::mask_pair(v.w, 6, nv);
+        uint4& u0 = vu[2 * (i >> 1)];
+        uint4& u1 = vu[2 * (i >> 1) + 1];
+        if (i & 1) {
+          u0.z = tile::mask_pair(u0.z, 0, nv); u0.w = tile::mask_pair(u0.w, 2, nv);
+          u1.z = tile::mask_pair(u1.z, 4, nv); u1.w = tile::mask_pair(u1.w, 6, nv);
+        } else {
+          u0.x = tile::mask_pair(u0.x, 0, nv); u0.y = tile::mask_pair(u0.y, 2, nv);
+          u1.x = tile::mask_pair(u1.x, 4, nv); u1.y = tile::mask_pair(u1.y, 6, nv);
+        }
       }
-      *reinterpret_cast<uint4*>(&ks[buf][e]) = kr[i];
-      *reinterpret_cast<uint4*>(&vs[buf][e]) = v;
     }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      *reinterpret_cast<uint4*>(&vs[buf][v_st ^ (32 * c)]) = vu[2 * c];
+      *reinterpret_cast<uint4*>(&vs[buf][v_st ^ (32 * c + 8)]) = vu[2 * c + 1];
+    }
+  };
+  // V operand i = 8 c + nb of a tile: unit 4 c + l / 16 of row 16 nb + l % 16
+  auto vread = [&](int buf, int i) {
+    return *reinterpret_cast<const uint4*>(&vs[buf][(v_rd ^ (32 * (i >> 3))) + 1024 * (i & 7)]);
   };
   // pages of a tile that hold keys: bit i for page i
   auto page_mask = [&](int bt4) {
@@ -323,23 +359,32 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
     }
     // O += P . V over the tile's two 32-token chunks, each V operand serving both row blocks;
     // the sums against a column of ones. Chunk outermost: consecutive products of one
-    // accumulator are 8 RB + RB MFMAs apart.
+    // accumulator are 8 RB + RB MFMAs apart. The V operands (i = 8 c + nb) are read
+    // PF_V_AHEAD products ahead of their use, so the LDS latency hides behind the MFMAs.
+    uint4 vq[PF_V_AHEAD];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
+    for (int i = 0; i < PF_V_AHEAD; ++i) vq[i] = vread(buf, i);
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb) {
-        const int vb = v_base[nb & 1];
-        const uint2 v0 =
-            *reinterpret_cast<const uint2*>(&vs[buf][(vb ^ (32 * c)) + 1024 * nb]);
-        const uint2 v1 =
-            *reinterpret_cast<const uint2*>(&vs[buf][(vb ^ (32 * c + 16)) + 1024 * nb]);
-        const uint4 vop = make_uint4(v0.x, v0.y, v1.x, v1.y);
+    for (int i = 0; i < 16; ++i) {
+      const int c = i >> 3, nb = i & 7;
+      const uint4 vop = vq[i % PF_V_AHEAD];
+      if (i + PF_V_AHEAD < 16) vq[i % PF_V_AHEAD] = vread(buf, i + PF_V_AHEAD);
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) acc[rb][nb] = tile::mfma_bf16(pk[rb][c], vop, acc[rb][nb]);
+      for (int rb = 0; rb < RB; ++rb) acc[rb][nb] = tile::mfma_bf16(pk[rb][c], vop, acc[rb][nb]);
+      if (nb == 7) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) lsum[rb] = tile::mfma_bf16(pk[rb][c], ones, lsum[rb]);
       }
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) lsum[rb] = tile::mfma_bf16(pk[rb][c], ones, lsum[rb]);
     }
+    // keep that order through the machine scheduler (it would sink the reads to their uses):
+    // PF_V_AHEAD reads, then one read per RB products, then the rest of the products
+    __builtin_amdgcn_sched_group_barrier(0x100, PF_V_AHEAD, 0);
+#pragma unroll
+    for (int i = 0; i < 16 - PF_V_AHEAD; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, RB, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, RB * (PF_V_AHEAD + 2), 0);
     bt_cur = bt_nxt;
     bt_nxt = bt_far;
   }
