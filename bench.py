@@ -576,24 +576,11 @@ def _cpu_prefill_attn(torch, q, kp, vp, bt, gpu_out) -> dict:
 
 
 XS_L, XS_E, XS_H, XS_I, XS_B, XS_K, XS_SLOTS, XS_SEED = 48, 128, 2048, 768, 64, 8, 3072, 5
-_PINNED_KEEP = []
-
-
 def _pinned_exact(torch, shape):
-    """A bf16 host tensor in page-locked memory of exactly its size (hipHostMalloc; torch's
-    pinned allocator rounds every block up to a power of two, 1.33x for these banks)."""
-    import ctypes
-    import math
+    """A bf16 host tensor in page-locked memory of exactly its size."""
+    from plastic_infer.kernel.pinned import alloc_pinned_exact
 
-    hip = ctypes.CDLL("libamdhip64.so")
-    nbytes = math.prod(shape) * 2
-    ptr = ctypes.c_void_p()
-    rc = hip.hipHostMalloc(ctypes.byref(ptr), ctypes.c_size_t(nbytes), ctypes.c_uint(0))
-    if rc != 0 or not ptr.value:
-        raise RuntimeError(f"hipHostMalloc of {nbytes} bytes failed ({rc})")
-    buf = (ctypes.c_uint8 * nbytes).from_address(ptr.value)
-    _PINNED_KEEP.append(buf)
-    return torch.frombuffer(buf, dtype=torch.bfloat16).view(shape)
+    return alloc_pinned_exact(shape, torch.bfloat16)
 
 
 def _pin_expert_banks(torch, markers: bool):

@@ -124,13 +124,24 @@ int pia_kv_pages_chunks_copy(void* const* chunks, int num_chunks, void* pages,
  *     pia_paged_decode_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim, page_size,
  *                                      bt_stride)
  * bytes, 4-byte aligned (may be NULL when that query returns 0). Calls that share a workspace
- * must be ordered (same stream): the kernels keep partials in it between their two launches.
+ * must be ordered (same stream): a launch keeps its partials and arrival counters in it.
  * bf16 with head_dim 128 and page_size 16 and Hq/Hkv in {1, 2, 4, 8} takes the fast kernel
  * (the batch's KV steps split over persistent waves, XCD-aware); every other supported
  * combination (f32/f16/bf16, head_dim <= 512, any page_size) takes the general kernel.
  * ------------------------------------------------------------------------------------------- */
 int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_heads,
                                          int head_dim, int page_size, int64_t bt_stride);
+
+/* Layout of the fast decode kernel's scratch for `waves` persistent waves (2 <= waves <= 4096;
+ * the workspace above is this layout at 4096 waves, the no-alloc entry point's static array at
+ * the waves of its launch). No counterpart in the reference: a host-only query, callable without
+ * a GPU, for callers and tests that size or check a scratch buffer. Bytes [0, *partials_offset)
+ * hold one 64-bit arrival counter per wave (from the first 8-byte boundary of a 4-byte aligned
+ * buffer); bytes [*partials_offset, *total_bytes) hold two partial slots per wave of
+ * (num_heads / num_kv_heads) rows of head_dim + 2 fp32. Returns 0, or PIA_EINVAL /
+ * PIA_EUNSUPPORTED (Hq / Hkv outside {1, 2, 4, 8}). */
+int pia_paged_decode_scratch_layout(int num_heads, int num_kv_heads, int waves,
+                                    int64_t* partials_offset, int64_t* total_bytes);
 
 int pia_paged_decode_attention(void* out, const void* q, int64_t q_seq_stride,
                                const void* k_pages, const void* v_pages,
@@ -292,8 +303,10 @@ int pia_moe_topk_align(float* topk_weights, int32_t* topk_ids, const void* logit
 
 /* ---------------------------------------------------------------------------------------------
  * Permute: x_perm[r, :] = hidden[sorted_token_ids[r] / topk, :] for r < *num_tokens_post_pad
- * and sorted_token_ids[r] < numel; padding rows (sentinel) are zero-filled; rows at or beyond
- * *num_tokens_post_pad are left untouched. Bit-exact row copy (row_bytes multiple of 4).
+ * and sorted_token_ids[r] < numel. Padding rows (sentinel: sorted_token_ids[r] >= numel) and rows
+ * at or beyond *num_tokens_post_pad are left untouched: a consumer skips sentinel rows, as the
+ * reference's grouped GEMM masks them (src/plastic_infer/kernel/triton/fused_moe.py:156-302).
+ * Bit-exact row copy (row_bytes multiple of 4).
  * route_pos (optional, the inverse map pia_moe_align_block_size writes): when given, each token
  * row is read once and written to its routes' rows (same result, a quarter of the reads for
  * top-8); NULL walks the destination rows in order.

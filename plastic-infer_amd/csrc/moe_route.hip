@@ -675,8 +675,9 @@ __global__ __launch_bounds__(1024) void moe_align_small(
 
 // ---------------------------------------------------------------------------------------------
 // Permute: a wave moves four destination rows (sixteen per 256-thread block) with the loads of
-// all four issued before their stores; 16-byte words when the row allows it. Rows past
-// *num_tokens_post_pad are left untouched, padding rows are zeroed.
+// all four issued before their stores; 16-byte words when the row allows it. Padding rows
+// (sentinel routes) and rows past *num_tokens_post_pad are left untouched: every consumer of a
+// plan skips sentinel rows, so writing them would only add HBM traffic.
 // ---------------------------------------------------------------------------------------------
 constexpr int PERM_ROWS_PER_WAVE = 4;
 constexpr int PERM_ROWS_PER_BLOCK = 4 * PERM_ROWS_PER_WAVE;
@@ -716,60 +717,40 @@ __global__ __launch_bounds__(256) void moe_permute_kernel(
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t c = c0 + lane + 64 * u;
-        if (live[j] && c < row_words) xp[(r0 + j) * row_words + c] = buf[j][u];
+        if (live[j] && !pad[j] && c < row_words) xp[(r0 + j) * row_words + c] = buf[j][u];
       }
   }
 }
 
-// Token-major permute (route_pos given): blocks [0, token_blocks) give one wave per token,
-// which reads the token's row once and stores it to each of its routes' rows; the remaining
-// blocks check 256 destination rows each and zero the padding rows among them.
+// Token-major permute (route_pos given): one wave per token reads the token's row once and
+// stores it to each of its routes' rows.
 template <typename W>
 __global__ __launch_bounds__(256) void moe_permute_tokens_kernel(
-    W* __restrict__ xp, const W* __restrict__ hidden, const int32_t* __restrict__ sorted,
-    const int32_t* __restrict__ route_pos, const int32_t* __restrict__ npp, int64_t max_rows,
-    int64_t numel, int topk, int64_t row_words, int64_t hidden_stride_words,
-    int64_t token_blocks) {
+    W* __restrict__ xp, const W* __restrict__ hidden, const int32_t* __restrict__ route_pos, const int32_t* __restrict__ npp, int64_t max_rows,
+    int64_t numel, int topk, int64_t row_words, int64_t hidden_stride_words) {
   constexpr int U = 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t nrows = min<int64_t>(max_rows, npp[0]);
-  if (int64_t(blockIdx.x) < token_blocks) {
-    const int64_t t = int64_t(blockIdx.x) * 4 + wave;
-    if (t >= numel / topk) return;
-    const int my_r = lane < topk ? route_pos[t * topk + lane] : -1;
-    const W* src = hidden + t * hidden_stride_words;
-    for (int64_t c0 = 0; c0 < row_words; c0 += 64 * U) {
-      W buf[U];
+  const int64_t t = int64_t(blockIdx.x) * 4 + wave;
+  if (t >= numel / topk) return;
+  const int my_r = lane < topk ? route_pos[t * topk + lane] : -1;
+  const W* src = hidden + t * hidden_stride_words;
+  for (int64_t c0 = 0; c0 < row_words; c0 += 64 * U) {
+    W buf[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + lane + 64 * u;
+      buf[u] = c < row_words ? src[c] : W{};
+    }
+    for (int sl = 0; sl < topk; ++sl) {
+      const int r = __shfl(my_r, sl, 64);
+      if (r < 0 || r >= nrows) continue;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int64_t c = c0 + lane + 64 * u;
-        buf[u] = c < row_words ? src[c] : W{};
-      }
-      for (int sl = 0; sl < topk; ++sl) {
-        const int r = __shfl(my_r, sl, 64);
-        if (r < 0 || r >= nrows) continue;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int64_t c = c0 + lane + 64 * u;
-          if (c < row_words) xp[int64_t(r) * row_words + c] = buf[u];
-        }
+        if (c < row_words) xp[int64_t(r) * row_words + c] = buf[u];
       }
     }
-    return;
-  }
-  const int64_t rbase = (int64_t(blockIdx.x) - token_blocks) * 256 + wave * 64;
-  const int64_t r = rbase + lane;
-  bool is_pad = false;
-  if (r < nrows) {
-    const int32_t route = sorted[r];
-    is_pad = route < 0 || route >= numel;
-  }
-  uint64_t pads = __ballot(is_pad);
-  while (pads) {
-    const int j = __builtin_ctzll(pads);
-    pads &= pads - 1;
-    W* dst = xp + (rbase + j) * row_words;
-    for (int64_t c = lane; c < row_words; c += 64) dst[c] = W{};
   }
 }
 
@@ -1045,19 +1026,18 @@ extern "C" int pia_moe_permute(void* x_perm, const void* hidden, const int32_t* 
   const bool v16 = row_bytes % 16 == 0 && hidden_row_stride_bytes % 16 == 0 &&
                    aligned(x_perm, 16) && aligned(hidden, 16);
   if (route_pos && topk <= 64) {
-    const int64_t token_blocks = ceil_div(numel / topk, 4);
-    const int64_t blocks = token_blocks + ceil_div(max_rows, 256);
+    const int64_t blocks = ceil_div(numel / topk, 4);
+    if (blocks == 0) return 0;
     if (blocks > 0x7fffffff) return fail(PIA_EINVAL, "moe_permute: too many rows");
     if (v16)
       hipLaunchKernelGGL(moe_permute_tokens_kernel<uint4>, dim3(unsigned(blocks)), dim3(256), 0,
-                         s, (uint4*)x_perm, (const uint4*)hidden, sorted_token_ids, route_pos,
-                         num_tokens_post_pad, max_rows, numel, topk, row_bytes / 16,
-                         hidden_row_stride_bytes / 16, token_blocks);
+                         s, (uint4*)x_perm, (const uint4*)hidden, route_pos, num_tokens_post_pad,
+                         max_rows, numel, topk, row_bytes / 16, hidden_row_stride_bytes / 16);
     else
       hipLaunchKernelGGL(moe_permute_tokens_kernel<uint32_t>, dim3(unsigned(blocks)), dim3(256),
-                         0, s, (uint32_t*)x_perm, (const uint32_t*)hidden, sorted_token_ids,
-                         route_pos, num_tokens_post_pad, max_rows, numel, topk, row_bytes / 4,
-                         hidden_row_stride_bytes / 4, token_blocks);
+                         0, s, (uint32_t*)x_perm, (const uint32_t*)hidden, route_pos,
+                         num_tokens_post_pad, max_rows, numel, topk, row_bytes / 4,
+                         hidden_row_stride_bytes / 4);
     return check_launch("moe_permute");
   }
   const unsigned blocks = unsigned(ceil_div(max_rows, PERM_ROWS_PER_BLOCK));

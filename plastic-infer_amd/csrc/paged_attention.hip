@@ -177,9 +177,24 @@ constexpr int SD_MAX_SEQS = 1024;   // sequences per launch (step-prefix table i
 constexpr int SD_MAX_WAVES = 4096;  // partial slots are sized for this many waves
 constexpr int SD_WAVES_PER_CU = 8;  // two single-wave workgroups per SIMD
 constexpr int SD_STEP_TOKENS = FD_PAGES_PER_WAVE * FD_P;  // 128 tokens per step
-// meta: one 64-bit arrival counter per wave w (for the cut segment whose first step lies in
-// w's range), from the first 8-byte boundary of the meta ints
-constexpr int SD_META_INTS = 2 * SD_MAX_WAVES + 2;
+
+// The decode scratch (a caller's workspace, or the no-alloc entry point's static array), laid
+// out for `waves` waves; every entry point takes its layout from here and nowhere else:
+//   [0, part_offset)           one 64-bit arrival counter per wave w (for the cut segment whose
+//                              first step lies in w's range), starting at the first 8-byte
+//                              boundary (the buffer need only be 4-byte aligned), padded to
+//                              256 bytes;
+//   [part_offset, total_bytes) two partial slots per wave, each G rows of D + 2 fp32.
+struct DecodeScratchLayout {
+  int64_t part_offset;
+  int64_t total_bytes;
+};
+constexpr DecodeScratchLayout decode_scratch_layout(int G, int waves) {
+  return {(int64_t(waves) * 8 + 8 + 255) / 256 * 256,
+          (int64_t(waves) * 8 + 8 + 255) / 256 * 256 +
+              int64_t(waves) * 2 * G * (FD_D + 2) * int64_t(sizeof(float))};
+}
+constexpr bool stream_group_ok(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
 constexpr int SD_EVEN_SHARE_PERMILLE = 515;                // even-XCD wave's share of a pair
 
 // Steps of a wave pair and the even wave's share of them, for T steps over NW waves.
@@ -1555,9 +1570,9 @@ int check_decode_args(const void* out, const void* q, int64_t q_seq_stride, cons
 }
 
 // The fast path (checked arguments): the stream kernel, in launches of up to SD_MAX_SEQS
-// sequences that reuse the same partial slots (ws_part: >= NW * 2 * G * (D + 2) floats) and
-// arrival counters (ws_meta: SD_META_INTS ints). Launches on one stream are ordered, so the
-// reuse is safe; each launch takes a fresh token for its counters.
+// sequences that reuse the same scratch (`scratch`, laid out by decode_scratch_layout for
+// `scratch_waves` waves, at least the NW waves of a launch). Launches on one stream are ordered,
+// so the reuse is safe; each launch takes a fresh token for its counters.
 // k_new != nullptr: append mode (the new tokens of the step in k_new / v_new, written into the
 // pools by the kernel; k_pages / v_pages are then written too).
 // Launch tokens for the arrival counters: the upper 48 bits of a 64-bit word, a process-wide
@@ -1572,11 +1587,19 @@ uint64_t next_stream_token() {
 int launch_stream_decode(void* out, const void* q, int64_t q_seq_stride, const void* k_pages,
                          const void* v_pages, const int32_t* block_tables, int64_t bt_stride,
                          const int32_t* context_lens, int num_seqs, int num_heads,
-                         int num_kv_heads, int64_t num_pages, float scale_log2, float* ws_part,
-                         int32_t* ws_meta, hipStream_t s, const void* k_new = nullptr,
-                         const void* v_new = nullptr, int64_t new_seq_stride = 0) {
+                         int num_kv_heads, int64_t num_pages, float scale_log2,
+                         unsigned char* scratch, int scratch_waves, hipStream_t s,
+                         const void* k_new = nullptr, const void* v_new = nullptr,
+                         int64_t new_seq_stride = 0) {
   const int G = num_heads / num_kv_heads;
   const int NW = stream_waves(G);
+  if (NW > scratch_waves) {
+    set_error("paged_decode: %d waves, the scratch holds %d", NW, scratch_waves);
+    return PIA_EUNSUPPORTED;
+  }
+  int32_t* ws_meta = reinterpret_cast<int32_t*>(scratch);
+  float* ws_part =
+      reinterpret_cast<float*>(scratch + decode_scratch_layout(G, scratch_waves).part_offset);
   uint16_t* kw = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(k_pages));
   uint16_t* vw = const_cast<uint16_t*>(reinterpret_cast<const uint16_t*>(v_pages));
   for (int b0 = 0; b0 < num_seqs; b0 += SD_MAX_SEQS) {
@@ -1632,7 +1655,6 @@ int launch_stream_decode(void* out, const void* q, int64_t q_seq_stride, const v
 // ordering) race on it.
 // ---------------------------------------------------------------------------------------------
 constexpr int64_t kNoAllocScratchBytes = int64_t(16) << 20;                  // 16 MiB per GPU
-constexpr int64_t kNoAllocMetaBytes = (int64_t(SD_META_INTS) * 4 + 255) / 256 * 256;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
@@ -1672,9 +1694,21 @@ extern "C" int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads,
       num_kv_heads <= 0 || num_heads % num_kv_heads || bt_stride <= 0)
     return 0;
   const int G = num_heads / num_kv_heads;
-  if (G == 1 || G == 2 || G == 4 || G == 8)  // two partial slots per wave + step-prefix table
-    return int64_t(SD_MAX_WAVES) * 2 * G * (FD_D + 2) * int64_t(sizeof(float)) +
-           int64_t(SD_META_INTS) * int64_t(sizeof(int32_t));
+  if (!stream_group_ok(G)) return 0;
+  return decode_scratch_layout(G, SD_MAX_WAVES).total_bytes;
+}
+
+extern "C" int pia_paged_decode_scratch_layout(int num_heads, int num_kv_heads, int waves,
+                                               int64_t* partials_offset, int64_t* total_bytes) {
+  if (!partials_offset || !total_bytes) return fail(PIA_EINVAL, "decode_scratch_layout: null pointer");
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads ||
+      !stream_group_ok(num_heads / num_kv_heads))
+    return fail(PIA_EUNSUPPORTED, "decode_scratch_layout: Hq / Hkv must be 1, 2, 4 or 8");
+  if (waves < 2 || waves > SD_MAX_WAVES)
+    return fail(PIA_EINVAL, "decode_scratch_layout: waves must be in [2, 4096]");
+  const DecodeScratchLayout lay = decode_scratch_layout(num_heads / num_kv_heads, waves);
+  *partials_offset = lay.part_offset;
+  *total_bytes = lay.total_bytes;
   return 0;
 }
 
@@ -1702,13 +1736,10 @@ extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_se
       return PIA_EINVAL;
     }
     if (!aligned(workspace, 4)) return fail(PIA_EINVAL, "paged_decode: workspace not 4-byte aligned");
-    const int G = num_heads / num_kv_heads;
-    float* ws_part = reinterpret_cast<float*>(workspace);
-    int32_t* ws_meta =
-        reinterpret_cast<int32_t*>(ws_part + int64_t(SD_MAX_WAVES) * 2 * G * (FD_D + 2));
     return launch_stream_decode(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride,
                                 context_lens, num_seqs, num_heads, num_kv_heads, num_pages,
-                                scale_log2, ws_part, ws_meta, s);
+                                scale_log2, static_cast<unsigned char*>(workspace),
+                                SD_MAX_WAVES, s);
   }
   return launch_generic_any(dtype, out, q, q_seq_stride, k_pages, v_pages, block_tables,
                             bt_stride, context_lens, nullptr, nullptr, num_seqs, num_seqs,
@@ -1744,13 +1775,10 @@ extern "C" int pia_paged_decode_append_attention(
     }
     if (!aligned(workspace, 4))
       return fail(PIA_EINVAL, "paged_decode_append: workspace not 4-byte aligned");
-    const int G = num_heads / num_kv_heads;
-    float* ws_part = reinterpret_cast<float*>(workspace);
-    int32_t* ws_meta =
-        reinterpret_cast<int32_t*>(ws_part + int64_t(SD_MAX_WAVES) * 2 * G * (FD_D + 2));
     return launch_stream_decode(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride,
                                 context_lens, num_seqs, num_heads, num_kv_heads, num_pages,
-                                scale_log2, ws_part, ws_meta, s, k_new, v_new, new_seq_stride);
+                                scale_log2, static_cast<unsigned char*>(workspace),
+                                SD_MAX_WAVES, s, k_new, v_new, new_seq_stride);
   }
   // any other shape: the new tokens into their slots, then the decode over the pool
   if (int rc = launch_kv_append(dtype, k_pages, v_pages, k_new, v_new, new_seq_stride,
@@ -1766,8 +1794,8 @@ extern "C" int pia_paged_decode_append_attention(
 extern "C" int64_t pia_paged_decode_noalloc_scratch_bytes(int num_heads, int num_kv_heads) {
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
   const int G = num_heads / num_kv_heads;
-  if (G != 1 && G != 2 && G != 4 && G != 8) return 0;
-  return kNoAllocMetaBytes + int64_t(stream_waves(G)) * 2 * G * (FD_D + 2) * int64_t(sizeof(float));
+  if (!stream_group_ok(G)) return 0;
+  return decode_scratch_layout(G, stream_waves(G)).total_bytes;
 }
 
 extern "C" int pia_paged_decode_attention_noalloc(void* out, const void* q, int64_t q_seq_stride,
@@ -1798,11 +1826,9 @@ extern "C" int pia_paged_decode_attention_noalloc(void* out, const void* q, int6
   }
   unsigned char* base = nullptr;
   if (int rc = scratch_ptr(&base)) return rc;
-  int32_t* ws_meta = reinterpret_cast<int32_t*>(base);
-  float* ws_part = reinterpret_cast<float*>(base + kNoAllocMetaBytes);
   return launch_stream_decode(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride,
                               context_lens, num_seqs, num_heads, num_kv_heads, num_pages,
-                              scale_log2, ws_part, ws_meta, s);
+                              scale_log2, base, stream_waves(num_heads / num_kv_heads), s);
 }
 
 extern "C" int pia_paged_attention(void* out, const void* q, const void* k_pages,

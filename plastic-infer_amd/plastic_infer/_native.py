@@ -32,6 +32,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_kv_pages_chunk_copy": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _L, _I, _I, _P]),
     "pia_kv_pages_chunks_copy": (_I, [_P, _I, _P, _P, _I, _I, _I, _I, _I, _L, _I, _I, _P]),
     "pia_paged_decode_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _L]),
+    "pia_paged_decode_scratch_layout": (_I, [_I, _I, _I, _P, _P]),
     "pia_paged_decode_attention": (
         _I, [_P, _P, _L, _P, _P, _P, _L, _P, _I, _I, _I, _I, _I, _L, _F, _I, _P, _L, _P]),
     "pia_paged_decode_append_attention": (
@@ -69,7 +70,7 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_prefill_hit_compact": (_I, [_P, _P, _P, _P, _L, _L, _I, _P]),
 }
 
-EXPECTED_ABI = 7
+EXPECTED_ABI = 8
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -38,6 +38,7 @@ import torch.nn.functional as F
 
 from ..kernel.moe_ops import moe_sum_reduce
 from ..kernel.paged_kv import decode_workspace_bytes, paged_decode_append_attention
+from ..kernel.pinned import alloc_pinned_exact
 from ..moe.fused import fused_experts_decode_impl, fused_topk, routed_ffn_routes
 from ..moe.offload_cache import OffloadMoeCache
 from .attention import build_rope_cache, rms_norm
@@ -101,10 +102,11 @@ def random_expert_banks(cfg: MoeModelConfig, device: torch.device, seed: int = 0
                         std: float = 0.02, pin=None) -> dict[str, list[torch.Tensor]]:
     """Random-init expert banks in pinned host memory: per layer gate_up [E, 2I, H] (gate rows
     then up rows) and down [E, H, I], drawn on the device one layer at a time and copied out.
-    pin(shape) allocates a pinned host tensor (default torch's pinned allocator)."""
+    pin(shape) allocates a pinned host tensor (default: page-locked memory of exactly the
+    bank's size, kernel.pinned.alloc_pinned_exact)."""
     g = torch.Generator(device=device).manual_seed(seed)
     E, H, I = cfg.n_experts, cfg.hidden_dim, cfg.moe_intermediate_dim
-    alloc = pin or (lambda shape: torch.empty(shape, dtype=cfg.dtype, pin_memory=True))
+    alloc = pin or (lambda shape: alloc_pinned_exact(shape, cfg.dtype))
     banks: dict[str, list[torch.Tensor]] = {"gate_up": [], "down": []}
     for _ in range(cfg.n_layers):
         for name, shape in (("gate_up", (E, 2 * I, H)), ("down", (E, H, I))):

@@ -113,10 +113,11 @@ def moe_permute(hidden: torch.Tensor, sorted_token_ids: torch.Tensor,
                 num_tokens_post_pad: torch.Tensor, topk: int,
                 out: torch.Tensor | None = None,
                 route_pos: torch.Tensor | None = None) -> torch.Tensor:
-    """x_perm[r] = hidden[sorted_token_ids[r] // topk] for r < num_tokens_post_pad; padding
-    rows are zero. Output has sorted_token_ids.numel() rows (rows past num_tokens_post_pad are
-    left as allocated). Bit-exact. With route_pos (moe_align_block_size's inverse map) every
-    token row is read once and written to all its routes."""
+    """x_perm[r] = hidden[sorted_token_ids[r] // topk] for r < num_tokens_post_pad and
+    sorted_token_ids[r] < numel. Output has sorted_token_ids.numel() rows; padding rows
+    (sentinel ids) and rows past num_tokens_post_pad are left as allocated (consumers skip
+    sentinel rows). Bit-exact. With route_pos (moe_align_block_size's inverse map) every token
+    row is read once and written to all its routes."""
     dev = N.require_device(hidden, sorted_token_ids, num_tokens_post_pad,
                            names=("hidden", "sorted_token_ids", "num_tokens_post_pad"))
     if route_pos is not None:

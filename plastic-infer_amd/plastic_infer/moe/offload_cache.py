@@ -38,6 +38,7 @@ Only bf16 / fp16 expert banks (the "bf16" schema) and decode on the GPU are buil
 from __future__ import annotations
 
 import math
+import warnings
 from dataclasses import dataclass
 
 import numpy as np
@@ -317,50 +318,82 @@ class OffloadMoeCache:
         if self.device.index is None:
             self.device = torch.device("cuda", torch.cuda.current_device())
         self.num_layers, self.num_experts = int(num_layers), int(num_experts)
-        self.cache_size = int(cache_size)
         self.cache_policy = cache_policy
         self.prefill_overlap = bool(prefill_overlap)
         self.prefill_hit_d2d = bool(prefill_hit_d2d)
         self.multi_bank_copy = bool(multi_bank_copy)
         self.quant_format = quant_format
         self.decode_target = decode_target
-        L, E, S = self.num_layers, self.num_experts, self.cache_size
-        if S < E:
-            raise ValueError(f"cache_size {S} < num_experts {E}")
-
+        L, E = self.num_layers, self.num_experts
         if cache_policy == "static":
             R = E // 2 if resident_per_layer is None else int(resident_per_layer)
             if not 0 <= R <= E:
                 raise ValueError(f"resident_per_layer must be in [0, {E}]")
             self.resident_per_layer = R
-            self.staging_base = L * R
-            staging = S - L * R
-            need = max(E - R, 2 * E if self.prefill_overlap else 0)
-            if staging < need:
-                raise ValueError(f"cache_size {S}: {L} x {R} resident slots leave {staging} "
-                                 f"staging slots, {need} needed")
-            self._staging = _StagingLru(staging)
         else:
-            if self.prefill_overlap and S < 2 * E:
-                raise ValueError("prefill overlap borrows two whole-layer buffers from the cache: "
-                                 "cache_size must be at least 2 * num_experts")
             self.resident_per_layer = 0
-            self.staging_base = 0
-            self._staging = None
-        self._maps = _DeviceSlotMaps(L, E, S, self.device)
+        self.validate_rebuild(int(cache_size))
+        if self.prefill_overlap and not self._overlap_fits(int(cache_size)):
+            raise ValueError("prefill overlap borrows two whole-layer buffers from the cache: "
+                             f"cache_size {cache_size} leaves fewer than 2 * num_experts "
+                             "borrowable slots")
+        self.cache_size = int(cache_size)
         self._banks: _BankSet | None = None
         self._prefill: _PrefillBuffers | None = None
         self._resident_slot = np.full((L, E), -1, np.int64)   # "static": fixed slot or -1
+        self._resident_choice: list[list[int]] | None = None
         self._pending_layer: int | None = None
         self._copy_stream = torch.cuda.Stream(device=self.device)
         self._host_ids = torch.empty(0, dtype=torch.int32, pin_memory=True)
-        self._host_plan = torch.empty(3 * max(E, S) + 2, dtype=torch.int64, pin_memory=True)
         self.collect_stats = False
         self.record_copy_start = False      # StagedRoutes.issued (overlap measurement)
+        # Opt-in routing histogram [L, E] (raw expert ids counted before they become slots):
+        # decode_routing_stats() reads it.
+        self.collect_decode_freq = False
+        self.decode_freq = torch.zeros((L, E), dtype=torch.int64, device=self.device)
+        # prefill_hit_compact (moe.offload_kernels) output: buffer rows, cache slots, count
+        self._prefill_hit_dst = torch.zeros(E, dtype=torch.int32, device=self.device)
+        self._prefill_hit_src = torch.zeros(E, dtype=torch.int32, device=self.device)
+        self._prefill_hit_num = torch.zeros(1, dtype=torch.int64, device=self.device)
+        self._set_geometry()
+
+    def _set_geometry(self) -> None:
+        """cache_size-shaped state: staging split, device maps and plan, host plan buffer,
+        stats (all cold)."""
+        L, E, S = self.num_layers, self.num_experts, self.cache_size
+        if self.cache_policy == "static":
+            self.staging_base = L * self.resident_per_layer
+            self._staging = _StagingLru(S - self.staging_base)
+        else:
+            self.staging_base = 0
+            self._staging = None
+        self._maps = _DeviceSlotMaps(L, E, S, self.device)
+        self._host_plan = torch.empty(3 * max(E, S) + 2, dtype=torch.int64, pin_memory=True)
         self._host_stats = np.zeros((L, N_STATS), np.int64)   # "static" and staged calls
         self.copied_bytes = 0
         self.prefill_hit_rows = 0
         self.prefill_total_rows = 0
+
+    def validate_rebuild(self, cache_size: int) -> None:
+        """Geometry check of a cache size, with no side effect (reference :410-423): at least
+        num_experts slots; under "static" also the resident experts of every layer plus a
+        staging area for one layer's other experts. rebuild() and the constructor call it, so an
+        invalid size is rejected with the current cache intact."""
+        L, E = self.num_layers, self.num_experts
+        if cache_size < E:
+            raise ValueError(f"cache_size {cache_size} < num_experts {E}")
+        if self.cache_policy == "static":
+            staging = cache_size - L * self.resident_per_layer
+            if staging < E - self.resident_per_layer:
+                raise ValueError(f"cache_size {cache_size}: {L} x {self.resident_per_layer} "
+                                 f"resident slots leave {staging} staging slots, "
+                                 f"{E - self.resident_per_layer} needed")
+
+    def _overlap_fits(self, cache_size: int) -> bool:
+        """Whether the two whole-layer prefill buffers fit in the slots that may be borrowed."""
+        free = cache_size - (self.num_layers * self.resident_per_layer
+                             if self.cache_policy == "static" else 0)
+        return free >= 2 * self.num_experts
 
     # ---- state views (the reference's attribute names) ----------------------------------------
 
@@ -375,6 +408,26 @@ class OffloadMoeCache:
     @property
     def step(self) -> torch.Tensor:
         return self._maps.clock
+
+    @property
+    def usage(self) -> torch.Tensor:
+        """[cache_size] int64: clock value at each slot's last use."""
+        return self._maps.usage
+
+    @property
+    def evict_slots(self) -> torch.Tensor:
+        """Copy plan of the last admission: destination slots (first num_indices entries)."""
+        return self._maps.plan_dst
+
+    @property
+    def src_indices(self) -> torch.Tensor:
+        """Copy plan of the last admission: layer-local host bank rows."""
+        return self._maps.plan_src
+
+    @property
+    def num_indices(self) -> torch.Tensor:
+        """[1] int64: entries in the copy plan of the last admission."""
+        return self._maps.plan_len
 
     @property
     def lru_stats(self) -> torch.Tensor:
@@ -425,6 +478,7 @@ class OffloadMoeCache:
 
     def _place_resident(self, resident_experts) -> None:
         L, E, R = self.num_layers, self.num_experts, self.resident_per_layer
+        self._resident_choice = resident_experts
         self._resident_slot.fill(-1)
         for l in range(L):
             chosen = np.arange(R) if resident_experts is None else \
@@ -458,6 +512,7 @@ class OffloadMoeCache:
         if expert_ids.dtype != torch.int32 or not expert_ids.is_contiguous():
             raise ValueError("expert_ids must be a contiguous int32 tensor")
         if self.cache_policy == "lru":
+            self._count_routes(int(layer_id), expert_ids)
             self._pending_layer = int(layer_id)
             self._maps.admit(int(layer_id), expert_ids.view(-1), self.collect_stats)
             return
@@ -498,6 +553,7 @@ class OffloadMoeCache:
         if ids.dtype != torch.int32:
             raise ValueError("topk_ids must be int32")
         n = ids.numel()
+        self._count_routes(layer, ids)
         compute = torch.cuda.current_stream(dev)
         if self._host_ids.numel() < n:
             self._host_ids = torch.empty(max(n, 2 * self._host_ids.numel()), dtype=torch.int32,
@@ -579,6 +635,16 @@ class OffloadMoeCache:
         self.copied_bytes += moved
         return StagedRoutes(layer, self._to_device(in_hbm, shape), self._to_device(copied, shape),
                             ready, int(np.unique(hs[hs >= 0]).size), cnt, moved, issued)
+
+    def _count_routes(self, layer: int, ids: torch.Tensor) -> None:
+        """decode_freq[layer][e] += routes to expert e (ids outside [0, E) are not counted),
+        when collect_decode_freq is set; on the current stream, no host synchronisation."""
+        if not self.collect_decode_freq:
+            return
+        E = self.num_experts
+        flat = ids.reshape(-1)
+        valid = (flat >= 0) & (flat < E)
+        self.decode_freq[layer].index_add_(0, flat.clamp(0, E - 1).long(), valid.long())
 
     def _copy_start_event(self) -> torch.cuda.Event | None:
         if not self.record_copy_start:
@@ -706,6 +772,41 @@ class OffloadMoeCache:
             self._maps.clock.zero_()
         self._pending_layer = None
 
+    def rebuild(self, cache_size: int) -> None:
+        """Resize the HBM slot cache to `cache_size` slots in place (reference :425-496).
+
+        The pinned host banks are kept and nothing is read again from the caller; the old slot
+        caches and prefill buffers (views of them) are dropped before the new ones are
+        allocated, the maps, plan and statistics restart cold, and under "static" the resident
+        experts (the same choice as before) are copied into their new slots before the call
+        returns. Prefill overlap is switched off when the new size leaves fewer than
+        2 * num_experts borrowable slots. The object stays the same, so holders of the cache
+        stay valid; tensors taken from it earlier (bank_views, the maps) do not."""
+        assert self._banks is not None, "set_bank_sources must run before rebuild"
+        self.validate_rebuild(int(cache_size))
+        sources = self._banks.sources
+        self._prefill = None
+        self._banks = None
+        self._maps = None
+        self._pending_layer = None
+        torch.cuda.synchronize(self.device)
+        torch.cuda.empty_cache()
+        self.cache_size = int(cache_size)
+        self._set_geometry()
+        self.decode_freq.zero_()
+        if self.prefill_overlap and not self._overlap_fits(self.cache_size):
+            warnings.warn(f"prefill overlap switched off by rebuild: cache_size "
+                          f"{self.cache_size} leaves fewer than 2 * num_experts borrowable "
+                          "slots", RuntimeWarning, stacklevel=2)
+            self.prefill_overlap = False
+        self._banks = _BankSet(sources, self.num_layers, self.num_experts, self.cache_size,
+                               self.device, self.multi_bank_copy)
+        if self.cache_policy == "static":
+            self._place_resident(self._resident_choice)
+        if self.prefill_overlap:
+            self._prefill = _PrefillBuffers(self._banks, self.num_experts, self.staging_base,
+                                            self.device)
+
     def reset_stats(self) -> None:
         self._maps.stats.zero_()
         self._host_stats[:] = 0
@@ -735,6 +836,39 @@ class OffloadMoeCache:
                          "missing_per_step": m / c if c else 0.0,
                          "miss_rate": m / a if a else 0.0})
         return {"per_layer": rows}
+
+    def record_decode_stats(self, layer_id: int) -> None:
+        """No-op: the admission accumulates lru_stats itself (reference :874-880)."""
+
+    def decode_routing_stats(self) -> dict:
+        """Routing concentration per layer from the decode_freq histogram (collect_decode_freq),
+        averaged over the layers that saw routes (reference :941-971): the mean and largest
+        working set (experts routed to at least once), the experts that cover 90 % of the
+        routes, the entropy of the routing normalised by log(num_experts), and the hit rate
+        of an oracle that keeps each layer's cache_size / num_layers most routed experts.
+        Empty when nothing was counted."""
+        freq = self.decode_freq.double().cpu()
+        total = freq.sum(dim=1)
+        valid = total > 0
+        if not bool(valid.any()):
+            return {}
+        per_layer = self.cache_size / self.num_layers
+        keep = max(1, int(round(per_layer)))
+        ranked = torch.sort(freq, dim=1, descending=True).values
+        f, t, r = freq[valid], total[valid], ranked[valid]
+        working = (f > 0).sum(dim=1).double()
+        share = torch.cumsum(r, dim=1) / t.unsqueeze(1)
+        cover90 = (share < 0.9).sum(dim=1).double() + 1
+        p = f / t.unsqueeze(1)
+        entropy = -(p * torch.log(p.clamp(min=1e-12))).sum(dim=1)
+        return {
+            "slots_per_layer": per_layer,
+            "working_set_mean": working.mean().item(),
+            "working_set_max": int(working.max().item()),
+            "experts_for_90pct": cover90.mean().item(),
+            "oracle_hit_at_slots": (r[:, :keep].sum(dim=1) / t).mean().item(),
+            "norm_entropy": (entropy / math.log(self.num_experts)).mean().item(),
+        }
 
 
 __all__ = ["OffloadMoeCache", "StagedRoutes", "POLICIES", "BANK_NAMES"]

@@ -1,33 +1,26 @@
 """Device-side bookkeeping of OffloadMoeCache (reference src/plastic_infer/moe/offload_kernels.py),
 on the HIP slot-cache kernels. Every call is one launch on the current stream with no host
-synchronisation, so the decode-time admission -> copy -> GEMM chain stays capturable."""
+synchronisation, so the decode-time admission -> copy -> GEMM chain stays capturable.
+
+The functions take the cache as their first argument, as the reference's do, and act on its
+device maps (``slot_for_id``, ``id_of_slot``, ``usage``, ``step``) and copy plan
+(``evict_slots``, ``src_indices``, ``num_indices``)."""
 
 from __future__ import annotations
 
 import torch
 
 from .. import _native as N
-from ..kernel.lru_ensure import lru_ensure
 
 
 def ensure_experts(cache, layer_id: int, expert_ids: torch.Tensor) -> None:
-    """Make this layer's routed experts resident and rewrite ``expert_ids`` to slot ids in
-    place (reference :19-40). ``id_base`` puts the layer's experts in the flat
-    ``layer * num_experts + expert`` id space of the maps and takes the plan back to
-    layer-local rows, so ``copy_missing`` reads this layer's own host bank."""
-    lru_ensure(
-        expert_ids,
-        cache.slot_for_id.view(-1),
-        cache.id_of_slot,
-        cache.usage,
-        cache.step,
-        expert_ids,
-        cache.src_indices,
-        cache.evict_slots,
-        cache.num_indices,
-        stats=cache.lru_stats[layer_id] if cache.collect_stats else None,
-        id_base=layer_id * cache.num_experts,
-    )
+    """Make this layer's routed experts resident and rewrite ``expert_ids`` (int32) to slot ids
+    in place (reference :19-40). Under the "lru" policy this is the device admission kernel
+    with ``id_base = layer * num_experts`` (the maps index flat ``layer * E + expert`` ids and
+    the plan holds layer-local rows, so ``cache.copy_missing()`` reads this layer's own host
+    banks); under "static" the misses are staged by DMA before the call returns its stream
+    order."""
+    cache.ensure_experts(int(layer_id), expert_ids)
 
 
 def ensure_experts_hybrid(cache, layer_id: int, expert_ids: torch.Tensor, max_fetch: int,
@@ -38,39 +31,31 @@ def ensure_experts_hybrid(cache, layer_id: int, expert_ids: torch.Tensor, max_fe
 
 def prefill_hit_compact(cache, layer_id: int, buffer_id: int) -> None:
     """Compact this layer's experts resident at or above slot 2E (the double buffers own the
-    slots below) into fixed-shape gather indices (reference :63-82): buffer rows in
-    ``_prefill_hit_dst``, cache slots in ``_prefill_hit_src``, the count in
-    ``_prefill_hit_num``."""
+    slots below) into fixed-shape gather indices (reference :63-82): buffer rows
+    ``buffer_id * E + e`` in ``cache._prefill_hit_dst``, their cache slots in
+    ``cache._prefill_hit_src`` (ascending e), the count in ``cache._prefill_hit_num``."""
     E = cache.num_experts
-    row = cache.slot_for_id[layer_id]
+    if not 0 <= int(layer_id) < cache.num_layers:
+        raise ValueError(f"layer_id {layer_id} outside [0, {cache.num_layers})")
+    if int(buffer_id) not in (0, 1):
+        raise ValueError(f"buffer_id must be 0 or 1, got {buffer_id}")
+    row = cache.slot_for_id[int(layer_id)]
     N.call("pia_prefill_hit_compact", row.data_ptr(), cache._prefill_hit_dst.data_ptr(),
-           cache._prefill_hit_src.data_ptr(), cache._prefill_hit_num.data_ptr(), buffer_id * E,
-           2 * E, E, N.stream_of(row.device))
+           cache._prefill_hit_src.data_ptr(), cache._prefill_hit_num.data_ptr(),
+           int(buffer_id) * E, 2 * E, E, N.stream_of(row.device))
 
 
 def materialize_layer(cache, layer_id: int) -> None:
-    """Slots [0, E) take this layer's experts in id order; the plan copies the whole layer
-    (reference :249-285)."""
-    dev = cache.slot_for_id.device
-    N.call("pia_slot_cache_materialize", cache.slot_for_id.data_ptr(), cache.slot_for_id.numel(),
-           cache.id_of_slot.data_ptr(), cache.usage.data_ptr(), cache.id_of_slot.numel(),
-           cache.step.data_ptr(), cache.evict_slots.data_ptr(), cache.src_indices.data_ptr(),
-           cache.num_indices.data_ptr(), int(layer_id), cache.num_experts, N.stream_of(dev))
+    """Slots [0, E) take this layer's experts in id order and the plan copies the whole layer
+    (reference :85-86, :191-206, kernel :249-285); ``cache.copy_missing()`` moves the rows."""
+    cache.materialize_layer(int(layer_id))
 
 
 def reset_cache(cache) -> None:
-    """Every expert non-resident, every slot empty, clock and plan zeroed (reference
-    :226-246)."""
-    dev = cache.slot_for_id.device
-    N.call("pia_slot_cache_reset", cache.slot_for_id.data_ptr(), cache.slot_for_id.numel(),
-           cache.id_of_slot.data_ptr(), cache.usage.data_ptr(), cache.id_of_slot.numel(),
-           cache.step.data_ptr(), cache.active_mask.data_ptr(), cache.num_experts,
-           cache.num_indices.data_ptr(), N.stream_of(dev))
+    """Every expert non-resident, every slot empty, clock and plan count zeroed (reference
+    :89-94, kernel :226-246)."""
+    cache.reset()
 
 
-def invalidate_slots(cache, slot_begin: int, slot_end: int) -> None:
-    """Empty slots [slot_begin, slot_end): owners become non-resident, usage 0 (the oldest)."""
-    dev = cache.slot_for_id.device
-    N.call("pia_slot_cache_invalidate", cache.slot_for_id.data_ptr(), cache.slot_for_id.numel(),
-           cache.id_of_slot.data_ptr(), cache.usage.data_ptr(), cache.id_of_slot.numel(),
-           int(slot_begin), int(slot_end), N.stream_of(dev))
+__all__ = ["ensure_experts", "ensure_experts_hybrid", "prefill_hit_compact", "materialize_layer",
+           "reset_cache"]

@@ -197,3 +197,28 @@ def test_append_decode_rejects_bad_new_rows(dev):
     with pytest.raises(ValueError, match="dtype"):
         paged_decode_append_attention(q.to(dev), kp.to(dev), vp.to(dev), bt.to(dev),
                                       lens_t.to(dev), kn.float().to(dev), vn.to(dev))
+
+
+def test_append_qwen3_8b_b256_full_shape(dev):
+    """The kernel the decode benchmark times, at its full size: one
+    paged_decode_append_attention call on the Qwen3-8B step (B = 256, L ~ U[512, 8192], a
+    160k-page pool, seed 2). The new tokens' slots hold NaN (K) / Inf (V) before the call. The
+    pools afterwards equal the oracle's write of the new rows (OP.scatter_slots on a host copy
+    of the poisoned pools) over the whole pool, bit for bit; all 256 rows are within 2e-2 of
+    the oracle's decode over the updated pools."""
+    from test_gpu_attention import oracle_max_err_all_rows, qwen3_8b_b256_inputs
+
+    P = 16
+    q, kp, vp, bt, lens, n_pages, page, offset, slots, k_new, v_new = qwen3_8b_b256_inputs(dev)
+    pg, of = page.to(dev), offset.to(dev)
+    kp[pg, :, :, of] = float("nan")
+    vp[pg, :, :, of] = float("inf")
+    kb, vb = kp.cpu(), vp.cpu()
+    out = paged_decode_append_attention(q, kp, vp, bt.to(dev), lens.to(torch.int32).to(dev),
+                                        k_new, v_new)
+    OP.scatter_slots(k_new.cpu(), v_new.cpu(), kb, vb, slots.tolist())
+    assert torch.equal(kp.cpu(), kb), "K pool differs from the oracle's write"
+    assert torch.equal(vp.cpu(), vb), "V pool differs from the oracle's write"
+    del kb, vb
+    worst = oracle_max_err_all_rows(out.cpu(), q, kp, vp, bt, lens, n_pages, P)
+    assert worst <= BF16_TOL, worst

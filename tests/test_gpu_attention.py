@@ -185,12 +185,11 @@ def test_decode_stream_graph_replays(dev):
         assert torch.equal(paged_decode_attention(qd, kd, vd, btd, ld, workspace=ws).cpu(), eager)
 
 
-def test_decode_qwen3_8b_b256_full_shape(dev):
-    """The Qwen3-8B decode step at full size (B = 256, L ~ U[512, 8192] including the new
-    token, 160k-page pool, block tables from one seeded permutation), generated on the device:
-    the 256-row scatter is checked bit for bit over the whole pool (the new rows at their slots,
-    every other element unchanged), then the attention of all 256 sequences against the oracle
-    over their own pages (2e-2), 64 sequences at a time."""
+def qwen3_8b_b256_inputs(dev):
+    """The Qwen3-8B decode step at full size: B = 256, L ~ U[512, 8192] including the new token,
+    a 160k-page pool, block tables from one seeded permutation (host generator, seed 2), pools,
+    new rows and q drawn on the device. Returns (q, kp, vp, bt, lens, n_pages, page, offset,
+    slots, k_new, v_new); bt / lens / n_pages / page / offset / slots on the host."""
     B, Hq, Hkv, D, P, N_ = 256, 32, 8, 128, 16, 160_000
     g = torch.Generator().manual_seed(2)
     lens = torch.randint(512, 8193, (B,), generator=g)
@@ -214,17 +213,17 @@ def test_decode_qwen3_8b_b256_full_shape(dev):
     k_new = torch.randn(B, Hkv, D, generator=gd, device=dev).to(torch.bfloat16)
     v_new = torch.randn(B, Hkv, D, generator=gd, device=dev).to(torch.bfloat16)
     q = torch.randn(B, Hq, D, generator=gd, device=dev).to(torch.bfloat16)
-    kb, vb = kp.clone(), vp.clone()
-    kv_scatter(k_new, v_new, kp, vp, slots.to(dev))
-    pg, of = page.to(dev), (last % P).to(dev)
-    kb[pg, :, :, of] = k_new
-    vb[pg, :, :, of] = v_new
-    assert torch.equal(kp, kb) and torch.equal(vp, vb)
-    del kb, vb
-    out = paged_decode_attention(q, kp, vp, bt.to(dev), lens.to(torch.int32).to(dev)).cpu()
+    return q, kp, vp, bt, lens, n_pages, page, last % P, slots, k_new, v_new
+
+
+def oracle_max_err_all_rows(out, q, kp, vp, bt, lens, n_pages, P=16, chunk=64):
+    """max |out - oracle| over every row: the oracle's decode over each sequence's own pages
+    (gathered from the device pools), `chunk` sequences at a time."""
+    dev = kp.device
+    B = q.shape[0]
     worst = 0.0
-    for b0 in range(0, B, 64):
-        seqs = list(range(b0, b0 + 64))
+    for b0 in range(0, B, chunk):
+        seqs = list(range(b0, min(B, b0 + chunk)))
         ids, tables = [], []
         for b in seqs:
             n = int(n_pages[b])
@@ -232,12 +231,30 @@ def test_decode_qwen3_8b_b256_full_shape(dev):
             ids += bt[b, :n].tolist()
         sel = torch.tensor(ids, device=dev)
         kl, vl = kp.index_select(0, sel).cpu(), vp.index_select(0, sel).cpu()
-        btl = torch.zeros(64, 512, dtype=torch.int32)
+        btl = torch.zeros(len(seqs), bt.shape[1], dtype=torch.int32)
         for i, t in enumerate(tables):
             btl[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
-        ref = OP.decode_batch(q[b0:b0 + 64].cpu(), kl, vl, btl, lens[seqs], P)
-        err = (out[b0:b0 + 64].float() - ref.float()).abs().max().item()
+        ref = OP.decode_batch(q[seqs].cpu(), kl, vl, btl, lens[seqs], P)
+        err = (out[seqs].float() - ref.float()).abs().max().item()
         worst = max(worst, err)
+    return worst
+
+
+def test_decode_qwen3_8b_b256_full_shape(dev):
+    """The Qwen3-8B decode step at full size through the two-launch path: the 256-row scatter
+    is checked bit for bit over the whole pool (the new rows at their slots, every other
+    element unchanged), then the attention of all 256 sequences against the oracle over their
+    own pages (2e-2), 64 sequences at a time."""
+    q, kp, vp, bt, lens, n_pages, page, offset, slots, k_new, v_new = qwen3_8b_b256_inputs(dev)
+    kb, vb = kp.clone(), vp.clone()
+    kv_scatter(k_new, v_new, kp, vp, slots.to(dev))
+    pg, of = page.to(dev), offset.to(dev)
+    kb[pg, :, :, of] = k_new
+    vb[pg, :, :, of] = v_new
+    assert torch.equal(kp, kb) and torch.equal(vp, vb)
+    del kb, vb
+    out = paged_decode_attention(q, kp, vp, bt.to(dev), lens.to(torch.int32).to(dev)).cpu()
+    worst = oracle_max_err_all_rows(out, q, kp, vp, bt, lens, n_pages)
     assert worst <= BF16_TOL, worst
 
 

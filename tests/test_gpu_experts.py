@@ -157,3 +157,38 @@ def test_pool_policy_matches_oracle_on_random_traffic(dev, bank):
         o.release(layer, ids)
         assert set(p.pool._pages) == o.resident()
     assert (p.hits, p.misses) == (o.hits, o.misses)
+
+
+def test_alloc_pinned_exact(dev):
+    """Exact-size page-locked host tensors: pinned, contiguous, of the asked shape and dtype;
+    rows move to and from the device bit for bit, also through the multi-bank index copy that
+    reads them through their device mapping; a tensor of 0 elements has its shape."""
+    from plastic_infer.kernel.pinned import alloc_pinned_exact
+
+    g = torch.Generator().manual_seed(61)
+    for dtype, shape in ((torch.bfloat16, (5, 3, 256)), (torch.float32, (7, 100)),
+                         (torch.float16, (1, 8))):
+        t = alloc_pinned_exact(shape, dtype)
+        assert t.shape == shape and t.dtype == dtype and t.is_contiguous() and t.is_pinned()
+        src = torch.randn(shape, generator=g).to(dtype)
+        t.copy_(src)
+        d = t.to(dev, non_blocking=True)
+        torch.cuda.synchronize(dev)
+        assert torch.equal(d.cpu(), src)
+        back = alloc_pinned_exact(shape, dtype)
+        back.copy_(d, non_blocking=True)
+        torch.cuda.synchronize(dev)
+        assert torch.equal(back, src)
+    bank = alloc_pinned_exact((6, 512), torch.bfloat16)
+    bank.copy_(torch.randn(6, 512, generator=g).to(torch.bfloat16))
+    dst = torch.zeros(4, 512, dtype=torch.bfloat16, device=dev)
+    dp = torch.tensor([dst.data_ptr()], dtype=torch.int64, device=dev)
+    sp = torch.tensor([device_ptr(bank)], dtype=torch.int64, device=dev)
+    fb = torch.tensor([1024], dtype=torch.int64, device=dev)
+    fast_index_copy_multi(dp, sp, fb, torch.tensor([3, 0], dtype=torch.int32, device=dev),
+                          torch.tensor([5, 2], dtype=torch.int32, device=dev))
+    exp = torch.zeros(4, 512, dtype=torch.bfloat16)
+    exp[3], exp[0] = bank[5], bank[2]
+    assert torch.equal(dst.cpu(), exp)
+    z = alloc_pinned_exact((0, 4), torch.bfloat16)
+    assert z.shape == (0, 4) and z.dtype == torch.bfloat16

@@ -84,13 +84,24 @@ def test_permute_token_major_matches_row_major(dev, seed, T, k, E, bs, H, dtype)
     ids = torch.tensor(rng.integers(-1, E + 1, size=(T, k)), dtype=torch.int32, device=dev)
     hidden = torch.randn(T, H, generator=torch.Generator().manual_seed(seed)).to(dtype).to(dev)
     s, _, npp, pos = moe_align_block_size(ids, bs, E, return_route_pos=True)
-    a = moe_permute(hidden, s, npp, k)
+    a = torch.full((s.numel(), H), 5.0, dtype=dtype, device=dev)
+    moe_permute(hidden, s, npp, k, out=a)
     b = torch.full_like(a, 3.0)
     moe_permute(hidden, s, npp, k, out=b, route_pos=pos)
-    n = int(npp.item())
-    assert torch.equal(a[:n], b[:n]) and bool((b[n:] == 3.0).all())
     rs, _, rnpp, _ = OM.moe_align_block_size(ids.cpu().numpy(), bs, E)
-    assert torch.equal(b[:rnpp].cpu(), OM.permute(hidden.cpu(), rs, rnpp, k))
+    ref = OM.permute(hidden.cpu(), rs, rnpp, k)
+    _check_permuted(a, 5.0, s, npp, T * k, ref)
+    _check_permuted(b, 3.0, s, npp, T * k, ref)
+
+
+def _check_permuted(out, fill, sorted_ids, npp, numel, ref):
+    """Rows of real routes equal the oracle's permute bit for bit; padding rows (sentinel ids)
+    and rows past npp still hold `fill` (the permute leaves them untouched)."""
+    n = int(npp.item())
+    real = (sorted_ids[:n] < numel).cpu()
+    got = out.cpu()
+    assert torch.equal(got[:n][real], ref[real])
+    assert bool((got[:n][~real] == fill).all()) and bool((got[n:] == fill).all())
 
 
 def test_align_empty(dev):
@@ -104,15 +115,15 @@ def test_permute_combine_t4096(dev):
     T, k = ids.shape
     s, e, npp, pos = moe_align_block_size(ids.to(dev), 64, 128, return_route_pos=True)
     hidden = wl.hidden.to(dev)
-    xp = moe_permute(hidden, s, npp, k)
+    xp = torch.full((s.numel(), hidden.shape[1]), 5.0, dtype=hidden.dtype, device=dev)
+    moe_permute(hidden, s, npp, k, out=xp)
     rs, _, rnpp, rpos = OM.moe_align_block_size(ids.numpy(), 64, 128)
     ref_xp = OM.permute(wl.hidden, rs, rnpp, k)
-    assert torch.equal(xp[:rnpp].cpu(), ref_xp)
-    # token-major path (each token row read once): same rows, and rows past npp untouched
+    _check_permuted(xp, 5.0, s, npp, T * k, ref_xp)
+    # token-major path (each token row read once): the same rows, the rest untouched
     xt = torch.full_like(xp, 7.0)
     moe_permute(hidden, s, npp, k, out=xt, route_pos=pos)
-    assert torch.equal(xt[:rnpp].cpu(), ref_xp)
-    assert bool((xt[rnpp:] == 7.0).all())
+    _check_permuted(xt, 7.0, s, npp, T * k, ref_xp)
     out = moe_unpermute(xp, pos, w.to(dev), T, k)              # identity expert stand-in
     ref = OM.unpermute(ref_xp, rpos, w.numpy(), T, k, torch.bfloat16)
     assert torch.equal(out.cpu(), ref)

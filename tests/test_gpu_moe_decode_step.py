@@ -188,3 +188,91 @@ def test_qwen3_30b_a3b_layer_shape_two_layers(dev):
             assert rel < 1e-2, (l, rel)
     assert torch.equal(logits["static"].cpu(), logits["lru"].cpu())
     assert torch.isfinite(logits["static"].float()).all()
+
+
+def test_qwen3_30b_a3b_full_depth_step(dev):
+    """Config 5 at full depth, in the order the product runs: one MoePagedDecoder.step over the
+    48-layer Qwen3-30B-A3B (64 rows x 4096 context, 32 q / 4 kv heads, 128 experts top-8,
+    expert slots for 50 % of the 6144 experts) under both residency policies, with the
+    overlapped FFN. The layer hook only keeps tensors (device gathers of the routed experts'
+    slot rows, enqueued on the compute stream; no synchronisation), so layers run as they do
+    in the product. After the step: the slot rows every route of layers 0, 23 and 47 read equal
+    the host banks bit for bit; the attention (2e-2) and routed FFN (1e-2 of its largest
+    magnitude) of sampled rows of those layers equal the oracle's; both policies give
+    bit-identical finite logits; the global LRU over 3072 slots admits every expert it is
+    routed to (hit rate 0: the 48 layers route ~6000 distinct experts per step), the static
+    policy serves the resident half from HBM (hit rate ~0.5)."""
+    from plastic_infer.exec.runner_moe_paged import qwen3_30b_a3b_config
+
+    cfg = qwen3_30b_a3b_config(n_layers=48, max_seq_len=4096)
+    cfg.vocab_size = 4096             # the LM head's size does not touch the path under test
+    L, E = cfg.n_layers, cfg.n_experts
+    B, ctx = 64, 4096
+    n_pages = L * B * ctx // P
+    w = random_dense_weights(cfg, dev, seed=51)
+    banks = random_expert_banks(cfg, dev, seed=52)
+    kp0, vp0 = _pools(dev, n_pages, cfg.n_kv_heads, cfg.head_dim, 53)
+    batch, tables = _batch(dev, cfg, [ctx] * B, n_pages, 54)
+    tokens = torch.randint(0, cfg.vocab_size, (B,), generator=torch.Generator().manual_seed(55))
+    tokens = tokens.to(dev)
+    checked = (0, 23, 47)
+    picks = [0, 21, 42, 63]
+    logits, rates = {}, {}
+    for policy in ("static", "lru"):
+        kp, vp = kp0.clone(), vp0.clone()
+        cache = _cache(dev, cfg, banks, policy)
+        cache.collect_stats = True
+        dec = MoePagedDecoder(w, cfg, cache, kp, vp, max_batch=B, overlap=True)
+        seen = {}
+
+        def hook(l, d, cache=cache):
+            if l not in checked:
+                return
+            # clamped so that the gather stays in bounds whatever the slots hold; every slot is
+            # checked to be a real one after the step
+            rows = d["slots"].reshape(-1).long().clamp(0, cache.cache_size - 1)
+            seen[l] = {k: d[k] for k in ("q", "attn", "moe_in", "topk_weights", "topk_ids",
+                                           "routed", "slots")}
+            seen[l]["rows"] = {n: cache.bank_caches[n].index_select(0, rows)
+                               for n in ("gate_up", "down")}
+
+        dec.layer_hook = hook
+        logits[policy] = dec.step(tokens, batch)
+        torch.cuda.synchronize(dev)
+        rates[policy] = cache.decode_miss_stats()
+        assert rates[policy]["layer_calls"] == L
+        for l in checked:
+            d = seen[l]
+            assert bool((d["slots"] >= 0).all()), (policy, l)
+            ids = d["topk_ids"].reshape(-1).long().cpu()
+            for name in ("gate_up", "down"):
+                host = banks[name][l].index_select(0, ids).to(dev)
+                assert torch.equal(d["rows"][name], host), (policy, l, name)
+            del d["rows"]
+            if policy != "static":
+                continue
+            sel = torch.tensor(picks, device=dev)
+            pages = sorted({p for b in picks for p in tables[b][l]})
+            remap = {p: i for i, p in enumerate(pages)}
+            psel = torch.tensor(pages, device=dev)
+            kl, vl = kp.index_select(0, psel).cpu(), vp.index_select(0, psel).cpu()
+            bt = torch.tensor([[remap[p] for p in tables[b][l]] for b in picks], dtype=torch.int32)
+            ref_attn = OP.decode_batch(d["q"][sel].cpu(), kl, vl, bt, [ctx] * len(picks), P)
+            err = (d["attn"][sel].cpu().float() - ref_attn.float()).abs().max().item()
+            assert err <= 2e-2, (l, err)
+            x, tw, ti = d["moe_in"][sel].cpu(), d["topk_weights"][sel].cpu(), \
+                d["topk_ids"][sel].cpu()
+            used = torch.unique(ti)
+            remap_e = torch.full((E,), -1, dtype=torch.int64)
+            remap_e[used] = torch.arange(used.numel())
+            ref_ffn = OF.fused_experts(x, banks["gate_up"][l][used], banks["down"][l][used], tw,
+                                       remap_e[ti.long()].to(torch.int32))
+            got = d["routed"][sel].cpu().float()
+            rel = (got - ref_ffn.float()).abs().max().item() / ref_ffn.float().abs().max().item()
+            assert rel < 1e-2, (l, rel)
+        del dec, cache, kp, vp, seen
+        torch.cuda.empty_cache()
+    assert torch.equal(logits["static"].cpu(), logits["lru"].cpu())
+    assert torch.isfinite(logits["static"].float()).all()
+    assert rates["lru"]["hit_rate"] == 0.0, rates["lru"]
+    assert 0.4 < rates["static"]["hit_rate"] < 0.6, rates["static"]

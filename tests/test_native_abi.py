@@ -51,18 +51,41 @@ def test_invalid_arguments_are_rejected_without_device_work():
     assert rc == -1 and b"num_heads % num_kv_heads" in lib.pia_last_error()
     rc = lib.pia_moe_topk(None, None, None, 0, 4, 8, 9, 1, 0, -1, None)
     assert rc == -1
-    # G = 4: two partial slots (128 accumulators + max + sum, fp32) per wave for up to 4096
-    # waves, then one 64-bit arrival counter per wave (4096, plus two ints to reach an 8-byte
-    # boundary from a 4-byte aligned workspace); independent of the batch
-    assert N.query("pia_paged_decode_workspace_bytes", 256, 32, 8, 128, 16, 512) == \
-        4096 * 2 * 4 * 130 * 4 + (2 * 4096 + 2) * 4
-    assert N.query("pia_paged_decode_workspace_bytes", 1, 32, 8, 128, 16, 4) == \
-        4096 * 2 * 4 * 130 * 4 + (2 * 4096 + 2) * 4
-    # G = 8: the same layout with eight q rows per partial slot
-    assert N.query("pia_paged_decode_workspace_bytes", 256, 64, 8, 128, 16, 512) == \
-        4096 * 2 * 8 * 130 * 4 + (2 * 4096 + 2) * 4
+    # the workspace is the decode scratch layout at 4096 waves, independent of the batch
+    for hq in (8, 16, 32, 64):
+        off, total = ctypes.c_int64(), ctypes.c_int64()
+        assert lib.pia_paged_decode_scratch_layout(hq, 8, 4096, ctypes.byref(off),
+                                                   ctypes.byref(total)) == 0
+        for b, bt in ((256, 512), (1, 4)):
+            assert N.query("pia_paged_decode_workspace_bytes", b, hq, 8, 128, 16, bt) == \
+                total.value
     # general kernel (head_dim 64, or G = 3): no workspace
     assert N.query("pia_paged_decode_workspace_bytes", 4, 4, 4, 64, 16, 8) == 0
     assert N.query("pia_paged_decode_workspace_bytes", 4, 24, 8, 128, 16, 8) == 0
     with pytest.raises(N.NativeError):
         N.call("pia_moe_sum_reduce", None, None, 1, 0, 4, 2, None)
+
+
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+def test_decode_scratch_layout(group):
+    """The one layout every decode entry point uses: the arrival counters (one 8-byte word per
+    wave, starting at the first 8-byte boundary of a buffer that is only 4-byte aligned) end
+    before the partials, which are exactly two slots of `group` rows x (128 + 2) fp32 per wave
+    and end at the total. A layout whose counters follow partial slots sized for another group
+    (a past fault of this kind) breaks the first or the last assertion."""
+    lib = N.load()
+    prev_total = 0
+    for waves in (2, 6, 256, 1024, 2048, 4094, 4096):
+        off, total = ctypes.c_int64(), ctypes.c_int64()
+        assert lib.pia_paged_decode_scratch_layout(8 * group, 8, waves, ctypes.byref(off),
+                                                   ctypes.byref(total)) == 0
+        assert off.value % 256 == 0
+        assert 4 + 8 * waves <= off.value, "counters overrun the partials"
+        assert total.value - off.value == waves * 2 * group * (128 + 2) * 4
+        assert total.value > prev_total
+        prev_total = total.value
+    off, total = ctypes.c_int64(), ctypes.c_int64()
+    assert lib.pia_paged_decode_scratch_layout(24, 8, 64, ctypes.byref(off),
+                                               ctypes.byref(total)) == -2
+    assert lib.pia_paged_decode_scratch_layout(32, 8, 4097, ctypes.byref(off),
+                                               ctypes.byref(total)) == -1
