@@ -269,8 +269,8 @@ def bench_prefill_write(torch, dev, args) -> dict:
     scatter_bytes = total * row * 2 * 2 + total * 8     # K+V read and written, slots
     gather_bytes = total * row * 2 * 2 + int(n_pages.sum()) * 4 + (PF_B + 1) * 8
     step_bytes = scatter_bytes + gather_bytes
-    dom, dom_bytes, dom_ms = (("kv_scatter_kernel", scatter_bytes, sc_ms) if sc_ms >= ga_ms
-                              else ("kv_gather_kernel", gather_bytes, ga_ms))
+    dom, dom_bytes, dom_ms = (("kv_scatter16_kernel", scatter_bytes, sc_ms) if sc_ms >= ga_ms
+                              else ("kv_gather16_kernel", gather_bytes, ga_ms))
     cpu = None
     if not args.no_cpu_baseline:
         cpu = _cpu_prefill_write(torch, k, v, slots, num_pages, total, scatter_bytes)
@@ -355,7 +355,7 @@ def bench_moe_permute(torch, dev, args) -> dict:
     comb_bytes = T * K * H * 2 + T * H * 2 + T * K * 4 + T * K * 4
     step_bytes = route_bytes + perm_bytes + comb_bytes
     phases = [("moe_topk_hist + moe_align_place", route_bytes, route_ms),
-              ("moe_permute_kernel", perm_bytes, perm_ms),
+              ("moe_permute_tokens_kernel", perm_bytes, perm_ms),
               ("moe_combine_kernel", comb_bytes, comb_ms)]
     dom, dom_bytes, dom_ms = max(phases, key=lambda x: x[2])
     cpu = None
