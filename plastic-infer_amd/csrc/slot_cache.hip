@@ -323,6 +323,155 @@ __global__ __launch_bounds__(LRU_THREADS) void lru_ensure_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------
+// Admission of queries longer than LRU_MAX_QUERY ids (caches of up to LRU_MAX_CACHED slots), with
+// the same decisions and no scratch memory: the query is not held in LDS. Hits take the new step
+// and every missing id is marked in slot_of_id itself (kMark, a value no slot takes); a scan of
+// the queried id range in ascending order then lists the marked ids in batches of up to
+// LRU_MAX_QUERY, and each batch takes, in order, the least-recently-used slots not touched by
+// this call (victims of earlier batches carry this call's step, so they are touched), exactly
+// the slots the ascending misses take one by one in the sequential rule. Ids left without a slot
+// are unmarked (-1). Finally every query position reads its slot back from the maps.
+// (Assumes consistent maps: id_of_slot[slot_of_id[g]] == g for every resident id g.)
+// ---------------------------------------------------------------------------------------------
+constexpr int32_t kMark = -2;
+constexpr int LRU_WIDE_MAX_QUERY = 1 << 24;
+
+// One batch: the n ids in miss_ids[0, n) (ascending) take the n smallest (usage, slot) of the
+// slots whose usage is not `step`, as far as such slots exist; maps, usage and the plan (at
+// plan_at) are written. Returns the number admitted. Starts and ends with the workgroup in step.
+__device__ int lru_wide_admit(int n, const int32_t* miss_ids, int32_t* victims,
+                              int32_t* __restrict__ slot_of_id, int64_t num_total,
+                              int32_t* __restrict__ id_of_slot, int64_t* __restrict__ usage,
+                              int C, int64_t step, int32_t* __restrict__ src_plan,
+                              int32_t* __restrict__ dst_plan, int plan_at, int64_t id_base,
+                              int* red, long long* red64) {
+  const int tid = threadIdx.x;
+  const int c0 = tid * LRU_SPT;
+  long long u[LRU_SPT];
+#pragma unroll
+  for (int s = 0; s < LRU_SPT; ++s) {
+    const int c = c0 + s;
+    u[s] = kUsageNone;
+    if (c < C) {
+      const int64_t v = usage[c];
+      if (v != step) u[s] = v;
+    }
+  }
+  int taken = 0;
+  while (taken < n) {
+    long long lmin = kUsageNone;
+#pragma unroll
+    for (int s = 0; s < LRU_SPT; ++s) lmin = min(lmin, u[s]);
+    const long long umin = block_min64(lmin, red64);
+    if (umin == kUsageNone) break;  // no evictable slot left
+    int cnt = 0;
+#pragma unroll
+    for (int s = 0; s < LRU_SPT; ++s) cnt += u[s] == umin ? 1 : 0;
+    int total;
+    int pos = taken + block_excl_scan(cnt, red, &total);
+#pragma unroll
+    for (int s = 0; s < LRU_SPT; ++s)
+      if (u[s] == umin) {
+        if (pos < n) victims[pos] = c0 + s;
+        ++pos;
+        u[s] = kUsageNone;
+      }
+    taken += min(total, n - taken);
+  }
+  __syncthreads();  // victims[] complete
+  for (int i = tid; i < n; i += LRU_THREADS) {
+    const int32_t e = miss_ids[i];
+    if (i >= taken) {  // no slot left for it
+      slot_of_id[e] = -1;
+      continue;
+    }
+    const int victim = victims[i];
+    const int32_t old = id_of_slot[victim];
+    if (old >= 0 && old < num_total) slot_of_id[old] = -1;
+    id_of_slot[victim] = e;
+    slot_of_id[e] = victim;
+    usage[victim] = step;
+    dst_plan[plan_at + i] = victim;
+    src_plan[plan_at + i] = int32_t(int64_t(e) - id_base);
+  }
+  __syncthreads();  // maps written; miss_ids / victims may be reused
+  return taken;
+}
+
+__global__ __launch_bounds__(LRU_THREADS) void lru_ensure_wide_kernel(
+    const int32_t* __restrict__ query, int K, int32_t* __restrict__ slot_of_id,
+    int64_t num_total, int32_t* __restrict__ id_of_slot, int64_t* __restrict__ usage, int C,
+    int64_t* __restrict__ step_ptr, int32_t* __restrict__ out, int32_t* __restrict__ src_plan,
+    int32_t* __restrict__ dst_plan, int64_t* __restrict__ num_copy, int64_t* __restrict__ stats,
+    int64_t id_base) {
+  __shared__ int32_t miss_ids[LRU_MAX_QUERY];
+  __shared__ int32_t victims[LRU_MAX_QUERY];
+  __shared__ int red[LRU_THREADS / 64 + 1];
+  __shared__ long long red64[LRU_THREADS / 64];
+  __shared__ int64_t step_lds;
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    const int64_t s = *step_ptr + 1;
+    *step_ptr = s;
+    step_lds = s;
+  }
+  __syncthreads();
+  const int64_t step = step_lds;
+  // hits take the step, missing ids are marked; the range of the valid ids
+  long long lo = kUsageNone, neg_hi = kUsageNone;
+  for (int i = tid; i < K; i += LRU_THREADS) {
+    const int64_t g = int64_t(query[i]) + id_base;
+    if (g < 0 || g >= num_total) continue;  // inert: never resident, never admitted
+    const int32_t s = slot_of_id[g];
+    if (s >= 0 && s < C) usage[s] = step;   // duplicated hits store the same value
+    else slot_of_id[g] = kMark;             // a map entry past the cache is not a hit
+    lo = min(lo, (long long)g);
+    neg_hi = min(neg_hi, -(long long)g);
+  }
+  lo = block_min64(lo, red64);
+  const long long hi = -block_min64(neg_hi, red64);
+  __syncthreads();  // marks and hit bumps are visible to the whole workgroup
+  // distinct hits: the slots that carry the new step
+  int nhit = 0;
+  for (int c = tid; c < C; c += LRU_THREADS) nhit += usage[c] == step ? 1 : 0;
+  const int hits = block_sum(nhit, red);
+  // the marked ids in ascending order, admitted a batch at a time
+  int admitted = 0, misses = 0, nb = 0;
+  for (long long base = lo; base <= hi; base += LRU_THREADS) {
+    const long long g = base + tid;
+    const int mk = (g <= hi && slot_of_id[g] == kMark) ? 1 : 0;
+    int total;
+    const int pos = block_excl_scan(mk, red, &total);
+    if (nb + total > LRU_MAX_QUERY) {  // uniform: the batch is full
+      admitted += lru_wide_admit(nb, miss_ids, victims, slot_of_id, num_total, id_of_slot,
+                                 usage, C, step, src_plan, dst_plan, admitted, id_base, red,
+                                 red64);
+      nb = 0;
+    }
+    if (mk) miss_ids[nb + pos] = int32_t(g);
+    nb += total;
+    misses += total;
+    __syncthreads();  // miss_ids of this chunk written
+  }
+  if (nb > 0)
+    admitted += lru_wide_admit(nb, miss_ids, victims, slot_of_id, num_total, id_of_slot, usage,
+                               C, step, src_plan, dst_plan, admitted, id_base, red, red64);
+  // out may alias query: each position is read and then written by the same thread
+  for (int i = tid; i < K; i += LRU_THREADS) {
+    const int64_t g = int64_t(query[i]) + id_base;
+    out[i] = (g >= 0 && g < num_total) ? slot_of_id[g] : -1;
+  }
+  if (tid == 0) {
+    *num_copy = admitted;
+    if (stats) {
+      stats[0] += hits + misses;
+      stats[1] += admitted;
+      stats[2] += 1;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Admission over caches larger than the LDS-resident kernel holds (16384 < C <= 2^24 slots):
 // the same decisions, with the slot state streamed from global memory. Phase 1 is shared.
 // Victims: the `take` = min(M, evictable) smallest (usage, slot) keys among the untouched
@@ -681,14 +830,23 @@ extern "C" int pia_lru_ensure(const int32_t* query, int64_t num_queries, int32_t
                               int64_t* stats, int64_t id_base, void* stream) {
   if (num_queries < 0 || num_total < 0 || num_cached < 0)
     return fail(PIA_EINVAL, "lru_ensure: negative size");
-  if (num_queries > LRU_MAX_QUERY)
-    return fail(PIA_EUNSUPPORTED, "lru_ensure: more than 2048 queries per call");
   if (num_cached < 1 || num_cached > LRU_STREAM_MAX_CACHED)
     return fail(PIA_EUNSUPPORTED, "lru_ensure: cache of 1..2^24 slots supported");
+  if (num_queries > LRU_MAX_QUERY &&
+      (num_queries > LRU_WIDE_MAX_QUERY || num_cached > LRU_MAX_CACHED))
+    return fail(PIA_EUNSUPPORTED, "lru_ensure: more than 2048 queries per call need a cache of "
+                                  "at most 16384 slots, and at most 2^24 queries");
   if (num_total > 0x7fffffff) return fail(PIA_EINVAL, "lru_ensure: id space beyond int32");
   if (!slot_of_id || !id_of_slot || !lru_usage || !lru_step || !num_copy ||
       (num_queries > 0 && (!query || !out_indices)) || !src_indices || !dst_indices)
     return fail(PIA_EINVAL, "lru_ensure: null pointer");
+  if (num_queries > LRU_MAX_QUERY) {
+    hipLaunchKernelGGL(lru_ensure_wide_kernel, dim3(1), dim3(LRU_THREADS), 0, as_stream(stream),
+                       query, int(num_queries), slot_of_id, num_total, id_of_slot, lru_usage,
+                       int(num_cached), lru_step, out_indices, src_indices, dst_indices,
+                       num_copy, stats, id_base);
+    return check_launch("lru_ensure_wide");
+  }
   if (num_cached > LRU_MAX_CACHED) {
     hipLaunchKernelGGL(lru_ensure_stream_kernel, dim3(1), dim3(LRU_THREADS), 0, as_stream(stream),
                        query, int(num_queries), slot_of_id, num_total, id_of_slot, lru_usage,

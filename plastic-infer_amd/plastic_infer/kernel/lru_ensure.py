@@ -29,7 +29,9 @@ class Stat(IntEnum):
 
 N_STATS = len(Stat)
 _STRATEGIES = ("seq", "insert")
-MAX_QUERY = 2048
+MAX_QUERY = 2048         # queries held in LDS; longer ones take the wide-query kernel
+MAX_QUERY_WIDE = 1 << 24
+MAX_CACHED_WIDE = 16384  # the wide-query kernel's cache limit
 MAX_CACHED = 1 << 24     # caches above 16384 slots take the streaming kernel
 
 
@@ -60,7 +62,9 @@ def lru_ensure(
     out_indices (K,) int32 out (may alias query); src_indices / dst_indices (>= min(K,
     num_cached),) int32 out; num_copy int64 [1] or () out; stats (3,) int64 accumulator or None.
     The distinct missing ids, ascending, take the least-recently-used slots not touched by
-    this call, lowest slot first on equal usage. K <= 2048, num_cached <= 2^24.
+    this call, lowest slot first on equal usage. num_cached <= 2^24; K <= 2048, or up to 2^24
+    with num_cached <= 16384 (a query longer than 2048 ids is admitted in ascending batches of
+    2048 distinct misses, with the same decisions).
     """
     if strategy is not None and strategy not in _STRATEGIES:
         raise KeyError(strategy)
@@ -94,8 +98,10 @@ def lru_ensure(
         N.require_device(stats, names=("stats",))
         _check(stats.dtype == torch.int64 and stats.numel() == N_STATS and stats.is_contiguous(),
                "stats must be a contiguous int64 [3] tensor")
-    if k > MAX_QUERY or num_cached > MAX_CACHED:
-        raise ValueError(f"lru_ensure supports K <= {MAX_QUERY} and num_cached <= {MAX_CACHED}")
+    if num_cached > MAX_CACHED or k > MAX_QUERY_WIDE or \
+            (k > MAX_QUERY and num_cached > MAX_CACHED_WIDE):
+        raise ValueError(f"lru_ensure supports num_cached <= {MAX_CACHED} with K <= {MAX_QUERY}, "
+                         f"and K <= {MAX_QUERY_WIDE} with num_cached <= {MAX_CACHED_WIDE}")
     N.call("pia_lru_ensure", query.data_ptr(), k, slot_of_id.data_ptr(), slot_of_id.numel(),
            id_of_slot.data_ptr(), lru_usage.data_ptr(), num_cached, lru_step.data_ptr(),
            out_indices.data_ptr(), src_indices.data_ptr(), dst_indices.data_ptr(),

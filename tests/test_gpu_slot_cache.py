@@ -45,8 +45,11 @@ class DevState:
     (0, 4, 16, 20, 12, 40),       # small cache, constant cross-layer eviction
     (1, 48, 128, 3072, 512, 12),  # Qwen3-30B-A3B decode shape: B=64 x top-8 over 50% slots
     (2, 2, 8, 8, 64, 30),         # many duplicates, cache exactly one layer
-    (3, 1, 2048, 2048, 2048, 4),  # the largest query
+    (3, 1, 2048, 2048, 2048, 4),  # the largest query held in LDS
     (4, 3, 1, 1, 3, 10),          # one slot
+    (5, 48, 128, 3072, 4096, 10), # 512 rows x top-8: the wide-query kernel
+    (6, 2, 6000, 5000, 6000, 5),  # up to 5000 misses a call: several batches of 2048
+    (7, 3, 40, 50, 2500, 12),     # long queries of few distinct ids, many duplicates
 ])
 def test_lru_ensure_matches_oracle(dev, seed, layers, experts, cached, k, calls):
     rng = np.random.default_rng(seed)
@@ -416,3 +419,23 @@ def test_two_pass_routed_ffn_is_bit_identical(dev, policy):
         moe_sum_reduce(buf, two)
         one = fused_experts_decode_impl(x, gu, dn, w, torch.maximum(routes.in_hbm, routes.copied))
         assert torch.equal(two.cpu(), one.cpu()), layer
+
+
+def test_lru_ensure_wide_query_limits(dev):
+    """More than 2048 ids a call are admitted for caches of up to 16384 slots; a longer query
+    on a larger cache is refused before any launch (nothing changes)."""
+    ds = DevState(dev, 40000, 20000)
+    q = torch.arange(3000, dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError):
+        lru_ensure(q, ds.slot_of_id, ds.id_of_slot, ds.usage, ds.step, q, ds.src, ds.dst, ds.num)
+    assert int(ds.step) == 0 and int((ds.slot_of_id >= 0).sum()) == 0
+    # 16384 slots, 3000 ids: the wide kernel, checked against the oracle, twice (hits second)
+    st, ds = SC.new_state(40000, 16384), DevState(dev, 40000, 16384)
+    rng = np.random.default_rng(8)
+    for c in range(2):
+        query = rng.choice(40000, size=3000)
+        out, src, dst, n, _ = SC.lru_ensure(st, query)
+        assert np.array_equal(ds.ensure(query, 0), out), c
+        assert int(ds.num) == n and np.array_equal(ds.dst[:n].cpu().numpy(), dst)
+        assert np.array_equal(ds.src[:n].cpu().numpy(), src)
+        ds.assert_equal(st)
