@@ -210,7 +210,9 @@ int pia_paged_decode_attention_noalloc(void* out, const void* q, int64_t q_seq_s
  * src/plastic_infer/exec/attention.py:189; offset q_start_pos = the explicit mask of
  * src/plastic_infer/exec/runner_paged.py:61-95). Pages whose block-table id is outside
  * [0, num_pages) hold no keys, as in pia_paged_decode_attention. A row with no admissible key
- * writes zeros.
+ * writes zeros. Non-finite inputs: a NaN in q or in an admissible key of a row makes that row's
+ * output NaN (IEEE semantics throughout); keys a row may not see are excluded by selection, so
+ * a NaN there does not reach it (the reference's additive offset mask lets it through).
  * ------------------------------------------------------------------------------------------- */
 int pia_paged_attention(void* out, const void* q, const void* k_pages, const void* v_pages,
                         const int32_t* block_tables, int64_t bt_stride,

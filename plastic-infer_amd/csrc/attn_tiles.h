@@ -73,6 +73,18 @@ __device__ __forceinline__ float max_col4(float v) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// NaN-propagating max over lanes l, l ^ 16, l ^ 32, l ^ 48, as max_col4 (IEEE 754-2019 maximum:
+// a NaN in any of the four gives NaN; on gfx950 v_maximum3_f32, which needs no quieting of its
+// inputs).
+__device__ __forceinline__ float maximum_col4(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float m = __builtin_elementwise_maximum(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned w = __float_as_uint(m);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // bf16 1.0 in every element: the B operand of a row sum by the matrix cores.
 __device__ __forceinline__ uint4 bf16_ones() {
   return make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);

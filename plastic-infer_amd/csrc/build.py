@@ -41,11 +41,8 @@ COMMON_FLAGS = [
     f"-I{CSRC}",
 ]
 
-# Per-file flags. paged_prefill.hip: its kernel never depends on NaN semantics (stale V words are
-# zeroed by integer masks, keys a row may not see are replaced by -inf selects), and without
-# IEEE NaN quieting each score skips a canonicalising v_max before the row max (about 20 fewer
-# VALU instructions per 64-key tile and wave).
-FILE_FLAGS = {"paged_prefill.hip": ["-fno-honor-nans"]}
+# Per-file flags (none at present).
+FILE_FLAGS: dict[str, list[str]] = {}
 
 
 def _hipcc() -> str:

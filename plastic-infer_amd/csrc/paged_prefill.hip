@@ -316,11 +316,16 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
             if (!(t < lim_r[rb] && ((pmask >> mb) & 1))) sc[rb][mb][j] = -INFINITY;
           }
       }
+      // the row max with IEEE 754-2019 maximum (a NaN score makes it NaN, and the row's output
+      // NaN, as the reference's softmax gives): v_maximum3_f32, no quieting of the scores
       float mx = -INFINITY;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
-        mx = fmaxf(mx, fmaxf(fmaxf(sc[rb][mb][0], sc[rb][mb][1]), fmaxf(sc[rb][mb][2], sc[rb][mb][3])));
-      mx = tile::max_col4(mx);
+        mx = __builtin_elementwise_maximum(
+            mx, __builtin_elementwise_maximum(
+                    __builtin_elementwise_maximum(sc[rb][mb][0], sc[rb][mb][1]),
+                    __builtin_elementwise_maximum(sc[rb][mb][2], sc[rb][mb][3])));
+      mx = tile::maximum_col4(mx);
       // move the reference point only for a large enough rise (or the first keys of the row)
       const float mref = (mx - m[rb]) * scale_log2 > PF_RESCALE ? mx : m[rb];
       alpha[rb] = m[rb] == mref ? 1.f : __builtin_amdgcn_exp2f((m[rb] - mref) * scale_log2);

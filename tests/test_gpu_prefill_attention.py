@@ -189,3 +189,38 @@ def test_prefill_many_ragged_sequences(dev):
                                  q_start_pos=offsets[b])[0]
         err = (out[cu[b]:cu[b + 1]].float() - ref.float()).abs().max().item()
         assert err <= BF16_TOL, (b, err)
+
+
+@pytest.mark.parametrize("G", [1, 4])
+def test_prefill_nan_key_reaches_exactly_the_rows_that_see_it(dev, G):
+    """A NaN in a K token inside the context: exactly the rows allowed to attend that token get
+    NaN, in the q heads of that kv head (their softmax has a NaN score); every other output is
+    finite and within the bf16 bar of the oracle on the pool without the NaN. (The reference's
+    explicit offset mask is additive, so there a NaN score stays NaN in masked positions too and
+    the whole head becomes NaN; the kernel replaces keys a row may not see by -inf.) Pins the
+    kernel's NaN behaviour: its row max is the NaN-propagating IEEE 754-2019 maximum."""
+    Hkv = 2
+    q_rows = [80, 40]
+    kv_lens = [200, 150]
+    offsets = [kv - n for kv, n in zip(kv_lens, q_rows)]
+    kp, vp, g = _pools(40 + G, 40, Hkv)
+    bt, tables = _tables(kv_lens, 40, g)
+    q = torch.randn(sum(q_rows), Hkv * G, D, generator=g).to(torch.bfloat16)
+    tok = 150                                     # a key of sequence 0, kv head 1
+    page, off = tables[0][tok // P], tok % P
+    kp_nan = kp.clone()
+    kp_nan[page, 1, 7, off] = float("nan")
+    out, cu = _run(dev, q, kp_nan, vp, bt, kv_lens, q_rows, offsets)
+    for b in range(2):
+        rows = q[cu[b]:cu[b + 1]][None]
+        ref = OP.paged_attention(rows, kp, vp, tables[b], P, kv_lens[b], causal=True,
+                                 q_start_pos=offsets[b])[0].float()
+        got = out[cu[b]:cu[b + 1]].float()
+        want = torch.zeros(got.shape, dtype=torch.bool)
+        if b == 0:
+            sees = torch.arange(q_rows[0]) + offsets[0] >= tok
+            assert bool(sees.any()) and bool((~sees).any())
+            want[sees, G:2 * G, :] = True
+        assert torch.equal(torch.isnan(got), want), b
+        err = (got[~want] - ref[~want]).abs().max().item()
+        assert err <= BF16_TOL, (b, err)
