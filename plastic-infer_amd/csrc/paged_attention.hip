@@ -210,9 +210,12 @@ __device__ __forceinline__ int stream_range_of(int st, int Dp, int Ce) {
   return 2 * p + (st - p * Dp >= Ce ? 1 : 0);
 }
 
+// All members are ints: with a bool the struct has three bytes of tail padding, and copies of
+// the cursor through selects then went via private memory, a scratch load and store per step
+// whose wait held the step behind every load issued before it.
 struct StreamCursor {
   int b, h, ls, ns, L;  // sequence, kv head, step in the segment, steps in it, its tokens
-  bool app;             // append mode: position L - 1 is the new token given in k_new / v_new
+  int app;              // append mode: position L - 1 is the new token given in k_new / v_new
 };
 
 // seq_len LDS word: the clamped context length, bit 30 set when (append mode) the row's raw
