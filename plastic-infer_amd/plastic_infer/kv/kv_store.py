@@ -19,7 +19,7 @@ Host chunks: [n_layers, n_kv_heads, head_dim, tokens_per_chunk] CPU tensors (pin
 from __future__ import annotations
 
 import array
-from collections import OrderedDict
+import heapq
 from dataclasses import dataclass, field
 from typing import Optional
 
@@ -171,7 +171,12 @@ class KVStore:
         self.gpu = KVPagedStorage(config, total_pages=config.max_pages,
                                   device=config.device, dtype=config.dtype)
         self._host_cache: dict[bytes, tuple[torch.Tensor, torch.Tensor]] = {}
-        self._host_lru: OrderedDict[bytes, None] = OrderedDict()
+        # Host chunks are replaced least recently used first. Each use stamps its key with the
+        # next tick; the heap keeps (tick, key) for every stamp handed out, and a popped entry
+        # whose tick is no longer its key's latest is dropped on the spot.
+        self._host_tick = 0
+        self._host_stamp: dict[bytes, int] = {}
+        self._host_heap: list[tuple[int, bytes]] = []
         self._max_host_chunks = config.max_host_chunks
         self._prefix_index: dict[bytes, ChunkKey] = {}
         self._host_reads: Optional[torch.cuda.Event] = None
@@ -301,19 +306,28 @@ class KVStore:
     # -- host LRU -----------------------------------------------------------------------------
 
     def _touch_host(self, full_key: bytes) -> None:
-        self._host_lru.pop(full_key, None)
-        self._host_lru[full_key] = None
+        """Mark a cached chunk as used now."""
+        self._host_tick += 1
+        self._host_stamp[full_key] = self._host_tick
+        heapq.heappush(self._host_heap, (self._host_tick, full_key))
+        if len(self._host_heap) > 4 * len(self._host_stamp) + 64:  # mostly superseded stamps
+            self._host_heap = [(t, k) for k, t in self._host_stamp.items()]
+            heapq.heapify(self._host_heap)
 
     def _evict_host_lru(self) -> None:
-        if not self._host_lru:
+        """Drop the cached chunk whose last use is the oldest (nothing when the cache is empty)."""
+        while self._host_heap:
+            tick, key = heapq.heappop(self._host_heap)
+            if self._host_stamp.get(key) != tick:
+                continue
+            del self._host_stamp[key]
+            if self._host_reads is not None:
+                # A prefix load may still be reading this chunk's pinned memory.
+                self._host_reads.synchronize()
+                self._host_reads = None
+            del self._host_cache[key]
+            self._prefix_index.pop(key, None)
             return
-        oldest, _ = self._host_lru.popitem(last=False)
-        if self._host_reads is not None:
-            # A prefix load may still be reading this chunk's pinned memory.
-            self._host_reads.synchronize()
-            self._host_reads = None
-        del self._host_cache[oldest]
-        self._prefix_index.pop(oldest, None)
 
     @property
     def host_cache_size(self) -> int:
