@@ -26,8 +26,17 @@
 // products cover the chunk's 16 K values once (fp32 products, fp32 sums: no rounding to a
 // narrower type anywhere, the epilogue's round() is the identity).
 // The four partial tiles meet in LDS and are summed in wave order (deterministic). Workgroups
-// are persistent over the items; W rows are streamed once per plan block, which is the HBM
-// bound at decode sizes (every expert's weights are read once per 16 routes it serves).
+// are persistent over the items and pipeline them: the next item's plan block and first K stage
+// are in flight through the current item's reduction and stores. W rows are streamed once per
+// plan block, which is the HBM bound at decode sizes (every expert's weights are read once per
+// 16 routes it serves).
+//
+// Kernel: moe_gemm_cols, for K <= EG_COLS_MAX_K (a K quarter would give each wave too little
+// to stream per item: 192 elements at the MoE down projection's K = 768). A work item is one
+// wave's: 16 plan rows against 16 W rows (16 output columns), or 16 gate rows plus the matching
+// 16 up rows when the activation is fused, over the whole K, with the same lane layout and
+// products as above. The waves of a workgroup are independent: no LDS, no barrier; the sibling
+// waves of a plan block re-read its A rows from L2. Items are pipelined the same way.
 #include <type_traits>
 
 #include "pia_internal.h"
@@ -49,6 +58,7 @@ constexpr int EG_ROWS = 16;       // plan rows per work item (MFMA M)
 constexpr int EG_WAVES = 4;       // waves per workgroup, one K quarter each
 constexpr int EG_U = 2;           // 32-wide K chunks per pipeline stage
 constexpr int EG_WGS_PER_CU = 4;  // persistent workgroups per compute unit
+constexpr int EG_COLS_MAX_K = 1024;  // K up to which moe_gemm_cols runs instead of the split
 
 // 16 bytes of zeros: the load source of masked-off lanes (plan padding, K tail, W row tail).
 __device__ __attribute__((aligned(16))) uint16_t g_zero8[8];
@@ -125,69 +135,110 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_splitk(
   const int nch = (K + CH - 1) / CH;
   const int cpw = (nch + EG_WAVES - 1) / EG_WAVES;
   const int c0 = min(nch, wv * cpw), c1 = min(nch, c0 + cpw);
+  const int ns = (c1 - c0 + EG_U - 1) / EG_U;  // pipeline stages of this wave per item
   const int half = n_rows >> 1;
   const E* zero = reinterpret_cast<const E*>(g_zero8);
+  // W row of column block cb relative to block 0's (the tile's rows are in four runs of 16)
+  auto w_off = [&](int cb) { return (FUSED ? ((cb < 2 ? 0 : half) + (cb & 1) * 16) : cb * 16) * K; };
 
-  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
-    const int64_t mb = item / n_tiles;
-    const int t = int(item - mb * n_tiles);
-    const int e = expert_ids[(mb * EG_ROWS) / block_m];
-    const bool e_ok = e >= 0 && e < num_experts;
-    const int64_t p = mb * EG_ROWS + li;
-    const int64_t r = p < rows ? int64_t(sorted[p]) : numel;
-    const bool a_ok = r >= 0 && r < numel;
-    const E* arow = a + (a_ok ? (r / a_div) * lda : 0);
-    const E* wbase = w + (e_ok ? int64_t(e) * n_rows * K : 0);
-    const E* wrow[4];
-    bool w_ok[4];
+  // One item's operands for this lane: plan row li of its 16 (route r; A row arow), the W row
+  // of column block 0 (wrow0; block cb at wrow0 + w_off[cb]), bit cb of wmask = block cb's
+  // row exists, e_ok = the plan block names an expert.
+  struct Item {
+    const E* arow;
+    const E* wrow0;
+    int64_t r;
+    int wmask;
+    bool a_ok, e_ok;
+  };
+  auto make_item = [&](int64_t it, int e, int64_t r) {
+    Item o;
+    const int t = int(it - (it / n_tiles) * n_tiles);
+    o.e_ok = e >= 0 && e < num_experts;
+    o.r = r;
+    o.a_ok = r >= 0 && r < numel;
+    o.arow = a + (o.a_ok ? (r / a_div) * lda : 0);
+    const int n0 = FUSED ? t * 32 + li : t * 64 + li;  // column block 0's row
+    o.wrow0 = w + (o.e_ok ? int64_t(e) * n_rows * K : 0) + int64_t(n0) * K;
+    o.wmask = 0;
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
-      int n;
-      bool ok;
-      if constexpr (FUSED) {
-        const int col = t * 32 + (cb & 1) * 16 + li;
-        ok = col < half;
-        n = (cb < 2 ? 0 : half) + col;
-      } else {
-        n = t * 64 + cb * 16 + li;
-        ok = n < n_rows;
-      }
-      w_ok[cb] = ok;
-      wrow[cb] = wbase + int64_t(ok ? n : 0) * K;
+      const bool ok = FUSED ? (t * 32 + (cb & 1) * 16 + li < half) : (n0 + cb * 16 < n_rows);
+      o.wmask |= ok ? (1 << cb) : 0;
     }
-    f32x4_t acc[4];
+    return o;
+  };
+  // an item's plan block: its expert (uniform) and this lane's route
+  auto item_expert = [&](int64_t it) { return expert_ids[((it / n_tiles) * EG_ROWS) / block_m]; };
+  auto item_route = [&](int64_t it) -> int64_t {
+    const int64_t p = (it / n_tiles) * EG_ROWS + li;
+    return p < rows ? int64_t(sorted[p]) : numel;
+  };
+
+  // Masked lanes read the zero vector instead, so every load is issued unconditionally and the
+  // compiler can keep a whole stage in flight while the previous one is multiplied.
+  auto load = [&](uint4(&va)[EG_U], uint4(&vb)[EG_U][4], const Item& o, int c) {
+#pragma unroll
+    for (int u = 0; u < EG_U; ++u) {
+      const int cc = c + u;
+      const int k = cc * CH + kg * V;
+      const bool k_ok = cc < c1 && k < K;
+      va[u] = *reinterpret_cast<const uint4*>((k_ok && o.a_ok) ? o.arow + k : zero);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+        vb[u][cb] = *reinterpret_cast<const uint4*>(
+            (k_ok && ((o.wmask >> cb) & 1)) ? o.wrow0 + w_off(cb) + k : zero);
+    }
+  };
+  f32x4_t acc[4];
+  auto mma = [&](const uint4(&va)[EG_U], const uint4(&vb)[EG_U][4]) {
+#pragma unroll
+    for (int u = 0; u < EG_U; ++u)
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma_vec<DT>(va[u], vb[u][cb], acc[cb]);
+  };
+
+  // Workgroups are persistent over the items, and items are pipelined: the next item's plan
+  // block is read when an item starts, and its first K stage is issued with the item's last
+  // stage, so it is in flight through the item's reduction and stores. Stage s of an item sits
+  // in register set x (s even) or y (s odd); the next item's first stage always goes to x (with
+  // an odd stage count, right after x's last product).
+  int64_t item = blockIdx.x;
+  if (item >= items) return;
+  Item cur = make_item(item, item_expert(item), item_route(item));
+  uint4 xa[EG_U], xb[EG_U][4], ya[EG_U], yb[EG_U][4];
+  if (cur.e_ok && ns > 0) load(xa, xb, cur, c0);
+  for (;;) {
+    const int64_t next = item + gridDim.x;
+    const bool has_next = next < items;
+    int e_next = -1;
+    int64_t r_next = numel;
+    if (has_next) {
+      e_next = item_expert(next);
+      r_next = item_route(next);
+    }
+    float w_cur = 1.0f;  // routing weight of plan row li (read by wave 0 for the epilogue)
+    if (mulw && wv == 0 && cur.a_ok) w_cur = topk_w[cur.r];
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    if (e_ok && c0 < c1) {
-      uint4 sa0[EG_U], sb0[EG_U][4], sa1[EG_U], sb1[EG_U][4];
-      // Masked lanes read the zero vector instead, so every load is issued unconditionally and
-      // the compiler can keep a whole stage in flight while the previous one is multiplied.
-      auto load = [&](uint4(&va)[EG_U], uint4(&vb)[EG_U][4], int c) {
-#pragma unroll
-        for (int u = 0; u < EG_U; ++u) {
-          const int cc = c + u;
-          const int k = cc * CH + kg * V;
-          const bool k_ok = cc < c1 && k < K;
-          va[u] = *reinterpret_cast<const uint4*>((k_ok && a_ok) ? arow + k : zero);
-#pragma unroll
-          for (int cb = 0; cb < 4; ++cb)
-            vb[u][cb] =
-                *reinterpret_cast<const uint4*>((k_ok && w_ok[cb]) ? wrow[cb] + k : zero);
+    Item nxt = cur;
+    if (has_next) nxt = make_item(next, e_next, r_next);
+    auto first_of_next = [&]() {
+      if (has_next && nxt.e_ok) load(xa, xb, nxt, c0);
+    };
+    for (int st = 0; st < ns; st += 2) {
+      if (st + 1 < ns && cur.e_ok) load(ya, yb, cur, c0 + (st + 1) * EG_U);
+      if (cur.e_ok) mma(xa, xb);
+      if (st + 1 < ns) {
+        if (st + 2 < ns) {
+          if (cur.e_ok) load(xa, xb, cur, c0 + (st + 2) * EG_U);
+        } else {
+          first_of_next();
         }
-      };
-      auto mma = [&](const uint4(&va)[EG_U], const uint4(&vb)[EG_U][4]) {
-#pragma unroll
-        for (int u = 0; u < EG_U; ++u)
-#pragma unroll
-          for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma_vec<DT>(va[u], vb[u][cb], acc[cb]);
-      };
-      load(sa0, sb0, c0);
-      for (int c = c0; c < c1; c += 2 * EG_U) {
-        load(sa1, sb1, c + EG_U);
-        mma(sa0, sb0);
-        load(sa0, sb0, c + 2 * EG_U);
-        mma(sa1, sb1);
+        if (cur.e_ok) mma(ya, yb);
+      } else {
+        first_of_next();
       }
     }
 
@@ -196,16 +247,14 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_splitk(
     for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
       for (int q = 0; q < 4; ++q) red[wv][cb][q][lane] = acc[cb][q];
-    if (tid < EG_ROWS) {
-      const int64_t pp = mb * EG_ROWS + tid;
-      const int64_t rr = pp < rows ? int64_t(sorted[pp]) : numel;
-      const bool ok = rr >= 0 && rr < numel;
-      blk_route[tid] = ok ? int32_t(rr) : -1;
-      blk_w[tid] = (mulw && ok) ? topk_w[rr] : 1.0f;
+    if (wv == 0 && lane < EG_ROWS) {  // lane l < 16 of wave 0 holds plan row l's route
+      blk_route[lane] = cur.a_ok ? int32_t(cur.r) : -1;
+      blk_w[lane] = w_cur;
     }
     __syncthreads();
 
     // MFMA output layout: lane l holds column l%16 of its block, rows 4*(l/16) + q.
+    const int t = int(item - (item / n_tiles) * n_tiles);
     if constexpr (!FUSED) {
       const int cb = wv;
       const int col = t * 64 + cb * 16 + li;
@@ -239,6 +288,163 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_splitk(
         }
       }
     }
+    if (!has_next) break;
+    cur = nxt;
+    item = next;
+  }
+}
+
+template <int DT, int ACT>
+__global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_cols(
+    eg_elem<DT>* __restrict__ out, const eg_elem<DT>* __restrict__ a,
+    const eg_elem<DT>* __restrict__ w,
+    const float* __restrict__ topk_w, const int32_t* __restrict__ sorted,
+    const int32_t* __restrict__ expert_ids, const int32_t* __restrict__ npp, int64_t max_rows,
+    int64_t numel, int block_m, int a_div, int64_t lda, int num_experts, int n_rows, int K,
+    int64_t ldo, int n_tiles, int mulw) {
+  using E = eg_elem<DT>;
+  constexpr int V = eg_vec<DT>, CH = 4 * V;  // elements per lane vector, K per chunk
+  constexpr bool FUSED = ACT != PIA_ACT_NONE;
+  constexpr int NB = FUSED ? 2 : 1;  // W row sets per item: the columns, or gate and up
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int li = lane & 15, kg = lane >> 4;
+  const int64_t rows = min(max_rows, int64_t(npp[0]));
+  const int64_t items = ((rows + EG_ROWS - 1) / EG_ROWS) * n_tiles;
+  const int nch = (K + CH - 1) / CH;
+  const int ns = (nch + EG_U - 1) / EG_U;  // pipeline stages per item
+  const int half = n_rows >> 1;
+  const int out_cols = FUSED ? half : n_rows;
+  const int64_t up_off = int64_t(half) * K;  // up row n's offset from gate row n
+
+  // One item's operands for this lane: plan row li (route r, A row arow), W row li of the
+  // column tile (wrow; the up row at wrow + up_off), col_ok = that column exists, e_ok = the
+  // plan block names an expert. A padding route or a missing column reads row 0 instead: its
+  // products land only in outputs that are never stored.
+  struct Item {
+    const E* arow;
+    const E* wrow;
+    int r;
+    bool a_ok, col_ok, e_ok;
+  };
+  // (routes and plan rows fit int32: the host checks numel and the plan size)
+  auto make_item = [&](int t, int e, int r) {
+    Item o;
+    const int col = t * EG_ROWS + li;
+    o.e_ok = e >= 0 && e < num_experts;
+    o.r = r;
+    o.a_ok = r >= 0 && r < numel;
+    o.col_ok = col < out_cols;
+    const int arow_i = o.a_ok ? (a_div == 1 ? r : r / a_div) : 0;  // A row 0 exists: numel > 0
+    o.arow = a + int64_t(arow_i) * lda;
+    o.wrow = w + (o.e_ok ? int64_t(e) * n_rows * K : 0) + int64_t(o.col_ok ? col : 0) * K;
+    return o;
+  };
+  auto block_expert = [&](int64_t mb) {  // wave-uniform: branches on it stay scalar
+    return __builtin_amdgcn_readfirstlane(expert_ids[(mb * EG_ROWS) / block_m]);
+  };
+  auto block_route = [&](int64_t mb) -> int {
+    const int64_t p = mb * EG_ROWS + li;
+    return p < rows ? sorted[p] : int(numel);
+  };
+
+  // Stage loads; every load is issued unconditionally so the compiler can keep a whole stage
+  // in flight while the previous one is multiplied. Only the last stage can reach past K: its
+  // lanes there read the row's last vector and zero their A vector (a zero product).
+  auto load = [&](uint4(&va)[EG_U], uint4(&vb)[EG_U][NB], const Item& o, int c) {
+    const bool tail = (c + EG_U) * CH > K;
+#pragma unroll
+    for (int u = 0; u < EG_U; ++u) {
+      const int k = (c + u) * CH + kg * V;
+      const int kk = tail ? min(k, K - V) : k;
+      va[u] = *reinterpret_cast<const uint4*>(o.arow + kk);
+      if (tail && k >= K) va[u] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        vb[u][j] = *reinterpret_cast<const uint4*>(o.wrow + j * up_off + kk);
+    }
+  };
+  f32x4_t acc[NB];
+  auto mma = [&](const uint4(&va)[EG_U], const uint4(&vb)[EG_U][NB]) {
+#pragma unroll
+    for (int u = 0; u < EG_U; ++u)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) acc[j] = mfma_vec<DT>(va[u], vb[u][j], acc[j]);
+  };
+
+  // Stage s of an item sits in register set x (s even) or y (s odd); the next item's first
+  // stage always goes to x (with an odd stage count, right after x's last product).
+  int64_t item = int64_t(blockIdx.x) * EG_WAVES + wv;
+  const int64_t stride = int64_t(gridDim.x) * EG_WAVES;
+  if (item >= items) return;
+  // item = mb * n_tiles + t, advanced without dividing
+  int64_t mb = item / n_tiles;
+  int t = int(item - mb * n_tiles);
+  const int64_t stride_mb = stride / n_tiles;
+  const int stride_t = int(stride - stride_mb * n_tiles);
+  Item cur = make_item(t, block_expert(mb), block_route(mb));
+  uint4 xa[EG_U], xb[EG_U][NB], ya[EG_U], yb[EG_U][NB];
+  if (cur.e_ok) load(xa, xb, cur, 0);
+  for (;;) {
+    const int64_t next = item + stride;
+    const bool has_next = next < items;
+    int t_next = t + stride_t;
+    int64_t mb_next = mb + stride_mb;
+    if (t_next >= n_tiles) {
+      t_next -= n_tiles;
+      ++mb_next;
+    }
+    int e_next = -1, r_next = int(numel);
+    if (has_next) {  // the next item's plan block, read now and used with its first stage
+      e_next = block_expert(mb_next);
+      r_next = block_route(mb_next);
+    }
+    const float w_cur = (mulw && cur.a_ok) ? topk_w[cur.r] : 1.0f;  // plan row li's weight
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    Item nxt = cur;
+    auto first_of_next = [&]() {  // called once, with the item's last stage
+      if (!has_next) return;
+      nxt = make_item(t_next, e_next, r_next);
+      if (nxt.e_ok) load(xa, xb, nxt, 0);
+    };
+    for (int st = 0; st < ns; st += 2) {
+      if (st + 1 < ns && cur.e_ok) load(ya, yb, cur, (st + 1) * EG_U);
+      if (cur.e_ok) mma(xa, xb);
+      if (st + 1 < ns) {
+        if (st + 2 < ns) {
+          if (cur.e_ok) load(xa, xb, cur, (st + 2) * EG_U);
+        } else {
+          first_of_next();
+        }
+        if (cur.e_ok) mma(ya, yb);
+      } else {
+        first_of_next();
+      }
+    }
+
+    // MFMA output layout: lane l holds column l%16 of the tile for plan rows 4*(l/16) + q; the
+    // route and weight of plan row i sit in lane i.
+    const int col = t * EG_ROWS + li;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = kg * 4 + q;
+      const int64_t rr = __shfl(cur.r, row, 64);
+      const float wr = __shfl(w_cur, row, 64);
+      if (rr < 0 || rr >= numel || col >= out_cols) continue;
+      if constexpr (!FUSED) {
+        out[rr * ldo + col] = to_dt<DT>(acc[0][q] * wr);
+      } else {
+        const float gr = from_dt<DT>(to_dt<DT>(acc[0][q] * wr));
+        const float ur = from_dt<DT>(to_dt<DT>(acc[1][q] * wr));
+        out[rr * ldo + col] = to_dt<DT>(act_fn<ACT>(gr) * ur);
+      }
+    }
+    if (!has_next) break;
+    cur = nxt;
+    item = next;
+    mb = mb_next;
+    t = t_next;
   }
 }
 
@@ -623,7 +829,7 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
   // bytes of A the plan can reach: rows ceil(numel / a_div), the last one k_dim long
   const int64_t a_bytes = ((ceil_div(numel, a_div) - 1) * lda + k_dim) * elt;
   const int64_t w_bytes = int64_t(n_rows) * k_dim * elt;
-  // the wide kernel is built for 16-bit storage; fp32 runs the split-K kernel at every size
+  // the wide kernel is built for 16-bit storage; fp32 runs the decode kernels at every size
   if (!f32 && numel >= PIA_EG_WIDE_MIN_ROUTES && a_bytes < (int64_t(1) << 31) &&
       w_bytes < (int64_t(1) << 31)) {
     const int64_t max_blocks = ceil_div(max_num_tokens_padded, block_m);
@@ -661,16 +867,20 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
 #undef PIA_TW
     return check_launch("moe_gemm_wide");
   }
-  const int n_tiles = int(ceil_div(out_cols, fused ? 32 : 64));
-  const int64_t ub = ceil_div(max_num_tokens_padded, EG_ROWS) * n_tiles;
+  const bool cols = k_dim <= EG_COLS_MAX_K;
+  const int n_tiles = int(ceil_div(out_cols, cols ? EG_ROWS : (fused ? 32 : 64)));
+  const int64_t n_items = ceil_div(max_num_tokens_padded, EG_ROWS) * n_tiles;
+  const int64_t ub = cols ? ceil_div(n_items, EG_WAVES) : n_items;
   const unsigned grid = unsigned(std::min<int64_t>(ub, int64_t(cus) * EG_WGS_PER_CU));
-#define PIA_EG(DT, ACT)                                                                           \
-  hipLaunchKernelGGL((moe_gemm_splitk<DT, ACT>), dim3(grid), dim3(EG_WAVES * 64), 0, s,            \
+#define PIA_EG_K(KERN, DT, ACT)                                                                   \
+  hipLaunchKernelGGL((KERN<DT, ACT>), dim3(grid), dim3(EG_WAVES * 64), 0, s,                       \
                      reinterpret_cast<eg_elem<DT>*>(out), reinterpret_cast<const eg_elem<DT>*>(a), \
                      reinterpret_cast<const eg_elem<DT>*>(w),                                     \
                      topk_weights, sorted_token_ids, expert_ids, num_tokens_post_pad,             \
                      max_num_tokens_padded, numel, block_m, a_div, lda, num_experts, n_rows,       \
                      k_dim, ldo, n_tiles, mulw)
+#define PIA_EG(DT, ACT)                                                                           \
+  if (cols) PIA_EG_K(moe_gemm_cols, DT, ACT); else PIA_EG_K(moe_gemm_splitk, DT, ACT)
 #define PIA_EG_ACT(DT)                                                                            \
   switch (activation) {                                                                           \
     case PIA_ACT_NONE: PIA_EG(DT, PIA_ACT_NONE); break;                                           \
@@ -687,7 +897,8 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
   }
 #undef PIA_EG_ACT
 #undef PIA_EG
-  return check_launch("moe_gemm_splitk");
+#undef PIA_EG_K
+  return check_launch(cols ? "moe_gemm_cols" : "moe_gemm_splitk");
 }
 
 extern "C" int pia_act_and_mul(void* out, const void* x, int64_t rows, int64_t d, int activation,
