@@ -1,12 +1,14 @@
 // Paged attention of many query rows per sequence (prefill, chunked prefill) on the matrix
 // cores, gfx950: bf16, head_dim 128, page size 16, Hq / Hkv = G in {1, 2, 4, 8}.
 //
-// Work item (one 256-thread workgroup): one kv head and 128 / G consecutive query positions of
-// one sequence, i.e. 128 (position, q head) rows that share the kv head's keys: row r is
-// position s0 + r / G, head h * G + r % G. Wave w owns rows 32 w .. 32 w + 31 (two 16-row MFMA
-// blocks). The keys are walked in 64-token tiles (four pages): K and V come from the pool into
-// registers one tile ahead, then into LDS (16-byte stores; double buffered, one barrier per
-// tile). Both tiles are [d][64 tokens], eight 16-byte units per row, unpadded and swizzled:
+// Work item (one workgroup of NW = 8 waves, or 4 when the sequences have few rows): one kv head
+// and 32 NW / G consecutive query positions of one sequence, i.e. 32 NW (position, q head) rows
+// that share the kv head's keys: row r is position s0 + r / G, head h * G + r % G. Wave w owns
+// rows 32 w .. 32 w + 31 (two 16-row MFMA blocks); two waves per SIMD. The keys are walked in
+// 64-token tiles (four pages): K and V come from the pool into registers a tile ahead (buffer
+// loads, no branch), then into LDS (16-byte stores, double buffered) in the middle of the tile
+// before theirs, one barrier per tile. With eight waves a tile is staged once for 256 rows.
+// Both tiles are [d][64 tokens], eight 16-byte units per row, unpadded and swizzled:
 //   K: unit u (tokens 8 u .. 8 u + 7) at u ^ ((d / 4) ^ 2 (d % 4)) % 8;
 //   V: unit 4 c + j holds tokens 32 c + 4 j .. + 3 then 32 c + 16 + 4 j .. + 3 (the order of the
 //      P operand's k slots below, so one 16-byte read is a whole B operand), at unit
@@ -56,38 +58,42 @@ using tile::f32x4_t;
 
 constexpr int PF_D = 128, PF_P = 16;
 constexpr int PF_RB = 2;              // 16-row MFMA blocks per wave
-constexpr int PF_ROWS = 64 * PF_RB;   // (position, head) rows per work item: 4 waves x 32
+constexpr int PF_WROWS = 16 * PF_RB;  // (position, head) rows per wave
 constexpr int PF_KT = 64;             // keys per tile: four pages
 constexpr int PF_MAX_SEQS = 1024;     // sequences per launch (tile prefix in LDS)
 constexpr int PF_V_AHEAD = 4;         // V operand reads in flight ahead of the P . V products
+// word 3 of a raw (stride 0) buffer descriptor on gfx9 parts; a load at or past the descriptor's
+// byte count returns zeros
+constexpr int PF_RSRC_WORD3 = 0x00020000;
 
 // lazy rescaling threshold (log2 units): a row's exponentials are taken against a reference
 // that trails its true max by at most this much, so probabilities stay <= 2^8
 constexpr float PF_RESCALE = 8.0f;
 
-template <int G>
-__global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
+template <int G, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void paged_prefill_mfma(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ kpool, const uint16_t* __restrict__ vpool,
     const int32_t* __restrict__ bt, int64_t bt_stride, const int32_t* __restrict__ kv_lens,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ offsets, int B, int Hkv,
     int64_t num_pages, float scale_log2) {
   constexpr int D = PF_D, P = PF_P, TILE = D * P;
-  constexpr int PPT = PF_ROWS / G;  // query positions per work item
+  constexpr int NT = 64 * NW;                 // threads per workgroup
+  constexpr int PPT = PF_WROWS * NW / G;  // query positions per work item
   constexpr int RB = PF_RB;
   constexpr int XCDS = 8;
   __shared__ __align__(16) uint16_t ks[2][PF_D * PF_KT];
   __shared__ __align__(16) uint16_t vs[2][PF_D * PF_KT];
   __shared__ int tile_pref[PF_MAX_SEQS + 1];
-  __shared__ int wsum[4];
+  __shared__ int wsum[NW];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int Hq = Hkv * G;
   const int64_t q_row = int64_t(Hq) * D;  // elements between query positions
 
-  // work items per sequence (ceil(rows / PPT)) and their prefix, scanned 256 sequences at a time
+  // work items per sequence (ceil(rows / PPT)) and their prefix, scanned NT sequences at a time
   if (tid == 0) tile_pref[0] = 0;
   int carry = 0;
-  for (int c0 = 0; c0 < B; c0 += 256) {
+  for (int c0 = 0; c0 < B; c0 += NT) {
     const int i = c0 + tid;
     const int n = i < B ? (cu_q ? cu_q[i + 1] - cu_q[i] : 1) : 0;
     const int t = n > 0 ? (n + PPT - 1) / PPT : 0;
@@ -102,7 +108,8 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
     int base = carry;
     for (int x = 0; x < wave; ++x) base += wsum[x];
     if (i < B) tile_pref[i + 1] = base + incl;
-    carry += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+#pragma unroll
+    for (int x = 0; x < NW; ++x) carry += wsum[x];
     __syncthreads();
   }
   // this workgroup's item: XCD x = blockIdx % 8 runs items [x * run, (x + 1) * run) in order
@@ -153,15 +160,19 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
   // every valid row of the item sees at least the keys below lim_min (the first row's limit)
   const int lim_min = offsets ? max(0, min(kv_len, off + s0 + 1)) : kv_len;
 
-  // tile loads: thread t moves piece t of each of the tile's four (page, head) K and V tiles:
-  // row d = t / 2, tokens 8 (t % 2) .. + 7 of page i
-  const int ld_d = tid >> 1, ld_half = tid & 1;
+  // tile loads: with four waves, thread t moves row d = t / 2, tokens 8 (t % 2) .. + 7 of each of
+  // the tile's four (page, head) K and V tiles; with eight, wave w moves pages 2 (w % 2) and
+  // 2 (w % 2) + 1 (the page pair is uniform in the wave), row d = 32 (w / 2) + l / 2, tokens
+  // 8 (l % 2) .. + 7. NCP: page pairs per thread, cp0: its first pair.
+  constexpr int NCP = NW == 4 ? 2 : 1;
+  const int cp0 = NW == 4 ? 0 : (wave & 1);
+  const int ld_d = NW == 4 ? tid >> 1 : 32 * (wave >> 1) + (lane >> 1), ld_half = tid & 1;
   const int ld_off = ld_d * P + ld_half * 8;  // the thread's piece inside a (page, head) tile
-  // kr[i]: the thread's K piece of page i; vu[2 c + e]: its V unit 4 c + 2 h + e (h = ld_half),
-  // tokens 8 h + 4 e .. + 3 of page 2 c in .x/.y and of page 2 c + 1 in .z/.w, loaded by
-  // eight-byte loads straight into place (a unit assembled from two 16-byte loads would need
-  // register copies that wait on the loads)
-  uint4 kr[4], vu[4];
+  // kr[q]: the thread's K piece of its page q (tile page 2 cp0 + q); vu[2 cc + e]: its V unit
+  // 4 c + 2 h + e (c = cp0 + cc, h = ld_half), tokens 8 h + 4 e .. + 3 of page 2 c in .x/.y and
+  // of page 2 c + 1 in .z/.w, loaded by eight-byte loads straight into place (a unit assembled
+  // from two 16-byte loads would need register copies that wait on the loads)
+  uint4 kr[2 * NCP], vu[2 * NCP];
   // block-table ids of a tile: lane i < 4 holds page 4 kt + i's id (-1 past the table). They
   // are loaded a tile ahead of the fetch that uses them, with one vector load, so no tile
   // waits on a chain of dependent block-table reads.
@@ -172,19 +183,27 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
   // ld_off + 4, hidden from the compiler so it does not fuse the two V loads into one
   int ld_off4 = ld_off + 4;
   asm volatile("" : "+v"(ld_off4));
+  // Pages go through buffer descriptors (an id outside the pool gets an empty one, whose loads
+  // return zeros), so the fetch has no branch: the wait for the block-table load issued before it
+  // then counts exactly the fetch's loads after it instead of waiting for all of them.
+  const uint32_t np32 = num_pages > 0x7fffffff ? 0x7fffffffu : uint32_t(num_pages);
+  auto page_rsrc = [&](const uint16_t* pool, int id) {
+    const bool ok = uint32_t(id) < np32;
+    const int64_t tile_off = (int64_t(ok ? id : 0) * Hkv + h) * TILE;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(pool + tile_off), 0,
+                                             ok ? TILE * 2 : 0, PF_RSRC_WORD3);
+  };
   auto fetch = [&](int bt4) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int id = __builtin_amdgcn_readlane(bt4, i);
-      uint2 v0 = make_uint2(0u, 0u), v1 = make_uint2(0u, 0u);
-      if (id >= 0 && int64_t(id) < num_pages) {  // uniform: one scalar base per page
-        const int64_t tile_off = (int64_t(id) * Hkv + h) * TILE;
-        kr[i] = *reinterpret_cast<const uint4*>(kpool + tile_off + ld_off);
-        v0 = *reinterpret_cast<const uint2*>(vpool + tile_off + ld_off);
-        v1 = *reinterpret_cast<const uint2*>(vpool + tile_off + ld_off4);
-      } else {
-        kr[i] = make_uint4(0u, 0u, 0u, 0u);
-      }
+    for (int q = 0; q < 2 * NCP; ++q) {
+      const int id = __builtin_amdgcn_readlane(bt4, 2 * cp0 + q);
+      const __amdgpu_buffer_rsrc_t kres = page_rsrc(kpool, id), vres = page_rsrc(vpool, id);
+      kr[q] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kres, 2 * ld_off,
+                                                                               0, 0));
+      const auto l0 = __builtin_amdgcn_raw_buffer_load_b64(vres, 2 * ld_off, 0, 0);
+      const auto l1 = __builtin_amdgcn_raw_buffer_load_b64(vres, 2 * ld_off4, 0, 0);
+      const uint2 v0 = make_uint2(l0[0], l0[1]), v1 = make_uint2(l1[0], l1[1]);
+      const int i = q;  // the thread's page q: V units 2 (q / 2), 2 (q / 2) + 1, half q % 2
       uint4& u0 = vu[2 * (i >> 1)];
       uint4& u1 = vu[2 * (i >> 1) + 1];
       if (i & 1) {
@@ -218,9 +237,9 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
   const int tail = kv_len - P * (npages - 1);  // keys on the last page, 1..16
   auto stage = [&](int buf, int kt) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<uint4*>(&ks[buf][st_base ^ (16 * i)]) = kr[i];
-      if (4 * kt + i == npages - 1 && tail < P) {  // uniform
+    for (int i = 0; i < 2 * NCP; ++i) {  // the thread's page i, tile page 2 cp0 + i
+      *reinterpret_cast<uint4*>(&ks[buf][st_base ^ (16 * (2 * cp0 + i))]) = kr[i];
+      if (4 * kt + 2 * cp0 + i == npages - 1 && tail < P) {  // uniform
         const int nv = tail - 8 * ld_half;
         uint4& u0 = vu[2 * (i >> 1)];
         uint4& u1 = vu[2 * (i >> 1) + 1];
@@ -234,9 +253,10 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
       }
     }
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      *reinterpret_cast<uint4*>(&vs[buf][v_st ^ (32 * c)]) = vu[2 * c];
-      *reinterpret_cast<uint4*>(&vs[buf][v_st ^ (32 * c + 8)]) = vu[2 * c + 1];
+    for (int cc = 0; cc < NCP; ++cc) {
+      const int c = cp0 + cc;
+      *reinterpret_cast<uint4*>(&vs[buf][v_st ^ (32 * c)]) = vu[2 * cc];
+      *reinterpret_cast<uint4*>(&vs[buf][v_st ^ (32 * c + 8)]) = vu[2 * cc + 1];
     }
   };
   // V operand i = 8 c + nb of a tile: unit 4 c + l / 16 of row 16 nb + l % 16
@@ -249,7 +269,7 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int id = __builtin_amdgcn_readlane(bt4, i);
-      mk |= (id >= 0 && int64_t(id) < num_pages) ? (1 << i) : 0;
+      mk |= uint32_t(id) < np32 ? (1 << i) : 0;
     }
     return mk;
   };
@@ -271,17 +291,23 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
   }
   const uint4 ones = tile::bf16_ones();
 
-  int bt_cur = bt_of(0), bt_nxt = bt_of(1);
-  if (nkt > 0) fetch(bt_cur);
+  // Tile 0 is staged before the loop; tile kt + 1 is staged in the middle of tile kt (after its
+  // softmax, before its P . V), from registers fetched a tile earlier, and the fetch of tile
+  // kt + 2 follows at once. The barrier at each tile's end publishes the next tile and frees
+  // the buffer the tile read. The fetches run unconditionally (past the last tile they load
+  // data no stage uses): with no branch around them, the wait for the block-table load issued
+  // before a fetch counts exactly the fetch's loads instead of waiting for all of them.
+  int bt_cur = bt_of(0), bt_nxt = bt_of(1), bt_far = bt_of(2);
+  fetch(bt_cur);
+  stage(0, 0);
+  fetch(bt_nxt);
+  __syncthreads();
   for (int kt = 0; kt < nkt; ++kt) {
     const int buf = kt & 1;
-    stage(buf, kt);
-    __syncthreads();
     const int pmask = page_mask(bt_cur);
     // a tile every valid row sees whole (interior of the causal triangle, all pages valid)
     const bool full = pmask == 0xF && (kt + 1) * PF_KT <= lim_min;
-    const int bt_far = bt_of(kt + 2);
-    if (kt + 1 < nkt) fetch(bt_nxt);
+    const int bt_next_far = bt_of(kt + 3);
 
     // S^T for the wave's rows: 4 token blocks (one per page) x 4 d chunks, each K operand
     // serving both row blocks; d chunk outermost, so consecutive products of one accumulator
@@ -362,6 +388,8 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
         }
       }
     }
+    stage(buf ^ 1, kt + 1);
+    fetch(bt_far);
     // O += P . V over the tile's two 32-token chunks, each V operand serving both row blocks;
     // the sums against a column of ones. Chunk outermost: consecutive products of one
     // accumulator are 8 RB + RB MFMAs apart. The V operands (i = 8 c + nb) are read
@@ -390,8 +418,10 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_mfma(
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, RB * (PF_V_AHEAD + 2), 0);
+    __syncthreads();
     bt_cur = bt_nxt;
     bt_nxt = bt_far;
+    bt_far = bt_next_far;
   }
 
   // out = O / sum for rows 4 g4 + j of each block
@@ -427,25 +457,35 @@ int launch_prefill_mfma(void* out, const void* q, const void* k_pages, const voi
                         int64_t total_q_rows, int Hq, int Hkv, int64_t num_pages,
                         float scale_log2, hipStream_t s) {
   const int G = Hq / Hkv;
-  const int ppt = PF_ROWS / G;
+  // eight waves (256 rows per item, one K / V tile staged for all of them) when the sequences
+  // average at least half an item, else four (128 rows)
+  const bool wide = 2 * total_q_rows >= int64_t(8 * PF_WROWS / G) * num_seqs;
+  const int ppt = (wide ? 8 : 4) * PF_WROWS / G;
   // work items: at most ceil(total rows / ppt) + one partial item per sequence
   const int64_t items = (ceil_div(total_q_rows, ppt) + num_seqs) * Hkv;
   const int64_t blocks = ceil_div(items, 8) * 8;
   if (blocks > 0x7fffffff)
     return fail(PIA_EINVAL, "paged_attention: too many query rows for the prefill kernel");
   const dim3 grid{unsigned(blocks), 1u, 1u};
-#define PIA_PF(GG)                                                                             \
-  hipLaunchKernelGGL((paged_prefill_mfma<GG>), grid, dim3(256), 0, s,                          \
+#define PIA_PF(GG, NW)                                                                         \
+  hipLaunchKernelGGL((paged_prefill_mfma<GG, NW>), grid, dim3(64 * NW), 0, s,                  \
                      reinterpret_cast<uint16_t*>(out), reinterpret_cast<const uint16_t*>(q),   \
                      reinterpret_cast<const uint16_t*>(k_pages),                               \
                      reinterpret_cast<const uint16_t*>(v_pages), bt, bt_stride, kv_lens, cu_q, \
                      offsets, num_seqs, Hkv, num_pages, scale_log2)
-  switch (G) {
-    case 1: PIA_PF(1); break;
-    case 2: PIA_PF(2); break;
-    case 4: PIA_PF(4); break;
-    default: PIA_PF(8); break;
+#define PIA_PF_G(NW)                  \
+  switch (G) {                        \
+    case 1: PIA_PF(1, NW); break;     \
+    case 2: PIA_PF(2, NW); break;     \
+    case 4: PIA_PF(4, NW); break;     \
+    default: PIA_PF(8, NW); break;    \
   }
+  if (wide) {
+    PIA_PF_G(8);
+  } else {
+    PIA_PF_G(4);
+  }
+#undef PIA_PF_G
 #undef PIA_PF
   return check_launch("paged_prefill_mfma");
 }
