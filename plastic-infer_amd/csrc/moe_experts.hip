@@ -36,7 +36,8 @@
 // wave's: 16 plan rows against 16 W rows (16 output columns), or 16 gate rows plus the matching
 // 16 up rows when the activation is fused, over the whole K, with the same lane layout and
 // products as above. The waves of a workgroup are independent: no LDS, no barrier; the sibling
-// waves of a plan block re-read its A rows from L2. Items are pipelined the same way.
+// waves of a plan block re-read its A rows from L2. Items are pipelined the same way, and each
+// item starts its K walk at its own stage (stage_rot below).
 #include <type_traits>
 
 #include "pia_internal.h"
@@ -112,6 +113,17 @@ __device__ __forceinline__ float act_fn(float g) {
   } else {
     return 0.5f * g * (1.0f + tanhf(0.7978845608028654f * (g + 0.044715f * g * g * g)));
   }
+}
+
+// First K stage of a work item of the column and wide kernels: a function of the first route of
+// its plan block and of its column tile only, so an item sums its K in the same order whichever workgroup, launch or
+// weight slot computes it (the routes of an expert keep their ids and their order when the
+// routed FFN is split over several calls). The weight rows of an expert are K elements apart,
+// so at a common K offset the concurrent items would all read the same offset of their rows;
+// starting each item at its own stage spreads those reads over the HBM channels.
+__device__ __forceinline__ int stage_rot(int first_route, int t, int ns) {
+  const uint32_t key = first_route > 0 ? uint32_t(first_route) : 0u;
+  return ns > 0 ? int((key * 5u + uint32_t(t)) % uint32_t(ns)) : 0;
 }
 
 template <int DT, int ACT>
@@ -323,7 +335,7 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_cols(
   struct Item {
     const E* arow;
     const E* wrow;
-    int r;
+    int r, rot;
     bool a_ok, col_ok, e_ok;
   };
   // (routes and plan rows fit int32: the host checks numel and the plan size)
@@ -337,6 +349,7 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_cols(
     const int arow_i = o.a_ok ? (a_div == 1 ? r : r / a_div) : 0;  // A row 0 exists: numel > 0
     o.arow = a + int64_t(arow_i) * lda;
     o.wrow = w + (o.e_ok ? int64_t(e) * n_rows * K : 0) + int64_t(o.col_ok ? col : 0) * K;
+    o.rot = stage_rot(__builtin_amdgcn_readfirstlane(r), t, ns);  // lane 0: plan row 0
     return o;
   };
   auto block_expert = [&](int64_t mb) {  // wave-uniform: branches on it stay scalar
@@ -350,6 +363,10 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_cols(
   // Stage loads; every load is issued unconditionally so the compiler can keep a whole stage
   // in flight while the previous one is multiplied. Only the last stage can reach past K: its
   // lanes there read the row's last vector and zero their A vector (a zero product).
+  auto chunk = [&](const Item& o, int st) {  // first chunk of stage st of an item
+    const int x = st + o.rot;
+    return (x >= ns ? x - ns : x) * EG_U;
+  };
   auto load = [&](uint4(&va)[EG_U], uint4(&vb)[EG_U][NB], const Item& o, int c) {
     const bool tail = (c + EG_U) * CH > K;
 #pragma unroll
@@ -383,7 +400,7 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_cols(
   const int stride_t = int(stride - stride_mb * n_tiles);
   Item cur = make_item(t, block_expert(mb), block_route(mb));
   uint4 xa[EG_U], xb[EG_U][NB], ya[EG_U], yb[EG_U][NB];
-  if (cur.e_ok) load(xa, xb, cur, 0);
+  if (cur.e_ok) load(xa, xb, cur, chunk(cur, 0));
   for (;;) {
     const int64_t next = item + stride;
     const bool has_next = next < items;
@@ -406,14 +423,14 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_cols(
     auto first_of_next = [&]() {  // called once, with the item's last stage
       if (!has_next) return;
       nxt = make_item(t_next, e_next, r_next);
-      if (nxt.e_ok) load(xa, xb, nxt, 0);
+      if (nxt.e_ok) load(xa, xb, nxt, chunk(nxt, 0));
     };
     for (int st = 0; st < ns; st += 2) {
-      if (st + 1 < ns && cur.e_ok) load(ya, yb, cur, (st + 1) * EG_U);
+      if (st + 1 < ns && cur.e_ok) load(ya, yb, cur, chunk(cur, st + 1));
       if (cur.e_ok) mma(xa, xb);
       if (st + 1 < ns) {
         if (st + 2 < ns) {
-          if (cur.e_ok) load(xa, xb, cur, (st + 2) * EG_U);
+          if (cur.e_ok) load(xa, xb, cur, chunk(cur, st + 2));
         } else {
           first_of_next();
         }
@@ -554,7 +571,8 @@ __device__ __forceinline__ void tg_sync() {
 // K advances in stages of 64: each operand row contributes one whole 128-byte line per stage,
 // fetched by a 16-byte direct load (global -> LDS through a buffer descriptor, no staging
 // registers) whose eight lanes 8 r .. 8 r + 7 cover row r's line. Two stage buffers: the loads
-// of stage s + 1 are in flight while stage s is multiplied. LDS holds each operand as 16-row x
+// of stage s + 1 are in flight while stage s is multiplied. An item walks its K stages from its
+// own first stage (stage_rot), so the workgroups do not all read one offset of their W rows. LDS holds each operand as 16-row x
 // 64 K fragments of 2 KiB: row r's 128 bytes at 128 r, its 16-byte K chunk c in slot c ^ (r % 8).
 // A direct load of 8 rows lands lane l at byte 16 l, so lane l fetches chunk (l % 8) ^ (l / 8)
 // of row l / 8. An MFMA operand read (ds_read_b128; lane: row l % 16, chunk 4 h + l / 16 of
@@ -653,9 +671,12 @@ __global__ __launch_bounds__(TW_THREADS, 1) void moe_gemm_wide(
       aoff[q] = rr >= 0 ? uint32_t(rr / a_div) * uint32_t(lda) * 2u + uint32_t(lc) * 16u : TG_OOB;
     }
     // direct loads of stage s into buf (stages past the last read out of range: zeros, no
-    // memory access), K offset in the scalar offset
+    // memory access), K offset in the scalar offset; the item's K stages start at rot (the
+    // column tiles of an expert, which share its A rows through L2, one stage apart)
+    const int rot = stage_rot(tile_route[0], t, nks);
     auto issue = [&](uint4* buf, int s) __attribute__((always_inline)) {
-      const int k0 = min(s, nks) * TW_BK;
+      const int sr = s + rot >= nks ? s + rot - nks : s + rot;
+      const int k0 = (s < nks ? sr : nks) * TW_BK;
       const bool kin = k0 + 8 * lc < K;
 #pragma unroll
       for (int q = 0; q < TW_AL; ++q)
