@@ -125,9 +125,10 @@ int pia_kv_pages_chunks_copy(void* const* chunks, int num_chunks, void* pages,
  *                                      bt_stride)
  * bytes, 4-byte aligned (may be NULL when that query returns 0). Calls that share a workspace
  * must be ordered (same stream): a launch keeps its partials and arrival counters in it.
- * bf16 with head_dim 128 and page_size 16 and Hq/Hkv in {1, 2, 4, 8} takes the fast kernel
- * (the batch's KV steps split over persistent waves, XCD-aware); every other supported
- * combination (f32/f16/bf16, head_dim <= 512, any page_size) takes the general kernel.
+ * bf16 or fp16 with head_dim 128 and page_size 16 and Hq/Hkv in {1, 2, 4, 8} takes the fast
+ * kernel (the batch's KV steps split over persistent waves, XCD-aware; the probabilities enter
+ * the P.V products rounded to the pools' dtype); every other supported combination
+ * (f32/f16/bf16, head_dim <= 512, any page_size) takes the general kernel.
  * ------------------------------------------------------------------------------------------- */
 int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_heads,
                                          int head_dim, int page_size, int64_t bt_stride);

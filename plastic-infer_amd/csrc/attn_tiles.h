@@ -1,6 +1,6 @@
-// Matrix-core building blocks shared by the paged attention kernels (gfx950): the bf16
+// Matrix-core building blocks shared by the paged attention kernels (gfx950): the bf16 / fp16
 // 16x16x32 MFMA, the transposing LDS read, the swizzled [d][64 tokens] K/V tile layout and the
-// bf16 pair pack and masking.
+// pair pack and masking.
 //
 // Operand layouts of v_mfma_f32_16x16x32_bf16 (lane l, g4 = l / 16, n16 = l % 16):
 //   A (16 x 32): lane l holds A[n16][8 g4 .. 8 g4 + 7]
@@ -10,6 +10,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "plastic_infer_amd.h"
 
 namespace pia {
 namespace tile {
@@ -88,6 +90,36 @@ __device__ __forceinline__ float maximum_col4(float v) {
 // bf16 1.0 in every element: the B operand of a row sum by the matrix cores.
 __device__ __forceinline__ uint4 bf16_ones() {
   return make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+}
+
+// The same three for either 16-bit storage type, DT = PIA_DTYPE_BF16 or PIA_DTYPE_F16: the
+// 16x16x32 MFMA (fp32 accumulate), two f32 -> one pair (round to nearest even) and 1.0 in every
+// element.
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+template <int DT>
+__device__ __forceinline__ f32x4_t mfma16(const uint4& a, const uint4& b, f32x4_t c) {
+  if constexpr (DT == PIA_DTYPE_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return mfma_bf16(a, b, c);
+}
+template <int DT>
+__device__ __forceinline__ uint32_t pack16x2(float lo, float hi) {
+  if constexpr (DT == PIA_DTYPE_F16) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t p = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+    return __builtin_bit_cast(uint32_t, p);
+  } else {
+    return pack_bf16x2(lo, hi);
+  }
+}
+template <int DT>
+__device__ __forceinline__ uint4 ones16() {
+  if constexpr (DT == PIA_DTYPE_F16)
+    return make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
+  else
+    return bf16_ones();
 }
 
 }  // namespace tile

@@ -1,7 +1,7 @@
 // Paged GQA attention over the KV pool layout [num_pages, Hkv, D, P] (token innermost).
 //
-// 1. paged_decode_stream<G> (G = Hq/Hkv in {1,2,4}): the decode hot path for bf16, D = 128,
-//    P = 16 (described where it is defined): the batch's 128-token steps split over persistent
+// 1. paged_decode_stream<G> (G = Hq/Hkv in {1,2,4}): the decode hot path for bf16 and fp16,
+//    D = 128, P = 16 (described where it is defined): the batch's 128-token steps split over persistent
 //    single waves (a fixed, XCD-aware split), two per SIMD. Per 8-page (128-token) step:
 //      K tile loads: lane l reads page l/8, rows d = 4i + (l&3), token half (l>>2)&1, so load i
 //        of the wave covers one whole 128-byte line of each of the 8 pages (32 loads / 8 pages).
@@ -92,6 +92,33 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t c) {
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const bf16x2_t p = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
   return __builtin_bit_cast(uint32_t, p);
+}
+
+// The fast kernels' two 16-bit storage types, DT = PIA_DTYPE_BF16 or PIA_DTYPE_F16: a dot
+// product of two element pairs accumulated in fp32, two fp32 packed into a pair and one fp32
+// rounded (both to nearest even), and one element (the low 16 bits) widened to fp32.
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+template <int DT>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (DT == PIA_DTYPE_F16)
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b),
+                                  c, false);
+  else
+    return dot2_bf16(a, b, c);
+}
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return tile::pack16x2<DT>(lo, hi);
+}
+template <int DT>
+__device__ __forceinline__ uint16_t to16(float v) {
+  if constexpr (DT == PIA_DTYPE_F16) return f32_to_half(v);
+  else return f32_to_bf16(v);
+}
+template <int DT>
+__device__ __forceinline__ float from16(uint32_t x) {
+  if constexpr (DT == PIA_DTYPE_F16) return half_to_f32(uint16_t(x & 0xffffu));
+  else return __uint_as_float((x & 0xffffu) << 16);
 }
 
 // 2^x with the hardware v_exp_f32 (no denormal-range fix-up branches): softmax arguments are
@@ -400,7 +427,7 @@ __device__ __forceinline__ void sd_flush_appends(const int64_t (*rec)[2], int n_
 // first global step or -1, arr_ns its steps, arr_row = b * Hkv + h) are written; count them in
 // on their segments' counters and merge every segment whose last partial this is. Partial
 // layout per slot: G rows of [D unnormalised output, running max (log2 units), row sum].
-template <int G>
+template <int G, int DT>
 __device__ __forceinline__ void sd_arrive_and_merge(const int (&arr_first)[2],
                                                     const int (&arr_ns)[2],
                                                     const int (&arr_row)[2], int Dp, int Ce,
@@ -472,13 +499,13 @@ __device__ __forceinline__ void sd_arrive_and_merge(const int (&arr_first)[2],
     uint16_t* orow = out + (int64_t(b) * Hkv * G + int64_t(h) * G) * D;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      orow[g * D + lane] = f32_to_bf16(lt[g] > 0.f ? o0[g] / lt[g] : 0.f);
-      orow[g * D + 64 + lane] = f32_to_bf16(lt[g] > 0.f ? o1[g] / lt[g] : 0.f);
+      orow[g * D + lane] = to16<DT>(lt[g] > 0.f ? o0[g] / lt[g] : 0.f);
+      orow[g * D + 64 + lane] = to16<DT>(lt[g] > 0.f ? o1[g] / lt[g] : 0.f);
     }
   }
 }
 
-template <int G, bool APPEND>
+template <int G, bool APPEND, int DT>
 __global__ __launch_bounds__(64, 2) void paged_decode_stream(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
     PoolIn<APPEND> kpool, PoolIn<APPEND> vpool,
@@ -601,7 +628,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_stream(
 #pragma unroll
       for (int t = 0; t < 8; ++t)
 #pragma unroll
-        for (int g = 0; g < G; ++g) sacc[t][g] = dot2_bf16(kk[t], qq[g], sacc[t][g]);
+        for (int g = 0; g < G; ++g) sacc[t][g] = dot2<DT>(kk[t], qq[g], sacc[t][g]);
     }
   };
 
@@ -653,10 +680,10 @@ __global__ __launch_bounds__(64, 2) void paged_decode_stream(
         for (int g = 0; g < G; ++g) {
           const uint4 wv = vr[4 * pgi + j];
           float a = acc[j][g];
-          a = dot2_bf16(wv.x, pr[0][g], a);
-          a = dot2_bf16(wv.y, pr[1][g], a);
-          a = dot2_bf16(wv.z, pr[2][g], a);
-          a = dot2_bf16(wv.w, pr[3][g], a);
+          a = dot2<DT>(wv.x, pr[0][g], a);
+          a = dot2<DT>(wv.y, pr[1][g], a);
+          a = dot2<DT>(wv.z, pr[2][g], a);
+          a = dot2<DT>(wv.w, pr[3][g], a);
           acc[j][g] = a;
         }
     }
@@ -728,7 +755,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_stream(
       const bool own0 = tok0 == tn, own1 = tok0 + 1 == tn;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float sn = wave_sum_dpp(dot2_bf16(kn, q_lds[lane & 3][lane >> 2][g], 0.f));
+        const float sn = wave_sum_dpp(dot2<DT>(kn, q_lds[lane & 3][lane >> 2][g], 0.f));
         sc[0][g] = own0 ? sn : sc[0][g];
         sc[1][g] = own1 ? sn : sc[1][g];
       }
@@ -743,7 +770,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_stream(
       const float p0 = fast_exp2(x0 - mnew), p1 = fast_exp2(x1 - mnew);
       lsum[g] = lsum[g] * alpha + (p0 + p1);
       m[g] = mnew;
-      pw[g] = pack_bf16x2(p0, p1);
+      pw[g] = pack2<DT>(p0, p1);
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[j][g] *= alpha;
     }
@@ -752,16 +779,16 @@ __global__ __launch_bounds__(64, 2) void paged_decode_stream(
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
     if (app_step) {
-      // p of the new token (the bf16 value the pool tokens' products use) times v_new, on the
+      // p of the new token (the 16-bit value the pool tokens' products use) times v_new, on the
       // even lanes (the odd lane of a pair accumulates the other token half); then k_new /
       // v_new go into the slot, unless its page id is outside the pool (then it is no key)
       const uint32_t half_sh = (tn & 1) ? 16u : 0u;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float pn = __uint_as_float(((p_lds[tn >> 1][g] >> half_sh) & 0xffffu) << 16);
+        const float pn = from16<DT>(p_lds[tn >> 1][g] >> half_sh);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float v = (lane & 1) ? 0.f : __uint_as_float(vn[j] << 16);
+          const float v = (lane & 1) ? 0.f : from16<DT>(vn[j]);
           acc[j][g] = pn > 0.f ? fmaf(pn, v, acc[j][g]) : acc[j][g];
         }
       }
@@ -837,7 +864,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_stream(
 #pragma unroll
             for (int j = 0; j < 4; ++j)
               out[(row0 + g) * D + 32 * j + (lane >> 1)] =
-                  f32_to_bf16(lsum[g] > 0.f ? acc[j][g] / lsum[g] : 0.f);
+                  to16<DT>(lsum[g] > 0.f ? acc[j][g] / lsum[g] : 0.f);
         }
       } else {
         const int slot = seg_first < start ? 0 : 1;
@@ -879,12 +906,12 @@ __global__ __launch_bounds__(64, 2) void paged_decode_stream(
   }
   if constexpr (APPEND) sd_flush_appends(app_rec, n_rec, k_new, v_new, kpool_w, vpool_w, lane);
   // All arrivals at the end of the range, so no fence drains a step's prefetch.
-  sd_arrive_and_merge<G>(arr_first, arr_ns, arr_row, Dp, Ce, ws_part, ws_meta, token, out, Hkv,
+  sd_arrive_and_merge<G, DT>(arr_first, arr_ns, arr_row, Dp, Ce, ws_part, ws_meta, token, out, Hkv,
                          lane);
 }
 
 // ---------------------------------------------------------------------------------------------
-// Stream decode kernel on the matrix cores (bf16, D = 128, P = 16), launched for G = 8.
+// Stream decode kernel on the matrix cores (bf16 or fp16, D = 128, P = 16), launched for G = 8.
 //
 // The same work split, cursor, partial slots, arrivals and merge as paged_decode_stream, one wave
 // per SIMD; only the tile work of a step differs. Eight q rows against 128 keys cost 2048
@@ -915,7 +942,7 @@ __global__ __launch_bounds__(64, 2) void paged_decode_stream(
 // ---------------------------------------------------------------------------------------------
 constexpr float SD_RESCALE = 8.0f;
 
-template <int G, bool APPEND>
+template <int G, bool APPEND, int DT>
 __global__ __launch_bounds__(64, 1) void paged_decode_mfma(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, int64_t q_seq_stride,
     PoolIn<APPEND> kpool, PoolIn<APPEND> vpool,
@@ -1035,7 +1062,7 @@ __global__ __launch_bounds__(64, 1) void paged_decode_mfma(
   f32x4_t acc[8], lsum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int nb = 0; nb < 8; ++nb) acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const uint4 ones = tile::bf16_ones();
+  const uint4 ones = tile::ones16<DT>();
   uint4 qreg[4];
 
   // d chunk outermost: consecutive products of one accumulator are four MFMAs apart
@@ -1046,7 +1073,7 @@ __global__ __launch_bounds__(64, 1) void paged_decode_mfma(
       for (int mb = 0; mb < 4; ++mb) {
         const uint2 lo = tile::read_tr16(&ks[(k_base[0] ^ (16 * mb)) + 2048 * kc]);
         const uint2 hi = tile::read_tr16(&ks[(k_base[1] ^ (16 * mb)) + 2048 * kc]);
-        sc[mb] = tile::mfma_bf16(make_uint4(lo.x, lo.y, hi.x, hi.y), qreg[kc],
+        sc[mb] = tile::mfma16<DT>(make_uint4(lo.x, lo.y, hi.x, hi.y), qreg[kc],
                                  kc == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sc[mb]);
       }
   };
@@ -1087,8 +1114,8 @@ __global__ __launch_bounds__(64, 1) void paged_decode_mfma(
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int j = 0; j < 4; ++j) p[hh][j] = fast_exp2(sc[2 * c + hh][j] - mref);
-      pk[c] = make_uint4(tile::pack_bf16x2(p[0][0], p[0][1]), tile::pack_bf16x2(p[0][2], p[0][3]),
-                         tile::pack_bf16x2(p[1][0], p[1][1]), tile::pack_bf16x2(p[1][2], p[1][3]));
+      pk[c] = make_uint4(tile::pack16x2<DT>(p[0][0], p[0][1]), tile::pack16x2<DT>(p[0][2], p[0][3]),
+                         tile::pack16x2<DT>(p[1][0], p[1][1]), tile::pack16x2<DT>(p[1][2], p[1][3]));
     }
   };
   // V words of tokens at or past `valid` or in pages outside the pool -> 0 (stale memory may
@@ -1118,7 +1145,7 @@ __global__ __launch_bounds__(64, 1) void paged_decode_mfma(
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb) acc[nb] = tile::mfma_bf16(pk[c], vr[8 * c + nb], acc[nb]);
+      for (int nb = 0; nb < 8; ++nb) acc[nb] = tile::mfma16<DT>(pk[c], vr[8 * c + nb], acc[nb]);
   };
 
   int gs = start;
@@ -1242,8 +1269,8 @@ __global__ __launch_bounds__(64, 1) void paged_decode_mfma(
     }
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      lsum = tile::mfma_bf16(pkA[c], ones, lsum);
-      lsum = tile::mfma_bf16(pkB[c], ones, lsum);
+      lsum = tile::mfma16<DT>(pkA[c], ones, lsum);
+      lsum = tile::mfma16<DT>(pkB[c], ones, lsum);
     }
     __builtin_amdgcn_sched_barrier(0);
     put_vnew(bufA, 0);
@@ -1288,7 +1315,7 @@ __global__ __launch_bounds__(64, 1) void paged_decode_mfma(
             const float inv = lsum[j] > 0.f ? 1.f / lsum[j] : 0.f;
             uint16_t* o = out + (row0 + 4 * g4 + j) * D + n16;
 #pragma unroll
-            for (int nb = 0; nb < 8; ++nb) o[16 * nb] = f32_to_bf16(acc[nb][j] * inv);
+            for (int nb = 0; nb < 8; ++nb) o[16 * nb] = to16<DT>(acc[nb][j] * inv);
           }
         }
       } else {
@@ -1325,7 +1352,7 @@ __global__ __launch_bounds__(64, 1) void paged_decode_mfma(
     ++gs;
   }
   if constexpr (APPEND) sd_flush_appends(app_rec, n_rec, k_new, v_new, kpool_w, vpool_w, lane);
-  sd_arrive_and_merge<G>(arr_first, arr_ns, arr_row, Dp, Ce, ws_part, ws_meta, token, out, Hkv,
+  sd_arrive_and_merge<G, DT>(arr_first, arr_ns, arr_row, Dp, Ce, ws_part, ws_meta, token, out, Hkv,
                          lane);
 }
 
@@ -1516,7 +1543,7 @@ int check_heads(int Hq, int Hkv, int D, int P, int64_t num_pages, int dtype) {
 
 bool fast_path(int dtype, int Hq, int Hkv, int D, int P) {
   const int G = Hq / Hkv;
-  return dtype == PIA_DTYPE_BF16 && D == FD_D && P == FD_P &&
+  return (dtype == PIA_DTYPE_BF16 || dtype == PIA_DTYPE_F16) && D == FD_D && P == FD_P &&
          (G == 1 || G == 2 || G == 4 || G == 8);
 }
 
@@ -1587,13 +1614,13 @@ uint64_t next_stream_token() {
   return (seq.fetch_add(1, std::memory_order_relaxed) & 0xffffffffffffull) << 16;
 }
 
-int launch_stream_decode(void* out, const void* q, int64_t q_seq_stride, const void* k_pages,
-                         const void* v_pages, const int32_t* block_tables, int64_t bt_stride,
-                         const int32_t* context_lens, int num_seqs, int num_heads,
-                         int num_kv_heads, int64_t num_pages, float scale_log2,
-                         unsigned char* scratch, int scratch_waves, hipStream_t s,
-                         const void* k_new = nullptr, const void* v_new = nullptr,
-                         int64_t new_seq_stride = 0) {
+template <int DT>
+int launch_stream_decode_dt(void* out, const void* q, int64_t q_seq_stride, const void* k_pages,
+                            const void* v_pages, const int32_t* block_tables, int64_t bt_stride,
+                            const int32_t* context_lens, int num_seqs, int num_heads,
+                            int num_kv_heads, int64_t num_pages, float scale_log2,
+                            unsigned char* scratch, int scratch_waves, hipStream_t s,
+                            const void* k_new, const void* v_new, int64_t new_seq_stride) {
   const int G = num_heads / num_kv_heads;
   const int NW = stream_waves(G);
   if (NW > scratch_waves) {
@@ -1618,12 +1645,12 @@ int launch_stream_decode(void* out, const void* q, int64_t q_seq_stride, const v
     const size_t lds = size_t(2 * Bs + 1) * sizeof(int32_t);
     const uint64_t token = next_stream_token();
 #define PIA_SD(GG, AP)                                                                         \
-  hipLaunchKernelGGL((paged_decode_stream<GG, AP>), dim3(unsigned(NW)), dim3(64), lds, s, o,   \
+  hipLaunchKernelGGL((paged_decode_stream<GG, AP, DT>), dim3(unsigned(NW)), dim3(64), lds, s, o, \
                      qq, q_seq_stride, (const uint16_t*)k_pages, (const uint16_t*)v_pages, bt, \
                      bt_stride, cl, Bs, num_kv_heads, num_pages, ws_part, ws_meta, scale_log2, \
                      kw, vw, kn, vn, new_seq_stride, token)
 #define PIA_SDM(GG, AP)                                                                        \
-  hipLaunchKernelGGL((paged_decode_mfma<GG, AP>), dim3(unsigned(NW)), dim3(64), lds, s, o, qq, \
+  hipLaunchKernelGGL((paged_decode_mfma<GG, AP, DT>), dim3(unsigned(NW)), dim3(64), lds, s, o, qq, \
                      q_seq_stride, (const uint16_t*)k_pages, (const uint16_t*)v_pages, bt,     \
                      bt_stride, cl, Bs, num_kv_heads, num_pages, ws_part, ws_meta, scale_log2, \
                      kw, vw, kn, vn, new_seq_stride, token)
@@ -1647,6 +1674,21 @@ int launch_stream_decode(void* out, const void* q, int64_t q_seq_stride, const v
     if (int rc = check_launch("paged_decode_stream")) return rc;
   }
   return 0;
+}
+
+// The fast decode launch for a 16-bit dtype (PIA_DTYPE_BF16 or PIA_DTYPE_F16, see fast_path).
+int launch_stream_decode(int dtype, void* out, const void* q, int64_t q_seq_stride,
+                         const void* k_pages, const void* v_pages, const int32_t* block_tables,
+                         int64_t bt_stride, const int32_t* context_lens, int num_seqs,
+                         int num_heads, int num_kv_heads, int64_t num_pages, float scale_log2,
+                         unsigned char* scratch, int scratch_waves, hipStream_t s,
+                         const void* k_new = nullptr, const void* v_new = nullptr,
+                         int64_t new_seq_stride = 0) {
+  auto* launch = dtype == PIA_DTYPE_F16 ? &launch_stream_decode_dt<PIA_DTYPE_F16>
+                                        : &launch_stream_decode_dt<PIA_DTYPE_BF16>;
+  return launch(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride, context_lens,
+                num_seqs, num_heads, num_kv_heads, num_pages, scale_log2, scratch, scratch_waves,
+                s, k_new, v_new, new_seq_stride);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1739,9 +1781,9 @@ extern "C" int pia_paged_decode_attention(void* out, const void* q, int64_t q_se
       return PIA_EINVAL;
     }
     if (!aligned(workspace, 4)) return fail(PIA_EINVAL, "paged_decode: workspace not 4-byte aligned");
-    return launch_stream_decode(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride,
-                                context_lens, num_seqs, num_heads, num_kv_heads, num_pages,
-                                scale_log2, static_cast<unsigned char*>(workspace),
+    return launch_stream_decode(dtype, out, q, q_seq_stride, k_pages, v_pages, block_tables,
+                                bt_stride, context_lens, num_seqs, num_heads, num_kv_heads,
+                                num_pages, scale_log2, static_cast<unsigned char*>(workspace),
                                 SD_MAX_WAVES, s);
   }
   return launch_generic_any(dtype, out, q, q_seq_stride, k_pages, v_pages, block_tables,
@@ -1778,9 +1820,9 @@ extern "C" int pia_paged_decode_append_attention(
     }
     if (!aligned(workspace, 4))
       return fail(PIA_EINVAL, "paged_decode_append: workspace not 4-byte aligned");
-    return launch_stream_decode(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride,
-                                context_lens, num_seqs, num_heads, num_kv_heads, num_pages,
-                                scale_log2, static_cast<unsigned char*>(workspace),
+    return launch_stream_decode(dtype, out, q, q_seq_stride, k_pages, v_pages, block_tables,
+                                bt_stride, context_lens, num_seqs, num_heads, num_kv_heads,
+                                num_pages, scale_log2, static_cast<unsigned char*>(workspace),
                                 SD_MAX_WAVES, s, k_new, v_new, new_seq_stride);
   }
   // any other shape: the new tokens into their slots, then the decode over the pool
@@ -1829,9 +1871,10 @@ extern "C" int pia_paged_decode_attention_noalloc(void* out, const void* q, int6
   }
   unsigned char* base = nullptr;
   if (int rc = scratch_ptr(&base)) return rc;
-  return launch_stream_decode(out, q, q_seq_stride, k_pages, v_pages, block_tables, bt_stride,
-                              context_lens, num_seqs, num_heads, num_kv_heads, num_pages,
-                              scale_log2, base, stream_waves(num_heads / num_kv_heads), s);
+  return launch_stream_decode(dtype, out, q, q_seq_stride, k_pages, v_pages, block_tables,
+                              bt_stride, context_lens, num_seqs, num_heads, num_kv_heads,
+                              num_pages, scale_log2, base, stream_waves(num_heads / num_kv_heads),
+                              s);
 }
 
 extern "C" int pia_paged_attention(void* out, const void* q, const void* k_pages,

@@ -185,11 +185,11 @@ def test_decode_stream_graph_replays(dev):
         assert torch.equal(paged_decode_attention(qd, kd, vd, btd, ld, workspace=ws).cpu(), eager)
 
 
-def qwen3_8b_b256_inputs(dev):
+def qwen3_8b_b256_inputs(dev, dtype=torch.bfloat16):
     """The Qwen3-8B decode step at full size: B = 256, L ~ U[512, 8192] including the new token,
     a 160k-page pool, block tables from one seeded permutation (host generator, seed 2), pools,
-    new rows and q drawn on the device. Returns (q, kp, vp, bt, lens, n_pages, page, offset,
-    slots, k_new, v_new); bt / lens / n_pages / page / offset / slots on the host."""
+    new rows and q drawn on the device in `dtype`. Returns (q, kp, vp, bt, lens, n_pages, page,
+    offset, slots, k_new, v_new); bt / lens / n_pages / page / offset / slots on the host."""
     B, Hq, Hkv, D, P, N_ = 256, 32, 8, 128, 16, 160_000
     g = torch.Generator().manual_seed(2)
     lens = torch.randint(512, 8193, (B,), generator=g)
@@ -204,15 +204,15 @@ def qwen3_8b_b256_inputs(dev):
     page = bt[torch.arange(B), last // P].long()
     slots = page * P + last % P
     gd = torch.Generator(device=dev).manual_seed(2)
-    kp = torch.empty(N_, Hkv, D, P, dtype=torch.bfloat16, device=dev)
+    kp = torch.empty(N_, Hkv, D, P, dtype=dtype, device=dev)
     vp = torch.empty_like(kp)
     for pool in (kp, vp):
         for s in range(0, N_, 20_000):
             pool[s:s + 20_000] = torch.randn(pool[s:s + 20_000].shape, generator=gd,
-                                             device=dev).to(torch.bfloat16)
-    k_new = torch.randn(B, Hkv, D, generator=gd, device=dev).to(torch.bfloat16)
-    v_new = torch.randn(B, Hkv, D, generator=gd, device=dev).to(torch.bfloat16)
-    q = torch.randn(B, Hq, D, generator=gd, device=dev).to(torch.bfloat16)
+                                             device=dev).to(dtype)
+    k_new = torch.randn(B, Hkv, D, generator=gd, device=dev).to(dtype)
+    v_new = torch.randn(B, Hkv, D, generator=gd, device=dev).to(dtype)
+    q = torch.randn(B, Hq, D, generator=gd, device=dev).to(dtype)
     return q, kp, vp, bt, lens, n_pages, page, last % P, slots, k_new, v_new
 
 
