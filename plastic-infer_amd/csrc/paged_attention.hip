@@ -1898,9 +1898,9 @@ extern "C" int pia_paged_attention(void* out, const void* q, const void* k_pages
   if (prefill_mfma_path(dtype, num_heads, num_kv_heads, head_dim, page_size, num_seqs,
                         total_q_rows, cu_q, scale) &&
       aligned(q, 16) && aligned(out, 16) && aligned(k_pages, 16) && aligned(v_pages, 16))
-    return launch_prefill_mfma(out, q, k_pages, v_pages, block_tables, bt_stride, kv_lens, cu_q,
-                               q_pos_offsets, num_seqs, total_q_rows, num_heads, num_kv_heads,
-                               num_pages, scale * kLog2e, as_stream(stream));
+    return launch_prefill_mfma(dtype, out, q, k_pages, v_pages, block_tables, bt_stride, kv_lens,
+                               cu_q, q_pos_offsets, num_seqs, total_q_rows, num_heads,
+                               num_kv_heads, num_pages, scale * kLog2e, as_stream(stream));
   return launch_generic_any(dtype, out, q, int64_t(num_heads) * head_dim, k_pages, v_pages,
                             block_tables, bt_stride, kv_lens, cu_q, q_pos_offsets, num_seqs,
                             total_q_rows, num_heads, num_kv_heads, head_dim, page_size,

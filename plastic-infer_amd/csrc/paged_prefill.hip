@@ -1,5 +1,5 @@
 // Paged attention of many query rows per sequence (prefill, chunked prefill) on the matrix
-// cores, gfx950: bf16, head_dim 128, page size 16, Hq / Hkv = G in {1, 2, 4, 8}.
+// cores, gfx950: bf16 or fp16 (DT), head_dim 128, page size 16, Hq / Hkv = G in {1, 2, 4, 8}.
 //
 // Work item (one workgroup of NW = 8 waves, or 4 when the sequences have few rows): one kv head
 // and 32 NW / G consecutive query positions of one sequence, i.e. 32 NW (position, q head) rows
@@ -21,7 +21,7 @@
 // reads in the K layout were conflict-free one by one, but the compiler pairs those of blocks nb
 // and nb + 2 into ds_read2st64_b64, whose two halves per lane share a bank: 8 conflict cycles.)
 // Per tile each wave runs
-//   S^T = K . Q^T   v_mfma_f32_16x16x32_bf16: A = K^T operands built by ds_read_b64_tr_b16
+//   S^T = K . Q^T   v_mfma_f32_16x16x32_{bf16,f16}: A = K^T operands built by ds_read_b64_tr_b16
 //                   (within each 16-lane group the eight-byte reads of the lanes form a 16 x 4
 //                   matrix, and lane i receives elements (4 k + i / 4, i % 4), k < 4; so lane r
 //                   of group g reads the four tokens 16 m + 4 (r % 4) .. of K row d0 + r / 4 and
@@ -32,7 +32,7 @@
 //   online softmax  per row in fp32, base 2 with the scale folded in; a row's 64 scores sit
 //                   in four lanes (l, l ^ 16, l ^ 32, l ^ 48), reduced by two lane swaps.
 //   O += P . V      the probabilities are the A operand straight from the score registers
-//                   (bf16): k slot 8 (l / 16) + j of 32-token chunk c is token
+//                   (rounded to DT): k slot 8 (l / 16) + j of 32-token chunk c is token
 //                   32 c + 4 (l / 16) + j for j < 4 and 32 c + 16 + 4 (l / 16) + j - 4 after,
 //                   and the B operand is V unit 4 c + l / 16 of row 16 nb + l % 16 (one 16-byte
 //                   LDS read), so both sides of every MFMA sum the same 32 tokens. O (16 rows x
@@ -70,7 +70,7 @@ constexpr int PF_RSRC_WORD3 = 0x00020000;
 // that trails its true max by at most this much, so probabilities stay <= 2^8
 constexpr float PF_RESCALE = 8.0f;
 
-template <int G, int NW>
+template <int G, int NW, int DT>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void paged_prefill_mfma(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ kpool, const uint16_t* __restrict__ vpool,
@@ -289,7 +289,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void paged_prefill_mfma(
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb) acc[rb][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
-  const uint4 ones = tile::bf16_ones();
+  const uint4 ones = tile::ones16<DT>();
 
   // Tile 0 is staged before the loop; tile kt + 1 is staged in the middle of tile kt (after its
   // softmax, before its P . V), from registers fetched a tile earlier, and the fetch of tile
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void paged_prefill_mfma(
         const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
-          sc[rb][mb] = tile::mfma_bf16(a, qreg[rb][kc],
+          sc[rb][mb] = tile::mfma16<DT>(a, qreg[rb][kc],
                                        kc == 0 ? f32x4_t{0.f, 0.f, 0.f, 0.f} : sc[rb][mb]);
       }
     }
@@ -368,8 +368,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void paged_prefill_mfma(
           for (int j = 0; j < 4; ++j)
             p[hh][j] = __builtin_amdgcn_exp2f(fmaf(sc[rb][2 * c + hh][j], scale_log2, nm));
         pk[rb][c] = make_uint4(
-            tile::pack_bf16x2(p[0][0], p[0][1]), tile::pack_bf16x2(p[0][2], p[0][3]),
-            tile::pack_bf16x2(p[1][0], p[1][1]), tile::pack_bf16x2(p[1][2], p[1][3]));
+            tile::pack16x2<DT>(p[0][0], p[0][1]), tile::pack16x2<DT>(p[0][2], p[0][3]),
+            tile::pack16x2<DT>(p[1][0], p[1][1]), tile::pack16x2<DT>(p[1][2], p[1][3]));
       }
     }
     // rescale O and the sums when some row's reference point moved: lane l's accumulator rows
@@ -403,10 +403,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void paged_prefill_mfma(
       const uint4 vop = vq[i % PF_V_AHEAD];
       if (i + PF_V_AHEAD < 16) vq[i % PF_V_AHEAD] = vread(buf, i + PF_V_AHEAD);
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) acc[rb][nb] = tile::mfma_bf16(pk[rb][c], vop, acc[rb][nb]);
+      for (int rb = 0; rb < RB; ++rb) acc[rb][nb] = tile::mfma16<DT>(pk[rb][c], vop, acc[rb][nb]);
       if (nb == 7) {
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) lsum[rb] = tile::mfma_bf16(pk[rb][c], ones, lsum[rb]);
+        for (int rb = 0; rb < RB; ++rb) lsum[rb] = tile::mfma16<DT>(pk[rb][c], ones, lsum[rb]);
       }
     }
     // keep that order through the machine scheduler (it would sink the reads to their uses):
@@ -436,7 +436,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void paged_prefill_mfma(
       uint16_t* o = out + (row0 + s) * q_row + int64_t(h * G + r % G) * D + n16;
       const float inv = lj > 0.f ? 1.f / lj : 0.f;
 #pragma unroll
-      for (int nb = 0; nb < 8; ++nb) o[16 * nb] = f32_to_bf16(acc[rb][nb][j] * inv);
+      for (int nb = 0; nb < 8; ++nb)
+        o[16 * nb] = DT == PIA_DTYPE_F16 ? f32_to_half(acc[rb][nb][j] * inv)
+                                         : f32_to_bf16(acc[rb][nb][j] * inv);
     }
 }
 
@@ -446,13 +448,14 @@ bool prefill_mfma_path(int dtype, int Hq, int Hkv, int D, int P, int num_seqs,
                        int64_t total_q_rows, const int32_t* cu_q, float scale) {
   const int G = Hq / Hkv;
   // scale > 0: the kernel keeps its running max in raw score units
-  return dtype == PIA_DTYPE_BF16 && D == PF_D && P == PF_P && scale > 0.f &&
+  return (dtype == PIA_DTYPE_BF16 || dtype == PIA_DTYPE_F16) && D == PF_D && P == PF_P &&
+         scale > 0.f &&
          (G == 1 || G == 2 || G == 4 || G == 8) && cu_q != nullptr && num_seqs <= PF_MAX_SEQS &&
          total_q_rows >= 4 * int64_t(num_seqs);
 }
 
-int launch_prefill_mfma(void* out, const void* q, const void* k_pages, const void* v_pages,
-                        const int32_t* bt, int64_t bt_stride, const int32_t* kv_lens,
+int launch_prefill_mfma(int dtype, void* out, const void* q, const void* k_pages,
+                        const void* v_pages, const int32_t* bt, int64_t bt_stride, const int32_t* kv_lens,
                         const int32_t* cu_q, const int32_t* offsets, int num_seqs,
                         int64_t total_q_rows, int Hq, int Hkv, int64_t num_pages,
                         float scale_log2, hipStream_t s) {
@@ -468,7 +471,7 @@ int launch_prefill_mfma(void* out, const void* q, const void* k_pages, const voi
     return fail(PIA_EINVAL, "paged_attention: too many query rows for the prefill kernel");
   const dim3 grid{unsigned(blocks), 1u, 1u};
 #define PIA_PF(GG, NW)                                                                         \
-  hipLaunchKernelGGL((paged_prefill_mfma<GG, NW>), grid, dim3(64 * NW), 0, s,                  \
+  hipLaunchKernelGGL((paged_prefill_mfma<GG, NW, DT>), grid, dim3(64 * NW), 0, s,              \
                      reinterpret_cast<uint16_t*>(out), reinterpret_cast<const uint16_t*>(q),   \
                      reinterpret_cast<const uint16_t*>(k_pages),                               \
                      reinterpret_cast<const uint16_t*>(v_pages), bt, bt_stride, kv_lens, cu_q, \
@@ -480,11 +483,20 @@ int launch_prefill_mfma(void* out, const void* q, const void* k_pages, const voi
     case 4: PIA_PF(4, NW); break;     \
     default: PIA_PF(8, NW); break;    \
   }
-  if (wide) {
-    PIA_PF_G(8);
-  } else {
-    PIA_PF_G(4);
+#define PIA_PF_D(NW)                           \
+  if (dtype == PIA_DTYPE_F16) {                \
+    constexpr int DT = PIA_DTYPE_F16;          \
+    PIA_PF_G(NW)                               \
+  } else {                                     \
+    constexpr int DT = PIA_DTYPE_BF16;         \
+    PIA_PF_G(NW)                               \
   }
+  if (wide) {
+    PIA_PF_D(8);
+  } else {
+    PIA_PF_D(4);
+  }
+#undef PIA_PF_D
 #undef PIA_PF_G
 #undef PIA_PF
   return check_launch("paged_prefill_mfma");

@@ -40,7 +40,8 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // and its launch (arguments already checked by pia_paged_attention).
 bool prefill_mfma_path(int dtype, int Hq, int Hkv, int D, int P, int num_seqs,
                        int64_t total_q_rows, const int32_t* cu_q, float scale);
-int launch_prefill_mfma(void* out, const void* q, const void* k_pages, const void* v_pages,
+int launch_prefill_mfma(int dtype, void* out, const void* q, const void* k_pages,
+                        const void* v_pages,
                         const int32_t* bt, int64_t bt_stride, const int32_t* kv_lens,
                         const int32_t* cu_q, const int32_t* offsets, int num_seqs,
                         int64_t total_q_rows, int Hq, int Hkv, int64_t num_pages,

@@ -1,11 +1,11 @@
 """GPU parity of multi-row paged attention on the matrix cores (pia_paged_attention's prefill
-kernel: bf16, head_dim 128, page size 16, G in {1, 2, 4, 8}, at least 4 query rows per sequence
-on average) against the oracle's paged attention (the reference's gather + SDPA, and the
+kernel: bf16 or fp16, head_dim 128, page size 16, G in {1, 2, 4, 8}, at least 4 query rows per
+sequence on average) against the oracle's paged attention (the reference's gather + SDPA, and the
 explicit offset mask of src/plastic_infer/exec/runner_paged.py:61-95, oracle/paged_kv.py).
 
 Bar: 2e-2 absolute on bf16 outputs (the bf16 attention bar of the decode tests: the kernel
 rounds the probabilities to bf16 for the P.V products, the oracle's CPU SDPA rounds its own
-intermediates). Invalid block-table ids inside a context and rows without any admissible key are
+intermediates); 5e-3 on fp16 outputs (the same with fp16's 11 significant bits). Invalid block-table ids inside a context and rows without any admissible key are
 checked against fp64 brute force with those keys removed.
 """
 
@@ -21,13 +21,14 @@ from plastic_infer.kernel import paged_attention
 pytestmark = pytest.mark.gpu
 
 BF16_TOL = 2e-2
+FP16_TOL = 5e-3
 P, D = 16, 128
 
 
-def _pools(seed, n_pages, Hkv):
+def _pools(seed, n_pages, Hkv, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
-    kp = torch.randn(n_pages, Hkv, D, P, generator=g).to(torch.bfloat16)
-    vp = torch.randn(n_pages, Hkv, D, P, generator=g).to(torch.bfloat16)
+    kp = torch.randn(n_pages, Hkv, D, P, generator=g).to(dtype)
+    vp = torch.randn(n_pages, Hkv, D, P, generator=g).to(dtype)
     return kp, vp, g
 
 
@@ -224,3 +225,45 @@ def test_prefill_nan_key_reaches_exactly_the_rows_that_see_it(dev, G):
         assert torch.equal(torch.isnan(got), want), b
         err = (got[~want] - ref[~want]).abs().max().item()
         assert err <= BF16_TOL, (b, err)
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_prefill_fp16_causal_chunks(dev, G):
+    """The chunk layouts of test_prefill_causal_chunks on fp16 pools and queries."""
+    Hkv = 2
+    q_rows = [100, 64, 37]
+    kv_lens = [300, 64, 1000]
+    offsets = [kv - n for kv, n in zip(kv_lens, q_rows)]
+    offsets[1] = 0
+    kp, vp, g = _pools(120 + G, 120, Hkv, torch.float16)
+    bt, tables = _tables(kv_lens, 120, g)
+    q = torch.randn(sum(q_rows), Hkv * G, D, generator=g).to(torch.float16)
+    out, cu = _run(dev, q, kp, vp, bt, kv_lens, q_rows, offsets)
+    assert out.dtype == torch.float16
+    for b in range(3):
+        rows = q[cu[b]:cu[b + 1]][None]
+        ref = OP.paged_attention(rows, kp, vp, tables[b], P, kv_lens[b], causal=True,
+                                 q_start_pos=offsets[b])[0]
+        err = (out[cu[b]:cu[b + 1]].float() - ref.float()).abs().max().item()
+        assert err <= FP16_TOL, (b, err)
+
+
+def test_prefill_fp16_stale_tail_and_long_chunk(dev):
+    """fp16: a 1024-row chunk at the end of a 4096-token context with Qwen3-8B heads, and a
+    short chunk whose last page holds NaN (K) / Inf (V) past its length."""
+    G, Hkv = 4, 8
+    q_rows, kv_lens = [1024, 40], [4096, 300]
+    offsets = [kv - n for kv, n in zip(kv_lens, q_rows)]
+    kp, vp, g = _pools(141, 300, Hkv, torch.float16)
+    bt, tables = _tables(kv_lens, 300, g)
+    kp[tables[1][-1], :, :, 300 % P:] = float("nan")
+    vp[tables[1][-1], :, :, 300 % P:] = float("inf")
+    q = torch.randn(sum(q_rows), Hkv * G, D, generator=g).to(torch.float16)
+    out, cu = _run(dev, q, kp, vp, bt, kv_lens, q_rows, offsets)
+    assert torch.isfinite(out.float()).all()
+    for b in range(2):
+        rows = q[cu[b]:cu[b + 1]][None]
+        ref = OP.paged_attention(rows, kp, vp, tables[b], P, kv_lens[b], causal=True,
+                                 q_start_pos=offsets[b])[0]
+        err = (out[cu[b]:cu[b + 1]].float() - ref.float()).abs().max().item()
+        assert err <= FP16_TOL, (b, err)
