@@ -125,7 +125,7 @@ int pia_kv_pages_chunks_copy(void* const* chunks, int num_chunks, void* pages,
  *                                      bt_stride)
  * bytes, 4-byte aligned (may be NULL when that query returns 0). Calls that share a workspace
  * must be ordered (same stream): a launch keeps its partials and arrival counters in it.
- * bf16 or fp16 with head_dim 128 and page_size 16 and Hq/Hkv in {1, 2, 4, 8} takes the fast
+ * bf16 or fp16 with head_dim 128 and page_size 16 and Hq/Hkv in 1..8 or 16 takes the fast
  * kernel (the batch's KV steps split over persistent waves, XCD-aware; the probabilities enter
  * the P.V products rounded to the pools' dtype); every other supported combination
  * (f32/f16/bf16, head_dim <= 512, any page_size) takes the general kernel.
@@ -140,7 +140,7 @@ int64_t pia_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv
  * hold one 64-bit arrival counter per wave (from the first 8-byte boundary of a 4-byte aligned
  * buffer); bytes [*partials_offset, *total_bytes) hold two partial slots per wave of
  * (num_heads / num_kv_heads) rows of head_dim + 2 fp32. Returns 0, or PIA_EINVAL /
- * PIA_EUNSUPPORTED (Hq / Hkv outside {1, 2, 4, 8}). */
+ * PIA_EUNSUPPORTED (Hq / Hkv outside 1..8 and 16). */
 int pia_paged_decode_scratch_layout(int num_heads, int num_kv_heads, int waves,
                                     int64_t* partials_offset, int64_t* total_bytes);
 
@@ -184,13 +184,13 @@ int pia_paged_decode_append_attention(void* out, const void* q, int64_t q_seq_st
  * No counterpart in the reference: it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * Same arguments and results as pia_paged_decode_attention without the workspace: the fast
- * kernel keeps its partials in a static device array of the library (16 MiB per GPU, held
+ * kernel keeps its partials in a static device array of the library (32 MiB per GPU, held
  * until the process ends; its address on each device is resolved on the first call there).
  * No hipMalloc / hipFree / allocating library routine is called. Every call on one GPU shares
  * that GPU's array: calls that overlap on one GPU (different streams, or unordered host
  * threads) race and must not be issued; calls ordered on one stream are safe. The array needs
  * no clearing (each launch writes what it reads). Returns PIA_EUNSUPPORTED when the partials
- * of the launch would not fit (pia_paged_decode_noalloc_scratch_bytes > 16 MiB).
+ * of the launch would not fit (pia_paged_decode_noalloc_scratch_bytes > 32 MiB).
  * ------------------------------------------------------------------------------------------- */
 int64_t pia_paged_decode_noalloc_scratch_bytes(int num_heads, int num_kv_heads);
 

@@ -15,8 +15,8 @@
 //    wave that writes a segment's last partial merges them in the same launch.
 //    Block-table ids outside [0, num_pages) inside a context are not dereferenced: their tokens
 //    are not keys (score -inf, V zeroed); a row with no key at all is written as zeros.
-// 2. paged_decode_mfma<8>: the same split, cursor, partials and merge for G = 8, with the tile
-//    work of a step on the matrix cores (QK^T and PV as bf16 16x16x32 MFMAs, K through a
+// 2. paged_decode_mfma<G> (G = 3, 5..8, 16): the same split, cursor, partials and merge, with
+//    the tile work of a step on the matrix cores (QK^T and PV as 16x16x32 MFMAs, K through a
 //    swizzled LDS tile and transposing reads, V straight into the MFMA operand registers).
 // 3. paged_attention_generic<DT, DPL>: any dtype / head_dim <= 512 / page size, several query
 //    rows per sequence with optional causal offsets. One wave per (query row, head); keys are
@@ -221,7 +221,9 @@ constexpr DecodeScratchLayout decode_scratch_layout(int G, int waves) {
           (int64_t(waves) * 8 + 8 + 255) / 256 * 256 +
               int64_t(waves) * 2 * G * (FD_D + 2) * int64_t(sizeof(float))};
 }
-constexpr bool stream_group_ok(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
+// Group sizes of the fast kernels: 1, 2, 4 on the vector ALU (paged_decode_stream), 3, 5..8 and 16
+// on the matrix cores (paged_decode_mfma, whose 16-row MFMA blocks hold up to 16 q rows).
+constexpr bool stream_group_ok(int G) { return (G >= 1 && G <= 8) || G == 16; }
 constexpr int SD_EVEN_SHARE_PERMILLE = 515;                // even-XCD wave's share of a pair
 
 // Steps of a wave pair and the even wave's share of them, for T steps over NW waves.
@@ -911,7 +913,8 @@ __global__ __launch_bounds__(64, 2) void paged_decode_stream(
 }
 
 // ---------------------------------------------------------------------------------------------
-// Stream decode kernel on the matrix cores (bf16 or fp16, D = 128, P = 16), launched for G = 8.
+// Stream decode kernel on the matrix cores (bf16 or fp16, D = 128, P = 16), launched for G = 3,
+// 5..8 and 16 (q rows G..15 of its 16-row MFMA blocks are zero).
 //
 // The same work split, cursor, partial slots, arrivals and merge as paged_decode_stream, one wave
 // per SIMD; only the tile work of a step differs. Eight q rows against 128 keys cost 2048
@@ -1544,14 +1547,14 @@ int check_heads(int Hq, int Hkv, int D, int P, int64_t num_pages, int dtype) {
 bool fast_path(int dtype, int Hq, int Hkv, int D, int P) {
   const int G = Hq / Hkv;
   return (dtype == PIA_DTYPE_BF16 || dtype == PIA_DTYPE_F16) && D == FD_D && P == FD_P &&
-         (G == 1 || G == 2 || G == 4 || G == 8);
+         Hq % Hkv == 0 && stream_group_ok(G);
 }
 
-// Whether a decode launch with G q rows per kv head runs the matrix-core engine: G = 8 only.
-// At G = 4 (Qwen3-8B, batch 256) the vector-ALU engine at two waves per SIMD measured 0.718 ms
-// per step against 0.740 ms for the matrix-core engine at one (its registers), so G <= 4 stays
-// on paged_decode_stream.
-bool stream_uses_mfma(int G) { return G == 8; }
+// Whether a decode launch with G q rows per kv head runs the matrix-core engine: every fast
+// group size but 1, 2 and 4. At G = 4 (Qwen3-8B, batch 256) the vector-ALU engine at two waves
+// per SIMD measured 0.718 ms per step against 0.740 ms for the matrix-core engine at one (its
+// registers), so the powers of two up to 4 stay on paged_decode_stream.
+bool stream_uses_mfma(int G) { return !(G == 1 || G == 2 || G == 4); }
 
 // Waves of a stream launch (CU count cached per device), capped by the partial slots the
 // workspace holds: two single-wave workgroups per SIMD for the vector-ALU engine, one for the
@@ -1659,6 +1662,11 @@ int launch_stream_decode_dt(void* out, const void* q, int64_t q_seq_stride, cons
         case 1: PIA_SD(1, true); break;
         case 2: PIA_SD(2, true); break;
         case 4: PIA_SD(4, true); break;
+        case 3: PIA_SDM(3, true); break;
+        case 5: PIA_SDM(5, true); break;
+        case 6: PIA_SDM(6, true); break;
+        case 7: PIA_SDM(7, true); break;
+        case 16: PIA_SDM(16, true); break;
         default: PIA_SDM(8, true); break;
       }
     } else {
@@ -1666,6 +1674,11 @@ int launch_stream_decode_dt(void* out, const void* q, int64_t q_seq_stride, cons
         case 1: PIA_SD(1, false); break;
         case 2: PIA_SD(2, false); break;
         case 4: PIA_SD(4, false); break;
+        case 3: PIA_SDM(3, false); break;
+        case 5: PIA_SDM(5, false); break;
+        case 6: PIA_SDM(6, false); break;
+        case 7: PIA_SDM(7, false); break;
+        case 16: PIA_SDM(16, false); break;
         default: PIA_SDM(8, false); break;
       }
     }
@@ -1699,7 +1712,7 @@ int launch_stream_decode(int dtype, void* out, const void* q, int64_t q_seq_stri
 // GPU shares that GPU's array: calls that overlap (two streams, or two host threads without
 // ordering) race on it.
 // ---------------------------------------------------------------------------------------------
-constexpr int64_t kNoAllocScratchBytes = int64_t(16) << 20;                  // 16 MiB per GPU
+constexpr int64_t kNoAllocScratchBytes = int64_t(32) << 20;                  // 32 MiB per GPU
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
@@ -1748,7 +1761,7 @@ extern "C" int pia_paged_decode_scratch_layout(int num_heads, int num_kv_heads, 
   if (!partials_offset || !total_bytes) return fail(PIA_EINVAL, "decode_scratch_layout: null pointer");
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads ||
       !stream_group_ok(num_heads / num_kv_heads))
-    return fail(PIA_EUNSUPPORTED, "decode_scratch_layout: Hq / Hkv must be 1, 2, 4 or 8");
+    return fail(PIA_EUNSUPPORTED, "decode_scratch_layout: Hq / Hkv must be 1..8 or 16");
   if (waves < 2 || waves > SD_MAX_WAVES)
     return fail(PIA_EINVAL, "decode_scratch_layout: waves must be in [2, 4096]");
   const DecodeScratchLayout lay = decode_scratch_layout(num_heads / num_kv_heads, waves);

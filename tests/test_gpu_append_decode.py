@@ -158,7 +158,7 @@ def test_append_decode_edge_rows(dev, G):
 
 @pytest.mark.parametrize("dtype,Hq,Hkv,D,P,tol", [
     (torch.float32, 4, 2, 64, 8, 1e-4),        # general kernel path: write kernel + decode
-    (torch.float16, 6, 2, 128, 16, BF16_TOL),  # G = 3: not a stream-kernel group size
+    (torch.float16, 6, 2, 128, 16, BF16_TOL),  # G = 3: the matrix-core kernel
     (torch.bfloat16, 8, 8, 96, 16, BF16_TOL),  # head_dim 96
 ])
 def test_append_decode_general_shapes(dev, dtype, Hq, Hkv, D, P, tol):

@@ -59,14 +59,15 @@ def test_invalid_arguments_are_rejected_without_device_work():
         for b, bt in ((256, 512), (1, 4)):
             assert N.query("pia_paged_decode_workspace_bytes", b, hq, 8, 128, 16, bt) == \
                 total.value
-    # general kernel (head_dim 64, or G = 3): no workspace
+    # general kernel (head_dim 64, or G = 9): no workspace; G = 3 runs a fast kernel
     assert N.query("pia_paged_decode_workspace_bytes", 4, 4, 4, 64, 16, 8) == 0
-    assert N.query("pia_paged_decode_workspace_bytes", 4, 24, 8, 128, 16, 8) == 0
+    assert N.query("pia_paged_decode_workspace_bytes", 4, 72, 8, 128, 16, 8) == 0
+    assert N.query("pia_paged_decode_workspace_bytes", 4, 24, 8, 128, 16, 8) > 0
     with pytest.raises(N.NativeError):
         N.call("pia_moe_sum_reduce", None, None, 1, 0, 4, 2, None)
 
 
-@pytest.mark.parametrize("group", [1, 2, 4, 8])
+@pytest.mark.parametrize("group", [1, 2, 3, 4, 5, 6, 7, 8, 16])
 def test_decode_scratch_layout(group):
     """The one layout every decode entry point uses: the arrival counters (one 8-byte word per
     wave, starting at the first 8-byte boundary of a buffer that is only 4-byte aligned) end
@@ -85,7 +86,7 @@ def test_decode_scratch_layout(group):
         assert total.value > prev_total
         prev_total = total.value
     off, total = ctypes.c_int64(), ctypes.c_int64()
-    assert lib.pia_paged_decode_scratch_layout(24, 8, 64, ctypes.byref(off),
+    assert lib.pia_paged_decode_scratch_layout(72, 8, 64, ctypes.byref(off),
                                                ctypes.byref(total)) == -2
     assert lib.pia_paged_decode_scratch_layout(32, 8, 4097, ctypes.byref(off),
                                                ctypes.byref(total)) == -1
