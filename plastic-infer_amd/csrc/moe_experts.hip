@@ -473,6 +473,12 @@ constexpr int TG_XCDS = 8;
 // is such an offset for every buffer here (the host keeps A and each expert's W below 2 GiB).
 constexpr int TG_RSRC_WORD3 = 0x00020000;
 constexpr uint32_t TG_OOB = 0x80000000u;
+// Cache-policy operand of a buffer load: the nt (non-temporal) bit. The W rows of the wide
+// kernel are streamed once per launch; with the hint they displace less of what the next
+// launches read (its A rows, the GEMM outputs): 263-267 -> 253-256 us for the first prefill
+// GEMM and 179-181 -> 171 us for the second, back to back on one box. The decode kernels load W
+// into registers, where the same hint measured slower (147 -> 161 us, 82 -> 97 us).
+constexpr int TG_POLICY_NT = 2;
 #ifndef PIA_EG_WIDE_MIN_ROUTES
 #define PIA_EG_WIDE_MIN_ROUTES 2048  // routes per call from which moe_gemm_wide is used
 #endif
@@ -686,7 +692,7 @@ __global__ __launch_bounds__(TW_THREADS, 1) void moe_gemm_wide(
       for (int q = 0; q < TW_WL; ++q)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             wres, (tg_lds_t*)(buf + (TW_AH + TW_WL * wv + q) * 64), 16,
-            kin ? woff[q] : TG_OOB, k0 * 2, 0, 0);
+            kin ? woff[q] : TG_OOB, k0 * 2, 0, TG_POLICY_NT);
     };
     f32x4_t acc[TW_RF][8];
 #pragma unroll
