@@ -16,7 +16,7 @@ with HIP events on the launch stream) and the CPU baseline (the oracle's restate
 reference torch path on this host's cores, on a bounded sample of the same inputs).
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-sample-seqs S] [--no-cpu-baseline]
-                  [--separate-write]
+                  [--separate-write] [--dtype bf16|fp16]   # fp16: the same step on fp16 pools
   python bench.py --calibrate-copy     # 1 GiB read + 1 GiB write elementwise copy, three times:
                                        # the known-size reference for HBM byte counters
   python bench.py --workload decode-gqa8     # Qwen3-30B-A3B attention layer: 64 x 4096 tokens,
@@ -36,6 +36,8 @@ reference torch path on this host's cores, on a bounded sample of the same input
                                              # expert double buffer, 48 layers of pinned banks
   python bench.py --workload prefill-attn    # chunked-prefill paged attention (matrix cores):
                                              # 8 x 1024-token chunks after 3072 context tokens
+  python bench.py --workload hbm-read        # the streaming-read rate of the box (fixed cost +
+                                             # rate over 26 MB .. 3.4 GB): the practical ceiling
 The default workload (decode) is the headline; the others print their own JSON line.
 """
 
@@ -60,10 +62,12 @@ LEN_LO, LEN_HI, SEED = 512, 8192, 2
 MAX_PAGES = LEN_HI // P
 WORKLOAD = "qwen3-8b paged decode: kv scatter + gqa paged attention, 1 layer"
 PMC_FILE = ROOT / "profiles" / "paged_decode_qwen3_8b_b256_pmc.json"
+PMC_FP16_FILE = ROOT / "profiles" / "paged_decode_qwen3_8b_b256_fp16_pmc.json"
 GQA8_PMC_FILE = ROOT / "profiles" / "paged_decode_gqa8_qwen3_30b_b64_pmc.json"
 
 
-def build_inputs(torch, dev):
+def build_inputs(torch, dev, dtype=None):
+    dtype = dtype or torch.bfloat16
     g = torch.Generator().manual_seed(SEED)
     lens = torch.randint(LEN_LO, LEN_HI + 1, (B,), generator=g)
     perm = torch.randperm(NUM_PAGES, generator=g)
@@ -77,16 +81,16 @@ def build_inputs(torch, dev):
     last = lens - 1
     slots = bt[torch.arange(B), last // P].to(torch.int64) * P + last % P
     gd = torch.Generator(device=dev).manual_seed(SEED)
-    kp = torch.empty(NUM_PAGES, HKV, D, P, dtype=torch.bfloat16, device=dev)
+    kp = torch.empty(NUM_PAGES, HKV, D, P, dtype=dtype, device=dev)
     vp = torch.empty_like(kp)
     step = 20_000
     for pool in (kp, vp):
         for s in range(0, NUM_PAGES, step):
             pool[s:s + step] = torch.randn(pool[s:s + step].shape, generator=gd,
-                                           device=dev).to(torch.bfloat16)
-    k_new = torch.randn(B, HKV, D, generator=gd, device=dev).to(torch.bfloat16)
-    v_new = torch.randn(B, HKV, D, generator=gd, device=dev).to(torch.bfloat16)
-    q = torch.randn(B, HQ, D, generator=gd, device=dev).to(torch.bfloat16)
+                                           device=dev).to(dtype)
+    k_new = torch.randn(B, HKV, D, generator=gd, device=dev).to(dtype)
+    v_new = torch.randn(B, HKV, D, generator=gd, device=dev).to(dtype)
+    q = torch.randn(B, HQ, D, generator=gd, device=dev).to(dtype)
     return dict(lens=lens, n_pages=n_pages, bt=bt, slots=slots, kp=kp, vp=vp, k_new=k_new,
                 v_new=v_new, q=q, bt_d=bt.to(dev), lens_d=lens.to(torch.int32).to(dev),
                 slots_d=slots.to(dev))
@@ -533,8 +537,9 @@ def bench_prefill_attn(torch, dev, args) -> dict:
          "batch": b, "chunk": chunk, "context_len": ctx},
         {"flops_per_step": flops, "hbm_bytes_per_step": hbm,
          "hbm_gbps": round(hbm / (k_ms / 1e3) / 1e9, 2), "wall_s_timed": round(wall, 4)},
-        {"kernel": "paged_prefill_mfma<4>", "bound": "mfma", "achieved": round(tflops, 2),
-         "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+        {"kernel": "paged_prefill_mfma<4, 8 waves, bf16>", "bound": "mfma",
+         "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+         "frac": round(tflops / 2500.0, 4), "traffic": None,
          "algorithmic_flops_per_launch": flops, "avg_launch_ms": round(k_ms, 4)},
         cpu)
 
@@ -609,6 +614,71 @@ def _pin_expert_banks(torch, markers: bool):
         if l % 8 == 7:
             print(f"bench: {l + 1}/{L} layers pinned", file=sys.stderr, flush=True)
     return banks
+
+
+def bench_hbm_read(torch, dev, args) -> dict:
+    """The box's streaming-read rate (pia_hbm_read_probe) for two access patterns: `flat` (the
+    buffer front to back) and `tiles` (distinct 4 KiB tiles drawn at random from a 12 GiB
+    buffer, the paged-KV access of the decode kernels). Reads of X bytes, X = 25 MiB .. 3.2 GiB
+    in doublings, each from a region that the reads before it did not touch for at least 10 GB
+    (the 256 MB last-level cache holds none of it) or from fresh random tiles, timed by events
+    around each launch: one untimed launch, then the mean of `steps` (at least 6). Per pattern
+    t(X) = fixed + X / rate, fitted by least squares over X >= 200 MB. `value` is the tiles
+    rate: the ceiling the paged decode kernels are compared with."""
+    from plastic_infer import _native as N
+
+    pool_bytes = 12 << 30
+    pool_tiles = pool_bytes // 4096
+    pool = torch.zeros(pool_bytes, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sizes = [(25 << 20) << i for i in range(8)]
+    reps = max(6, args.steps)
+    out = {}
+    for pattern in ("flat", "tiles"):
+        rows, off = [], 0
+        for X in sizes:
+            times = []
+            for r in range(reps + 1):
+                ids, n = None, 0
+                if pattern == "tiles":
+                    n = X // 4096
+                    ids = torch.randperm(pool_tiles, device=dev)[:n].to(torch.int32)
+                elif off + X > pool_bytes:
+                    off = 0
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                N.call("pia_hbm_read_probe", pool.data_ptr() + (off if ids is None else 0),
+                       X if ids is None else pool_bytes, None if ids is None else ids.data_ptr(),
+                       n, sink.data_ptr(), N.stream_of(dev))
+                b.record(stream)
+                b.synchronize()
+                if r > 0:
+                    times.append(a.elapsed_time(b) / 1e3)
+                if ids is None:
+                    off += (X + (4 << 20)) & ~((2 << 20) - 1)
+            t = statistics.mean(times)
+            rows.append({"bytes": X, "mean_us": round(t * 1e6, 2),
+                         "min_us": round(min(times) * 1e6, 2), "gbps": round(X / t / 1e9, 1)})
+        fit = [r for r in rows if r["bytes"] >= 200e6]
+        xs = [r["bytes"] for r in fit]
+        ts = [r["mean_us"] / 1e6 for r in fit]
+        mx, mt = statistics.mean(xs), statistics.mean(ts)
+        slope = sum((x - mx) * (t - mt) for x, t in zip(xs, ts)) / sum((x - mx) ** 2 for x in xs)
+        out[pattern] = {"fixed_us": round((mt - slope * mx) * 1e6, 2),
+                        "rate_gbps": round(1.0 / slope / 1e9, 1),
+                        "rate_frac_of_8tbps": round(1.0 / slope / 1e9 / HBM_PEAK_GBPS, 4),
+                        "per_size": rows}
+    rate = out["tiles"]["rate_gbps"]
+    return {"metric": "HBM streaming-read GB/s, random 4 KiB tiles (fit: fixed cost + bytes / "
+                      "rate)",
+            "value": rate, "unit": "GB/s", "n_gpus": 1, "steps": reps,
+            "higher_is_better": True, "vs_baseline": None, "dtype": "u8",
+            "data": "zero-filled 12 GiB buffer; flat regions never re-read within 10 GB, tiles "
+                    "drawn without repeats per launch",
+            "config": {"workload": "pia_hbm_read_probe: 16-byte loads, 4 x 256-thread "
+                                   "workgroups per CU", "sizes_bytes": sizes},
+            "hbm_frac": round(rate / HBM_PEAK_GBPS, 4), "patterns": out}
 
 
 def bench_expert_stream(torch, dev, args) -> dict:
@@ -1466,10 +1536,13 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--separate-write", action="store_true",
                     help="decode: write the new rows with kv_scatter, then attend (two calls)")
+    ap.add_argument("--dtype", choices=("bf16", "fp16"), default="bf16",
+                    help="decode: storage dtype of the pools, q and the new rows")
     ap.add_argument("--workload", choices=("decode", "decode-gqa8", "prefill-write",
                                            "moe-permute", "expert-stream", "moe-experts",
                                            "moe-experts-prefill", "prefill-stream", "kv-sink",
-                                           "host-stream", "decode-step", "prefill-attn"),
+                                           "host-stream", "decode-step", "prefill-attn",
+                                           "hbm-read"),
                     default="decode")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -1498,14 +1571,15 @@ def main() -> int:
                "moe-experts-prefill": lambda t, d, a: bench_moe_experts(t, d, a, 4096),
                "prefill-stream": bench_prefill_stream, "kv-sink": bench_kv_sink,
                "host-stream": bench_host_stream, "decode-step": bench_decode_step,
-               "prefill-attn": bench_prefill_attn,
+               "prefill-attn": bench_prefill_attn, "hbm-read": bench_hbm_read,
                }[args.workload]
         print(f"bench: workload {args.workload}", file=sys.stderr, flush=True)
         print(json.dumps(run(torch, dev, args)), flush=True)
         return 0
     print(f"bench: generating inputs (B={B}, pool={NUM_PAGES} pages)", file=sys.stderr, flush=True)
-    inp = build_inputs(torch, dev)
-    out = torch.empty(B, HQ, D, dtype=torch.bfloat16, device=dev)
+    kv_dtype = {"bf16": torch.bfloat16, "fp16": torch.float16}[args.dtype]
+    inp = build_inputs(torch, dev, kv_dtype)
+    out = torch.empty(B, HQ, D, dtype=kv_dtype, device=dev)
     ws = torch.empty(decode_workspace_bytes(B, HQ, HKV, D, P, MAX_PAGES), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
 
@@ -1558,9 +1632,10 @@ def main() -> int:
     launch_bytes = attn_bytes if separate else step_bytes
     attn_gbps = launch_bytes / (attn_ms / 1e3) / 1e9
     traffic = None
-    if PMC_FILE.exists():
+    pmc_file = PMC_FILE if args.dtype == "bf16" else PMC_FP16_FILE
+    if pmc_file.exists() and not separate:
         try:
-            traffic = json.loads(PMC_FILE.read_text()).get("hbm_bytes_per_launch")
+            traffic = json.loads(pmc_file.read_text()).get("hbm_bytes_per_launch")
         except (OSError, ValueError):
             traffic = None
     result = {
@@ -1574,7 +1649,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": args.dtype,
         "data": "synthetic (seeded N(0,1) K/V/q, seeded lengths and block tables)",
         "config": {"workload": WORKLOAD, "batch": B, "q_heads": HQ, "kv_heads": HKV,
                    "head_dim": D, "page_size": P, "context_len": f"U[{LEN_LO},{LEN_HI}]",
@@ -1586,8 +1661,8 @@ def main() -> int:
         "step": "kv_scatter + paged_decode_attention" if separate
                 else "paged_decode_append_attention (write + attention, one call)",
         "roofline": {
-            "kernel": ("paged_decode_stream<4> (one attention call)"
-                       if separate else "paged_decode_stream<4, append> "
+            "kernel": (f"paged_decode_stream<4, {args.dtype}> (one attention call)"
+                       if separate else f"paged_decode_stream<4, append, {args.dtype}> "
                        "(one write + attention launch)"),
             "bound": "hbm", "achieved": round(attn_gbps, 2), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,

@@ -479,6 +479,18 @@ int pia_prefill_hit_compact(const int32_t* slot_row, int32_t* dst, int32_t* src,
                             int64_t buffer_base, int64_t threshold, int num_experts,
                             void* stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * HBM streaming-read probe. No counterpart in the reference: a measurement aid for the
+ * rooflines of the kernels above (bench.py --workload hbm-read times it over fresh regions and
+ * fits fixed cost + rate). src: 16-byte aligned device memory of `bytes` bytes (a positive
+ * multiple of 16). tile_ids NULL: reads the whole buffer front to back. tile_ids non-NULL
+ * (device i32[n_tiles]): reads the 4 KiB tiles src + 4096 * tile_ids[i], skipping ids outside
+ * [0, bytes / 4096) - the paged-KV access pattern. Persistent grid, 16-byte loads, data
+ * discarded; *sink (device, 4-byte aligned) is written only for one 32-bit fold of the data.
+ * ------------------------------------------------------------------------------------------- */
+int pia_hbm_read_probe(const void* src, int64_t bytes, const int32_t* tile_ids, int64_t n_tiles,
+                       uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

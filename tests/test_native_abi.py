@@ -65,6 +65,9 @@ def test_invalid_arguments_are_rejected_without_device_work():
     assert N.query("pia_paged_decode_workspace_bytes", 4, 24, 8, 128, 16, 8) > 0
     with pytest.raises(N.NativeError):
         N.call("pia_moe_sum_reduce", None, None, 1, 0, 4, 2, None)
+    # the read probe checks its arguments before any launch
+    with pytest.raises(N.NativeError):
+        N.call("pia_hbm_read_probe", None, 4096, None, 0, None, None)
 
 
 @pytest.mark.parametrize("group", [1, 2, 3, 4, 5, 6, 7, 8, 16])
