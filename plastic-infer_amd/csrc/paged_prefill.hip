@@ -263,15 +263,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void paged_prefill_mfma(
   auto vread = [&](int buf, int i) {
     return *reinterpret_cast<const uint4*>(&vs[buf][(v_rd ^ (32 * (i >> 3))) + 1024 * (i & 7)]);
   };
-  // pages of a tile that hold keys: bit i for page i
+  // pages of a tile that hold keys: bit i for page i (lane i < 4 holds page i's id)
   auto page_mask = [&](int bt4) {
-    int mk = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int id = __builtin_amdgcn_readlane(bt4, i);
-      mk |= uint32_t(id) < np32 ? (1 << i) : 0;
-    }
-    return mk;
+    return int(__ballot(lane < 4 && uint32_t(bt4) < np32) & 0xFull);
   };
 
   // m[rb]: the row's running max in raw score units, the reference point of its exponentials.
@@ -334,13 +328,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void paged_prefill_mfma(
     for (int rb = 0; rb < RB; ++rb) {
       // on boundary tiles, keys the row may not see (tokens 64 kt + 16 mb + 4 g4 + j) -> -inf
       if (!full) {
+        // token 64 kt + 16 mb + 4 g4 + j is visible to the row when 16 mb + j < rel (one
+        // per-lane value and immediates: written with the token index per element, the
+        // compiler computed all sixteen indices ahead of the branch, on every tile)
+        const int rel = lim_r[rb] - (kt * PF_KT + 4 * g4);
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int t = kt * PF_KT + 16 * mb + 4 * g4 + j;
-            if (!(t < lim_r[rb] && ((pmask >> mb) & 1))) sc[rb][mb][j] = -INFINITY;
-          }
+          for (int j = 0; j < 4; ++j)
+            if (!(16 * mb + j < rel && ((pmask >> mb) & 1))) sc[rb][mb][j] = -INFINITY;
       }
       // the row max with IEEE 754-2019 maximum (a NaN score makes it NaN, and the row's output
       // NaN, as the reference's softmax gives): v_maximum3_f32, no quieting of the scores
