@@ -18,9 +18,13 @@
 // 2. paged_decode_mfma<G> (G = 3, 5..8, 16): the same split, cursor, partials and merge, with
 //    the tile work of a step on the matrix cores (QK^T and PV as 16x16x32 MFMAs, K through a
 //    swizzled LDS tile and transposing reads, V straight into the MFMA operand registers).
-// 3. paged_attention_generic<DT, DPL>: any dtype / head_dim <= 512 / page size, several query
-//    rows per sequence with optional causal offsets. One wave per (query row, head); keys are
-//    processed 64 at a time (lane = key for QK, lane = head-dim element for PV).
+// 3. paged_attention_tiled<DT, C, VEC, R>: everything else up to head_dim 512 and G * head_dim
+//    8192 (any dtype and page size, several query rows per sequence with optional causal
+//    offsets). One workgroup per (query row, kv head) serves its G q heads from K / V chunks of
+//    C keys staged once in LDS (described where it is defined).
+// 4. paged_attention_generic<DT, DPL>: what the tiled kernel's LDS or register budget does not
+//    take (G * head_dim above 8192). One wave per (query row, head); keys are processed 64 at a
+//    time (lane = key for QK, lane = head-dim element for PV).
 #include <algorithm>
 #include <atomic>
 #include <mutex>
@@ -1452,11 +1456,277 @@ __global__ __launch_bounds__(64) void paged_attention_generic(
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Tiled general kernel (paged_attention_tiled<DT, C, VEC, R>): what the fast kernels do not take
+// (any storage type, head_dim <= 512, any page size, any Hq / Hkv with G * head_dim <= 8192,
+// several rows per sequence with causal offsets). One 256-thread workgroup per (query row, kv
+// head) serves the kv head's G q heads, so each key and value is read once per row instead of
+// once per q head. Keys go in chunks of C tokens (32; 16 above head_dim 128): the chunk's K and
+// V rows are staged in LDS as fp32, [C][Dp] with Dp = D4 + 4 and D4 = head_dim rounded up to 4
+// (the pad columns stay zero; the 4-word row skew keeps a quarter-wave's 16-byte reads on
+// distinct banks), with one 16-byte load of VEC consecutive tokens of one d when the page size
+// is a multiple of VEC (else one element per load). S lanes (S = 1, 2 or 4, as many as leave no
+// thread idle) score key t for head g against q pre-scaled by scale * log2(e), each over every
+// S-th 4-word group of d, in fp32; a head's C * S lanes are consecutive lanes of one wave, so
+// its chunk max and sum are lane-xor reductions; online softmax in fp32, base 2 (a NaN score
+// makes its row's output NaN). Thread (g, d pair) accumulates O[g][d], O[g][d + 1] in
+// registers, up to R pairs per thread. Keys past a row's limit and on pages whose id is outside
+// the pool are not keys; their K / V words are zeros in LDS. Latency is hidden by several
+// workgroups per CU (small LDS and register footprint), not by prefetching the next chunk into
+// registers, which measured slower for the registers it holds.
+// ---------------------------------------------------------------------------------------------
+constexpr int PT_THREADS = 256;
+constexpr int PT_MAX_GD = 8192;            // G * head_dim limit: 16 pairs per thread
+constexpr size_t PT_MAX_LDS = 128 * 1024;  // dynamic LDS limit (of 160 KiB per CU)
+
+// Workgroup barrier after this wave's LDS accesses are done, with no memory fence: the kernel
+// shares nothing through global memory. The empty asm statements keep the compiler from moving
+// LDS accesses across it.
+__device__ __forceinline__ void pt_lds_sync() {
+  asm volatile("" ::: "memory");
+  // s_waitcnt fields: vmcnt [3:0] and [15:14] (63: no wait), expcnt [6:4] (7: no wait),
+  // lgkmcnt [11:8] (0)
+  __builtin_amdgcn_s_waitcnt(0xF | (7 << 4) | (3 << 14));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ float pt_xor_max(float v, int from, int to) {
+  for (int o = from; o >= to; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float pt_xor_sum(float v, int from, int to) {
+  for (int o = from; o >= to; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+template <int DT, int C, int VEC, int R>
+__global__ __launch_bounds__(PT_THREADS) void paged_attention_tiled(
+    void* __restrict__ out_, const void* __restrict__ q_, int64_t q_row_stride,
+    const void* __restrict__ kp_, const void* __restrict__ vp_,
+    const int32_t* __restrict__ bt, int64_t bt_stride, const int32_t* __restrict__ kv_lens,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ offsets, int num_seqs, int Hq,
+    int Hkv, int D, int P, int64_t num_pages, float scale_log2, int S) {
+  using E = Elem<DT>;
+  using T = typename E::T;
+  static_assert(64 % C == 0, "a head's lanes must lie in one wave");
+  T* out = reinterpret_cast<T*>(out_);
+  const T* q = reinterpret_cast<const T*>(q_);
+  const T* kp = reinterpret_cast<const T*>(kp_);
+  const T* vp = reinterpret_cast<const T*>(vp_);
+  extern __shared__ float4 pt_lds4[];
+  __shared__ int64_t tok_base[C];  // element offset of key t (its page tile + slot), -1: no key
+  const int G = Hq / Hkv, D4 = (D + 3) & ~3, Dp = D4 + 4, D2 = D4 / 2;
+  float* ks = reinterpret_cast<float*>(pt_lds4);  // [C][Dp]
+  float* vs = ks + C * Dp;                         // [C][Dp]
+  float* qs = vs + C * Dp;                         // [G][D4], pre-scaled, zero past D
+  float* ps = qs + G * D4;                         // [G][C]: the chunk's probabilities
+  float* hm = ps + G * C;                          // [G]: running max (log2 units)
+  float* hl = hm + G;                              // [G]: running sum
+  float* ha = hl + G;                              // [G]: the chunk's rescale factor
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int h = blockIdx.y;
+  int b = int(row), s = 0;
+  if (cu_q) {
+    int lo = 0, hi = num_seqs - 1;  // largest b with cu_q[b] <= row
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (int64_t(cu_q[mid]) <= row) lo = mid; else hi = mid - 1;
+    }
+    b = lo;
+    s = int(row - cu_q[b]);
+  }
+  const int kv_len = clamp_len(kv_lens[b], bt_stride, P);
+  int limit = kv_len;
+  if (offsets) limit = min(limit, offsets[b] + s + 1);
+  if (limit < 0) limit = 0;
+  const int64_t qoff = row * q_row_stride + int64_t(h) * G * D;
+  for (int i = tid; i < 2 * C * Dp; i += PT_THREADS) ks[i] = 0.f;  // pad columns stay zero
+  for (int i = tid; i < G * D4; i += PT_THREADS) {
+    const int g = i / D4, d = i - g * D4;
+    qs[i] = d < D ? E::load(q, qoff + int64_t(g) * D + d) * scale_log2 : 0.f;
+  }
+  for (int g = tid; g < G; g += PT_THREADS) {
+    hm[g] = -INFINITY;
+    hl[g] = 0.f;
+  }
+  float2 acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = make_float2(0.f, 0.f);
+  const int32_t* btb = bt + int64_t(b) * bt_stride;
+  const int64_t DP = int64_t(D) * P;
+  const int lanes = C * S;  // lanes of one head in the scoring phase
+  const int sl = tid % S, t_me = (tid / S) % C;
+
+  for (int c0 = 0; c0 < limit; c0 += C) {
+    if (tid < C) {
+      const int j = c0 + tid;
+      int64_t base = -1;
+      if (j < limit) {
+        const int lp = j / P, off = j - lp * P;
+        const int64_t phys = btb[lp];
+        if (phys >= 0 && phys < num_pages) base = (phys * Hkv + h) * DP + off;
+      }
+      tok_base[tid] = base;
+    }
+    pt_lds_sync();  // also: the previous chunk's products are done with ks / vs / ps
+    if constexpr (VEC > 1) {
+      // VEC consecutive keys of one d per 16-byte load: the group lies in one page (the page
+      // size is a multiple of VEC and so is c0); keys of it past the limit are zeroed
+      for (int i = tid; i < (C / VEC) * D; i += PT_THREADS) {
+        const int tg = i % (C / VEC), d = i / (C / VEC), t0 = tg * VEC;
+        const int64_t b0 = tok_base[t0];
+        uint4 kw = make_uint4(0u, 0u, 0u, 0u), vw = make_uint4(0u, 0u, 0u, 0u);
+        if (b0 >= 0) {
+          kw = *reinterpret_cast<const uint4*>(kp + b0 + int64_t(d) * P);
+          vw = *reinterpret_cast<const uint4*>(vp + b0 + int64_t(d) * P);
+        }
+        const T* ke = reinterpret_cast<const T*>(&kw);
+        const T* ve = reinterpret_cast<const T*>(&vw);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const bool ok = c0 + t0 + e < limit;
+          ks[(t0 + e) * Dp + d] = ok ? E::load(ke, e) : 0.f;
+          vs[(t0 + e) * Dp + d] = ok ? E::load(ve, e) : 0.f;
+        }
+      }
+    } else {
+      for (int i = tid; i < C * D; i += PT_THREADS) {
+        const int t = i % C, d = i / C;
+        const int64_t b0 = tok_base[t];
+        ks[t * Dp + d] = b0 >= 0 ? E::load(kp, b0 + int64_t(d) * P) : 0.f;
+        vs[t * Dp + d] = b0 >= 0 ? E::load(vp, b0 + int64_t(d) * P) : 0.f;
+      }
+    }
+    pt_lds_sync();
+    // scores of the chunk, its max and sum per head; the head's running max, sum and rescale
+    for (int g0 = 0; g0 < G; g0 += PT_THREADS / lanes) {
+      const int g = g0 + tid / lanes, t = t_me;
+      float x = -INFINITY;
+      if (g < G) {
+        const float4* qg = reinterpret_cast<const float4*>(qs + g * D4);
+        const float4* kt = reinterpret_cast<const float4*>(ks + t * Dp);
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll 4
+        for (int i = sl; i < D4 / 4; i += S) {
+          const float4 qv = qg[i], kv = kt[i];
+          a0 = fmaf(qv.x, kv.x, a0);
+          a1 = fmaf(qv.y, kv.y, a1);
+          a2 = fmaf(qv.z, kv.z, a2);
+          a3 = fmaf(qv.w, kv.w, a3);
+        }
+        x = pt_xor_sum((a0 + a1) + (a2 + a3), S / 2, 1);
+        if (tok_base[t] < 0) x = -INFINITY;
+      }
+      const float mx = pt_xor_max(x, lanes / 2, S);
+      const float mo = g < G ? hm[g] : -INFINITY;
+      const float mn = fmaxf(mo, mx);
+      const float pr = x == -INFINITY ? 0.f : fast_exp2(x - mn);
+      const float sum = pt_xor_sum(sl == 0 ? pr : 0.f, lanes / 2, 1);
+      if (g < G && sl == 0) {
+        ps[g * C + t] = pr;
+        if (t == 0) {  // every lane of the head has read hm[g] above
+          const float al = mo == -INFINITY ? 0.f : fast_exp2(mo - mn);
+          hm[g] = mn;
+          hl[g] = hl[g] * al + sum;
+          ha[g] = al;
+        }
+      }
+    }
+    pt_lds_sync();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int idx = tid + r * PT_THREADS;
+      if (idx < G * D2) {
+        const int g = idx / D2, d = 2 * (idx - g * D2);
+        const float al = ha[g];
+        float2 a = make_float2(acc[r].x * al, acc[r].y * al);
+        const float4* pg = reinterpret_cast<const float4*>(ps + g * C);
+#pragma unroll 2
+        for (int t4 = 0; t4 < C / 4; ++t4) {
+          const float4 pw = pg[t4];
+          const float* v0 = vs + (4 * t4) * Dp + d;
+          const float2 w0 = *reinterpret_cast<const float2*>(v0);
+          const float2 w1 = *reinterpret_cast<const float2*>(v0 + Dp);
+          const float2 w2 = *reinterpret_cast<const float2*>(v0 + 2 * Dp);
+          const float2 w3 = *reinterpret_cast<const float2*>(v0 + 3 * Dp);
+          a.x = fmaf(pw.x, w0.x, a.x);
+          a.y = fmaf(pw.x, w0.y, a.y);
+          a.x = fmaf(pw.y, w1.x, a.x);
+          a.y = fmaf(pw.y, w1.y, a.y);
+          a.x = fmaf(pw.z, w2.x, a.x);
+          a.y = fmaf(pw.z, w2.y, a.y);
+          a.x = fmaf(pw.w, w3.x, a.x);
+          a.y = fmaf(pw.w, w3.y, a.y);
+        }
+        acc[r] = a;
+      }
+    }
+  }
+  pt_lds_sync();  // hl final
+  const int64_t ooff = (row * Hq + int64_t(h) * G) * D;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int idx = tid + r * PT_THREADS;
+    if (idx < G * D2) {
+      const int g = idx / D2, d = 2 * (idx - g * D2);
+      const float l = hl[g];
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      if (d < D) E::store(out, ooff + int64_t(g) * D + d, acc[r].x * inv);
+      if (d + 1 < D) E::store(out, ooff + int64_t(g) * D + d + 1, acc[r].y * inv);
+    }
+  }
+}
+
+// Dynamic LDS of paged_attention_tiled: K and V chunks, q, probabilities, per-head running
+// max / sum / rescale.
+inline size_t tiled_lds_bytes(int C, int G, int D) {
+  const int D4 = (D + 3) & ~3;
+  return size_t(2 * C * (D4 + 4) + G * D4 + G * C + 3 * G) * sizeof(float);
+}
+
 template <int DT>
 int launch_generic(void* out, const void* q, int64_t q_row_stride, const void* kp, const void* vp,
                    const int32_t* bt, int64_t bt_stride, const int32_t* kv_lens,
                    const int32_t* cu_q, const int32_t* offsets, int num_seqs, int64_t rows, int Hq,
                    int Hkv, int D, int P, int64_t num_pages, float scale_log2, hipStream_t s) {
+  const int G = Hq / Hkv;
+  const int C = D <= 128 ? 32 : 16;  // 16 above 128: four workgroups' chunks fit one CU's LDS
+  const size_t lds = tiled_lds_bytes(C, G, D);
+  const int64_t pairs = int64_t(G) * (((D + 3) & ~3) / 2);  // (g, d pair) items
+  if (pairs <= PT_MAX_GD / 2 && D <= 512 && lds <= PT_MAX_LDS) {
+    using T = typename Elem<DT>::T;
+    constexpr int VEC = 16 / int(sizeof(T));
+    const bool vec = P % VEC == 0 && aligned(kp, 16) && aligned(vp, 16);
+    int S = 1;  // lanes per (head, key) score: as many as leave no thread idle, <= 64 / C
+    while (S < 4 && int64_t(G) * C * S * 2 <= PT_THREADS && C * S * 2 <= 64) S *= 2;
+    const bool small = pairs <= 4 * PT_THREADS;
+    const dim3 tgrid = dim3(unsigned(rows), unsigned(Hkv));
+#define PIA_TILED(CC, VV, RR)                                                                  \
+  {                                                                                            \
+    auto* kern = &paged_attention_tiled<DT, CC, VV, RR>;                                       \
+    if (lds > 65536)                                                                           \
+      if (int rc = check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),          \
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,   \
+                                                 int(lds)),                                    \
+                             "paged_attention_tiled: LDS size"))                               \
+        return rc;                                                                             \
+    hipLaunchKernelGGL(kern, tgrid, dim3(PT_THREADS), lds, s, out, q, q_row_stride, kp, vp,   \
+                       bt, bt_stride, kv_lens, cu_q, offsets, num_seqs, Hq, Hkv, D, P,         \
+                       num_pages, scale_log2, S);                                              \
+  }
+#define PIA_TILED_R(CC, VV) \
+  if (small) PIA_TILED(CC, VV, 4) else PIA_TILED(CC, VV, 16)
+    if (C == 32) {
+      if (vec) PIA_TILED_R(32, VEC) else PIA_TILED_R(32, 1)
+    } else {
+      if (vec) PIA_TILED_R(16, VEC) else PIA_TILED_R(16, 1)
+    }
+#undef PIA_TILED_R
+#undef PIA_TILED
+    return check_launch("paged_attention_tiled");
+  }
   dim3 grid = dim3(unsigned(rows), unsigned(Hq));
 #define PIA_GEN(DPL)                                                                        \
   hipLaunchKernelGGL((paged_attention_generic<DT, DPL>), grid, dim3(64), 0, s, out, q,      \

@@ -398,6 +398,12 @@ GEN_CASES = [  # (seed, n_pages, Hkv, G, D, P, table, kv_len, Sq, mode)
     (3, 5, 2, 4, 256, 16, [1], 1, 1, "none"),
     (4, 8, 4, 2, 96, 2, [7, 0, 6, 1, 5], 9, 2, "offset"),
     (5, 40, 2, 3, 128, 8, list(range(39, 0, -1)), 300, 5, "offset"),
+    # G * head_dim 2304: 16 accumulator pairs per thread, 16-key chunks
+    (6, 14, 1, 9, 256, 16, [13, 2, 7, 0, 11, 4, 9, 1, 12, 5], 150, 3, "offset"),
+    # head_dim 202 (zero pad columns to 204), 5-token pages: element loads
+    (7, 9, 2, 2, 202, 5, [8, 1, 6, 3, 0, 4, 7], 33, 2, "top_left"),
+    # G * head_dim 10240, above the tiled kernel's limit: one wave per (row, q head)
+    (8, 4, 1, 20, 512, 4, [3, 1, 2], 10, 1, "none"),
 ]
 
 
