@@ -16,7 +16,9 @@ with HIP events on the launch stream) and the CPU baseline (the oracle's restate
 reference torch path on this host's cores, on a bounded sample of the same inputs).
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--cpu-sample-seqs S] [--no-cpu-baseline]
-                  [--separate-write] [--dtype bf16|fp16]   # fp16: the same step on fp16 pools
+                  [--separate-write] [--dtype bf16|fp16|fp32]
+                  # fp16: the same step on fp16 pools (the same kernel); fp32: on fp32 pools,
+                  # which the general tiled kernel serves (write and attention as two calls)
   python bench.py --calibrate-copy     # 1 GiB read + 1 GiB write elementwise copy, three times:
                                        # the known-size reference for HBM byte counters
   python bench.py --workload decode-gqa8     # Qwen3-30B-A3B attention layer: 64 x 4096 tokens,
@@ -63,6 +65,7 @@ MAX_PAGES = LEN_HI // P
 WORKLOAD = "qwen3-8b paged decode: kv scatter + gqa paged attention, 1 layer"
 PMC_FILE = ROOT / "profiles" / "paged_decode_qwen3_8b_b256_pmc.json"
 PMC_FP16_FILE = ROOT / "profiles" / "paged_decode_qwen3_8b_b256_fp16_pmc.json"
+PMC_FP32_FILE = ROOT / "profiles" / "paged_attention_tiled_qwen3_8b_b256_fp32_pmc.json"
 GQA8_PMC_FILE = ROOT / "profiles" / "paged_decode_gqa8_qwen3_30b_b64_pmc.json"
 
 
@@ -96,15 +99,16 @@ def build_inputs(torch, dev, dtype=None):
                 slots_d=slots.to(dev))
 
 
-def algorithmic_bytes(lens, n_pages, seqs=None):
+def algorithmic_bytes(lens, n_pages, seqs=None, elem=2):
     """Bytes a step must move at minimum: K+V of every context token, q in, out, the block
-    table entries and lengths read, and the scatter (new rows read + written, slots)."""
+    table entries and lengths read, and the scatter (new rows read + written, slots); elem is
+    the storage type's size in bytes."""
     idx = range(len(lens)) if seqs is None else seqs
     tok = sum(int(lens[b]) for b in idx)
     pages = sum(int(n_pages[b]) for b in idx)
     nb = len(list(idx))
-    kv_row = 2 * HKV * D * 2                       # K + V bytes of one token, one layer
-    attn = tok * kv_row + nb * HQ * D * 2 * 2 + pages * 4 + nb * 4
+    kv_row = 2 * HKV * D * elem                    # K + V bytes of one token, one layer
+    attn = tok * kv_row + nb * HQ * D * elem * 2 + pages * 4 + nb * 4
     scatter = nb * kv_row * 2 + nb * 8
     return attn, scatter
 
@@ -172,7 +176,7 @@ def cpu_baseline(torch, inp, n_seqs, gpu_out):
         step()
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
-    attn, sc = algorithmic_bytes(inp["lens"], inp["n_pages"], seqs)
+    attn, sc = algorithmic_bytes(inp["lens"], inp["n_pages"], seqs, inp["kp"].element_size())
     model, phys = cpu_info()
     return {
         "value": round((attn + sc) / t / 1e9, 3), "unit": "GB/s", "cores": threads,
@@ -1536,8 +1540,9 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--separate-write", action="store_true",
                     help="decode: write the new rows with kv_scatter, then attend (two calls)")
-    ap.add_argument("--dtype", choices=("bf16", "fp16"), default="bf16",
-                    help="decode: storage dtype of the pools, q and the new rows")
+    ap.add_argument("--dtype", choices=("bf16", "fp16", "fp32"), default="bf16",
+                    help="decode: storage dtype of the pools, q and the new rows (fp32: the "
+                         "general tiled kernel, write and attention as two calls)")
     ap.add_argument("--workload", choices=("decode", "decode-gqa8", "prefill-write",
                                            "moe-permute", "expert-stream", "moe-experts",
                                            "moe-experts-prefill", "prefill-stream", "kv-sink",
@@ -1577,13 +1582,15 @@ def main() -> int:
         print(json.dumps(run(torch, dev, args)), flush=True)
         return 0
     print(f"bench: generating inputs (B={B}, pool={NUM_PAGES} pages)", file=sys.stderr, flush=True)
-    kv_dtype = {"bf16": torch.bfloat16, "fp16": torch.float16}[args.dtype]
+    kv_dtype = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[args.dtype]
     inp = build_inputs(torch, dev, kv_dtype)
     out = torch.empty(B, HQ, D, dtype=kv_dtype, device=dev)
     ws = torch.empty(decode_workspace_bytes(B, HQ, HKV, D, P, MAX_PAGES), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
 
-    separate = args.separate_write
+    # fp32 pools: the append entry point runs its write kernel and then the general kernel, so
+    # the step is timed as the two calls and the attention call alone carries the roofline
+    separate = args.separate_write or args.dtype == "fp32"
 
     def step(ev_a=None, ev_b=None):
         if separate:
@@ -1624,7 +1631,8 @@ def main() -> int:
     # the step is one launch unless the write is separate: then the attention call's events
     attn_ms = statistics.mean(a.elapsed_time(b) for a, b in ev) if separate else ms_step
 
-    attn_bytes, scatter_bytes = algorithmic_bytes(inp["lens"], inp["n_pages"])
+    attn_bytes, scatter_bytes = algorithmic_bytes(inp["lens"], inp["n_pages"],
+                                                  elem=inp["kp"].element_size())
     step_bytes = attn_bytes + scatter_bytes
     gbps = step_bytes / (ms_step / 1e3) / 1e9
     # the dominant launch: the attention call alone (separate write) or the one call that also
@@ -1632,8 +1640,10 @@ def main() -> int:
     launch_bytes = attn_bytes if separate else step_bytes
     attn_gbps = launch_bytes / (attn_ms / 1e3) / 1e9
     traffic = None
-    pmc_file = PMC_FILE if args.dtype == "bf16" else PMC_FP16_FILE
-    if pmc_file.exists() and not separate:
+    # the counter files hold the dominant launch: the one write + attention launch (bf16, fp16)
+    # or the attention call alone (fp32)
+    pmc_file = {"bf16": PMC_FILE, "fp16": PMC_FP16_FILE, "fp32": PMC_FP32_FILE}[args.dtype]
+    if pmc_file.exists() and (args.dtype == "fp32" or not separate):
         try:
             traffic = json.loads(pmc_file.read_text()).get("hbm_bytes_per_launch")
         except (OSError, ValueError):
@@ -1661,7 +1671,9 @@ def main() -> int:
         "step": "kv_scatter + paged_decode_attention" if separate
                 else "paged_decode_append_attention (write + attention, one call)",
         "roofline": {
-            "kernel": (f"paged_decode_stream<4, {args.dtype}> (one attention call)"
+            "kernel": ("paged_attention_tiled<fp32, 32-key chunks, 16-byte loads> "
+                       "(one attention call)" if args.dtype == "fp32" else
+                       f"paged_decode_stream<4, {args.dtype}> (one attention call)"
                        if separate else f"paged_decode_stream<4, append, {args.dtype}> "
                        "(one write + attention launch)"),
             "bound": "hbm", "achieved": round(attn_gbps, 2), "peak": HBM_PEAK_GBPS,
