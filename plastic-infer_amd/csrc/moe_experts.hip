@@ -565,6 +565,141 @@ __device__ __forceinline__ void tg_sync() {
 }
 
 // ---------------------------------------------------------------------------------------------
+// moe_gemm_stream: the column kernel's products for 16-bit storage without a fused activation
+// and K in {512, 768, 1024} (the MoE down projection at decode sizes), with the weight rows read
+// the way HBM delivers fastest. A load instruction whose 64 lanes all fall in one 4 KiB block
+// streams at ~7 TB/s on this GPU, while one that touches a 16-byte vector in each of 16 W rows
+// (the MFMA operand layout, rows K elements apart) stays near 5.6 TB/s, at the same bytes in
+// flight. So each wave here reads the 16 W rows of a column tile, which are one contiguous
+// 32 K-byte block, with 1 KiB-contiguous loads, stores them in its own LDS buffer (rows 16 bytes
+// apart in bank order) and reads the MFMA operands from there. One wave per workgroup, as many
+// as are resident at once; the (plan block, column tile) pairs, in order, are split evenly over
+// them, so a wave streams one contiguous run of an expert's weights and loads the plan rows'
+// A operands (whose loads have the 16-row shape) into registers once per plan block it enters.
+// The next tile's W is in flight while the current tile is multiplied; K is summed in order.
+// ---------------------------------------------------------------------------------------------
+typedef uint32_t cs_u32x4 __attribute__((ext_vector_type(4)));
+constexpr int CS_MAX_WAVES_PER_CU = 8;
+
+template <int DT, int NI>  // NI = K / 32: 1 KiB load instructions per W tile, MFMA chunks per tile
+__global__ __launch_bounds__(64) void moe_gemm_stream(
+    eg_elem<DT>* __restrict__ out, const eg_elem<DT>* __restrict__ a,
+    const eg_elem<DT>* __restrict__ w, const float* __restrict__ topk_w,
+    const int32_t* __restrict__ sorted, const int32_t* __restrict__ expert_ids,
+    const int32_t* __restrict__ npp, int64_t max_rows, int64_t numel, int block_m, int a_div,
+    int64_t lda, int num_experts, int n_rows, int64_t ldo, int n_tiles, int mulw) {
+  static_assert(DT != PIA_DTYPE_F32, "16-bit storage only");
+  using E = eg_elem<DT>;
+  constexpr int K = 32 * NI, KV = K / 8;  // K and the 16-byte vectors of one W row
+  constexpr int PITCH = KV + 1;           // LDS row pitch in vectors
+  extern __shared__ cs_u32x4 cs_w[];      // [16][PITCH]: the current tile's W rows
+  const int lane = threadIdx.x;
+  const int li = lane & 15, kg = lane >> 4;
+  const int64_t rows = min(max_rows, int64_t(npp[0]));
+  // the tiles of every plan block in order, (mb, t) = (g / n_tiles, g % n_tiles), split evenly
+  // over the persistent waves: wave b takes [g0, g1)
+  const int64_t n_g = ((rows + EG_ROWS - 1) / EG_ROWS) * n_tiles;
+  const int64_t g0 = n_g * blockIdx.x / gridDim.x, g1 = n_g * (blockIdx.x + 1) / gridDim.x;
+
+  // W tile t of expert e: rows t * 16 .. + 16, one contiguous block; lane l of load i takes
+  // vector i * 64 + l of it. Buffer loads with the expert's descriptor in scalar registers and
+  // the whole offset in the per-lane operand, which the range check covers: rows past n_rows
+  // lie past the descriptor's byte count and read as zeros (their columns are not stored), and
+  // a tile loaded only to keep every path's loads alike starts at TG_OOB (zeros, no access).
+  cs_u32x4 wr[NI];  // a native vector type: an array of it stays in registers
+  auto load_tile = [&](int e, int t, bool real) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<E*>(w + int64_t(e) * n_rows * K), 0, n_rows * K * 2, TG_RSRC_WORD3);
+    const uint32_t off = real ? uint32_t(t * EG_ROWS * K * 2 + lane * 16) : TG_OOB;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      wr[i] = __builtin_amdgcn_raw_buffer_load_b128(wres, int(off + uint32_t(i) * 1024u), 0,
+                                                    TG_POLICY_NT);
+  };
+  // LDS accesses of one wave complete in order; the fences keep the compiler from moving this
+  // wave's stores across its reads of the previous tile, or its later reads across the stores
+  auto stage_tile = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int v = i * 64 + lane, row = v / KV;
+      cs_w[v + row] = wr[i];  // row * PITCH + (v - row * KV)
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  };
+  // the first tile from g on whose plan block names an expert (padding blocks name none)
+  auto next_valid = [&](int64_t g, int64_t& mb, int& t, int& e) __attribute__((always_inline)) {
+    while (g < g1) {
+      mb = g / n_tiles;
+      t = int(g - mb * n_tiles);
+      e = __builtin_amdgcn_readfirstlane(expert_ids[(mb * EG_ROWS) / block_m]);
+      if (e >= 0 && e < num_experts) return g;
+      g = (mb + 1) * n_tiles;  // the next plan block
+    }
+    return g1;
+  };
+
+  int64_t mb;
+  int t, e;
+  int64_t g = next_valid(g0, mb, t, e);
+  if (g >= g1) return;
+  load_tile(e, t, true);
+  stage_tile();
+  int64_t a_mb = -1;  // plan block whose A operands are in av
+  uint4 av[NI];
+  int64_t rq[4];  // route of output row 4 kg + q (the MFMA output layout), numel if none
+  float wq[4];    // its top-k weight (1 without the multiply)
+  while (true) {
+    if (mb != a_mb) {  // route r of plan row li, its weight and A operands for every K chunk
+      a_mb = mb;
+      const int64_t p = mb * EG_ROWS + li;
+      const int r = p < rows ? sorted[p] : int(numel);
+      const bool a_ok = r >= 0 && r < numel;
+      const E* arow = a + int64_t(a_ok ? (a_div == 1 ? r : r / a_div) : 0) * lda;
+      const float wt = (mulw && a_ok) ? topk_w[r] : 1.0f;
+#pragma unroll
+      for (int c = 0; c < NI; ++c)
+        av[c] = *reinterpret_cast<const uint4*>(arow + c * 32 + kg * 8);
+      // the output rows' routes and weights now, while the wait for them is this branch's: a
+      // load pending at the branch's end would make the products wait for every load
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int rr = __shfl(r, kg * 4 + q, 64);
+        rq[q] = rr >= 0 && rr < numel ? rr : numel;
+        wq[q] = __shfl(wt, kg * 4 + q, 64);
+      }
+    }
+    int64_t mb_n;
+    int t_n, e_n;
+    const int64_t g_n = next_valid(g + 1, mb_n, t_n, e_n);
+    // in flight while this tile is multiplied. Issued on every path (after the range's last
+    // tile as out-of-range loads): with the loads on one path only, the compiler would have to
+    // wait for every outstanding load, these included, before the products.
+    const bool last = g_n >= g1;
+    load_tile(last ? e : e_n, last ? t : t_n, !last);
+    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NI; ++c) {
+      const cs_u32x4 x = cs_w[li * PITCH + c * 4 + kg];
+      acc = mfma_16x16x32<DT>(av[c], uint4{x.x, x.y, x.z, x.w}, acc);
+    }
+    // output layout: lane l holds column l % 16 for plan rows 4 (l / 16) + q
+    const int col = t * EG_ROWS + li;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (rq[q] < numel && col < n_rows) out[rq[q] * ldo + col] = to_dt<DT>(acc[q] * wq[q]);
+    if (g_n >= g1) break;
+    stage_tile();
+    g = g_n;
+    mb = mb_n;
+    t = t_n;
+    e = e_n;
+  }
+}
+
+inline size_t stream_lds_bytes(int k) { return size_t(EG_ROWS) * (k / 8 + 1) * 16; }
+
+// ---------------------------------------------------------------------------------------------
 // moe_gemm_wide: the many-routes-per-expert case (prefill), one work item per (expert, column
 // tile of 256 W rows) that holds all of the expert's plan rows up to TW_BM (an expert with more
 // gets further row tiles). Every W byte is then streamed from HBM by exactly one workgroup,
@@ -895,6 +1030,43 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
     return check_launch("moe_gemm_wide");
   }
   const bool cols = k_dim <= EG_COLS_MAX_K;
+  if (!f32 && !fused && (k_dim == 512 || k_dim == 768 || k_dim == 1024) &&
+      w_bytes < (int64_t(1) << 31)) {
+    const int n_tiles = int(ceil_div(n_rows, EG_ROWS));
+    const int64_t n_items = ceil_div(max_num_tokens_padded, EG_ROWS) * n_tiles;  // tiles
+    const size_t lds = stream_lds_bytes(k_dim);
+    // persistent waves: as many as are resident at once (registers and LDS decide), so no wave
+    // starts its items only after others have finished theirs
+#define PIA_CS(DT, NI)                                                                            \
+  {                                                                                               \
+    auto* kern = &moe_gemm_stream<DT, NI>;                                                        \
+    int per_cu = 0;                                                                               \
+    if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(                          \
+                               &per_cu, reinterpret_cast<const void*>(kern), 64, lds),            \
+                           "moe_gemm_stream: occupancy"))                                          \
+      return rc;                                                                                  \
+    per_cu = std::max(1, std::min(per_cu, CS_MAX_WAVES_PER_CU));                                  \
+    const unsigned grid = unsigned(std::min<int64_t>(n_items, int64_t(cus) * per_cu));           \
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64), lds, s,                                        \
+                       reinterpret_cast<eg_elem<DT>*>(out),                                       \
+                       reinterpret_cast<const eg_elem<DT>*>(a),                                   \
+                       reinterpret_cast<const eg_elem<DT>*>(w), topk_weights, sorted_token_ids,    \
+                       expert_ids, num_tokens_post_pad, max_num_tokens_padded, numel, block_m,     \
+                       a_div, lda, num_experts, n_rows, ldo, n_tiles, mulw);                      \
+  }
+#define PIA_CS_K(DT)                                                                              \
+  if (k_dim == 512) PIA_CS(DT, 16)                                                                \
+  else if (k_dim == 768) PIA_CS(DT, 24)                                                           \
+  else PIA_CS(DT, 32)
+    if (dtype == PIA_DTYPE_BF16) {
+      PIA_CS_K(PIA_DTYPE_BF16)
+    } else {
+      PIA_CS_K(PIA_DTYPE_F16)
+    }
+#undef PIA_CS_K
+#undef PIA_CS
+    return check_launch("moe_gemm_stream");
+  }
   const int n_tiles = int(ceil_div(out_cols, cols ? EG_ROWS : (fused ? 32 : 64)));
   const int64_t n_items = ceil_div(max_num_tokens_padded, EG_ROWS) * n_tiles;
   const int64_t ub = cols ? ceil_div(n_items, EG_WAVES) : n_items;

@@ -92,6 +92,11 @@ def test_act_and_mul(dev, activation, dtype, rows, d):
     (12, 512, 2048, 768, 128, 8, torch.bfloat16, "silu", False), # Qwen3-30B-A3B prefill chunk
     (13, 2400, 256, 128, 64, 8, torch.bfloat16, "silu", False),  # ~300 routes per expert
     (14, 2100, 136, 72, 3, 2, torch.float16, "gelu", True),      # ~1400 per expert: 5 row tiles
+    # second GEMM at K = I in {512, 768, 1024} below 2048 routes: the streaming kernel, here
+    # with 8-row column tails on the last expert (read past its rows: zeros, not stored)
+    (15, 40, 1000, 768, 9, 3, torch.bfloat16, "silu", True),
+    (16, 33, 2040, 1024, 5, 2, torch.float16, "gelu", False),
+    (17, 3, 520, 512, 40, 8, torch.bfloat16, "silu", False),     # 24 routes over 40 experts
     # fp32 storage (split-K kernel at every size; K a multiple of 4 suffices)
     (20, 64, 2048, 768, 128, 8, torch.float32, "silu", False),
     (21, 5, 100, 36, 7, 3, torch.float32, "gelu", True),         # K = 100 and 36: not / 8
