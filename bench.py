@@ -628,7 +628,9 @@ def bench_hbm_read(torch, dev, args) -> dict:
     (the 256 MB last-level cache holds none of it) or from fresh random tiles, timed by events
     around each launch: one untimed launch, then the mean of `steps` (at least 6). Per pattern
     t(X) = fixed + X / rate, fitted by least squares over X >= 200 MB. `value` is the tiles
-    rate: the ceiling the paged decode kernels are compared with."""
+    rate: the ceiling the paged decode kernels are compared with. `row_shapes`: 3 GiB read as
+    16-row blocks (the weight tiles of the expert GEMMs) with every load instruction covering
+    R rows x 1024 / R bytes, R = 16 (the MFMA operand layout) .. 1 (1 KiB contiguous)."""
     from plastic_infer import _native as N
 
     pool_bytes = 12 << 30
@@ -673,6 +675,28 @@ def bench_hbm_read(torch, dev, args) -> dict:
                         "rate_gbps": round(1.0 / slope / 1e9, 1),
                         "rate_frac_of_8tbps": round(1.0 / slope / 1e9 / HBM_PEAK_GBPS, 4),
                         "per_size": rows}
+    # the load shape of a GEMM weight tile (pia_hbm_read_rows_probe): 3 GiB of 16-row blocks,
+    # R rows x 1024 / R bytes per load instruction, regions rotated through the buffer as above
+    shapes, off, X = [], 0, 3 << 30
+    for row_bytes in (1536, 4096):
+        for r_per in (16, 8, 4, 2, 1):
+            times = []
+            for r in range(reps + 1):
+                if off + X > pool_bytes:
+                    off = 0
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                N.call("pia_hbm_read_rows_probe", pool.data_ptr() + off, X, row_bytes, r_per,
+                       sink.data_ptr(), N.stream_of(dev))
+                b.record(stream)
+                b.synchronize()
+                if r > 0:
+                    times.append(a.elapsed_time(b) / 1e3)
+                off += (X + (4 << 20)) & ~((2 << 20) - 1)
+            read = X // (16 * row_bytes) * 16 * row_bytes
+            t = statistics.mean(times)
+            shapes.append({"row_bytes": row_bytes, "rows_per_load": r_per,
+                           "mean_us": round(t * 1e6, 2), "gbps": round(read / t / 1e9, 1)})
     rate = out["tiles"]["rate_gbps"]
     return {"metric": "HBM streaming-read GB/s, random 4 KiB tiles (fit: fixed cost + bytes / "
                       "rate)",
@@ -682,7 +706,11 @@ def bench_hbm_read(torch, dev, args) -> dict:
                     "drawn without repeats per launch",
             "config": {"workload": "pia_hbm_read_probe: 16-byte loads, 4 x 256-thread "
                                    "workgroups per CU", "sizes_bytes": sizes},
-            "hbm_frac": round(rate / HBM_PEAK_GBPS, 4), "patterns": out}
+            "hbm_frac": round(rate / HBM_PEAK_GBPS, 4), "patterns": out,
+            "row_shapes": {"bytes": X, "per_shape": shapes,
+                           "what": "16-row blocks of row_bytes, rows_per_load rows x 1024 / "
+                                   "rows_per_load bytes per load instruction (16: the MFMA "
+                                   "operand layout; 1: 1 KiB of the block)"}}
 
 
 def bench_expert_stream(torch, dev, args) -> dict:

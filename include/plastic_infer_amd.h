@@ -491,6 +491,15 @@ int pia_prefill_hit_compact(const int32_t* slot_row, int32_t* dst, int32_t* src,
 int pia_hbm_read_probe(const void* src, int64_t bytes, const int32_t* tile_ids, int64_t n_tiles,
                        uint32_t* sink, void* stream);
 
+/* The same probe for the load shape of a GEMM weight tile (no counterpart in the reference):
+ * reads src as 16-row blocks of row_bytes each (contiguous), one wave per block, every load
+ * instruction covering rows_per_load rows x 1024 / rows_per_load bytes: 16 is the MFMA
+ * operand layout of the expert GEMMs (a 16-byte vector of each of 16 rows), 1 reads 1 KiB of
+ * the block contiguously. rows_per_load in {1, 2, 4, 8, 16}; row_bytes a positive multiple of
+ * 64 and of 1024 / rows_per_load; bytes >= 16 * row_bytes (whole blocks are read). */
+int pia_hbm_read_rows_probe(const void* src, int64_t bytes, int row_bytes, int rows_per_load,
+                            uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -8,6 +8,11 @@
 //   tiles: 4 KiB tiles at the given tile indices (the paged-KV access: a page of one kv head is
 //          a 4 KiB tile at bf16 / head_dim 128 / page 16), one wave per tile, two tiles in
 //          flight per wave (each lane 4 x 16 bytes of each).
+//   rows:  16-row blocks (16 x row_bytes, contiguous; a weight tile of the expert GEMMs), one
+//          wave per block, four loads in flight per lane, each load instruction shaped as R
+//          rows x 1024 / R bytes: R = 16 is the MFMA operand layout (lane l reads a 16-byte
+//          vector of row l % 16), R = 1 reads 1 KiB of the block contiguously. Same bytes and
+//          the same grid for every R, so the rates compare the load shape alone.
 #include <algorithm>
 
 #include "pia_internal.h"
@@ -71,6 +76,38 @@ __global__ __launch_bounds__(HP_THREADS) void hbm_read_tiles_kernel(
   if (acc == 0x9e3779b9u) sink[0] = acc;
 }
 
+// 16-row blocks, R rows per load instruction (64 / R lanes, 1024 / R contiguous bytes per row);
+// R = 1: 1 KiB of the block per instruction. row16 = row_bytes / 16, a multiple of 64 / R (and
+// of 4). The block's loads go group by group (R rows each; R = 1: one group, the whole block),
+// HP_UNROLL in flight per lane; the per-lane offset is fixed, so every shape costs the same
+// address arithmetic per load.
+template <int R>
+__global__ __launch_bounds__(HP_THREADS) void hbm_read_rows_kernel(const uint4* __restrict__ p,
+                                                                   int64_t n_blocks, int row16,
+                                                                   uint32_t* __restrict__ sink) {
+  constexpr int WAVES = HP_THREADS / 64, LPR = 64 / R, NG = R == 1 ? 1 : 16 / R;
+  const int lane = threadIdx.x & 63;
+  const int block16 = 16 * row16, per_group = row16 / 4 / NG;  // instructions per group
+  const int lane_off = R == 1 ? lane : (lane / LPR) * row16 + lane % LPR;
+  const int group16 = R == 1 ? 0 : R * row16;
+  uint32_t acc = 0;
+  for (int64_t b = int64_t(blockIdx.x) * WAVES + (threadIdx.x >> 6); b < n_blocks;
+       b += int64_t(gridDim.x) * WAVES) {
+    for (int g = 0; g < NG; ++g) {
+      const uint4* base = p + b * block16 + g * group16 + lane_off;
+      for (int c = 0; c < per_group; c += HP_UNROLL) {
+        uint4 v[HP_UNROLL];
+#pragma unroll
+        for (int u = 0; u < HP_UNROLL; ++u)
+          v[u] = hp_load(base + (c + u < per_group ? c + u : per_group - 1) * LPR);
+#pragma unroll
+        for (int u = 0; u < HP_UNROLL; ++u) acc ^= v[u].x ^ v[u].w;
+      }
+    }
+  }
+  if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
 }  // namespace
 }  // namespace pia
 
@@ -101,4 +138,34 @@ extern "C" int pia_hbm_read_probe(const void* src, int64_t bytes, const int32_t*
   hipLaunchKernelGGL(hbm_read_probe_kernel, dim3(grid), dim3(HP_THREADS), 0, as_stream(stream),
                      reinterpret_cast<const uint4*>(src), n16, sink);
   return check_launch("hbm_read_probe");
+}
+
+extern "C" int pia_hbm_read_rows_probe(const void* src, int64_t bytes, int row_bytes,
+                                       int rows_per_load, uint32_t* sink, void* stream) {
+  if (!src || !sink) return fail(PIA_EINVAL, "hbm_read_rows_probe: null pointer");
+  const int R = rows_per_load;
+  if (R != 1 && R != 2 && R != 4 && R != 8 && R != 16)
+    return fail(PIA_EINVAL, "hbm_read_rows_probe: rows_per_load must be 1, 2, 4, 8 or 16");
+  if (row_bytes <= 0 || row_bytes % 64 || (R > 1 && row_bytes % (1024 / R)))
+    return fail(PIA_EINVAL, "hbm_read_rows_probe: row_bytes must be a positive multiple of 64 "
+                            "and of 1024 / rows_per_load");
+  if (bytes < 16 * int64_t(row_bytes))
+    return fail(PIA_EINVAL, "hbm_read_rows_probe: bytes must hold one 16-row block");
+  if (!aligned(src, 16) || !aligned(sink, 4))
+    return fail(PIA_EINVAL, "hbm_read_rows_probe: src must be 16-byte aligned, sink 4-byte aligned");
+  const int64_t n_blocks = bytes / (16 * int64_t(row_bytes));
+  const int64_t waves_per_wg = HP_THREADS / 64;
+  const unsigned grid = unsigned(std::min<int64_t>(ceil_div(n_blocks, waves_per_wg),
+                                                   int64_t(device_cus()) * 2));
+  const uint4* p = reinterpret_cast<const uint4*>(src);
+  const int row16 = row_bytes / 16;
+  hipStream_t s = as_stream(stream);
+  switch (R) {
+    case 1: hipLaunchKernelGGL(hbm_read_rows_kernel<1>, dim3(grid), dim3(HP_THREADS), 0, s, p, n_blocks, row16, sink); break;
+    case 2: hipLaunchKernelGGL(hbm_read_rows_kernel<2>, dim3(grid), dim3(HP_THREADS), 0, s, p, n_blocks, row16, sink); break;
+    case 4: hipLaunchKernelGGL(hbm_read_rows_kernel<4>, dim3(grid), dim3(HP_THREADS), 0, s, p, n_blocks, row16, sink); break;
+    case 8: hipLaunchKernelGGL(hbm_read_rows_kernel<8>, dim3(grid), dim3(HP_THREADS), 0, s, p, n_blocks, row16, sink); break;
+    default: hipLaunchKernelGGL(hbm_read_rows_kernel<16>, dim3(grid), dim3(HP_THREADS), 0, s, p, n_blocks, row16, sink); break;
+  }
+  return check_launch("hbm_read_rows_probe");
 }

@@ -567,10 +567,12 @@ __device__ __forceinline__ void tg_sync() {
 // ---------------------------------------------------------------------------------------------
 // moe_gemm_stream: the column kernel's products for 16-bit storage without a fused activation
 // and K in {512, 768, 1024} (the MoE down projection at decode sizes), with the weight rows read
-// the way HBM delivers fastest. A load instruction whose 64 lanes all fall in one 4 KiB block
-// streams at ~7 TB/s on this GPU, while one that touches a 16-byte vector in each of 16 W rows
-// (the MFMA operand layout, rows K elements apart) stays near 5.6 TB/s, at the same bytes in
-// flight. So each wave here reads the 16 W rows of a column tile, which are one contiguous
+// in the shape HBM delivers fastest. Loaded straight into the MFMA operand layout, each load
+// instruction takes a 16-byte vector from each of 16 W rows: 64 bytes of a row, half of a
+// 128-byte line. A once-read stream in that shape runs at 5.7-6.0 TB/s on this GPU, while the
+// same bytes with 8, 4, 2 or 1 rows per instruction (128 bytes of a row or more) run at
+// 6.7-7.2 TB/s (pia_hbm_read_rows_probe, same grid and bytes in
+// flight). So each wave here reads the 16 W rows of a column tile, which are one contiguous
 // 32 K-byte block, with 1 KiB-contiguous loads, stores them in its own LDS buffer (rows 16 bytes
 // apart in bank order) and reads the MFMA operands from there. One wave per workgroup, as many
 // as are resident at once; the (plan block, column tile) pairs, in order, are split evenly over

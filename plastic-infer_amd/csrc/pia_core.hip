@@ -32,4 +32,4 @@ int device_cus() {
 
 extern "C" const char* pia_last_error(void) { return pia::g_last_error; }
 
-extern "C" int pia_abi_version(void) { return 9; }
+extern "C" int pia_abi_version(void) { return 10; }

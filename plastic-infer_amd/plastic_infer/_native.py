@@ -69,9 +69,10 @@ _SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "pia_slot_cache_invalidate": (_I, [_P, _L, _P, _P, _L, _L, _L, _P]),
     "pia_prefill_hit_compact": (_I, [_P, _P, _P, _P, _L, _L, _I, _P]),
     "pia_hbm_read_probe": (_I, [_P, _L, _P, _L, _P, _P]),
+    "pia_hbm_read_rows_probe": (_I, [_P, _L, _I, _I, _P, _P]),
 }
 
-EXPECTED_ABI = 9
+EXPECTED_ABI = 10
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -68,6 +68,12 @@ def test_invalid_arguments_are_rejected_without_device_work():
     # the read probe checks its arguments before any launch
     with pytest.raises(N.NativeError):
         N.call("pia_hbm_read_probe", None, 4096, None, 0, None, None)
+    # the rows probe too: a shape it does not take, a row it cannot split, no whole block
+    fake = 1 << 20  # never dereferenced: every call below fails its checks first
+    for row_bytes, r, nbytes in ((1536, 3, 1 << 20), (1088, 2, 1 << 20), (96, 16, 1 << 20),
+                                 (4096, 16, 4096)):
+        with pytest.raises(N.NativeError):
+            N.call("pia_hbm_read_rows_probe", fake, nbytes, row_bytes, r, fake, None)
 
 
 @pytest.mark.parametrize("group", [1, 2, 3, 4, 5, 6, 7, 8, 16])
