@@ -1214,7 +1214,7 @@ def bench_moe_experts(torch, dev, args, tokens: int) -> dict:
     step_bytes = g1_bytes + g2_bytes + sum_bytes
     step_flops = g1_flops + g2_flops
     # the dominant kernel's bound: the larger of its HBM time and its MFMA time at peak
-    dom_name = "moe_gemm_splitk" if numel < 2048 else "moe_gemm_wide"
+    dom_name = "moe_gemm_stream_fused" if numel < 2048 else "moe_gemm_wide"
     dom_name += "<bf16, silu> (first expert GEMM)"
     t_hbm = g1_bytes / (HBM_PEAK_GBPS * 1e9)
     t_mfma = g1_flops / (MFMA_BF16_PEAK_TFLOPS * 1e12)

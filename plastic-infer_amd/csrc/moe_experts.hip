@@ -702,6 +702,160 @@ __global__ __launch_bounds__(64) void moe_gemm_stream(
 inline size_t stream_lds_bytes(int k) { return size_t(EG_ROWS) * (k / 8 + 1) * 16; }
 
 // ---------------------------------------------------------------------------------------------
+// moe_gemm_stream_fused: the first expert GEMM with its fused activation (gate rows and the
+// matching up rows) for 16-bit storage at K in {2048, 4096}, with the weight rows read in whole
+// lines as in moe_gemm_stream. A work item is (16 plan rows, 16 output columns): 16 gate rows
+// and 16 up rows. The four waves of a workgroup split K in quarters, as in moe_gemm_splitk;
+// a wave holds its quarter of the plan rows' A operands in registers (loaded once per plan
+// block) and streams its quarter of the item's 32 W rows in sub-stages of 256 K (512 bytes of
+// each row): 16 loads of 2 rows x 512 bytes, written into the wave's own LDS buffer (row pitch
+// 33 vectors) and read from there as MFMA operands; the next sub-stage (the next item's first
+// at an item's end) is in flight during the products. The four partial tiles are summed in
+// wave order through LDS and the activation applied as in moe_gemm_splitk: each output sums
+// its K in the same order as there, so the two kernels give the same bits. Workgroups are as
+// many as are resident and take equal runs of the (plan block, column tile) pairs.
+// ---------------------------------------------------------------------------------------------
+constexpr int SF_SUB = 256;                  // K per sub-stage
+constexpr int SF_PITCH = SF_SUB / 8 + 1;     // LDS row pitch in 16-byte vectors
+constexpr int SF_ROWS = 2 * EG_ROWS;         // W rows per item: gate, then up
+constexpr int SF_LOADS = SF_ROWS * SF_SUB * 2 / 1024;  // 1 KiB loads per sub-stage (16)
+
+template <int DT, int ACT, int KQ>  // KQ = K / 4: the K of one wave
+__global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_stream_fused(
+    eg_elem<DT>* __restrict__ out, const eg_elem<DT>* __restrict__ a,
+    const eg_elem<DT>* __restrict__ w, const float* __restrict__ topk_w,
+    const int32_t* __restrict__ sorted, const int32_t* __restrict__ expert_ids,
+    const int32_t* __restrict__ npp, int64_t max_rows, int64_t numel, int block_m, int a_div,
+    int64_t lda, int num_experts, int n_rows, int64_t ldo, int n_tiles, int mulw) {
+  static_assert(DT != PIA_DTYPE_F32 && ACT != PIA_ACT_NONE, "16-bit storage, fused activation");
+  using E = eg_elem<DT>;
+  constexpr int K = 4 * KQ, NS = KQ / SF_SUB, AC = KQ / 32;  // sub-stages, A chunks per wave
+  __shared__ cs_u32x4 sf_w[EG_WAVES][SF_ROWS * SF_PITCH];    // each wave's sub-stage
+  __shared__ float red[EG_WAVES][2][4][64];                  // [wave][gate / up][q][lane]
+  __shared__ int32_t blk_route[EG_ROWS];
+  __shared__ float blk_w[EG_ROWS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, kg = lane >> 4;
+  const int half = n_rows >> 1;
+  const int64_t rows = min(max_rows, int64_t(npp[0]));
+  const int64_t n_g = ((rows + EG_ROWS - 1) / EG_ROWS) * n_tiles;
+  const int64_t g0 = n_g * blockIdx.x / gridDim.x, g1 = n_g * (blockIdx.x + 1) / gridDim.x;
+  cs_u32x4* buf = sf_w[wv];
+
+  // Sub-stage j of item (e, t) for this wave: K [wv KQ + 256 j, + 256) of the item's W rows
+  // (row r < 16: gate row 16 t + r, else up row half + 16 t + r - 16). Load i takes rows 2 i
+  // and 2 i + 1, lane l row 2 i + l / 32 at vector l % 32. Rows past the gate half are not
+  // loaded (offset past the descriptor: zeros); real == false loads nothing at all.
+  cs_u32x4 wr[SF_LOADS];
+  auto load_sub = [&](int e, int t, int j, bool real) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<E*>(w + int64_t(e) * n_rows * K), 0, n_rows * K * 2, TG_RSRC_WORD3);
+    const uint32_t kb = uint32_t(wv * KQ + j * SF_SUB) * 2u + uint32_t(lane & 31) * 16u;
+#pragma unroll
+    for (int i = 0; i < SF_LOADS; ++i) {
+      const int r = 2 * i + (lane >> 5);
+      const int col = t * EG_ROWS + (r & 15);
+      const int n = (r < EG_ROWS ? 0 : half) + col;
+      const uint32_t off = real && col < half ? uint32_t(n) * uint32_t(K) * 2u + kb : TG_OOB;
+      wr[i] = __builtin_amdgcn_raw_buffer_load_b128(wres, int(off), 0, TG_POLICY_NT);
+    }
+  };
+  // into this wave's LDS buffer, after its reads of the previous sub-stage (LDS is in order)
+  auto stage_sub = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+    for (int i = 0; i < SF_LOADS; ++i) buf[(2 * i + (lane >> 5)) * SF_PITCH + (lane & 31)] = wr[i];
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  };
+  auto next_valid = [&](int64_t g, int64_t& mb, int& t, int& e) __attribute__((always_inline)) {
+    while (g < g1) {
+      mb = g / n_tiles;
+      t = int(g - mb * n_tiles);
+      e = __builtin_amdgcn_readfirstlane(expert_ids[(mb * EG_ROWS) / block_m]);
+      if (e >= 0 && e < num_experts) return g;
+      g = (mb + 1) * n_tiles;
+    }
+    return g1;
+  };
+
+  int64_t mb;
+  int t, e;
+  int64_t g = next_valid(g0, mb, t, e);
+  if (g >= g1) return;
+  load_sub(e, t, 0, true);
+  stage_sub();
+  int64_t a_mb = -1;
+  uint4 av[AC];
+  while (true) {
+    const bool new_block = mb != a_mb;
+    if (new_block) {  // this wave's K quarter of the plan rows' A operands
+      a_mb = mb;
+      const int64_t p = mb * EG_ROWS + li;
+      const int r = p < rows ? sorted[p] : int(numel);
+      const bool a_ok = r >= 0 && r < numel;
+      const E* arow = a + int64_t(a_ok ? (a_div == 1 ? r : r / a_div) : 0) * lda + wv * KQ;
+#pragma unroll
+      for (int c = 0; c < AC; ++c)
+        av[c] = *reinterpret_cast<const uint4*>(arow + c * 32 + kg * 8);
+    }
+    int64_t mb_n;
+    int t_n, e_n;
+    const int64_t g_n = next_valid(g + 1, mb_n, t_n, e_n);
+    f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      // the next sub-stage's loads on every path (after the run's last item: none in memory)
+      if (j + 1 < NS) load_sub(e, t, j + 1, true);
+      else load_sub(g_n < g1 ? e_n : e, g_n < g1 ? t_n : t, 0, g_n < g1);
+#pragma unroll
+      for (int c = 0; c < SF_SUB / 32; ++c)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const cs_u32x4 x = buf[(b * EG_ROWS + li) * SF_PITCH + c * 4 + kg];
+          acc[b] = mfma_16x16x32<DT>(av[j * (SF_SUB / 32) + c], uint4{x.x, x.y, x.z, x.w}, acc[b]);
+        }
+      stage_sub();
+    }
+
+    __syncthreads();  // the previous item's epilogue is done with red / blk_*
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[wv][b][q][lane] = acc[b][q];
+    if (new_block && wv == 0 && lane < EG_ROWS) {  // lane l < 16: plan row l
+      const int64_t p = mb * EG_ROWS + lane;
+      const int r = p < rows ? sorted[p] : int(numel);
+      const bool ok = r >= 0 && r < numel;
+      blk_route[lane] = ok ? r : -1;
+      blk_w[lane] = (mulw && ok) ? topk_w[r] : 1.0f;
+    }
+    __syncthreads();
+    {  // wave wv: output rows 4 kg + wv of the tile, column t 16 + li
+      const int q = wv, row = kg * 4 + q, col = t * EG_ROWS + li;
+      float gs = red[0][0][q][lane], us = red[0][1][q][lane];
+#pragma unroll
+      for (int x = 1; x < EG_WAVES; ++x) {
+        gs += red[x][0][q][lane];
+        us += red[x][1][q][lane];
+      }
+      const int32_t rr = blk_route[row];
+      if (rr >= 0 && col < half) {
+        const float wr_ = blk_w[row];
+        const float gr = from_dt<DT>(to_dt<DT>(gs * wr_));
+        const float ur = from_dt<DT>(to_dt<DT>(us * wr_));
+        out[int64_t(rr) * ldo + col] = to_dt<DT>(act_fn<ACT>(gr) * ur);
+      }
+    }
+    if (g_n >= g1) break;
+    g = g_n;
+    mb = mb_n;
+    t = t_n;
+    e = e_n;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // moe_gemm_wide: the many-routes-per-expert case (prefill), one work item per (expert, column
 // tile of 256 W rows) that holds all of the expert's plan rows up to TW_BM (an expert with more
 // gets further row tiles). Every W byte is then streamed from HBM by exactly one workgroup,
@@ -1032,6 +1186,44 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
     return check_launch("moe_gemm_wide");
   }
   const bool cols = k_dim <= EG_COLS_MAX_K;
+  if (!f32 && fused && (k_dim == 2048 || k_dim == 4096) && w_bytes < (int64_t(1) << 31)) {
+    const int n_tiles = int(ceil_div(out_cols, EG_ROWS));
+    const int64_t n_items = ceil_div(max_num_tokens_padded, EG_ROWS) * n_tiles;
+#define PIA_SF(DT, ACT, KQ)                                                                       \
+  {                                                                                               \
+    auto* kern = &moe_gemm_stream_fused<DT, ACT, KQ>;                                             \
+    int per_cu = 0;                                                                               \
+    if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(                          \
+                               &per_cu, reinterpret_cast<const void*>(kern), EG_WAVES * 64, 0),   \
+                           "moe_gemm_stream_fused: occupancy"))                                    \
+      return rc;                                                                                  \
+    per_cu = std::max(1, per_cu);                                                                 \
+    const unsigned grid = unsigned(std::min<int64_t>(n_items, int64_t(cus) * per_cu));           \
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(EG_WAVES * 64), 0, s,                               \
+                       reinterpret_cast<eg_elem<DT>*>(out),                                       \
+                       reinterpret_cast<const eg_elem<DT>*>(a),                                   \
+                       reinterpret_cast<const eg_elem<DT>*>(w), topk_weights, sorted_token_ids,    \
+                       expert_ids, num_tokens_post_pad, max_num_tokens_padded, numel, block_m,     \
+                       a_div, lda, num_experts, n_rows, ldo, n_tiles, mulw);                      \
+  }
+#define PIA_SF_K(DT, ACT)                                                                         \
+  if (k_dim == 2048) PIA_SF(DT, ACT, 512) else PIA_SF(DT, ACT, 1024)
+#define PIA_SF_ACT(DT)                                                                            \
+  switch (activation) {                                                                           \
+    case PIA_ACT_SILU: PIA_SF_K(DT, PIA_ACT_SILU); break;                                         \
+    case PIA_ACT_GELU: PIA_SF_K(DT, PIA_ACT_GELU); break;                                         \
+    default: PIA_SF_K(DT, PIA_ACT_GELU_TANH); break;                                              \
+  }
+    if (dtype == PIA_DTYPE_BF16) {
+      PIA_SF_ACT(PIA_DTYPE_BF16)
+    } else {
+      PIA_SF_ACT(PIA_DTYPE_F16)
+    }
+#undef PIA_SF_ACT
+#undef PIA_SF_K
+#undef PIA_SF
+    return check_launch("moe_gemm_stream_fused");
+  }
   if (!f32 && !fused && (k_dim == 512 || k_dim == 768 || k_dim == 1024) &&
       w_bytes < (int64_t(1) << 31)) {
     const int n_tiles = int(ceil_div(n_rows, EG_ROWS));
