@@ -1224,8 +1224,10 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
 #undef PIA_SF
     return check_launch("moe_gemm_stream_fused");
   }
+  // (32-bit buffer offsets: the last tile of an expert starts below n_rows but reaches up to 15
+  // rows past it, and offsets from TG_OOB up read zeros)
   if (!f32 && !fused && (k_dim == 512 || k_dim == 768 || k_dim == 1024) &&
-      w_bytes < (int64_t(1) << 31)) {
+      w_bytes + 16 * int64_t(k_dim) * 2 < (int64_t(1) << 31)) {
     const int n_tiles = int(ceil_div(n_rows, EG_ROWS));
     const int64_t n_items = ceil_div(max_num_tokens_padded, EG_ROWS) * n_tiles;  // tiles
     const size_t lds = stream_lds_bytes(k_dim);
