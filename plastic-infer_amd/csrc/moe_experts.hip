@@ -702,10 +702,11 @@ __global__ __launch_bounds__(64) void moe_gemm_stream(
 inline size_t stream_lds_bytes(int k) { return size_t(EG_ROWS) * (k / 8 + 1) * 16; }
 
 // ---------------------------------------------------------------------------------------------
-// moe_gemm_stream_fused: the first expert GEMM with its fused activation (gate rows and the
-// matching up rows) for 16-bit storage at K in {2048, 4096}, with the weight rows read in whole
-// lines as in moe_gemm_stream. A work item is (16 plan rows, 16 output columns): 16 gate rows
-// and 16 up rows. The four waves of a workgroup split K in quarters, as in moe_gemm_splitk;
+// moe_gemm_stream_fused: the expert GEMMs of 16-bit storage at K in {1024, 2048, 3072, 4096}
+// with an activation (gate rows and the matching up rows), and at K in {2048, 3072, 4096}
+// without one, with the weight rows read in whole lines as in moe_gemm_stream. A work item is
+// (16 plan rows, 32 W rows): 16 output columns from 16 gate rows and 16 up rows, or 32 output
+// columns without an activation. The four waves of a workgroup split K in quarters, as in moe_gemm_splitk;
 // a wave holds its quarter of the plan rows' A operands in registers (loaded once per plan
 // block) and streams its quarter of the item's 32 W rows in sub-stages of 256 K (512 bytes of
 // each row): 16 loads of 2 rows x 512 bytes, written into the wave's own LDS buffer (row pitch
@@ -727,7 +728,8 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_stream_fused(
     const int32_t* __restrict__ sorted, const int32_t* __restrict__ expert_ids,
     const int32_t* __restrict__ npp, int64_t max_rows, int64_t numel, int block_m, int a_div,
     int64_t lda, int num_experts, int n_rows, int64_t ldo, int n_tiles, int mulw) {
-  static_assert(DT != PIA_DTYPE_F32 && ACT != PIA_ACT_NONE, "16-bit storage, fused activation");
+  static_assert(DT != PIA_DTYPE_F32, "16-bit storage");
+  constexpr bool FUSED = ACT != PIA_ACT_NONE;
   using E = eg_elem<DT>;
   constexpr int K = 4 * KQ, NS = KQ / SF_SUB, AC = KQ / 32;  // sub-stages, A chunks per wave
   __shared__ cs_u32x4 sf_w[EG_WAVES][SF_ROWS * SF_PITCH];    // each wave's sub-stage
@@ -744,9 +746,10 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_stream_fused(
   cs_u32x4* buf = sf_w[wv];
 
   // Sub-stage j of item (e, t) for this wave: K [wv KQ + 256 j, + 256) of the item's W rows
-  // (row r < 16: gate row 16 t + r, else up row half + 16 t + r - 16). Load i takes rows 2 i
-  // and 2 i + 1, lane l row 2 i + l / 32 at vector l % 32. Rows past the gate half are not
-  // loaded (offset past the descriptor: zeros); real == false loads nothing at all.
+  // (with an activation row r < 16 is gate row 16 t + r, else up row half + 16 t + r - 16;
+  // without, row 32 t + r). Load i takes rows 2 i and 2 i + 1, lane l row 2 i + l / 32 at
+  // vector l % 32. Rows past the last column are not loaded (offset past the descriptor:
+  // zeros); real == false loads nothing at all.
   cs_u32x4 wr[SF_LOADS];
   auto load_sub = [&](int e, int t, int j, bool real) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
@@ -755,9 +758,17 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_stream_fused(
 #pragma unroll
     for (int i = 0; i < SF_LOADS; ++i) {
       const int r = 2 * i + (lane >> 5);
-      const int col = t * EG_ROWS + (r & 15);
-      const int n = (r < EG_ROWS ? 0 : half) + col;
-      const uint32_t off = real && col < half ? uint32_t(n) * uint32_t(K) * 2u + kb : TG_OOB;
+      int n;
+      bool ok;
+      if constexpr (FUSED) {
+        const int col = t * EG_ROWS + (r & 15);
+        n = (r < EG_ROWS ? 0 : half) + col;
+        ok = col < half;
+      } else {
+        n = t * SF_ROWS + r;
+        ok = n < n_rows;
+      }
+      const uint32_t off = real && ok ? uint32_t(n) * uint32_t(K) * 2u + kb : TG_OOB;
       wr[i] = __builtin_amdgcn_raw_buffer_load_b128(wres, int(off), 0, TG_POLICY_NT);
     }
   };
@@ -831,8 +842,8 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_stream_fused(
       blk_w[lane] = (mulw && ok) ? topk_w[r] : 1.0f;
     }
     __syncthreads();
-    {  // wave wv: output rows 4 kg + wv of the tile, column t 16 + li
-      const int q = wv, row = kg * 4 + q, col = t * EG_ROWS + li;
+    {  // wave wv: output rows 4 kg + wv of the tile
+      const int q = wv, row = kg * 4 + q;
       float gs = red[0][0][q][lane], us = red[0][1][q][lane];
 #pragma unroll
       for (int x = 1; x < EG_WAVES; ++x) {
@@ -840,11 +851,19 @@ __global__ __launch_bounds__(EG_WAVES * 64) void moe_gemm_stream_fused(
         us += red[x][1][q][lane];
       }
       const int32_t rr = blk_route[row];
-      if (rr >= 0 && col < half) {
-        const float wr_ = blk_w[row];
-        const float gr = from_dt<DT>(to_dt<DT>(gs * wr_));
-        const float ur = from_dt<DT>(to_dt<DT>(us * wr_));
-        out[int64_t(rr) * ldo + col] = to_dt<DT>(act_fn<ACT>(gr) * ur);
+      const float wr_ = blk_w[row];
+      if constexpr (FUSED) {  // column 16 t + li: gate block 0, up block 1
+        const int col = t * EG_ROWS + li;
+        if (rr >= 0 && col < half) {
+          const float gr = from_dt<DT>(to_dt<DT>(gs * wr_));
+          const float ur = from_dt<DT>(to_dt<DT>(us * wr_));
+          out[int64_t(rr) * ldo + col] = to_dt<DT>(act_fn<ACT>(gr) * ur);
+        }
+      } else {  // columns 32 t + li (block 0) and 32 t + 16 + li (block 1)
+        const int col = t * SF_ROWS + li;
+        if (rr >= 0 && col < n_rows) out[int64_t(rr) * ldo + col] = to_dt<DT>(gs * wr_);
+        if (rr >= 0 && col + EG_ROWS < n_rows)
+          out[int64_t(rr) * ldo + col + EG_ROWS] = to_dt<DT>(us * wr_);
       }
     }
     if (g_n >= g1) break;
@@ -1186,8 +1205,9 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
     return check_launch("moe_gemm_wide");
   }
   const bool cols = k_dim <= EG_COLS_MAX_K;
-  if (!f32 && fused && (k_dim == 2048 || k_dim == 4096) && w_bytes < (int64_t(1) << 31)) {
-    const int n_tiles = int(ceil_div(out_cols, EG_ROWS));
+  if (!f32 && k_dim % 1024 == 0 && k_dim <= 4096 && (fused || k_dim > EG_COLS_MAX_K) &&
+      w_bytes < (int64_t(1) << 31)) {
+    const int n_tiles = int(ceil_div(out_cols, fused ? EG_ROWS : SF_ROWS));
     const int64_t n_items = ceil_div(max_num_tokens_padded, EG_ROWS) * n_tiles;
 #define PIA_SF(DT, ACT, KQ)                                                                       \
   {                                                                                               \
@@ -1207,9 +1227,13 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
                        a_div, lda, num_experts, n_rows, ldo, n_tiles, mulw);                      \
   }
 #define PIA_SF_K(DT, ACT)                                                                         \
-  if (k_dim == 2048) PIA_SF(DT, ACT, 512) else PIA_SF(DT, ACT, 1024)
+  if (k_dim == 1024) PIA_SF(DT, ACT, 256)                                                         \
+  else if (k_dim == 2048) PIA_SF(DT, ACT, 512)                                                    \
+  else if (k_dim == 3072) PIA_SF(DT, ACT, 768)                                                    \
+  else PIA_SF(DT, ACT, 1024)
 #define PIA_SF_ACT(DT)                                                                            \
   switch (activation) {                                                                           \
+    case PIA_ACT_NONE: PIA_SF_K(DT, PIA_ACT_NONE); break;                                         \
     case PIA_ACT_SILU: PIA_SF_K(DT, PIA_ACT_SILU); break;                                         \
     case PIA_ACT_GELU: PIA_SF_K(DT, PIA_ACT_GELU); break;                                         \
     default: PIA_SF_K(DT, PIA_ACT_GELU_TANH); break;                                              \

@@ -97,6 +97,11 @@ def test_act_and_mul(dev, activation, dtype, rows, d):
     (15, 40, 1000, 768, 9, 3, torch.bfloat16, "silu", True),
     (16, 33, 2040, 1024, 5, 2, torch.float16, "gelu", False),
     (17, 3, 520, 512, 40, 8, torch.bfloat16, "silu", False),     # 24 routes over 40 experts
+    # K a multiple of 1024 up to 4096 streams through LDS in K quarters: second GEMMs at
+    # K = 2048 and 3072 (no activation, column tails), a first GEMM at K = 3072
+    (18, 20, 520, 2048, 6, 2, torch.bfloat16, "silu", False),
+    (19, 9, 1000, 3072, 5, 3, torch.float16, "gelu", True),
+    (23, 7, 3072, 64, 4, 2, torch.bfloat16, "gelu_tanh", False),
     # fp32 storage (split-K kernel at every size; K a multiple of 4 suffices)
     (20, 64, 2048, 768, 128, 8, torch.float32, "silu", False),
     (21, 5, 100, 36, 7, 3, torch.float32, "gelu", True),         # K = 100 and 36: not / 8
