@@ -38,6 +38,7 @@
 // products as above. The waves of a workgroup are independent: no LDS, no barrier; the sibling
 // waves of a plan block re-read its A rows from L2. Items are pipelined the same way, and each
 // item starts its K walk at its own stage (stage_rot below).
+#include <atomic>
 #include <type_traits>
 
 #include "pia_internal.h"
@@ -1212,12 +1213,16 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
 #define PIA_SF(DT, ACT, KQ)                                                                       \
   {                                                                                               \
     auto* kern = &moe_gemm_stream_fused<DT, ACT, KQ>;                                             \
-    int per_cu = 0;                                                                               \
-    if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(                          \
-                               &per_cu, reinterpret_cast<const void*>(kern), EG_WAVES * 64, 0),   \
-                           "moe_gemm_stream_fused: occupancy"))                                    \
-      return rc;                                                                                  \
-    per_cu = std::max(1, per_cu);                                                                 \
+    static std::atomic<int> cached{0}; /* resident workgroups per CU, queried once */             \
+    int per_cu = cached.load(std::memory_order_relaxed);                                          \
+    if (per_cu == 0) {                                                                            \
+      if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(                        \
+                                 &per_cu, reinterpret_cast<const void*>(kern), EG_WAVES * 64, 0), \
+                             "moe_gemm_stream_fused: occupancy"))                                  \
+        return rc;                                                                                \
+      per_cu = std::max(1, per_cu);                                                               \
+      cached.store(per_cu, std::memory_order_relaxed);                                            \
+    }                                                                                             \
     const unsigned grid = unsigned(std::min<int64_t>(n_items, int64_t(cus) * per_cu));           \
     hipLaunchKernelGGL(kern, dim3(grid), dim3(EG_WAVES * 64), 0, s,                               \
                        reinterpret_cast<eg_elem<DT>*>(out),                                       \
@@ -1260,12 +1265,16 @@ extern "C" int pia_moe_expert_gemm(void* out, const void* a, const void* w,
 #define PIA_CS(DT, NI)                                                                            \
   {                                                                                               \
     auto* kern = &moe_gemm_stream<DT, NI>;                                                        \
-    int per_cu = 0;                                                                               \
-    if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(                          \
-                               &per_cu, reinterpret_cast<const void*>(kern), 64, lds),            \
-                           "moe_gemm_stream: occupancy"))                                          \
-      return rc;                                                                                  \
-    per_cu = std::max(1, std::min(per_cu, CS_MAX_WAVES_PER_CU));                                  \
+    static std::atomic<int> cached{0}; /* resident workgroups per CU, queried once */             \
+    int per_cu = cached.load(std::memory_order_relaxed);                                          \
+    if (per_cu == 0) {                                                                            \
+      if (int rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(                        \
+                                 &per_cu, reinterpret_cast<const void*>(kern), 64, lds),          \
+                             "moe_gemm_stream: occupancy"))                                        \
+        return rc;                                                                                \
+      per_cu = std::max(1, std::min(per_cu, CS_MAX_WAVES_PER_CU));                                \
+      cached.store(per_cu, std::memory_order_relaxed);                                            \
+    }                                                                                             \
     const unsigned grid = unsigned(std::min<int64_t>(n_items, int64_t(cus) * per_cu));           \
     hipLaunchKernelGGL(kern, dim3(grid), dim3(64), lds, s,                                        \
                        reinterpret_cast<eg_elem<DT>*>(out),                                       \
